@@ -1,0 +1,452 @@
+/* xt_oracle.c - CPU restatement of the reference's FP8 / EVA02-L path. TEST INFRASTRUCTURE ONLY: the product never
+ * links, loads or calls this file; tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it as the
+ * checker. Built with -O2 -ffp-contract=off (no fast-math): every fused multiply-add is an explicit fmaf().
+ * Conventions and the reference lines each part follows are in xt_oracle.h.
+ */
+#include "xt_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
+
+static inline uint32_t f2u(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+static inline float u2f(uint32_t u)
+{
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * E4M3 codec. OCP E4M3 "fn": bias 7, 3 mantissa bits, subnormals m/8 * 2^-6, max finite 448 (0x7E), 0x7F NaN.
+ * Encode = round to nearest even, then saturate to +-448 (kern_common.cuh:99 __NV_SATFINITE; export_eva.py:65
+ * clips to +-448 before the RNE cast, which is the same map for finite inputs).
+ * ------------------------------------------------------------------------------------------------------------- */
+uint8_t xo_e4m3_encode(float x)
+{
+    uint32_t u, a, e, m, keep, rem;
+    uint8_t sign;
+    float ax, q;
+
+    u = f2u(x);
+    sign = (uint8_t)((u >> 24) & 0x80);
+    a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7f;          /* NaN stays NaN */
+    ax = u2f(a);
+    if (ax >= 448.0f) return sign | 0x7e;             /* saturate (covers +-inf) */
+    if (ax < 0x1p-6f) {                               /* subnormal range: multiples of 2^-9 */
+        q = nearbyintf(ax * 512.0f);                  /* exact scaling, RNE to an integer 0..8 */
+        return sign | (uint8_t)q;                     /* 8 -> 0x08 = 2^-6, the smallest normal */
+    }
+    e = (a >> 23) - 127;                              /* unbiased exponent, -6..8 */
+    m = a & 0x7fffffu;
+    keep = m >> 20;
+    rem = m & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (keep & 1))) keep++;
+    if (keep == 8) {
+        keep = 0;
+        e++;
+    }
+    return sign | (uint8_t)(((e + 7) << 3) | keep);
+}
+
+float xo_e4m3_decode(uint8_t b)
+{
+    int s, e, m;
+    float v;
+
+    s = b >> 7;
+    e = (b >> 3) & 15;
+    m = b & 7;
+    if (e == 15 && m == 7) return NAN;
+    v = e ? ldexpf(1.0f + m / 8.0f, e - 7) : ldexpf(m / 8.0f, -6);
+    return s ? -v : v;
+}
+
+void xo_e4m3_encode_bits(uint32_t first, uint32_t count, uint8_t *out, int threads)
+{
+    int64_t i;
+
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for num_threads(threads) schedule(static)
+#else
+    (void)threads;
+#endif
+    for (i = 0; i < (int64_t)count; i++) out[i] = xo_e4m3_encode(u2f(first + (uint32_t)i));
+}
+
+void xo_e4m3_encode_n(const float *x, size_t n, uint8_t *out)
+{
+    size_t i;
+
+    for (i = 0; i < n; i++) out[i] = xo_e4m3_encode(x[i]);
+}
+
+/* bf16 / fp16, round to nearest even */
+uint16_t xo_f32_to_bf16(float x)
+{
+    uint32_t u;
+
+    u = f2u(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1);
+    return (uint16_t)(u >> 16);
+}
+
+float xo_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t xo_f32_to_f16(float x)
+{
+    uint32_t u, a, sign, e, m, keep, rem, shift;
+    float ax;
+
+    u = f2u(x);
+    sign = (u >> 16) & 0x8000u;
+    a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds to inf */
+    ax = u2f(a);
+    if (ax < 0x1p-14f) {                                    /* fp16 subnormal: multiples of 2^-24 */
+        return (uint16_t)(sign | (uint32_t)nearbyintf(ax * 0x1p24f));
+    }
+    e = (a >> 23) - 127;
+    m = a & 0x7fffffu;
+    shift = 13;
+    keep = m >> shift;
+    rem = m & ((1u << shift) - 1);
+    if (rem > (1u << (shift - 1)) || (rem == (1u << (shift - 1)) && (keep & 1))) keep++;
+    if (keep == 1024) {
+        keep = 0;
+        e++;
+    }
+    return (uint16_t)(sign | ((e + 15) << 10) | keep);
+}
+
+float xo_f16_to_f32(uint16_t h)
+{
+    uint32_t s, e, m;
+    float v;
+
+    s = h >> 15;
+    e = (h >> 10) & 31;
+    m = h & 1023;
+    if (e == 31) v = m ? NAN : INFINITY;
+    else if (e == 0) v = ldexpf((float)m, -24);
+    else v = ldexpf(1.0f + m / 1024.0f, (int)e - 15);
+    return s ? -v : v;
+}
+
+float xo_block_scale(float amax)
+{
+    /* a block whose |max| is below 2^-116 (where 448 / amax would leave the normal range) is a zero block */
+    return amax < 0x1p-116f ? 1.0f : amax / 448.0f;
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Packing (export_eva.py:64-66 per tensor -> per block; eva.h:408 + kern_common.cuh:106 for activations)
+ * ------------------------------------------------------------------------------------------------------------- */
+void xo_quant_act(const float *x, int M, int K, int ldx, uint8_t *q, int ldq, float *s, int lds)
+{
+    int m, kb, j;
+    float amax, sc, inv;
+    const float *xr;
+
+    for (m = 0; m < M; m++)
+        for (kb = 0; kb < K / 128; kb++) {
+            xr = x + (size_t)m * ldx + kb * 128;
+            for (j = 0, amax = 0.0f; j < 128; j++) amax = fmaxf(amax, fabsf(xr[j]));
+            sc = xo_block_scale(amax);
+            inv = 1.0f / sc;
+            s[(size_t)kb * lds + m] = sc;
+            for (j = 0; j < 128; j++) q[(size_t)m * ldq + kb * 128 + j] = xo_e4m3_encode(xr[j] * inv);
+        }
+}
+
+void xo_quant_w(const float *w, int N, int K, uint8_t *q, float *s)
+{
+    int nb, kb, n, k, NB, KB;
+    float amax, sc;
+
+    NB = (N + 127) / 128;
+    KB = K / 128;
+    memset(q, 0, (size_t)NB * 128 * K);
+    for (nb = 0; nb < NB; nb++)
+        for (kb = 0; kb < KB; kb++) {
+            amax = 0.0f;
+            for (n = nb * 128; n < nb * 128 + 128 && n < N; n++)
+                for (k = kb * 128; k < kb * 128 + 128; k++) amax = fmaxf(amax, fabsf(w[(size_t)n * K + k]));
+            sc = xo_block_scale(amax);
+            s[(size_t)nb * KB + kb] = sc;
+            for (n = nb * 128; n < nb * 128 + 128 && n < N; n++)
+                for (k = kb * 128; k < kb * 128 + 128; k++)
+                    q[(size_t)n * K + k] = xo_e4m3_encode(w[(size_t)n * K + k] / sc);
+        }
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Block-scaled GEMM references. The fp64 form follows kcheck.c:117-126 (fp64 loops over decoded E4M3 operands on
+ * sampled rows), with the scale product moved inside the K-block sum.
+ * ------------------------------------------------------------------------------------------------------------- */
+static float E4LUT[256];
+static int e4lut_ready;
+
+static void e4lut_init(void)
+{
+    int i;
+
+    if (e4lut_ready) return;
+    for (i = 0; i < 256; i++) E4LUT[i] = xo_e4m3_decode((uint8_t)i);
+    e4lut_ready = 1;
+}
+
+void xo_gemm_bs_f64_rows(const uint8_t *qa, int lda, const float *sa, int lds, const uint8_t *qw, const float *sw,
+                         int N, int K, const int *rows, int nrows, double *out)
+{
+    int r, n, kb, k, m, KB;
+    double acc, part;
+
+    e4lut_init();
+    KB = K / 128;
+#pragma omp parallel for private(n, kb, k, m, acc, part) schedule(static)
+    for (r = 0; r < nrows; r++) {
+        m = rows[r];
+        for (n = 0; n < N; n++) {
+            acc = 0.0;
+            for (kb = 0; kb < KB; kb++) {
+                part = 0.0;
+                for (k = kb * 128; k < kb * 128 + 128; k++)
+                    part += (double)E4LUT[qa[(size_t)m * lda + k]] * (double)E4LUT[qw[(size_t)n * K + k]];
+                acc += part * (double)sa[(size_t)kb * lds + m] * (double)sw[(size_t)(n / 128) * KB + kb];
+            }
+            out[(size_t)r * N + n] = acc;
+        }
+    }
+}
+
+int xo_max_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* Scalar "repo convention" loop: one row, all N columns, decoded operands. */
+static void gemm_row_scalar(const float *a, const float *wd, const float *sa_row, const float *sw, int N, int K,
+                            float *acc)
+{
+    int n, kb, k, KB;
+    float part, sc;
+
+    KB = K / 128;
+    for (n = 0; n < N; n++) {
+        acc[n] = 0.0f;
+        for (kb = 0; kb < KB; kb++) {
+            part = 0.0f;
+            for (k = kb * 128; k < kb * 128 + 128; k++) part = fmaf(a[k], wd[(size_t)n * K + k], part);
+            sc = sa_row[kb] * sw[(size_t)(n / 128) * KB + kb];
+            acc[n] = fmaf(part, sc, acc[n]);
+        }
+    }
+}
+
+#if defined(__x86_64__)
+/* AVX2 + FMA: 2 rows x 4 columns register block, 8 lanes along k, horizontal sum per K block. */
+__attribute__((target("avx2,fma"))) static inline float hsum8(__m256 v)
+{
+    __m128 lo, hi;
+
+    lo = _mm256_castps256_ps128(v);
+    hi = _mm256_extractf128_ps(v, 1);
+    lo = _mm_add_ps(lo, hi);
+    lo = _mm_add_ps(lo, _mm_movehl_ps(lo, lo));
+    lo = _mm_add_ss(lo, _mm_shuffle_ps(lo, lo, 1));
+    return _mm_cvtss_f32(lo);
+}
+
+__attribute__((target("avx2,fma"))) static void gemm_rows2_avx2(const float *a0, const float *a1, const float *wd,
+                                                               const float *sa0, const float *sa1, const float *sw,
+                                                               int N, int K, float *acc0, float *acc1)
+{
+    int n, kb, k, j, KB;
+    __m256 c[2][4], va0, va1, vw;
+    float sc;
+
+    KB = K / 128;
+    for (n = 0; n < N; n += 4) {
+        float r0[4] = {0, 0, 0, 0}, r1[4] = {0, 0, 0, 0};
+        int nn = N - n < 4 ? N - n : 4;
+        for (kb = 0; kb < KB; kb++) {
+            for (j = 0; j < 4; j++) c[0][j] = c[1][j] = _mm256_setzero_ps();
+            for (k = kb * 128; k < kb * 128 + 128; k += 8) {
+                va0 = _mm256_loadu_ps(a0 + k);
+                va1 = _mm256_loadu_ps(a1 + k);
+                for (j = 0; j < nn; j++) {
+                    vw = _mm256_loadu_ps(wd + (size_t)(n + j) * K + k);
+                    c[0][j] = _mm256_fmadd_ps(va0, vw, c[0][j]);
+                    c[1][j] = _mm256_fmadd_ps(va1, vw, c[1][j]);
+                }
+            }
+            for (j = 0; j < nn; j++) {
+                sc = sa0[kb] * sw[(size_t)((n + j) / 128) * KB + kb];
+                r0[j] = fmaf(hsum8(c[0][j]), sc, r0[j]);
+                sc = sa1[kb] * sw[(size_t)((n + j) / 128) * KB + kb];
+                r1[j] = fmaf(hsum8(c[1][j]), sc, r1[j]);
+            }
+        }
+        for (j = 0; j < nn; j++) {
+            acc0[n + j] = r0[j];
+            acc1[n + j] = r1[j];
+        }
+    }
+}
+#endif
+
+void xo_gemm_bs_f32(const uint8_t *qa, int lda, const float *sa, int lds, const uint8_t *qw, const float *sw, int N,
+                    int K, int m0, int m1, float *cf, uint16_t *cb, int ldc, int threads, int avx2)
+{
+    float *wd;
+    int KB, m, n, kb, mi;
+    size_t i;
+
+    e4lut_init();
+    KB = K / 128;
+    wd = (float *)malloc((size_t)N * K * sizeof(float));
+    if (!wd) return;
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for num_threads(threads) schedule(static)
+#else
+    (void)threads;
+#endif
+    for (n = 0; n < N; n++)
+        for (i = 0; i < (size_t)K; i++) wd[(size_t)n * K + i] = E4LUT[qw[(size_t)n * K + i]];
+#ifdef _OPENMP
+#pragma omp parallel num_threads(threads) private(m, n, kb, mi)
+#endif
+    {
+        float *a0 = (float *)malloc((size_t)2 * K * sizeof(float));
+        float *acc = (float *)malloc((size_t)2 * N * sizeof(float));
+        float sar[2][64];
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (m = m0; m < m1; m += 2) {
+            int two = (m + 1 < m1) ? 2 : 1;
+            for (mi = 0; mi < two; mi++) {
+                for (i = 0; i < (size_t)K; i++) a0[(size_t)mi * K + i] = E4LUT[qa[(size_t)(m + mi) * lda + i]];
+                for (kb = 0; kb < KB && kb < 64; kb++) sar[mi][kb] = sa[(size_t)kb * lds + m + mi];
+            }
+#if defined(__x86_64__)
+            if (avx2 && two == 2)
+                gemm_rows2_avx2(a0, a0 + K, wd, sar[0], sar[1], sw, N, K, acc, acc + N);
+            else
+#endif
+                for (mi = 0; mi < two; mi++) gemm_row_scalar(a0 + (size_t)mi * K, wd, sar[mi], sw, N, K, acc + (size_t)mi * N);
+            for (mi = 0; mi < two; mi++)
+                for (n = 0; n < N; n++) {
+                    if (cf) cf[(size_t)(m + mi) * ldc + n] = acc[(size_t)mi * N + n];
+                    if (cb) cb[(size_t)(m + mi) * ldc + n] = xo_f32_to_bf16(acc[(size_t)mi * N + n]);
+                }
+        }
+        free(a0);
+        free(acc);
+    }
+    free(wd);
+}
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * LayerNorm over 1024 -> E4M3 with 1x128 scales (kern_common.cuh:147-186 k_ln / ln_row<1>: two-pass mean and
+ * variance, eps 1e-6, y = (x - mean) * rstd * gamma + beta), restated in the summation order of the device kernel
+ * so the packed bytes are comparable bit for bit: lane l of a 64-lane wave owns elements [8l, 8l+8) and
+ * [512+8l, 512+8l+8), sums them in that order, and the 64 lane sums meet in an xor butterfly (32, 16, ..., 1).
+ * rstd = 1 / sqrt(var + eps) with IEEE sqrt and division (the reference's rsqrtf under fast-math is not restated).
+ * ------------------------------------------------------------------------------------------------------------- */
+static float wave_sum64(float *v)
+{
+    float t[64];
+    int off, i;
+
+    for (off = 32; off >= 1; off >>= 1) {
+        for (i = 0; i < 64; i++) t[i] = v[i] + v[i ^ off];
+        memcpy(v, t, sizeof(t));
+    }
+    return v[0];
+}
+
+static inline int ln_elem(int lane, int j) { return j < 8 ? 8 * lane + j : 512 + 8 * lane + (j - 8); }
+
+void xo_ln_quant(const uint16_t *x, const float *g, const float *b, int M, uint8_t *q, float *s, int lds, float *y)
+{
+    int m;
+
+#pragma omp parallel for schedule(static)
+    for (m = 0; m < M; m++) {
+        float v[1024], ls[64], yy[1024], mean, var, rstd, d, amax, sc, inv;
+        int l, j, kb, e;
+
+        for (e = 0; e < 1024; e++) v[e] = xo_f16_to_f32(x[(size_t)m * 1024 + e]);
+        for (l = 0; l < 64; l++) {
+            ls[l] = 0.0f;
+            for (j = 0; j < 16; j++) ls[l] += v[ln_elem(l, j)];
+        }
+        mean = wave_sum64(ls) * (1.0f / 1024.0f);
+        for (l = 0; l < 64; l++) {
+            ls[l] = 0.0f;
+            for (j = 0; j < 16; j++) {
+                d = v[ln_elem(l, j)] - mean;
+                ls[l] = fmaf(d, d, ls[l]);
+            }
+        }
+        var = wave_sum64(ls) * (1.0f / 1024.0f);
+        rstd = 1.0f / sqrtf(var + 1e-6f);
+        for (e = 0; e < 1024; e++) yy[e] = fmaf((v[e] - mean) * rstd, g[e], b[e]);
+        if (y) memcpy(y + (size_t)m * 1024, yy, sizeof(yy));
+        for (kb = 0; kb < 8; kb++) {
+            for (e = kb * 128, amax = 0.0f; e < kb * 128 + 128; e++) amax = fmaxf(amax, fabsf(yy[e]));
+            sc = xo_block_scale(amax);
+            inv = 1.0f / sc;
+            s[(size_t)kb * lds + m] = sc;
+            for (e = kb * 128; e < kb * 128 + 128; e++) q[(size_t)m * 1024 + e] = xo_e4m3_encode(yy[e] * inv);
+        }
+    }
+}
+
+/* kcheck.c:21-22, 106-107: the reference kernel checker's LCG operand generators */
+void xo_lcg_frand(uint32_t *rs, size_t n, float *out)
+{
+    size_t i;
+
+    for (i = 0; i < n; i++) {
+        *rs = *rs * 1664525u + 1013904223u;
+        out[i] = (float)(*rs >> 8) / 8388608.0f - 1.0f;
+    }
+}
+
+void xo_lcg_e4m3(uint32_t *rs, size_t n, uint8_t *out)
+{
+    size_t i;
+    uint8_t b;
+
+    for (i = 0; i < n; i++) {
+        do {
+            *rs = *rs * 1664525u + 1013904223u;
+            b = (uint8_t)(*rs >> 24);
+        } while ((b & 0x7F) == 0x7F || ((b >> 3) & 15) > 9);
+        out[i] = b;
+    }
+}

@@ -1,0 +1,188 @@
+// quant.hip - E4M3 packing with per-block fp32 scales (activations 1x128, weights 128x128) and the standalone
+// block-scaled GEMM. Reference roles: q2 / st4 / st8h (src/engine/kern_common.cuh:97-128) for activations,
+// fp8() (src/tools/export_eva.py:64-66) for weights, gemm8 (kern_common.cuh:271-356) for the GEMM.
+#include "gemm_core.h"
+#include "xt_abi.h"
+
+// ---- activations: x [M][ldx] (bf16 or fp32) -> q [M][ldq] E4M3, s [K/128][lds] ----
+// One thread per 8 consecutive elements; the 16 threads of one 128-element block are 16 aligned lanes.
+template <typename TIn>
+__device__ __forceinline__ void load8(const TIn *p, float *v);
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t *p, float *v)
+{
+    const uint4 u = *(const uint4 *)p;
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+template <>
+__device__ __forceinline__ void load8<float>(const float *p, float *v)
+{
+    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <typename TIn>
+__global__ void __launch_bounds__(256) k_quant_act(const TIn *__restrict__ x, int ldx, int M, int K,
+                                                   uint8_t *__restrict__ q, int ldq, float *__restrict__ s, int lds)
+{
+    const int cpr = K >> 3;  // 8-element chunks per row
+    const long total = (long)M * cpr;
+    for (long t = (long)blockIdx.x * 256 + threadIdx.x; t < total; t += (long)gridDim.x * 256) {
+        // the 16 lanes of a block share every trip: total and the stride are multiples of 16
+        const int row = (int)(t / cpr), ch = (int)(t - (long)row * cpr);
+        float v[8], amax = 0.f;
+        load8<TIn>(x + (size_t)row * ldx + ch * 8, v);
+#pragma unroll
+        for (int i = 0; i < 8; i++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+        amax = group_max<16>(amax);
+        const float sc = block_scale(amax), inv = 1.0f / sc;
+        uint2 o;
+        o.x = e4_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+        o.y = e4_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+        *(uint2 *)(q + (size_t)row * ldq + ch * 8) = o;
+        if ((ch & 15) == 0) s[(size_t)(ch >> 4) * lds + row] = sc;
+    }
+}
+
+// ---- weights: w [N][K] fp32 -> q [ceil(N/128)*128][K] E4M3 (pad rows zero), s [ceil(N/128)][K/128] ----
+// One 256-thread block per 128 x 128 block: 64 elements per thread, |max| through LDS, then q = sat_rne(w / s).
+__global__ void __launch_bounds__(256) k_quant_w(const float *__restrict__ w, int N, int K, uint8_t *__restrict__ q,
+                                                 float *__restrict__ s)
+{
+    __shared__ float red[4];
+    const int kb = blockIdx.x, nb = blockIdx.y, KB = K >> 7;
+    const int t = threadIdx.x, c = t & 15, r0 = t >> 4;  // 16 threads x 8 columns cover a 128-wide row
+    float amax = 0.f;
+    for (int r = r0; r < 128; r += 16) {
+        const int n = nb * 128 + r;
+        if (n < N) {
+            float v[8];
+            load8<float>(w + (size_t)n * K + kb * 128 + c * 8, v);
+#pragma unroll
+            for (int i = 0; i < 8; i++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+        }
+    }
+    amax = wave_max(amax);
+    if ((t & 63) == 0) red[t >> 6] = amax;
+    __syncthreads();
+    amax = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const float sc = block_scale(amax);
+    if (t == 0) s[(size_t)nb * KB + kb] = sc;
+    for (int r = r0; r < 128; r += 16) {
+        const int n = nb * 128 + r;
+        uint2 o = make_uint2(0, 0);
+        if (n < N) {
+            float v[8];
+            load8<float>(w + (size_t)n * K + kb * 128 + c * 8, v);
+            o.x = e4_pack4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
+            o.y = e4_pack4(v[4] / sc, v[5] / sc, v[6] / sc, v[7] / sc);
+        }
+        *(uint2 *)(q + (size_t)n * K + kb * 128 + c * 8) = o;
+    }
+}
+
+// ---- encoder check: E4M3 of the fp32 bit patterns first .. first + count - 1 ----
+__global__ void __launch_bounds__(256) k_e4m3_bits(uint32_t first, uint32_t count, uint8_t *__restrict__ out)
+{
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u)
+        out[i] = (uint8_t)e4_pack2(__uint_as_float(first + i), 0.f);
+}
+
+// ---- standalone block-scaled GEMM: C [M][ldc] = bf16 or fp32 of the block-scaled product ----
+template <int BM, int BN, int WM, int WN, int OUT>  // OUT 0: bf16, 1: fp32
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64) k_gemm(const uint8_t *__restrict__ A, int lda,
+                                                                  const float *__restrict__ sa, int lds,
+                                                                  const uint8_t *__restrict__ W,
+                                                                  const float *__restrict__ sw, void *__restrict__ Cp,
+                                                                  int ldc, int M, int N, int K)
+{
+    using C = BsCfg<BM, BN, WM, WN>;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    v4f acc[C::TM][C::TN];
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, lane = threadIdx.x & 63;
+    bs_mainloop<BM, BN, WM, WN>(A, lda, sa, lds, W, sw, M, K, m0, n0, smem, acc);
+    int wm0, wn0;
+    bs_wave_origin<BM, BN, WM, WN>(wm0, wn0);
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            const int col = n0 + wn0 + 16 * j + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = m0 + wm0 + 16 * i + 4 * (lane >> 4) + r;
+                if (row < M && col < N) {
+                    if (OUT == 0) ((uint16_t *)Cp)[(size_t)row * ldc + col] = f2bf(acc[i][j][r]);
+                    else ((float *)Cp)[(size_t)row * ldc + col] = acc[i][j][r];
+                }
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// C-ABI launchers
+// ---------------------------------------------------------------------------------------------------------------
+static int grid_for(long threads)
+{
+    long b = (threads + 255) / 256;
+    return (int)(b < 1 ? 1 : b > 65535 ? 65535 : b);
+}
+
+extern "C" int eva_k_quant_act(const void *x, int in_kind, int ldx, int M, int K, void *q, int ldq, float *s, int lds,
+                               void *stream)
+{
+    if (M < 0 || K % 128 || ldx < K || ldq < K || lds < M || (in_kind != 0 && in_kind != 1) || ldx % 8 || ldq % 8)
+        return xt_fail("eva_k_quant_act",
+                       "bad shape (K % 128, ldx >= K, ldq >= K, lds >= M, ldx and ldq multiples of 8, in_kind 0 or 1)");
+    if (((uintptr_t)x | (uintptr_t)q) & 15) return xt_fail("eva_k_quant_act", "x and q must be 16-byte aligned");
+    if (!M) return 0;
+    const long thr = (long)M * (K / 8);
+    if (in_kind == 0)
+        hipLaunchKernelGGL(k_quant_act<uint16_t>, dim3(grid_for(thr)), dim3(256), 0, (hipStream_t)stream,
+                           (const uint16_t *)x, ldx, M, K, (uint8_t *)q, ldq, s, lds);
+    else
+        hipLaunchKernelGGL(k_quant_act<float>, dim3(grid_for(thr)), dim3(256), 0, (hipStream_t)stream, (const float *)x,
+                           ldx, M, K, (uint8_t *)q, ldq, s, lds);
+    return xt_check("eva_k_quant_act");
+}
+
+extern "C" int eva_k_quant_w(const float *w, int N, int K, void *q, float *s, void *stream)
+{
+    if (N <= 0 || K <= 0 || K % 128) return xt_fail("eva_k_quant_w", "bad shape (N > 0, K % 128 == 0)");
+    if (((uintptr_t)w | (uintptr_t)q) & 15) return xt_fail("eva_k_quant_w", "w and q must be 16-byte aligned");
+    hipLaunchKernelGGL(k_quant_w, dim3(K / 128, (N + 127) / 128), dim3(256), 0, (hipStream_t)stream, w, N, K,
+                       (uint8_t *)q, s);
+    return xt_check("eva_k_quant_w");
+}
+
+extern "C" int eva_k_e4m3_bits(uint32_t first, uint32_t count, void *out, void *stream)
+{
+    if (!count) return 0;
+    hipLaunchKernelGGL(k_e4m3_bits, dim3(grid_for(count)), dim3(256), 0, (hipStream_t)stream, first, count,
+                       (uint8_t *)out);
+    return xt_check("eva_k_e4m3_bits");
+}
+
+extern "C" int eva_k_gemm(const void *qa, int lda, const float *sa, int lds, const void *qw, const float *sw, int M,
+                          int N, int K, void *c, int ldc, int out_kind, void *stream)
+{
+    if (M < 0 || N <= 0 || K <= 0 || K % 128 || lda < K || lda % 16 || lds < M || ldc < N ||
+        (out_kind != 0 && out_kind != 1))
+        return xt_fail("eva_k_gemm", "bad shape (K % 128, lda >= K and a multiple of 16, lds >= M, ldc >= N, out_kind 0 or 1)");
+    if (((uintptr_t)qa | (uintptr_t)qw) & 15) return xt_fail("eva_k_gemm", "qa and qw must be 16-byte aligned");
+    if (!M) return 0;
+    const dim3 grid((N + 127) / 128, (M + 127) / 128);
+    if (out_kind == 0)
+        hipLaunchKernelGGL((k_gemm<128, 128, 64, 64, 0>), grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t *)qa,
+                           lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+    else
+        hipLaunchKernelGGL((k_gemm<128, 128, 64, 64, 1>), grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t *)qa,
+                           lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+    return xt_check("eva_k_gemm");
+}

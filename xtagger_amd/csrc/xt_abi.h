@@ -1,0 +1,24 @@
+// xt_abi.h - error convention of the C-ABI: every entry point returns 0, or -1 after printing
+// "eva: <what>: <reason>" to stderr (the reference's EVA_CU convention, src/engine/eva.h:153-176).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+
+static inline int xt_fail(const char *what, const char *why)
+{
+    fprintf(stderr, "eva: %s: %s\n", what, why);
+    return -1;
+}
+
+static inline int xt_hip(hipError_t r, const char *what)
+{
+    if (r == hipSuccess) return 0;
+    return xt_fail(what, hipGetErrorString(r));
+}
+
+static inline int xt_check(const char *what) { return xt_hip(hipGetLastError(), what); }
+
+#define XT_HIP(call)                                 \
+    do {                                             \
+        if (xt_hip((call), #call)) return -1;        \
+    } while (0)

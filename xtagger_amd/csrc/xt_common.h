@@ -1,0 +1,95 @@
+// xt_common.h - device helpers shared by the EVA02-L kernels for gfx950 (CDNA4): E4M3 / bf16 / fp16 codecs, wave64
+// reductions and the MFMA operand types. Compiled with -ffp-contract=off: every fused multiply-add is written as
+// __builtin_fmaf so host restatements can follow the same rounding steps.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+#define XT_D 1024       // model width
+#define XT_T 1025       // tokens per image: cls + 32 x 32 patches
+#define XT_NP 1024      // patches per image
+#define XT_K0P 592      // patch operand columns (588 + 4 zero)
+#define XT_HID 2730     // SwiGLU hidden units
+#define XT_HIDP 2816    // hidden padded to 22 blocks of 128
+#define XT_NH 16        // heads
+#define XT_HD 64        // head dim
+#define XT_TP 1088      // attention rows padded to 17 x 64
+#define XT_EPS 1e-6f
+#define XT_E4MAX 448.0f
+
+// ---- E4M3 (OCP "fn") ----
+// Hardware v_cvt_pk_fp8_f32 rounds to nearest even on gfx950; the clamp to +-448 first gives saturation
+// (the reference's __NV_SATFINITE, kern_common.cuh:99). NaN inputs are outside the contract.
+__device__ __forceinline__ float e4_clamp(float x) { return __builtin_fminf(__builtin_fmaxf(x, -XT_E4MAX), XT_E4MAX); }
+
+// two floats -> bytes 0, 1 of the result
+__device__ __forceinline__ uint32_t e4_pack2(float a, float b)
+{
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(e4_clamp(a), e4_clamp(b), 0, false) & 0xffffu;
+}
+
+// four floats -> one little-endian 32-bit word
+__device__ __forceinline__ uint32_t e4_pack4(float a, float b, float c, float d)
+{
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(e4_clamp(a), e4_clamp(b), 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(e4_clamp(c), e4_clamp(d), w, true);
+}
+
+// Block scale from a block |max|: amax / 448 (IEEE division), 1 for a zero block (|max| < 2^-116).
+__device__ __forceinline__ float block_scale(float amax) { return amax < 0x1p-116f ? 1.0f : amax / XT_E4MAX; }
+
+// ---- bf16 / fp16 (round to nearest even) ----
+__device__ __forceinline__ uint16_t f2bf(float x)
+{
+    uint32_t u = __float_as_uint(x);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ uint16_t f2h(float x)
+{
+    _Float16 h = (_Float16)x;
+    return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float h2f(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
+
+// ---- wave64 reductions (xor butterfly: every lane ends with the same value) ----
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+// max over aligned groups of G lanes (G a power of two <= 64)
+template <int G>
+__device__ __forceinline__ float group_max(float v)
+{
+#pragma unroll
+    for (int off = G / 2; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+template <int G>
+__device__ __forceinline__ float group_sum(float v)
+{
+#pragma unroll
+    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ v4f mfma_e4m3_16x16x128(v8i a, v8i b)
+{
+    v4f z = {0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
+}
