@@ -1,0 +1,264 @@
+"""Benchmark of the block-scaled FP8 EVA02-L path on one MI355X; prints one JSON line.
+
+value: TFLOP/s of one "step" = the four EVA02-L layer GEMMs at batch 8 (M = 8200 token rows) with their fused
+epilogues, exactly as the forward runs them: qkv 1024->3072 (+ RoPE, bf16 attention layouts), out-proj 1024->1024
+(+ fp16 residual), fc1 1024->2x2730 (+ SwiGLU, E4M3 1x128 repack, row sums), fc2 2730->1024 (+ folded MLP LayerNorm,
+residual). Operands are resident in HBM: activations N(0,1) packed E4M3 with 1x128 fp32 scales, weights N(0,0.02)
+packed per 128x128 block. FLOPs are counted on unpadded shapes: 206.33 GFLOP per step.
+
+Also reported: the single qkv GEMM at M=1025 (batch 1, bf16 out), the full wd forward at batch 32 (448^2 inputs,
+images/s, graph replays with inputs resident), the dominant kernel's roofline (fc1, timed with HIP events on its
+stream), and the oracle's CPU block-scaled GEMM on the same step (cpu_baseline).
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "FP8 block-GEMM TFLOP/s (% FP8 MFMA peak) + EVA02-L 448² images/s, 1 GPU"
+PEAK_FP8 = 5000.0   # TFLOP/s, MI355X dense FP8 (OCP E4M3) MFMA
+T, D, HID, HIDP = 1025, 1024, 2730, 2816
+
+
+def gemm_flops(M):
+    return {"qkv": 2.0 * M * 3 * D * D, "oproj": 2.0 * M * D * D, "fc1": 2.0 * M * 2 * HID * D,
+            "fc2": 2.0 * M * D * HID}
+
+
+class LayerStep:
+    """Packed operands and output buffers for the four layer GEMMs at M rows (nb = M / 1025 images)."""
+
+    def __init__(self, torch, L, M, seed=0):
+        dev = torch.device("cuda:0")
+        self.torch, self.L, self.M = torch, L, M
+        self.nb = M // T
+        self.st = torch.cuda.current_stream().cuda_stream
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.lds = lds = (M + 255) // 256 * 256
+        t = lambda *s, dt=torch.uint8: torch.zeros(*s, dtype=dt, device=dev)
+        x = torch.randn(M, D, generator=g, device=dev)
+        h = torch.randn(M, HIDP, generator=g, device=dev) * 0.3
+        h[:, HID:] = 0
+        self.a8, self.as_ = t(M, D), t(8, lds, dt=torch.float32)
+        self.m8, self.ms = t(M, HIDP), t(22, lds, dt=torch.float32)
+        ck = lambda rc, w: L.check(rc, w)
+        ck(L.lib.eva_k_quant_act(L.ptr(x), 1, D, M, D, L.ptr(self.a8), D, L.ptr(self.as_), lds, self.st), "act")
+        ck(L.lib.eva_k_quant_act(L.ptr(h), 1, HIDP, M, HIDP, L.ptr(self.m8), HIDP, L.ptr(self.ms), lds, self.st), "h")
+        self.stat = torch.ones(22, lds, 2, dtype=torch.float32, device=dev)
+        self.stat[..., 1] = 2.0
+        scratch = torch.empty(2 * HIDP * D, dtype=torch.float32, device=dev)
+
+        def packw(n_in, k_in, n_out, k_out, perm=0, colscale=None):
+            w16 = (torch.randn(n_in, max(k_in, 1), generator=g, device=dev) * 0.02).half()
+            q, s = t(n_out, k_out), t(n_out // 128, k_out // 128, dt=torch.float32)
+            ck(L.lib.eva_k_prep_w(L.ptr(w16), k_in, n_in, k_in, n_out, k_out, perm,
+                                  L.ptr(colscale) if colscale is not None else None, L.ptr(scratch), L.ptr(q), L.ptr(s),
+                                  self.st), "prep")
+            return q, s
+
+        self.wqkv, self.sqkv = packw(3 * D, D, 3 * D, D, perm=1)
+        self.wo, self.so = packw(D, D, D, D)
+        self.w12, self.s12 = packw(2 * 2736, D, 2 * HIDP, D)
+        self.w2, self.s2 = packw(D, HID, D, HIDP)
+        self.cn = torch.randn(D, generator=g, device=dev) * 0.1
+        self.dn = torch.randn(D, generator=g, device=dev) * 0.01
+        self.cs = torch.rand(1024, 32, 2, generator=g, device=dev)
+        nb = self.nb
+        self.q = t(nb, 16, 1088, 64, dt=torch.int16)
+        self.k = t(nb, 16, 1088, 64, dt=torch.int16)
+        self.vt = t(nb, 16, 64, 1088, dt=torch.int16)
+        self.x = (torch.randn(M, D, generator=g, device=dev)).half()
+        self.fc1_out8 = t(M, HIDP)
+        self.fc1_ms = t(22, lds, dt=torch.float32)
+        self.fc1_stat = t(22, lds, 2, dt=torch.float32)
+        torch.cuda.synchronize()
+
+    def qkv(self):
+        L = self.L
+        return L.lib.eva_k_qkv(L.ptr(self.a8), L.ptr(self.as_), self.lds, L.ptr(self.wqkv), L.ptr(self.sqkv),
+                               L.ptr(self.cs), L.ptr(self.q), L.ptr(self.k), L.ptr(self.vt), self.M, self.st)
+
+    def oproj(self):
+        L = self.L
+        return L.lib.eva_k_oproj(L.ptr(self.a8), L.ptr(self.as_), self.lds, L.ptr(self.wo), L.ptr(self.so),
+                                 L.ptr(self.x), self.M, self.st)
+
+    def fc1(self):
+        L = self.L
+        return L.lib.eva_k_fc1(L.ptr(self.a8), L.ptr(self.as_), self.lds, L.ptr(self.w12), L.ptr(self.s12),
+                               L.ptr(self.fc1_out8), L.ptr(self.fc1_ms), L.ptr(self.fc1_stat), self.M, self.st)
+
+    def fc2(self):
+        L = self.L
+        return L.lib.eva_k_fc2(L.ptr(self.m8), L.ptr(self.ms), self.lds, L.ptr(self.w2), L.ptr(self.s2),
+                               L.ptr(self.stat), L.ptr(self.cn), L.ptr(self.dn), L.ptr(self.x), self.M, self.st)
+
+    def step(self):
+        for f in (self.qkv, self.oproj, self.fc1, self.fc2):
+            if f() != 0:
+                raise RuntimeError("layer GEMM launch failed")
+
+
+def time_launches(torch, fn, iters):
+    """Average duration of `iters` back-to-back launches, HIP events on the launch stream."""
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(iters):
+        if fn() != 0:
+            raise RuntimeError("launch failed")
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def bench_cfg1(torch, L, iters=50):
+    """Single block-scaled GEMM at the qkv shape, M=1025, bf16 out (TFLOP/s)."""
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream().cuda_stream
+    M, N, K = T, 3 * D, D
+    x = torch.randn(M, K, device=dev).bfloat16()
+    w = torch.randn(N, K, device=dev) * 0.02
+    qa = torch.empty(M, K, dtype=torch.uint8, device=dev)
+    sa = torch.empty(K // 128, M, device=dev)
+    qw = torch.empty(N, K, dtype=torch.uint8, device=dev)
+    sw = torch.empty(N // 128, K // 128, device=dev)
+    c = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    L.check(L.lib.eva_k_quant_act(L.ptr(x), 0, K, M, K, L.ptr(qa), K, L.ptr(sa), M, st), "qa")
+    L.check(L.lib.eva_k_quant_w(L.ptr(w), N, K, L.ptr(qw), L.ptr(sw), st), "qw")
+    f = lambda: L.lib.eva_k_gemm(L.ptr(qa), K, L.ptr(sa), M, L.ptr(qw), L.ptr(sw), M, N, K, L.ptr(c), N, 0, st)
+    time_launches(torch, f, 5)
+    ms = time_launches(torch, f, iters)
+    return 2.0 * M * N * K / ms / 1e9, ms
+
+
+def bench_forward(torch, nb=32, iters=5):
+    """Full wd forward (24 blocks + head 10861) at batch nb on a synthetic v2 blob: images/s with inputs resident."""
+    from xtagger_amd import blob
+    from xtagger_amd.engine import Engine
+    path = os.path.join(os.environ.get("TMPDIR", "/tmp"), "xtag_bench_eva02_v2.bin")
+    if not os.path.exists(path):
+        blob.write_v2(path, blob.synth_model(seed=0, nt=10861))
+    e = Engine(path, device=0, nb=nb)
+    e.ready()
+    inp = blob.synth_inputs(nb, seed=7)
+    e.submit(0, inp)                       # inputs land in the device buffer; later replays reuse them
+    e.wait(0, nb)
+    for _ in range(2):
+        e.run()
+    e.sync()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        e.run()
+    e.sync()
+    dt = (time.perf_counter() - t0) / iters
+    e.close()
+    return nb / dt, dt * 1e3
+
+
+def cpu_baseline(orc, M=T, rows=None):
+    """The oracle's block-scaled GEMM (E4M3 LUT decode, fp32 128-element dot per block, fma(partial, sa*sw, acc),
+    bf16 out; AVX2 + FMA, OpenMP) on the four layer GEMMs at M rows."""
+    import numpy as np
+    r = np.random.default_rng(0)
+    thr = len(os.sched_getaffinity(0))
+    total, secs = 0.0, 0.0
+    for N, K in ((3 * D, D), (D, D), (2 * HIDP, D), (D, HIDP)):
+        x = r.standard_normal((M, K)).astype(np.float32)
+        w = (r.standard_normal((N, K)) * 0.02).astype(np.float32)
+        qa, sa = orc.quant_act(x)
+        qw, sw = orc.quant_w(w)
+        t0 = time.perf_counter()
+        orc.gemm_f32(qa, sa, qw, sw, N, threads=thr, avx2=1, want_bf16=True)
+        secs += time.perf_counter() - t0
+        n_alg = {3 * D: 3 * D, D: D, 2 * HIDP: 2 * HID}[N]
+        k_alg = HID if K == HIDP else K
+        total += 2.0 * M * n_alg * k_alg
+    return total / secs / 1e12, thr, secs
+
+
+def traffic_from_profiles():
+    """HBM bytes per fc1 launch from the committed rocprofv3 PMC summary, if present."""
+    p = os.path.join(ROOT, "profiles", "fc1_m8200_hbm_traffic.txt")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.split("=")[1])
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-forward", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path has no collectives: images "
+              f"shard across GPUs with one engine per GPU)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from xtagger_amd import lib as L
+
+    M = 8 * T
+    st = LayerStep(torch, L, M)
+    fl = gemm_flops(M)
+    step_flops = sum(fl.values())
+    for _ in range(args.warmup):
+        st.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        st.step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    tflops = step_flops / (ms * 1e-3) / 1e12
+
+    per = {}
+    for name in ("qkv", "oproj", "fc1", "fc2"):
+        f = getattr(st, name)
+        time_launches(torch, f, 3)
+        kms = time_launches(torch, f, max(args.steps, 20))
+        per[name] = {"us": round(kms * 1e3, 2), "tflops": round(fl[name] / (kms * 1e-3) / 1e12, 1)}
+    fc1_ms = per["fc1"]["us"] * 1e-3
+    achieved = fl["fc1"] / (fc1_ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": "k_fc1 (M=8200)", "achieved": round(achieved, 1), "peak": PEAK_FP8,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP8, 4), "traffic": traffic_from_profiles(),
+            "algorithmic_flops_per_launch": fl["fc1"]}
+
+    cfg1, cfg1_ms = bench_cfg1(torch, L)
+    out = {"metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "e4m3 (fp32 accumulate)", "data": "synthetic",
+           "config": {"workload": "EVA02-L layer GEMMs with fused epilogues: qkv 1024->3072 +RoPE, proj 1024->1024 "
+                                  "+residual, fc1 1024->2x2730 +SwiGLU +E4M3 repack, fc2 2730->1024 +folded LN "
+                                  "+residual; M=8200 (batch 8); 1x128 act / 128x128 weight fp32 block scales",
+                      "M": M, "gflop_per_step": round(step_flops / 1e9, 2)},
+           "pct_fp8_peak": round(100 * tflops / PEAK_FP8, 2), "per_kernel": per,
+           "cfg1_qkv_gemm_m1025": {"tflops": round(cfg1, 1), "us": round(cfg1_ms * 1e3, 2)},
+           "roofline": roof}
+    if not args.no_forward:
+        ips, fms = bench_forward(torch)
+        out["forward_b32"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
+                              "tflops": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1)}
+    if not args.no_cpu:
+        from oracle import oracle as O
+        cpu_tf, thr, secs = cpu_baseline(O)
+        out["cpu_baseline"] = {"value": round(cpu_tf, 4), "unit": "TFLOP/s", "cores": thr, "kind": "port",
+                               "sample": f"the four layer GEMMs at M=1025 (batch 1, 51.6 GFLOP), block-scaled E4M3 "
+                                         f"semantics, bf16 out, AVX2+FMA C loop, OpenMP; {secs:.1f} s"}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -42,6 +42,46 @@ extern "C" {
 #define EVA_HIDP 2816                         /* hidden padded to 22 blocks of 128 (reference: 2736) */
 #define EVA_IN ((size_t)EVA_NP * EVA_K0P)     /* halves per model input */
 
+/* ---- engine (eva.h:109-151) ----
+ * Caller-allocated like the reference's eva struct. Callers read nt, nt0 and hpn[buf] (procimg.h:1689, 1981);
+ * everything else lives behind impl. */
+typedef struct eva_impl eva_impl;
+typedef struct {
+    uint32_t nt, ntp, nt0;                    /* nt = nt0 tags of the file + extra head rows */
+    uint32_t nb;                              /* model inputs per launch */
+    uint16_t *hpn[EVA_NBUF];                  /* with extra rows: fp16 head inputs [nb][1024] of each batch */
+    float *hout[EVA_NBUF];                    /* sigmoid scores [nb][nt] of each batch */
+    eva_impl *impl;
+} eva;
+
+/* eva.h:573. Reads the weight blob header and starts the device bring-up on its own thread. The blob is the
+ * reference's "EVA2" version-2 file (fp16 block weights, export_eva.py without a calibration file); the bring-up
+ * packs every block GEMM weight to E4M3 with 128x128 scales on the GPU, so no calibration pass is needed.
+ * pool / poolb: the caller's input pool (page-locked at bring-up; may be NULL). extra: head rows past the file's
+ * tags (tag stealing), written with eva_head_put. Batch EVA_NB. */
+int eva_open(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra);
+/* eva_open with the batch (model inputs per launch, 1..EVA_NBMAX) as a runtime parameter */
+int eva_open_nb(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra, uint32_t nb);
+int eva_ready(eva *e);                                              /* eva.h:607 */
+int eva_poll(eva *e);                                               /* eva.h:620 */
+/* eva.h:627. n <= nb inputs, each an fp16 [1024][592] patch operand (BGR in [-1,1], element c*196 + ky*14 + kx,
+ * columns 588..591 zero); buf < EVA_NBUF. Runs of inputs adjacent in memory go in one copy. */
+int eva_submit(eva *e, uint32_t buf, uint16_t *const *in, uint32_t n);
+int eva_query(eva *e, uint32_t buf);                                /* eva.h:662 */
+const float *eva_wait(eva *e, uint32_t buf);                        /* eva.h:667: scores [n][nt] */
+int eva_head_put(eva *e, uint32_t j, const uint16_t *w, float bias); /* eva.h:645: head row j, fp16 [1024] */
+int eva_head_get(eva *e, uint16_t *w, float *bias);                 /* eva.h:653: the file's nt0 rows */
+void eva_close(eva *e);                                             /* eva.h:704 */
+
+/* Resident-input path (no reference counterpart; used by benchmarks): the device input buffer
+ * [nb][1024][592] fp16, one forward on the engine stream with no host copies, the device scores [nb][nt] fp32,
+ * the engine stream, and a blocking wait on it. */
+void *eva_dev_input(eva *e);
+int eva_run(eva *e);
+const float *eva_dev_output(eva *e);
+void *eva_stream_handle(eva *e);
+int eva_sync(eva *e);
+
 /* ---- kernel launchers (device pointers; stream = hipStream_t or NULL) ---- */
 
 /* Activation packing (kern_common.cuh:97-128 q2 / st4 / st8h): x [M][ldx], in_kind 0 = bf16, 1 = fp32,
@@ -57,6 +97,49 @@ int eva_k_e4m3_bits(uint32_t first, uint32_t count, void *out, void *stream);
  * C [M][ldc] = sum_kb sa[kb][m] sw[n/128][kb] sum_k qa[m][k] qw[n][k]; out_kind 0 = bf16 (RNE), 1 = fp32. */
 int eva_k_gemm(const void *qa, int lda, const float *sa, int lds, const void *qw, const float *sw, int M, int N, int K,
                void *c, int ldc, int out_kind, void *stream);
+
+/* LayerNorm -> E4M3 (kern_common.cuh:147-186 k_ln): x fp16 [rows][1024] -> q [rows][1024], s [8][lds];
+ * eps 1e-6, two-pass mean / variance, y = fma((x - mean) * rstd, gamma, beta). */
+int eva_k_ln(const void *x, const float *g, const float *b, void *q, float *s, int rows, int lds, void *stream);
+/* QKV projection with the attention layouts as its epilogue (eva_kernels.cu:41-114 k_qkv): rows = nb * 1025;
+ * w from eva_k_prep_w(perm 1); cs [1024][32][2] RoPE (cos, sin) of patch tokens; q, k bf16 [nb][16][1088][64],
+ * vt bf16 [nb][16][64][1088] (padded rows are never written; keep them zero). */
+int eva_k_qkv(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *cs, void *q,
+              void *k, void *vt, int rows, void *stream);
+/* Attention (kern_common.cuh:403-543 flash8, eva_kernels.cu:116-122 k_flash) -> o8 E4M3 [nb*1025][1024] with 1x128
+ * scales os [8][lds]; o32 (may be NULL) receives the fp32 output before packing. */
+int eva_k_flash(const void *q, const void *k, const void *vt, void *o8, float *os, int lds, int nb, float *o32,
+                void *stream);
+/* Out-projection + residual (eva_kernels.cu:134-162 k_oproj): x fp16 [rows][1024] += a8 . Wo^T */
+int eva_k_oproj(const void *a8, const float *as, int lds, const void *w, const float *ws, void *x, int rows,
+                void *stream);
+/* fc1 + SwiGLU + E4M3 repack + row partials (eva_kernels.cu:211-279 k_fc1): h8 [rows][1024] x W12 [5632][1024]
+ * (16-unit g / x chunks) -> m8 [rows][2816] E4M3, ms [22][lds], stat [22][lds][2] = (sum h, sum h^2). */
+int eva_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8, float *ms,
+              float *stat, int rows, void *stream);
+/* fc2 with the MLP LayerNorm folded + residual (eva_kernels.cu:286-334 k_fc2): x += rstd (m8 . W~^T - mean c) + d */
+int eva_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *stat,
+              const float *cn, const float *dn, void *x, int rows, void *stream);
+/* Tag head (kern_common.cuh:679-727 k_headmv, here a block-scaled FP8 GEMM): out [nb][nt] = sigmoid(pq . Wh^T + hb) */
+int eva_k_head(const void *pq, const float *ps, int lds, const void *w, const float *ws, const float *hb, float *out,
+               int nb, int nt, void *stream);
+/* Patch embedding + position (eva_kernels.cu:126-130 k_pe, 21-33 k_embed): in fp16 [nb*1024][592], pe fp16
+ * [1024][592], pos fp32 [1025][1024] -> x fp16 [nb*1025][1024] */
+int eva_k_pe(const void *in, const void *pe, const float *pos, void *x, int nb, void *stream);
+/* Mean over patch tokens 1..1024 (eva_kernels.cu:402-431 k_pool): x [nb*1025][1024] -> p fp32 [nb][1024] */
+int eva_k_pool(const void *x, float *p, int nb, void *stream);
+/* Final LayerNorm (kern_common.cuh:188-192 k_lnh) -> fp16 pn [rows][1024] -> E4M3 q [rows][1024], s [8][lds] */
+int eva_k_lnh(const float *p, const float *g, const float *b, void *pn, void *q, float *s, int rows, int lds,
+              void *stream);
+/* Weight packing from fp16 (export_eva.py:52-119 transforms, per 128x128 block): w16 [n_in][ldw] -> fp32 scratch
+ * [n_out][k_out] (zero past n_in / k_in; perm 1 pair-splits the q and k heads of Wqkv; colscale may be NULL) ->
+ * q [ceil(n_out/128)*128][k_out], s [ceil(n_out/128)][k_out/128]. */
+int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_out, int perm, const float *colscale,
+                 float *scratch, void *q, float *s, void *stream);
+/* MLP-LN fold terms (export_eva.py:117-119): c[n] = sum_k dec(q[n][k]) s[n/128][k/128] over the packed W~
+ * [1024][2816], d[n] = sum_{k<2730} w2[n][k] beta[k] */
+int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const float *beta, float *c, float *d,
+                  void *stream);
 
 #ifdef __cplusplus
 }

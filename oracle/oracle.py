@@ -38,6 +38,17 @@ _SIGS = {
     "xo_gemm_bs_f32": (None, [_p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _p, _p, _i, _i, _i]),
     "xo_max_threads": (_i, []),
     "xo_ln_quant": (None, [_p, _p, _p, _i, _p, _p, _i, _p]),
+    "xo_qkv_epi": (None, [_p, _i, _p, _p, _p, _p]),
+    "xo_attention": (None, [_p, _p, _p, _i, _p, _i]),
+    "xo_fc1_epi": (None, [_p, _i, _p, _p]),
+    "xo_fc2_epi": (None, [_p, _i, _p, _p, _p, _p]),
+    "xo_oproj_epi": (None, [_p, _i, _p]),
+    "xo_embed": (None, [_p, _p, _p, _i, _p]),
+    "xo_pool": (None, [_p, _i, _p]),
+    "xo_lnh": (None, [_p, _p, _p, _i, _p, _p, _p, _i]),
+    "xo_fold_w2": (None, [_p, _i, _p, _p, _p, _p]),
+    "xo_fold_c": (None, [_p, _p, _p]),
+    "xo_forward": (_i, [_p, _p, _i, _i, _p, _p, _i]),
     "xo_lcg_frand": (None, [_p, C.c_size_t, _p]),
     "xo_lcg_e4m3": (None, [_p, C.c_size_t, _p]),
 }
@@ -47,8 +58,20 @@ for _n, (_r, _a) in _SIGS.items():
     _fn.argtypes = _a
 
 
+_LIVE = []   # arrays whose addresses were handed out for the C call in progress
+
+
 def _ptr(a):
-    return None if a is None else C.c_void_p(a.ctypes.data)
+    """Address of a numpy array; the array is kept alive until the next _done() (so temporaries made by _c() inline
+    in a call's argument list cannot be freed before the C function reads them)."""
+    if a is None:
+        return None
+    _LIVE.append(a)
+    return C.c_void_p(a.ctypes.data)
+
+
+def _done():
+    _LIVE.clear()
 
 
 def _c(a, dt):
@@ -57,6 +80,7 @@ def _c(a, dt):
 
 
 def e4m3_encode_bits(first, count, threads=0):
+    _done()
     out = np.empty(count, np.uint8)
     lib.xo_e4m3_encode_bits(first, count, _ptr(out), threads)
     return out
@@ -64,6 +88,7 @@ def e4m3_encode_bits(first, count, threads=0):
 
 def e4m3_encode(x):
     """fp32 array -> E4M3 bytes (via the bit-pattern encoder, vectorised)."""
+    _done()
     x = _c(x, np.float32)
     out = np.empty(x.shape, np.uint8)
     lib.xo_e4m3_encode_n(_ptr(x), x.size, _ptr(out))
@@ -74,11 +99,13 @@ E4M3_LUT = np.array([lib.xo_e4m3_decode(i) for i in range(256)], np.float32)
 
 
 def e4m3_decode(q):
+    _done()
     return E4M3_LUT[np.asarray(q, np.uint8)]
 
 
 def quant_act(x, lds=None):
     """x fp32 [M][K] -> (q uint8 [M][K], s fp32 [K/128][lds])."""
+    _done()
     x = _c(x, np.float32)
     M, K = x.shape
     lds = lds or M
@@ -90,6 +117,7 @@ def quant_act(x, lds=None):
 
 def quant_w(w):
     """w fp32 [N][K] -> (q uint8 [ceil(N/128)*128][K], s fp32 [ceil(N/128)][K/128])."""
+    _done()
     w = _c(w, np.float32)
     N, K = w.shape
     NB = (N + 127) // 128
@@ -100,6 +128,7 @@ def quant_w(w):
 
 
 def gemm_f64_rows(qa, sa, qw, sw, N, rows):
+    _done()
     qa = _c(qa, np.uint8)
     sa = _c(sa, np.float32)
     qw = _c(qw, np.uint8)
@@ -113,6 +142,7 @@ def gemm_f64_rows(qa, sa, qw, sw, N, rows):
 
 
 def gemm_f32(qa, sa, qw, sw, N, m0=0, m1=None, threads=0, avx2=1, want_bf16=False):
+    _done()
     qa = _c(qa, np.uint8)
     sa = _c(sa, np.float32)
     qw = _c(qw, np.uint8)
@@ -128,6 +158,7 @@ def gemm_f32(qa, sa, qw, sw, N, m0=0, m1=None, threads=0, avx2=1, want_bf16=Fals
 
 def ln_quant(x16, g, b, lds=None):
     """x fp16 bits uint16 [M][1024] -> (q [M][1024], s [8][lds], y fp32 [M][1024])."""
+    _done()
     x16 = _c(x16, np.uint16)
     M = x16.shape[0]
     lds = lds or M
@@ -139,6 +170,7 @@ def ln_quant(x16, g, b, lds=None):
 
 
 def max_threads():
+    _done()
     return lib.xo_max_threads()
 
 
@@ -157,3 +189,130 @@ class Lcg:
         out = np.empty(n, np.uint8)
         lib.xo_lcg_e4m3(_ptr(self.rs), n, _ptr(out))
         return out
+
+
+# ---------------------------------------------------------------- EVA02-L pieces
+TP = 1088
+
+
+def qkv_epi(acc, nb, cs):
+    _done()
+    acc = _c(acc, np.float32)
+    q = np.zeros((nb, 16, TP, 64), np.uint16)
+    k = np.zeros((nb, 16, TP, 64), np.uint16)
+    vt = np.zeros((nb, 16, 64, TP), np.uint16)
+    lib.xo_qkv_epi(_ptr(acc), nb, _ptr(_c(cs, np.float32)), _ptr(q), _ptr(k), _ptr(vt))
+    return q, k, vt
+
+
+def attention(q, k, vt, nb, threads=0):
+    _done()
+    o = np.empty((nb * 1025, 1024), np.float64)
+    lib.xo_attention(_ptr(_c(q, np.uint16)), _ptr(_c(k, np.uint16)), _ptr(_c(vt, np.uint16)), nb, _ptr(o), threads)
+    return o
+
+
+def fc1_epi(acc):
+    _done()
+    acc = _c(acc, np.float32)
+    M = acc.shape[0]
+    h = np.empty((M, 2816), np.float32)
+    stat = np.empty((22, M, 2), np.float32)
+    lib.xo_fc1_epi(_ptr(acc), M, _ptr(h), _ptr(stat))
+    return h, stat
+
+
+def fc2_epi(acc, stat, c, d, x16):
+    _done()
+    acc = _c(acc, np.float32)
+    x = _c(x16, np.uint16).copy()
+    lib.xo_fc2_epi(_ptr(acc), acc.shape[0], _ptr(_c(stat, np.float32)), _ptr(_c(c, np.float32)),
+                   _ptr(_c(d, np.float32)), _ptr(x))
+    return x
+
+
+def oproj_epi(acc, x16):
+    _done()
+    acc = _c(acc, np.float32)
+    x = _c(x16, np.uint16).copy()
+    lib.xo_oproj_epi(_ptr(acc), acc.shape[0], _ptr(x))
+    return x
+
+
+def embed(inp16, pe16, pos, nb):
+    _done()
+    x = np.zeros((nb * 1025, 1024), np.uint16)
+    lib.xo_embed(_ptr(_c(inp16, np.uint16)), _ptr(_c(pe16, np.uint16)), _ptr(_c(pos, np.float32)), nb, _ptr(x))
+    return x
+
+
+def pool(x16, nb):
+    _done()
+    p = np.empty((nb, 1024), np.float32)
+    lib.xo_pool(_ptr(_c(x16, np.uint16)), nb, _ptr(p))
+    return p
+
+
+def lnh(p, g, b, lds=None):
+    _done()
+    p = _c(p, np.float32)
+    nb = p.shape[0]
+    lds = lds or nb
+    pn = np.empty((nb, 1024), np.uint16)
+    q = np.empty((nb, 1024), np.uint8)
+    s = np.zeros((8, lds), np.float32)
+    lib.xo_lnh(_ptr(p), _ptr(_c(g, np.float32)), _ptr(_c(b, np.float32)), nb, _ptr(pn), _ptr(q), _ptr(s), lds)
+    return pn, q, s
+
+
+def fold_w2(w2_16, gamma, beta):
+    _done()
+    w2 = _c(w2_16, np.uint16)
+    wt = np.empty((1024, 2816), np.float32)
+    d = np.empty(1024, np.float32)
+    lib.xo_fold_w2(_ptr(w2), w2.shape[1], _ptr(_c(gamma, np.float32)), _ptr(_c(beta, np.float32)), _ptr(wt), _ptr(d))
+    return wt, d
+
+
+def fold_c(q, s):
+    _done()
+    c = np.empty(1024, np.float32)
+    lib.xo_fold_c(_ptr(_c(q, np.uint8)), _ptr(_c(s, np.float32)), _ptr(c))
+    return c
+
+
+class _Model(C.Structure):
+    _fields_ = [("pe", C.c_void_p), ("pos", C.c_void_p), ("cs", C.c_void_p),
+                ("ln1w", C.c_void_p * 24), ("ln1b", C.c_void_p * 24), ("ln2w", C.c_void_p * 24),
+                ("ln2b", C.c_void_p * 24), ("mlnw", C.c_void_p * 24), ("mlnb", C.c_void_p * 24),
+                ("wqkv", C.c_void_p * 24), ("wo", C.c_void_p * 24), ("w12", C.c_void_p * 24), ("w2", C.c_void_p * 24),
+                ("fnw", C.c_void_p), ("fnb", C.c_void_p), ("hw", C.c_void_p), ("hb", C.c_void_p), ("nt", C.c_int)]
+
+
+def forward(m, inp16, nl=24, threads=0):
+    """Full oracle forward from model tensors m (xtagger_amd.blob layout) on fp16 inputs [nb][1024][592]."""
+    _done()
+    keep = []
+
+    def P(a, dt):
+        a = np.ascontiguousarray(a, dtype=dt)
+        keep.append(a)
+        return a.ctypes.data
+
+    md = _Model()
+    md.pe, md.pos, md.cs = P(m["pe"].view(np.uint16), np.uint16), P(m["pos"], np.float32), P(m["rope"], np.float32)
+    for i, L in enumerate(m["layers"][:nl]):
+        md.ln1w[i], md.ln1b[i] = P(L["ln1w"], np.float32), P(L["ln1b"], np.float32)
+        md.ln2w[i], md.ln2b[i] = P(L["ln2w"], np.float32), P(L["ln2b"], np.float32)
+        md.mlnw[i], md.mlnb[i] = P(L["mlnw"], np.float32), P(L["mlnb"], np.float32)
+        md.wqkv[i], md.wo[i] = P(L["wqkv"].view(np.uint16), np.uint16), P(L["wo"].view(np.uint16), np.uint16)
+        md.w12[i], md.w2[i] = P(L["w12"].view(np.uint16), np.uint16), P(L["w2"].view(np.uint16), np.uint16)
+    md.fnw, md.fnb = P(m["fnw"], np.float32), P(m["fnb"], np.float32)
+    md.hw, md.hb = P(m["hw"].view(np.uint16), np.uint16), P(m["hb"], np.float32)
+    md.nt = m["nt"]
+    x = np.ascontiguousarray(inp16, dtype=np.float16).view(np.uint16)
+    nb = x.shape[0]
+    out = np.empty((nb, m["nt"]), np.float32)
+    pn = np.empty((nb, 1024), np.uint16)
+    lib.xo_forward(C.byref(md), _ptr(x), nb, nl, _ptr(out), _ptr(pn), threads)
+    return out, pn

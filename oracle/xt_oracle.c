@@ -450,3 +450,343 @@ void xo_lcg_e4m3(uint32_t *rs, size_t n, uint8_t *out)
         out[i] = b;
     }
 }
+
+/* =================================================================================================================
+ * EVA02-L forward pieces
+ * =============================================================================================================== */
+static float f16f(uint16_t h) { return xo_f16_to_f32(h); }
+
+void xo_qkv_epi(const float *acc, int nb, const float *cs, uint16_t *q, uint16_t *k, uint16_t *vt)
+{
+    int m, M = nb * XO_T;
+
+#pragma omp parallel for schedule(static)
+    for (m = 0; m < M; m++) {
+        int b = m / XO_T, t = m % XO_T, part, h, i, d;
+        const float *a = acc + (size_t)m * 3072;
+        for (part = 0; part < 2; part++) {
+            uint16_t *dst = part ? k : q;
+            for (h = 0; h < 16; h++)
+                for (i = 0; i < 32; i++) {
+                    float f0 = a[part * 1024 + h * 64 + 2 * i], f1 = a[part * 1024 + h * 64 + 2 * i + 1], g0;
+                    if (t >= 1) {
+                        float c = cs[((size_t)(t - 1) * 32 + i) * 2], sn = cs[((size_t)(t - 1) * 32 + i) * 2 + 1];
+                        g0 = f0 * c - f1 * sn;
+                        f1 = f1 * c + f0 * sn;
+                        f0 = g0;
+                    }
+                    dst[(((size_t)b * 16 + h) * XO_TP + t) * 64 + 2 * i] = xo_f32_to_bf16(f0);
+                    dst[(((size_t)b * 16 + h) * XO_TP + t) * 64 + 2 * i + 1] = xo_f32_to_bf16(f1);
+                }
+        }
+        for (h = 0; h < 16; h++)
+            for (d = 0; d < 64; d++)
+                vt[(((size_t)b * 16 + h) * 64 + d) * XO_TP + t] = xo_f32_to_bf16(a[2048 + h * 64 + d]);
+    }
+}
+
+void xo_attention(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int nb, double *o, int threads)
+{
+    int bh;
+
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+#else
+    (void)threads;
+#endif
+    for (bh = 0; bh < nb * 16; bh++) {
+        int b = bh / 16, h = bh % 16, t, j, d;
+        double *Q = (double *)malloc(sizeof(double) * XO_T * 64);
+        double *Kd = (double *)malloc(sizeof(double) * XO_T * 64);
+        double *V = (double *)malloc(sizeof(double) * XO_T * 64);
+        double *s = (double *)malloc(sizeof(double) * XO_T);
+        for (t = 0; t < XO_T; t++)
+            for (d = 0; d < 64; d++) {
+                Q[t * 64 + d] = xo_bf16_to_f32(q[((size_t)bh * XO_TP + t) * 64 + d]);
+                Kd[t * 64 + d] = xo_bf16_to_f32(k[((size_t)bh * XO_TP + t) * 64 + d]);
+                V[t * 64 + d] = xo_bf16_to_f32(vt[((size_t)bh * 64 + d) * XO_TP + t]);
+            }
+        for (t = 0; t < XO_T; t++) {
+            double mx = -INFINITY, l = 0.0, acc[64];
+            for (j = 0; j < XO_T; j++) {
+                double a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+                for (d = 0; d < 64; d += 4) {
+                    a0 += Q[t * 64 + d] * Kd[j * 64 + d];
+                    a1 += Q[t * 64 + d + 1] * Kd[j * 64 + d + 1];
+                    a2 += Q[t * 64 + d + 2] * Kd[j * 64 + d + 2];
+                    a3 += Q[t * 64 + d + 3] * Kd[j * 64 + d + 3];
+                }
+                s[j] = (a0 + a1) + (a2 + a3);
+                if (s[j] > mx) mx = s[j];
+            }
+            for (d = 0; d < 64; d++) acc[d] = 0.0;
+            for (j = 0; j < XO_T; j++) {
+                double p = exp2(s[j] - mx);
+                l += p;
+                for (d = 0; d < 64; d++) acc[d] += p * V[j * 64 + d];
+            }
+            for (d = 0; d < 64; d++) o[((size_t)b * XO_T + t) * 1024 + h * 64 + d] = acc[d] / l;
+        }
+        free(Q);
+        free(Kd);
+        free(V);
+        free(s);
+    }
+}
+
+void xo_fc1_epi(const float *acc, int M, float *h, float *stat)
+{
+    int m;
+
+#pragma omp parallel for schedule(static)
+    for (m = 0; m < M; m++) {
+        int u, blk;
+        for (u = 0; u < XO_HIDP; u++) {
+            int c = u / 16, w = u % 16;
+            float g = acc[(size_t)m * 2 * XO_HIDP + 32 * c + w], x = acc[(size_t)m * 2 * XO_HIDP + 32 * c + 16 + w];
+            float e = expf(-g), den = 1.0f + e, sg = g / den;
+            h[(size_t)m * XO_HIDP + u] = sg * x;
+        }
+        for (blk = 0; blk < XO_HIDP / 128; blk++) {
+            float s = 0.0f, q = 0.0f, v;
+            for (u = blk * 128; u < blk * 128 + 128; u++) {
+                v = h[(size_t)m * XO_HIDP + u];
+                s += v;
+                q = fmaf(v, v, q);
+            }
+            stat[((size_t)blk * M + m) * 2] = s;
+            stat[((size_t)blk * M + m) * 2 + 1] = q;
+        }
+    }
+}
+
+void xo_fc2_epi(const float *acc, int M, const float *stat, const float *c, const float *d, uint16_t *x)
+{
+    int m;
+
+#pragma omp parallel for schedule(static)
+    for (m = 0; m < M; m++) {
+        float S = 0.0f, Q = 0.0f, mean, var, rstd, nm, y;
+        int blk, n;
+        for (blk = 0; blk < XO_HIDP / 128; blk++) {
+            S += stat[((size_t)blk * M + m) * 2];
+            Q += stat[((size_t)blk * M + m) * 2 + 1];
+        }
+        mean = S / (float)XO_HID;
+        var = Q / (float)XO_HID - mean * mean;
+        var = fmaxf(var, 0.0f);
+        rstd = 1.0f / sqrtf(var + 1e-6f);
+        nm = -mean * rstd;
+        for (n = 0; n < XO_D; n++) {
+            y = fmaf(rstd, acc[(size_t)m * XO_D + n], fmaf(nm, c[n], d[n]));
+            x[(size_t)m * XO_D + n] = xo_f32_to_f16(f16f(x[(size_t)m * XO_D + n]) + y);
+        }
+    }
+}
+
+void xo_oproj_epi(const float *acc, int M, uint16_t *x)
+{
+    size_t i;
+
+    for (i = 0; i < (size_t)M * XO_D; i++) x[i] = xo_f32_to_f16(f16f(x[i]) + acc[i]);
+}
+
+void xo_embed(const uint16_t *in, const uint16_t *pe, const float *pos, int nb, uint16_t *x)
+{
+    int r;
+    float *pef = (float *)malloc(sizeof(float) * 1024 * 592);
+
+    for (r = 0; r < 1024 * 592; r++) pef[r] = f16f(pe[r]);
+#pragma omp parallel for schedule(static)
+    for (r = 0; r < nb * 1024; r++) {
+        int b = r / 1024, p = r % 1024, n, kk;
+        float a[592];
+        for (kk = 0; kk < 592; kk++) a[kk] = f16f(in[(size_t)r * 592 + kk]);
+        for (n = 0; n < XO_D; n++) {
+            double dot = 0.0;
+            for (kk = 0; kk < 592; kk++) dot += (double)a[kk] * (double)pef[(size_t)n * 592 + kk];
+            x[((size_t)b * XO_T + 1 + p) * XO_D + n] = xo_f32_to_f16((float)dot + pos[(size_t)(1 + p) * XO_D + n]);
+        }
+        if (p == 0)
+            for (n = 0; n < XO_D; n++) x[(size_t)b * XO_T * XO_D + n] = xo_f32_to_f16(pos[n]);
+    }
+    free(pef);
+}
+
+void xo_pool(const uint16_t *x, int nb, float *p)
+{
+    int b, n, t;
+
+    for (b = 0; b < nb; b++)
+        for (n = 0; n < XO_D; n++) {
+            float s = 0.0f;
+            for (t = 1; t < XO_T; t++) s += f16f(x[((size_t)b * XO_T + t) * XO_D + n]);
+            p[(size_t)b * XO_D + n] = s * (1.0f / 1024.0f);
+        }
+}
+
+/* LayerNorm of one 1024-row in the device order (see xo_ln_quant) */
+static void ln_row_dev(const float *v, const float *g, const float *b, float *y)
+{
+    float ls[64], mean, var, rstd, d;
+    int l, j, e;
+
+    for (l = 0; l < 64; l++) {
+        ls[l] = 0.0f;
+        for (j = 0; j < 16; j++) ls[l] += v[ln_elem(l, j)];
+    }
+    mean = wave_sum64(ls) * (1.0f / 1024.0f);
+    for (l = 0; l < 64; l++) {
+        ls[l] = 0.0f;
+        for (j = 0; j < 16; j++) {
+            d = v[ln_elem(l, j)] - mean;
+            ls[l] = fmaf(d, d, ls[l]);
+        }
+    }
+    var = wave_sum64(ls) * (1.0f / 1024.0f);
+    rstd = 1.0f / sqrtf(var + 1e-6f);
+    for (e = 0; e < 1024; e++) y[e] = fmaf((v[e] - mean) * rstd, g[e], b[e]);
+}
+
+void xo_lnh(const float *p, const float *g, const float *b, int nb, uint16_t *pn, uint8_t *q, float *s, int lds)
+{
+    int r, e;
+    float y[1024], yq[1024];
+
+    for (r = 0; r < nb; r++) {
+        ln_row_dev(p + (size_t)r * 1024, g, b, y);
+        for (e = 0; e < 1024; e++) {
+            pn[(size_t)r * 1024 + e] = xo_f32_to_f16(y[e]);
+            yq[e] = f16f(pn[(size_t)r * 1024 + e]);
+        }
+        /* 1x128 packing of the fp16 values; row r of a one-row act quant into the planes */
+        {
+            int kb;
+            for (kb = 0; kb < 8; kb++) {
+                float amax = 0.0f, sc, inv;
+                for (e = kb * 128; e < kb * 128 + 128; e++) amax = fmaxf(amax, fabsf(yq[e]));
+                sc = xo_block_scale(amax);
+                inv = 1.0f / sc;
+                s[(size_t)kb * lds + r] = sc;
+                for (e = kb * 128; e < kb * 128 + 128; e++) q[(size_t)r * 1024 + e] = xo_e4m3_encode(yq[e] * inv);
+            }
+        }
+    }
+}
+
+void xo_fold_w2(const uint16_t *w2, int ldw2, const float *gamma, const float *beta, float *wt, float *d)
+{
+    int n, k;
+
+    for (n = 0; n < XO_D; n++) {
+        float dd = 0.0f;
+        for (k = 0; k < XO_HIDP; k++) {
+            float w = k < XO_HID ? f16f(w2[(size_t)n * ldw2 + k]) : 0.0f;
+            wt[(size_t)n * XO_HIDP + k] = k < XO_HID ? w * gamma[k] : 0.0f;
+            if (k < XO_HID) dd = fmaf(w, beta[k], dd);
+        }
+        d[n] = dd;
+    }
+}
+
+void xo_fold_c(const uint8_t *q, const float *s, float *c)
+{
+    int n, k;
+
+    e4lut_init();
+    for (n = 0; n < XO_D; n++) {
+        float cc = 0.0f;
+        for (k = 0; k < XO_HIDP; k++)
+            cc = fmaf(E4LUT[q[(size_t)n * XO_HIDP + k]], s[(size_t)(n / 128) * (XO_HIDP / 128) + k / 128], cc);
+        c[n] = cc;
+    }
+}
+
+/* fp16 [rows][ld] (first cols columns) -> fp32 [rows_out][cols_out], zero padded */
+static float *f16_to_f32_pad(const uint16_t *w, int rows, int cols, int ld, int rows_out, int cols_out)
+{
+    float *o = (float *)calloc((size_t)rows_out * cols_out, sizeof(float));
+    int r, c;
+
+    for (r = 0; r < rows; r++)
+        for (c = 0; c < cols; c++) o[(size_t)r * cols_out + c] = f16f(w[(size_t)r * ld + c]);
+    return o;
+}
+
+int xo_forward(const xo_model *md, const uint16_t *in, int nb, int nl, float *out, uint16_t *pn, int threads)
+{
+    const int avx = getenv("XO_SCALAR") ? 0 : 1;
+    const int M = nb * XO_T, nt = md->nt, NBh = (nt + 127) / 128;
+    uint16_t *x = (uint16_t *)malloc(sizeof(uint16_t) * M * XO_D);
+    uint8_t *h8 = (uint8_t *)malloc((size_t)M * XO_HIDP);
+    float *hs = (float *)malloc(sizeof(float) * 22 * M);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)M * 2 * XO_HIDP);
+    float *hf = (float *)malloc(sizeof(float) * (size_t)M * XO_HIDP);
+    float *stat = (float *)malloc(sizeof(float) * 22 * M * 2);
+    uint16_t *q = (uint16_t *)calloc((size_t)nb * 16 * XO_TP * 64, 2);
+    uint16_t *k = (uint16_t *)calloc((size_t)nb * 16 * XO_TP * 64, 2);
+    uint16_t *vt = (uint16_t *)calloc((size_t)nb * 16 * XO_TP * 64, 2);
+    double *o = (double *)malloc(sizeof(double) * (size_t)M * XO_D);
+    float *of = (float *)malloc(sizeof(float) * (size_t)M * XO_D);
+    uint8_t *wq = (uint8_t *)malloc((size_t)2 * XO_HIDP * XO_D);
+    float *ws = (float *)malloc(sizeof(float) * 44 * 22);
+    float *cfold = (float *)malloc(sizeof(float) * XO_D), *dfold = (float *)malloc(sizeof(float) * XO_D);
+    float *pool = (float *)malloc(sizeof(float) * nb * XO_D);
+    uint8_t *pq = (uint8_t *)malloc((size_t)nb * XO_D);
+    float *ps = (float *)malloc(sizeof(float) * 8 * nb);
+    float *logit = (float *)malloc(sizeof(float) * nb * NBh * 128);
+    float *wf;
+    int i, r, n;
+
+    xo_embed(in, md->pe, md->pos, nb, x);
+    for (i = 0; i < nl; i++) {
+        /* attention */
+        xo_ln_quant(x, md->ln1w[i], md->ln1b[i], M, h8, hs, M, NULL);
+        wf = f16_to_f32_pad(md->wqkv[i], 3072, XO_D, XO_D, 3072, XO_D);
+        xo_quant_w(wf, 3072, XO_D, wq, ws);
+        free(wf);
+        xo_gemm_bs_f32(h8, XO_D, hs, M, wq, ws, 3072, XO_D, 0, M, acc, NULL, 3072, threads, avx);
+        xo_qkv_epi(acc, nb, md->cs, q, k, vt);
+        xo_attention(q, k, vt, nb, o, threads);
+        for (r = 0; r < M * XO_D; r++) of[r] = (float)o[r];
+        xo_quant_act(of, M, XO_D, XO_D, h8, XO_D, hs, M);
+        wf = f16_to_f32_pad(md->wo[i], XO_D, XO_D, XO_D, XO_D, XO_D);
+        xo_quant_w(wf, XO_D, XO_D, wq, ws);
+        free(wf);
+        xo_gemm_bs_f32(h8, XO_D, hs, M, wq, ws, XO_D, XO_D, 0, M, acc, NULL, XO_D, threads, avx);
+        xo_oproj_epi(acc, M, x);
+        /* MLP */
+        xo_ln_quant(x, md->ln2w[i], md->ln2b[i], M, h8, hs, M, NULL);
+        wf = f16_to_f32_pad(md->w12[i], 2 * 2736, XO_D, XO_D, 2 * XO_HIDP, XO_D);
+        xo_quant_w(wf, 2 * XO_HIDP, XO_D, wq, ws);
+        free(wf);
+        xo_gemm_bs_f32(h8, XO_D, hs, M, wq, ws, 2 * XO_HIDP, XO_D, 0, M, acc, NULL, 2 * XO_HIDP, threads, avx);
+        xo_fc1_epi(acc, M, hf, stat);
+        xo_quant_act(hf, M, XO_HIDP, XO_HIDP, h8, XO_HIDP, hs, M);
+        wf = (float *)malloc(sizeof(float) * XO_D * XO_HIDP);
+        xo_fold_w2(md->w2[i], 2736, md->mlnw[i], md->mlnb[i], wf, dfold);
+        xo_quant_w(wf, XO_D, XO_HIDP, wq, ws);
+        free(wf);
+        xo_fold_c(wq, ws, cfold);
+        xo_gemm_bs_f32(h8, XO_HIDP, hs, M, wq, ws, XO_D, XO_HIDP, 0, M, acc, NULL, XO_D, threads, avx);
+        xo_fc2_epi(acc, M, stat, cfold, dfold, x);
+    }
+    xo_pool(x, nb, pool);
+    xo_lnh(pool, md->fnw, md->fnb, nb, pn, pq, ps, nb);
+    {
+        uint8_t *hq = (uint8_t *)malloc((size_t)NBh * 128 * XO_D);
+        float *hsc = (float *)malloc(sizeof(float) * NBh * 8);
+        wf = f16_to_f32_pad(md->hw, nt, XO_D, XO_D, nt, XO_D);
+        xo_quant_w(wf, nt, XO_D, hq, hsc);
+        free(wf);
+        xo_gemm_bs_f32(pq, XO_D, ps, nb, hq, hsc, nt, XO_D, 0, nb, logit, NULL, nt, threads, 1);
+        for (r = 0; r < nb; r++)
+            for (n = 0; n < nt; n++) out[(size_t)r * nt + n] = 1.0f / (1.0f + expf(-(logit[(size_t)r * nt + n] + md->hb[n])));
+        free(hq);
+        free(hsc);
+    }
+    free(x); free(h8); free(hs); free(acc); free(hf); free(stat); free(q); free(k); free(vt); free(o); free(of);
+    free(wq); free(ws); free(cfold); free(dfold); free(pool); free(pq); free(ps); free(logit);
+    return 0;
+}

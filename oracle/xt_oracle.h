@@ -56,6 +56,62 @@ int xo_max_threads(void);
 /* x fp16 [M][1024] -> q [M][1024], s [8][lds]; also y fp32 [M][1024] if y != NULL */
 void xo_ln_quant(const uint16_t *x, const float *g, const float *b, int M, uint8_t *q, float *s, int lds, float *y);
 
+/* ---- EVA02-L pieces (M = nb * 1025 token rows; Tp = 1088 padded attention rows) ---- */
+#define XO_D 1024
+#define XO_T 1025
+#define XO_TP 1088
+#define XO_HID 2730
+#define XO_HIDP 2816
+/* qkv epilogue (eva_kernels.cu:60-113): acc fp32 [M][3072] natural columns q | k | v (head-major, 64 each; q rows
+ * of the weight carry log2(e)/8). RoPE on q, k of patch tokens t >= 1 with pair (2i, 2i+1) and angle
+ * cs[(t-1)*32 + i] = (cos, sin) (eva_kernels.cu:74-79, export_eva.py:72-74), then bf16 (RNE).
+ * q, k: [nb][16][1088][64]; vt: [nb][16][64][1088] (v transposed). Rows t >= 1025 are not written. */
+void xo_qkv_epi(const float *acc, int nb, const float *cs, uint16_t *q, uint16_t *k, uint16_t *vt);
+/* softmax attention in fp64 (exp2 domain: scores already carry log2(e)/8), one output row per token:
+ * o [nb * 1025][1024] at column h * 64 (flash8's math, kern_common.cuh:403-543, without its E4M3 roundings) */
+void xo_attention(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int nb, double *o, int threads);
+/* fc1 epilogue (eva_kernels.cu:233-268): acc [M][5632] with g / x interleaved in 16-unit chunks
+ * (export_eva.py:60-62) -> h = silu(g) * x, fp32 [M][2816] in unit order; stat [22][M][2] = (sum h, sum h^2) over
+ * each 128-unit block. silu(g) = g / (1 + exp(-g)), exact form (the reference's tanh.approx is not restated). */
+void xo_fc1_epi(const float *acc, int M, float *h, float *stat);
+/* fc2 epilogue with the MLP LayerNorm folded (eva_kernels.cu:300-333, export_eva.py:101-104, 117-119):
+ * mean = S / 2730, var = Q / 2730 - mean^2, rstd = 1 / sqrt(var + 1e-6), S, Q summed over the 22 blocks in order;
+ * x = f16(x + fma(rstd, acc, fma(-mean * rstd, c, d))). x fp16 [M][1024] in place. */
+void xo_fc2_epi(const float *acc, int M, const float *stat, const float *c, const float *d, uint16_t *x);
+/* out-projection epilogue (eva_kernels.cu:150-160): x = f16(x + acc) */
+void xo_oproj_epi(const float *acc, int M, uint16_t *x);
+/* patch embedding + position (k_pe + k_embed, eva_kernels.cu:21-33, 126-130): in fp16 [nb*1024][592],
+ * pe fp16 [1024][592], pos fp32 [1025][1024] -> x fp16 [nb*1025][1024]; x[b,0] = f16(pos[0]),
+ * x[b,1+p] = f16((float)dot + pos[1+p]) with the dot in fp64 */
+void xo_embed(const uint16_t *in, const uint16_t *pe, const float *pos, int nb, uint16_t *x);
+/* mean over tokens 1..1024 (k_pool, eva_kernels.cu:402-431), tokens summed in order: x [nb*1025][1024] -> p [nb][1024] */
+void xo_pool(const uint16_t *x, int nb, float *p);
+/* final LayerNorm (k_lnh) -> fp16 pn [nb][1024] -> E4M3 of pn with 1x128 scales q [nb][1024], s [8][lds] */
+void xo_lnh(const float *p, const float *g, const float *b, int nb, uint16_t *pn, uint8_t *q, float *s, int lds);
+/* MLP-LN fold of fc2 (export_eva.py:101-104, 117-119): w2 fp16 [1024][ldw2] (k < 2730 used), gamma, beta [>=2730]
+ * -> wt fp32 [1024][2816] = w2 * gamma (zero past 2730), d[n] = sum_k w2[n][k] * beta[k] (fp32, in k order) */
+void xo_fold_w2(const uint16_t *w2, int ldw2, const float *gamma, const float *beta, float *wt, float *d);
+/* c[n] = sum_k dec(q[n][k]) * s[n/128][k/128] over [1024][2816] (fp32, in k order) */
+void xo_fold_c(const uint8_t *q, const float *s, float *c);
+
+/* Full wd forward (eva.h:227-310) from the reference's v2 blob tensors (export_eva.py layout, fp16 block weights,
+ * HIDP 2736). Weights are packed here with xo_quant_w exactly as the device does. nl layers (24 for the model);
+ * out [nb][nt] sigmoid scores, pn [nb][1024] fp16 head inputs. */
+typedef struct {
+    const uint16_t *pe;          /* [1024][592] */
+    const float *pos, *cs;       /* [1025][1024], [1024][32][2] */
+    const float *ln1w[24], *ln1b[24], *ln2w[24], *ln2b[24], *mlnw[24], *mlnb[24];
+    const uint16_t *wqkv[24];    /* [3072][1024] */
+    const uint16_t *wo[24];      /* [1024][1024] */
+    const uint16_t *w12[24];     /* [2*2736][1024], 16-unit g / x chunks */
+    const uint16_t *w2[24];      /* [1024][2736] */
+    const float *fnw, *fnb;
+    const uint16_t *hw;          /* [ntp][1024] */
+    const float *hb;             /* [ntp] */
+    int nt;
+} xo_model;
+int xo_forward(const xo_model *m, const uint16_t *in, int nb, int nl, float *out, uint16_t *pn, int threads);
+
 /* kcheck.c:21-22 LCG (rs = rs * 1664525 + 1013904223): frand() in [-1, 1), and kcheck.c:106-107 E4M3 bytes
  * (top byte of the state, redrawn while NaN or exponent field > 9). *rs is the running state. */
 void xo_lcg_frand(uint32_t *rs, size_t n, float *out);

@@ -32,3 +32,33 @@ def test_bad_shapes_rejected_without_gpu():
     assert L.lib.eva_k_gemm(None, 100, None, 1, None, None, 1, 128, 100, None, 128, 0, None) == -1
     assert L.lib.eva_k_quant_act(None, 0, 100, 1, 100, None, 100, None, 1, None) == -1
     assert L.lib.eva_k_quant_w(None, 128, 100, None, None, None) == -1
+
+
+def test_open_rejects_bad_header(tmp_path):
+    """eva.h:580-586: a file that is not an EVA2 v2 blob fails eva_open with -1 (no device call)."""
+    from xtagger_amd.engine import Engine
+    p = tmp_path / "bad.bin"
+    p.write_bytes(b"NOPE" + b"\0" * 300)
+    import pytest
+    with pytest.raises(RuntimeError):
+        Engine(str(p))
+    import struct
+    p.write_bytes(struct.pack("<4sIII", b"EVA2", 3, 10861, 100) + b"\0" * 300)
+    with pytest.raises(RuntimeError):
+        Engine(str(p))
+    with pytest.raises(RuntimeError):
+        Engine(str(tmp_path / "missing.bin"))
+
+
+def test_blob_roundtrip_small(tmp_path):
+    """The v2 writer / reader agree and the byte layout is the one eva.h walks (256-byte aligned tensors)."""
+    from xtagger_amd import blob
+    import numpy as np
+    m = blob.synth_model(seed=1, nt=17, nl=24, head_std=0.02)
+    n = blob.write_v2(str(tmp_path / "b.bin"), m)
+    r = blob.read_v2(str(tmp_path / "b.bin"))
+    assert r["nt"] == 17 and r["hw"].shape == (24, 1024)
+    assert np.array_equal(r["layers"][5]["w2"], m["layers"][5]["w2"])
+    assert np.array_equal(r["rope"], m["rope"])
+    raw = open(tmp_path / "b.bin", "rb").read()
+    assert raw[:4] == b"EVA2" and len(raw) == 256 + n

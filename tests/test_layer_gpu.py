@@ -1,0 +1,411 @@
+"""GPU parity of the EVA02-L layer kernels (LayerNorm, qkv + RoPE, attention, out-projection, fc1 + SwiGLU, fc2 +
+folded LN, patch embed, pool, final LN, head, weight preparation) against the oracle, through the C-ABI.
+
+Bit-exact where the kernel's arithmetic is restated in the oracle step for step (LayerNorm, pool, final LN, weight
+packing, fold terms, attention output packing given the kernel's fp32 output). Where a fused epilogue follows a
+block-scaled GEMM, the oracle applies the same epilogue to the fp64 product of the same packed operands, and the
+check is a tolerance: the matrix core's summation differs from fp64 by ~1e-5 relative, which can move a value across
+one bf16 / fp16 / E4M3 rounding boundary.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+T, D, TP, HIDP = 1025, 1024, 1088, 2816
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ok(rc, what):
+    assert rc == 0, f"{what} returned {rc}"
+    torch.cuda.synchronize()
+
+
+_KEEP = []                                                   # device copies stay alive until the test ends
+
+
+@pytest.fixture(autouse=True)
+def _release_device_copies():
+    yield
+    _KEEP.clear()
+
+
+def _d(a, dev):
+    t = a.to(dev) if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    _KEEP.append(t)
+    return t
+
+
+def _ulp_diff_f16(a, b):
+    a = a.view(np.int16).astype(np.int32)
+    b = b.view(np.int16).astype(np.int32)
+    a = np.where(a < 0, -32768 - a, a)
+    b = np.where(b < 0, -32768 - b, b)
+    return np.abs(a - b)
+
+
+def _ulp_diff_bf16(a, b):
+    return _ulp_diff_f16(a, b)  # same ordering trick on 16-bit sign-magnitude patterns
+
+
+def _bf16_f32(u16):
+    return (np.asarray(u16, np.uint32) << 16).view(np.float32)
+
+
+def _f16_f32(u16):
+    return np.asarray(u16, np.uint16).view(np.float16).astype(np.float32)
+
+
+def _check_close(name, got, ref, scale, unit):
+    """|got - ref| <= unit * |ref| + 2e-4 * scale: one rounding unit of the output type (2^-7 bf16, 2^-10 fp16) plus
+    the GEMM summation difference (the matrix core vs fp64, ~1e-5 of the terms), which dominates where terms cancel."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    bound = unit * np.abs(ref) + 2e-4 * scale
+    worst = float((err / bound).max())
+    _say(f"  {name}: worst err / bound {worst:.3f}, elements differing {np.mean(err > 0):.2e}")
+    assert worst <= 1.0, name
+
+
+def _packed_act(orc, M, K, seed, scale=1.0):
+    r = np.random.default_rng(seed)
+    x = (r.standard_normal((M, K)) * scale).astype(np.float32)
+    q, s = orc.quant_act(x)
+    return x, q, s
+
+
+def _packed_w(orc, N, K, seed, std=0.02):
+    r = np.random.default_rng(seed)
+    w = (r.standard_normal((N, K)) * std).astype(np.float32)
+    q, s = orc.quant_w(w)
+    return w, q, s
+
+
+# ---------------------------------------------------------------- LayerNorm / pool / final LN: bit-exact
+@pytest.mark.parametrize("M", [1025, 37, 1])
+def test_ln_bitexact(dev, xt, orc, M):
+    _say(f"k_ln M={M}")
+    r = np.random.default_rng(M)
+    x = (r.standard_normal((M, D)) * 2 + 0.3).astype(np.float16)
+    x[0, :] = 1.0                                            # constant row: variance 0
+    g = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    b = (0.02 * r.standard_normal(D)).astype(np.float32)
+    lds = M + 5
+    d_q = torch.zeros((M, D), dtype=torch.uint8, device=dev)
+    d_s = torch.zeros((8, lds), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_ln(xt.ptr(_d(x, dev)), xt.ptr(_d(g, dev)), xt.ptr(_d(b, dev)), xt.ptr(d_q), xt.ptr(d_s), M, lds,
+                        _st()), "eva_k_ln")
+    q, s, _ = orc.ln_quant(x.view(np.uint16), g, b, lds=lds)
+    assert (d_q.cpu().numpy() == q).all()
+    assert (d_s.cpu().numpy() == s).all()
+
+
+def test_pool_lnh_bitexact(dev, xt, orc):
+    nb = 3
+    _say("k_pool + k_lnh")
+    r = np.random.default_rng(9)
+    x = (r.standard_normal((nb * T, D)) * 3).astype(np.float16)
+    g = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    b = (0.02 * r.standard_normal(D)).astype(np.float32)
+    d_p = torch.zeros((nb, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_pool(xt.ptr(_d(x, dev)), xt.ptr(d_p), nb, _st()), "eva_k_pool")
+    p = orc.pool(x.view(np.uint16), nb)
+    assert (d_p.cpu().numpy() == p).all()
+    d_pn = torch.zeros((nb, D), dtype=torch.int16, device=dev)
+    d_q = torch.zeros((nb, D), dtype=torch.uint8, device=dev)
+    d_s = torch.zeros((8, 4), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_lnh(xt.ptr(d_p), xt.ptr(_d(g, dev)), xt.ptr(_d(b, dev)), xt.ptr(d_pn), xt.ptr(d_q), xt.ptr(d_s),
+                         nb, 4, _st()), "eva_k_lnh")
+    pn, q, s = orc.lnh(p, g, b, lds=4)
+    assert (d_pn.cpu().numpy().view(np.uint16) == pn).all()
+    assert (d_q.cpu().numpy() == q).all()
+    assert (d_s.cpu().numpy() == s).all()
+
+
+# ---------------------------------------------------------------- weight preparation: bit-exact
+def test_prep_qkv_pair_split_bitexact(dev, xt, orc):
+    _say("eva_k_prep_w qkv")
+    r = np.random.default_rng(11)
+    w16 = (r.standard_normal((3 * D, D)) * 0.02).astype(np.float16)
+    d_q = torch.zeros((3 * D, D), dtype=torch.uint8, device=dev)
+    d_s = torch.zeros((24, 8), dtype=torch.float32, device=dev)
+    scratch = torch.empty((3 * D, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_prep_w(xt.ptr(_d(w16, dev)), D, 3 * D, D, 3 * D, D, 1, None, xt.ptr(scratch), xt.ptr(d_q),
+                            xt.ptr(d_s), _st()), "eva_k_prep_w")
+    q, s = orc.quant_w(w16.astype(np.float32))               # natural order
+    # the split only permutes rows inside each 64-row head of q and k: same scales, permuted codes
+    assert (d_s.cpu().numpy() == s).all()
+    perm = np.arange(3 * D)
+    for h in range(32):
+        for pc in range(64):
+            j, i = pc >> 4, pc & 15
+            perm[h * 64 + pc] = h * 64 + 2 * (16 * (j >> 1) + i) + (j & 1)
+    assert (d_q.cpu().numpy() == q[perm]).all()
+
+
+def test_prep_fc_fold_bitexact(dev, xt, orc):
+    _say("eva_k_prep_w w12 / w2 fold + eva_k_fold_cd")
+    r = np.random.default_rng(12)
+    w12 = (r.standard_normal((2 * 2736, D)) * 0.02).astype(np.float16)
+    d_q = torch.zeros((2 * HIDP, D), dtype=torch.uint8, device=dev)
+    d_s = torch.zeros((44, 8), dtype=torch.float32, device=dev)
+    scratch = torch.empty((2 * HIDP, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_prep_w(xt.ptr(_d(w12, dev)), D, 2 * 2736, D, 2 * HIDP, D, 0, None, xt.ptr(scratch), xt.ptr(d_q),
+                            xt.ptr(d_s), _st()), "prep w12")
+    wpad = np.zeros((2 * HIDP, D), np.float32)
+    wpad[:2 * 2736] = w12.astype(np.float32)
+    q, s = orc.quant_w(wpad)
+    assert (d_q.cpu().numpy() == q).all() and (d_s.cpu().numpy() == s).all()
+
+    w2 = np.zeros((D, 2736), np.float16)
+    w2[:, :2730] = (r.standard_normal((D, 2730)) * 0.02).astype(np.float16)
+    gamma = np.zeros(2736, np.float32)
+    beta = np.zeros(2736, np.float32)
+    gamma[:2730] = 1 + 0.1 * r.standard_normal(2730)
+    beta[:2730] = 0.02 * r.standard_normal(2730)
+    d_q2 = torch.zeros((D, HIDP), dtype=torch.uint8, device=dev)
+    d_s2 = torch.zeros((8, 22), dtype=torch.float32, device=dev)
+    d_w2, d_gamma, d_beta = _d(w2, dev), _d(gamma, dev), _d(beta, dev)
+    _ok(xt.lib.eva_k_prep_w(xt.ptr(d_w2), 2736, D, 2730, D, HIDP, 0, xt.ptr(d_gamma), xt.ptr(scratch), xt.ptr(d_q2),
+                            xt.ptr(d_s2), _st()), "prep w2")
+    wt, dref = orc.fold_w2(w2.view(np.uint16), gamma, beta)
+    q2, s2 = orc.quant_w(wt)
+    assert (d_q2.cpu().numpy() == q2).all() and (d_s2.cpu().numpy() == s2).all()
+    d_c = torch.zeros(D, dtype=torch.float32, device=dev)
+    d_dd = torch.zeros(D, dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_fold_cd(xt.ptr(d_q2), xt.ptr(d_s2), xt.ptr(d_w2), 2736, xt.ptr(d_beta), xt.ptr(d_c), xt.ptr(d_dd),
+                             _st()), "fold_cd")
+    cref = orc.fold_c(q2, s2)
+    assert (d_c.cpu().numpy() == cref).all()
+    assert (d_dd.cpu().numpy() == dref).all()
+    # the fold identity: LN(h) W2^T = rstd (h W~^T - mean c) + d with unpacked W~ (export_eva.py:101-104)
+    h = r.standard_normal((4, 2730)).astype(np.float64) * 0.3
+    mu, var = h.mean(1, keepdims=True), h.var(1, keepdims=True)
+    ln = (h - mu) / np.sqrt(var + 1e-6) * gamma[:2730] + beta[:2730]
+    w2d = w2[:, :2730].astype(np.float64)
+    lhs = ln @ w2d.T
+    wtd = wt[:, :2730].astype(np.float64)
+    rhs = (h @ wtd.T - mu * wtd.sum(1)) / np.sqrt(var + 1e-6) + w2d @ beta[:2730].astype(np.float64)
+    assert np.allclose(lhs, rhs, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- fused GEMM epilogues
+def _acc_ref(orc, qa, sa, qw, sw, N):
+    return orc.gemm_f64_rows(qa, sa, qw, sw, N, np.arange(qa.shape[0])).astype(np.float32)
+
+
+def test_qkv_rope_layouts(dev, xt, orc):
+    nb = 2
+    M = nb * T
+    _say("k_qkv")
+    _, qa, sa = _packed_act(orc, M, D, 21)
+    r = np.random.default_rng(22)
+    w16 = (r.standard_normal((3 * D, D)) * 0.02).astype(np.float16)
+    ang = r.random((1024, 32)) * 6.28
+    cs = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+    d_wq = torch.zeros((3 * D, D), dtype=torch.uint8, device=dev)
+    d_ws = torch.zeros((24, 8), dtype=torch.float32, device=dev)
+    scratch = torch.empty((3 * D, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_prep_w(xt.ptr(_d(w16, dev)), D, 3 * D, D, 3 * D, D, 1, None, xt.ptr(scratch), xt.ptr(d_wq),
+                            xt.ptr(d_ws), _st()), "prep")
+    kw = [torch.zeros((nb, 16, TP, 64), dtype=torch.int16, device=dev) for _ in range(2)]
+    d_vt = torch.zeros((nb, 16, 64, TP), dtype=torch.int16, device=dev)
+    _ok(xt.lib.eva_k_qkv(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa, dev)), M, xt.ptr(d_wq), xt.ptr(d_ws), xt.ptr(_d(cs, dev)),
+                         xt.ptr(kw[0]), xt.ptr(kw[1]), xt.ptr(d_vt), M, _st()), "eva_k_qkv")
+    qw, sw = orc.quant_w(w16.astype(np.float32))
+    acc = _acc_ref(orc, qa, sa, qw, sw, 3 * D)
+    q, k, vt = orc.qkv_epi(acc, nb, cs)
+    scale = np.abs(acc).max()
+    for name, got, ref in (("q", kw[0], q), ("k", kw[1], k), ("vt", d_vt, vt)):
+        g = got.cpu().numpy().view(np.uint16)
+        _check_close(name, _bf16_f32(g), _bf16_f32(ref), scale, 2.0 ** -7)
+    # padded rows untouched
+    assert (kw[0].cpu().numpy()[:, :, T:] == 0).all() and (d_vt.cpu().numpy()[:, :, :, T:] == 0).all()
+
+
+def _attn_inputs(nb, seed):
+    r = np.random.default_rng(seed)
+    q = np.zeros((nb, 16, TP, 64), np.float32)
+    k = np.zeros((nb, 16, TP, 64), np.float32)
+    vt = np.zeros((nb, 16, 64, TP), np.float32)
+    q[:, :, :T] = r.standard_normal((nb, 16, T, 64)) * 0.6
+    k[:, :, :T] = r.standard_normal((nb, 16, T, 64)) * 0.6
+    vt[:, :, :, :T] = r.standard_normal((nb, 16, 64, T))
+    q[0, 3, 5] *= 12.0                                        # a few peaked rows exercise the lazy rescale
+    k[0, 3, 700] = q[0, 3, 5]
+    bf = lambda a: torch.from_numpy(a).to(torch.bfloat16)
+    return bf(q), bf(k), bf(vt)
+
+
+def test_flash_parity(dev, xt, orc):
+    nb = 2
+    M = nb * T
+    _say("k_flash")
+    q, k, vt = _attn_inputs(nb, 31)
+    lds = M + 7
+    d_o8 = torch.zeros((M, D), dtype=torch.uint8, device=dev)
+    d_os = torch.zeros((8, lds), dtype=torch.float32, device=dev)
+    d_o32 = torch.zeros((M, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_flash(xt.ptr(_d(q, dev)), xt.ptr(_d(k, dev)), xt.ptr(_d(vt, dev)), xt.ptr(d_o8), xt.ptr(d_os), lds,
+                           nb, xt.ptr(d_o32), _st()), "eva_k_flash")
+    ref = orc.attention(q.view(torch.int16).numpy(), k.view(torch.int16).numpy(), vt.view(torch.int16).numpy(), nb)
+    o = d_o32.cpu().numpy().astype(np.float64)
+    err = np.abs(o - ref)
+    rel = err.max() / np.abs(ref).max()
+    _say(f"  o32 max err / max|ref| {rel:.3g}, normwise {np.linalg.norm(o - ref) / np.linalg.norm(ref):.3g}")
+    # P enters the PV product in bf16 (relative 2^-9 per weight)
+    assert rel <= 4e-3
+    assert np.linalg.norm(o - ref) <= 2e-3 * np.linalg.norm(ref)
+    # packing of the kernel's own fp32 output is bit-exact
+    q8, s8 = orc.quant_act(d_o32.cpu().numpy(), lds=lds)
+    assert (d_o8.cpu().numpy() == q8).all()
+    assert (d_os.cpu().numpy()[:, :M] == s8[:, :M]).all()
+    # same kernel without the fp32 side output
+    d_o8b = torch.zeros_like(d_o8)
+    _ok(xt.lib.eva_k_flash(xt.ptr(_d(q, dev)), xt.ptr(_d(k, dev)), xt.ptr(_d(vt, dev)), xt.ptr(d_o8b), xt.ptr(d_os), lds,
+                           nb, None, _st()), "eva_k_flash")
+    assert torch.equal(d_o8b, d_o8)
+
+
+def test_flash_row_sums_and_permutation(dev, xt, orc):
+    """Invariants: V = ones gives o = 1 exactly for every query; permuting keys (with V) leaves o unchanged."""
+    nb = 1
+    q, k, vt = _attn_inputs(nb, 41)
+    vt1 = torch.zeros_like(vt)
+    vt1[:, :, :, :T] = 1.0
+    d_o8 = torch.zeros((T, D), dtype=torch.uint8, device=dev)
+    d_os = torch.zeros((8, T), dtype=torch.float32, device=dev)
+    d_o32 = torch.zeros((T, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_flash(xt.ptr(_d(q, dev)), xt.ptr(_d(k, dev)), xt.ptr(_d(vt1, dev)), xt.ptr(d_o8), xt.ptr(d_os), T,
+                           nb, xt.ptr(d_o32), _st()), "flash ones")
+    o = d_o32.cpu().numpy()
+    assert np.abs(o - 1.0).max() <= 4e-3                    # sum of bf16-rounded p over the fp32 sum of p
+    perm = np.random.default_rng(5).permutation(T)
+    kp, vp = k.clone(), vt.clone()
+    kp[:, :, :T] = k[:, :, perm]
+    vp[:, :, :, :T] = vt[:, :, :, perm]
+    d_o32b = torch.zeros_like(d_o32)
+    _ok(xt.lib.eva_k_flash(xt.ptr(_d(q, dev)), xt.ptr(_d(kp, dev)), xt.ptr(_d(vp, dev)), xt.ptr(d_o8), xt.ptr(d_os), T,
+                           nb, xt.ptr(d_o32b), _st()), "flash perm")
+    _ok(xt.lib.eva_k_flash(xt.ptr(_d(q, dev)), xt.ptr(_d(k, dev)), xt.ptr(_d(vt, dev)), xt.ptr(d_o8), xt.ptr(d_os), T,
+                           nb, xt.ptr(d_o32), _st()), "flash")
+    a, b = d_o32.cpu().numpy(), d_o32b.cpu().numpy()
+    assert np.abs(a - b).max() <= 4e-3 * np.abs(a).max()
+
+
+def test_oproj_residual(dev, xt, orc):
+    M = 2 * T
+    _say("k_oproj")
+    _, qa, sa = _packed_act(orc, M, D, 51)
+    _, qw, sw = _packed_w(orc, D, D, 52)
+    x = (np.random.default_rng(53).standard_normal((M, D)) * 2).astype(np.float16)
+    d_x = _d(x, dev)
+    _ok(xt.lib.eva_k_oproj(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa, dev)), M, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)),
+                           xt.ptr(d_x), M, _st()), "eva_k_oproj")
+    acc = _acc_ref(orc, qa, sa, qw, sw, D)
+    ref = orc.oproj_epi(acc, x.view(np.uint16))
+    _check_close("x", _f16_f32(d_x.cpu().numpy().view(np.uint16)), _f16_f32(ref), np.abs(acc).max(), 2.0 ** -10)
+
+
+def test_fc1_swiglu_pack(dev, xt, orc):
+    M = 2 * T
+    _say("k_fc1")
+    _, qa, sa = _packed_act(orc, M, D, 61)
+    r = np.random.default_rng(62)
+    w = (r.standard_normal((2 * HIDP, D)) * 0.02).astype(np.float32)
+    units = np.arange(HIDP)
+    pad = units[units >= 2730]                                # pad units have zero g and x rows, as in the blob
+    w[32 * (pad // 16) + pad % 16] = 0
+    w[32 * (pad // 16) + 16 + pad % 16] = 0
+    qw, sw = orc.quant_w(w)
+    lds = M + 3
+    sa_l = np.zeros((8, lds), np.float32)
+    sa_l[:, :M] = sa
+    d_m8 = torch.zeros((M, HIDP), dtype=torch.uint8, device=dev)
+    d_ms = torch.zeros((22, lds), dtype=torch.float32, device=dev)
+    d_st = torch.zeros((22, lds, 2), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_fc1(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa_l, dev)), lds, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)),
+                         xt.ptr(d_m8), xt.ptr(d_ms), xt.ptr(d_st), M, _st()), "eva_k_fc1")
+    h, stat = orc.fc1_epi(_acc_ref(orc, qa, sa, qw, sw, 2 * HIDP))
+    q, s = orc.quant_act(h)
+    ms = d_ms.cpu().numpy()[:, :M]
+    assert np.abs(ms / s - 1).max() < 1e-4
+    m8 = d_m8.cpu().numpy()
+    same = m8 == q
+    _say(f"  E4M3 codes differing: {np.mean(~same):.2e}")
+    assert np.mean(~same) < 2e-3
+    dq = orc.e4m3_decode(m8) * np.repeat(ms.T, 128, 1)
+    assert np.abs(dq - h).max() <= 2.0 ** -3 * np.abs(h).max() + 1e-6
+    st = d_st.cpu().numpy()[:, :M]
+    assert np.abs(st[..., 0] - stat[..., 0]).max() <= 1e-4 * np.abs(stat[..., 1]).max() ** 0.5 + 1e-5
+    assert np.abs(st[..., 1] / np.maximum(stat[..., 1], 1e-12) - 1).max() < 1e-4
+    assert (m8[:, 2730:] == 0).all()                          # pad units of h are exactly zero
+
+
+def test_fc2_folded_ln(dev, xt, orc):
+    M = 2 * T
+    _say("k_fc2")
+    r = np.random.default_rng(71)
+    h = (r.standard_normal((M, HIDP)) * 0.3).astype(np.float32)
+    h[:, 2730:] = 0
+    qa, sa = orc.quant_act(h)
+    stat = np.stack([h.reshape(M, 22, 128).sum(2).T, (h.astype(np.float64) ** 2).reshape(M, 22, 128).sum(2).T], -1)
+    stat = stat.astype(np.float32)
+    _, qw, sw = _packed_w(orc, D, HIDP, 72)
+    c = (r.standard_normal(D) * 0.5).astype(np.float32)
+    d = (r.standard_normal(D) * 0.1).astype(np.float32)
+    x = (r.standard_normal((M, D)) * 2).astype(np.float16)
+    d_x = _d(x, dev)
+    _ok(xt.lib.eva_k_fc2(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa, dev)), M, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)),
+                         xt.ptr(_d(stat, dev)), xt.ptr(_d(c, dev)), xt.ptr(_d(d, dev)), xt.ptr(d_x), M, _st()),
+        "eva_k_fc2")
+    acc = _acc_ref(orc, qa, sa, qw, sw, D)
+    ref = orc.fc2_epi(acc, stat, c, d, x.view(np.uint16))
+    S, Q = stat[..., 0].sum(0), stat[..., 1].sum(0)
+    mean = S / 2730.0
+    rstd = 1.0 / np.sqrt(np.maximum(Q / 2730.0 - mean ** 2, 0) + 1e-6)
+    scale = np.abs(rstd[:, None] * acc).max()
+    _check_close("x", _f16_f32(d_x.cpu().numpy().view(np.uint16)), _f16_f32(ref), scale, 2.0 ** -10)
+
+
+@pytest.mark.parametrize("nb,nt", [(32, 10861), (64, 13461), (1, 300)])
+def test_head_sigmoid(dev, xt, orc, nb, nt):
+    _say(f"k_head nb={nb} nt={nt}")
+    _, qa, sa = _packed_act(orc, nb, D, 81)
+    _, qw, sw = _packed_w(orc, nt, D, 82, std=0.05)
+    hb = (np.random.default_rng(83).standard_normal(nt) * 0.1).astype(np.float32)
+    d_out = torch.zeros((nb, nt), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_head(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa, dev)), nb, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)),
+                          xt.ptr(_d(hb, dev)), xt.ptr(d_out), nb, nt, _st()), "eva_k_head")
+    logit = orc.gemm_f64_rows(qa, sa, qw, sw, nt, np.arange(nb))
+    ref = 1.0 / (1.0 + np.exp(-(logit + hb)))
+    err = np.abs(d_out.cpu().numpy() - ref).max()
+    _say(f"  sigmoid max |err| {err:.2e}")
+    assert err < 1e-4
+
+
+def test_patch_embed(dev, xt, orc):
+    nb = 2
+    _say("k_pe")
+    from xtagger_amd import blob
+    r = np.random.default_rng(91)
+    inp = blob.synth_inputs(nb, seed=92)
+    pe = np.zeros((D, 592), np.float16)
+    pe[:, :588] = (r.standard_normal((D, 588)) * 0.02).astype(np.float16)
+    pos = (r.standard_normal((T, D)) * 0.02).astype(np.float32)
+    d_x = torch.zeros((nb * T, D), dtype=torch.int16, device=dev)
+    _ok(xt.lib.eva_k_pe(xt.ptr(_d(inp, dev)), xt.ptr(_d(pe, dev)), xt.ptr(_d(pos, dev)), xt.ptr(d_x), nb, _st()),
+        "eva_k_pe")
+    ref = orc.embed(inp.view(np.uint16), pe.view(np.uint16), pos, nb)
+    got = d_x.cpu().numpy().view(np.uint16)
+    _check_close("x", _f16_f32(got), _f16_f32(ref), np.abs(_f16_f32(ref)).max(), 2.0 ** -10)
+    assert (got[::T] == ref[::T]).all()                      # cls rows are pos[0] exactly

@@ -1,0 +1,176 @@
+"""The reference's eva02.bin version-2 weight blob (src/tools/export_eva.py:122-153; read by src/engine/eva.h:573-604
+and eva.h:380-430 with EVA_VER 2): writer for synthetic random-init EVA02-L weights, and a reader.
+
+Layout: 16-byte header "EVA2", u32 version 2, u32 nt (tags), u32 nbytes, 240 zero bytes, then the tensors, each on
+a 256-byte boundary of the blob:
+    pe fp16 [1024][592] (c * 196 + ky * 14 + kx, columns 588..591 zero), pos fp32 [1025][1024] (cls and conv bias
+    folded), rope fp32 [1024][32][2] (cos, sin per rotary pair), then 24 x [ln1 w, b fp32 [1024], Wqkv fp16
+    [3072][1024] (q rows carry log2(e) / sqrt(64)), Wo fp16 [1024][1024], ln2 w, b, W12 fp16 [2 * 2736][1024] (g / x
+    interleaved in 16-unit chunks, pad units zero), mlp-LN w, b fp32 [2736], W2 fp16 [1024][2736]], fc_norm w, b,
+    head fp16 [ntp][1024], head bias fp32 [ntp] (ntp = nt rounded up to 8).
+
+Synthetic weights (no checkpoint is available offline): block weights N(0, 0.02); LayerNorm gamma 1 + N(0, 0.1),
+beta N(0, 0.02); pe and pos N(0, 0.02); head N(0, head_std), bias N(0, 0.1). The rope table follows EVA02's 2-D
+rotary embedding as an assumption (the real table lives in the ONNX constants): pair p < 16 rotates with the patch
+row, p >= 16 with the column, angle = pos * 16 / 32 * 10000^(-(p % 16) / 16).
+"""
+import struct
+
+import numpy as np
+
+D, T, NP, K0, K0P, HID, HIDP_V2, NL, NH = 1024, 1025, 1024, 588, 592, 2730, 2736, 24, 16
+QSCALE = float(np.log2(np.e)) / 8.0
+
+
+def rope_table():
+    t = np.arange(NP)
+    r, c = (t // 32).astype(np.float64), (t % 32).astype(np.float64)
+    p = np.arange(32)
+    theta = 10000.0 ** (-(p % 16) / 16.0)
+    pos = np.where(p[None, :] < 16, r[:, None], c[:, None]) * (16.0 / 32.0)
+    ang = pos * theta[None, :]
+    return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+
+
+def interleave(gx):
+    """[g (HIDP rows) | x (HIDP rows)] -> 16-unit chunks [g c | x c] (export_eva.py:60-62)."""
+    return gx.reshape(2, HIDP_V2 // 16, 16, -1).transpose(1, 0, 2, 3).reshape(2 * HIDP_V2, -1)
+
+
+class _Blob:
+    def __init__(self):
+        self.buf = bytearray()
+        self.off = {}
+
+    def put(self, name, a, dt):
+        self.buf += b"\0" * (-len(self.buf) % 256)
+        self.off[name] = len(self.buf)
+        self.buf += np.ascontiguousarray(a, dtype=dt).tobytes()
+
+
+def synth_model(seed=0, nt=10861, nl=NL, head_std=0.02):
+    """Random-init EVA02-L tensors in the v2 export layout (fp16 / fp32 numpy arrays)."""
+    r = np.random.default_rng(seed)
+    f16, f32 = np.float16, np.float32
+
+    def n(shape, std):
+        return (r.standard_normal(shape, dtype=np.float32) * std).astype(f32)
+
+    m = {"nt": nt, "nl": nl}
+    pe = np.zeros((D, K0P), f32)
+    pe[:, :K0] = n((D, K0), 0.02)
+    m["pe"] = pe.astype(f16)
+    m["pos"] = n((T, D), 0.02)
+    m["rope"] = rope_table()
+    layers = []
+    for _ in range(nl):
+        L = {}
+        L["ln1w"], L["ln1b"] = 1 + n(D, 0.1), n(D, 0.02)
+        wqkv = n((3 * D, D), 0.02)
+        wqkv[:D] *= QSCALE
+        L["wqkv"] = wqkv.astype(f16)
+        L["wo"] = n((D, D), 0.02).astype(f16)
+        L["ln2w"], L["ln2b"] = 1 + n(D, 0.1), n(D, 0.02)
+        w12 = np.zeros((2 * HIDP_V2, D), f32)
+        w12[:HID] = n((HID, D), 0.02)
+        w12[HIDP_V2:HIDP_V2 + HID] = n((HID, D), 0.02)
+        L["w12"] = interleave(w12).astype(f16)
+        mw, mb = np.zeros(HIDP_V2, f32), np.zeros(HIDP_V2, f32)
+        mw[:HID], mb[:HID] = 1 + n(HID, 0.1), n(HID, 0.02)
+        L["mlnw"], L["mlnb"] = mw, mb
+        w2 = np.zeros((D, HIDP_V2), f32)
+        w2[:, :HID] = n((D, HID), 0.02)
+        L["w2"] = w2.astype(f16)
+        layers.append(L)
+    m["layers"] = layers
+    m["fnw"], m["fnb"] = 1 + n(D, 0.1), n(D, 0.02)
+    ntp = (nt + 7) & ~7
+    hw = np.zeros((ntp, D), f32)
+    hw[:nt] = n((nt, D), head_std)
+    hb = np.zeros(ntp, f32)
+    hb[:nt] = n(nt, 0.1)
+    m["hw"], m["hb"] = hw.astype(f16), hb
+    return m
+
+
+def write_v2(path, m):
+    """Write model tensors m (synth_model layout, 24 layers) as an eva02.bin v2 file."""
+    assert m["nl"] == NL, "the v2 blob always holds 24 layers"
+    b = _Blob()
+    b.put("pe", m["pe"], np.float16)
+    b.put("pos", m["pos"], np.float32)
+    b.put("rope", m["rope"], np.float32)
+    for i, L in enumerate(m["layers"]):
+        b.put(f"ln1w{i}", L["ln1w"], np.float32)
+        b.put(f"ln1b{i}", L["ln1b"], np.float32)
+        b.put(f"wqkv{i}", L["wqkv"], np.float16)
+        b.put(f"wo{i}", L["wo"], np.float16)
+        b.put(f"ln2w{i}", L["ln2w"], np.float32)
+        b.put(f"ln2b{i}", L["ln2b"], np.float32)
+        b.put(f"w12{i}", L["w12"], np.float16)
+        b.put(f"mlnw{i}", L["mlnw"], np.float32)
+        b.put(f"mlnb{i}", L["mlnb"], np.float32)
+        b.put(f"w2{i}", L["w2"], np.float16)
+    b.put("fnw", m["fnw"], np.float32)
+    b.put("fnb", m["fnb"], np.float32)
+    b.put("hw", m["hw"], np.float16)
+    b.put("hb", m["hb"], np.float32)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<4sIII", b"EVA2", 2, m["nt"], len(b.buf)))
+        f.write(b"\0" * 240)
+        f.write(b.buf)
+    return len(b.buf)
+
+
+def read_v2(path):
+    """Parse an eva02.bin v2 file into the synth_model dictionary layout (arrays view the file bytes)."""
+    raw = np.fromfile(path, np.uint8)
+    magic, ver, nt, nbytes = struct.unpack("<4sIII", raw[:16].tobytes())
+    if magic != b"EVA2" or ver != 2:
+        raise ValueError(f"{path} is not an eva02.bin v2")
+    blob = raw[256:256 + nbytes]
+    if blob.size != nbytes:
+        raise ValueError(f"{path} is truncated")
+    off = [0]
+
+    def take(shape, dt):
+        off[0] = (off[0] + 255) & ~255
+        cnt = int(np.prod(shape)) * np.dtype(dt).itemsize
+        a = blob[off[0]:off[0] + cnt].view(dt).reshape(shape)
+        off[0] += cnt
+        return a
+
+    ntp = (nt + 7) & ~7
+    m = {"nt": nt, "nl": NL}
+    m["pe"] = take((D, K0P), np.float16)
+    m["pos"] = take((T, D), np.float32)
+    m["rope"] = take((NP, 32, 2), np.float32)
+    m["layers"] = []
+    for _ in range(NL):
+        L = {}
+        L["ln1w"], L["ln1b"] = take(D, np.float32), take(D, np.float32)
+        L["wqkv"] = take((3 * D, D), np.float16)
+        L["wo"] = take((D, D), np.float16)
+        L["ln2w"], L["ln2b"] = take(D, np.float32), take(D, np.float32)
+        L["w12"] = take((2 * HIDP_V2, D), np.float16)
+        L["mlnw"], L["mlnb"] = take(HIDP_V2, np.float32), take(HIDP_V2, np.float32)
+        L["w2"] = take((D, HIDP_V2), np.float16)
+        m["layers"].append(L)
+    m["fnw"], m["fnb"] = take(D, np.float32), take(D, np.float32)
+    m["hw"] = take((ntp, D), np.float16)
+    m["hb"] = take(ntp, np.float32)
+    if off[0] != nbytes:
+        raise ValueError(f"{path}: layout mismatch ({off[0]} vs {nbytes} bytes)")
+    return m
+
+
+def synth_inputs(nb, seed=1):
+    """nb patch operands fp16 [1024][592] from 448^2 RGB images with pixels U[0, 1]: BGR scaled to [-1, 1], element
+    c * 196 + ky * 14 + kx of patch (py, px), columns 588..591 zero (procimg.h:858-866, 1606-1607)."""
+    r = np.random.default_rng(seed)
+    img = r.random((nb, 448, 448, 3), dtype=np.float32)
+    bgr = img[..., ::-1] * 2.0 - 1.0
+    p = bgr.reshape(nb, 32, 14, 32, 14, 3).transpose(0, 1, 3, 5, 2, 4).reshape(nb, NP, K0)
+    out = np.zeros((nb, NP, K0P), np.float16)
+    out[:, :, :K0] = p.astype(np.float16)
+    return out

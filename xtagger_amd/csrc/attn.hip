@@ -1,0 +1,201 @@
+// attn.hip - fused attention for EVA02-L (T = 1025 tokens, 16 heads of 64), the role of the reference's flash8
+// (src/engine/kern_common.cuh:403-543) on CDNA4 bf16 matrix cores, with the output packed to E4M3 1x128 blocks
+// for the out-projection.
+//
+// Per (image, head pair, 128-query block): 8 waves, waves 0-3 on head 2p and 4-7 on head 2p+1, 32 queries each.
+// Scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_bf16: A = 32 keys, B = 32 queries), so every lane
+// owns one query and 16 keys of a 32-key tile. Lane group g = lane >> 5 holds accumulator rows 8j + 4g + i; the K
+// fragment of lane l is read from key row pi(l & 31) with pi(8j + 4g + i) = 16(j >> 1) + 8g + 4(j & 1) + i, which
+// makes accumulators 8s .. 8s+7 exactly the keys 16s + 8g .. 16s + 8g + 7: P, converted to bf16 in place, is the
+// B operand of O^T += V^T P^T with V^T read as 16 contiguous bytes. No value moves between lanes.
+// Softmax runs in the exp2 domain (q carries log2(e)/8 from the weights) with the reference's lazy rescale: the
+// running max is refreshed only when some query of the wave grows past it by more than 8 (kern_common.cuh:480-493),
+// so p <= 2^8; l sums the fp32 p before their bf16 rounding (kern_common.cuh:505-506).
+// K and V^T tiles of 64 keys for both heads are double-buffered in LDS by buffer_load ... lds.
+#include "gemm_core.h"
+#include "xt_abi.h"
+
+#define FA_QB 128                    // queries per block
+#define FA_KT 64                     // keys per LDS tile
+#define FA_NKT ((XT_T + FA_KT - 1) / FA_KT)  // 17 key tiles
+#define FA_TILE (FA_KT * 128)        // bytes of one K or V^T tile of one head
+#define FA_STAGE (4 * FA_TILE)       // K head 0 | K head 1 | V^T head 0 | V^T head 1
+#define FA_RESCALE 8.0f
+
+__device__ __forceinline__ v8bf frag_bf(const uint8_t *tile, int row, int chunk)
+{
+    return __builtin_bit_cast(v8bf, *(const uint4 *)(tile + swz(row, chunk)));
+}
+
+__device__ __forceinline__ v8bf pack_p(const v16f &s, int base)
+{
+    typedef float v8f __attribute__((ext_vector_type(8)));
+    const v8f f = {s[base], s[base + 1], s[base + 2], s[base + 3], s[base + 4], s[base + 5], s[base + 6], s[base + 7]};
+    return __builtin_convertvector(f, v8bf);
+}
+
+template <int DBG>
+__global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
+                                               const uint16_t *__restrict__ vt, uint8_t *__restrict__ o8,
+                                               float *__restrict__ os, int lds, float *__restrict__ o32)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * FA_STAGE + 8 * 32 * 4];
+    float *xamax = (float *)(smem + 2 * FA_STAGE);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, l32 = lane & 31;
+    const int hsel = w >> 2, qt = w & 3, b = blockIdx.z;
+    const int head = 2 * blockIdx.y + hsel;
+    const int q0 = blockIdx.x * FA_QB + 32 * qt;
+    const bool active = q0 < XT_T;
+
+    // operand loads: per stage 32 x 1 KB, 4 per wave (K: 8 contiguous KB per head; V^T: 64 rows of 128 B, stride Tp)
+    const size_t hbase0 = ((size_t)b * XT_NH + 2 * blockIdx.y) * XT_TP * XT_HD;  // elements, head 2p
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(k + hbase0, 2u * XT_TP * XT_HD * 2u);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vt + hbase0, 2u * XT_TP * XT_HD * 2u);
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const int r8 = lane >> 3, ch = (lane & 7) ^ r8;
+    auto issue = [&](uint8_t *st, int kt) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int seg = wu * 4 + i;                 // 0..31: [K h0 | K h1 | V h0 | V h1] x 8 segments
+            const int tsel = seg >> 3, hh = tsel & 1, rowb = 8 * (seg & 7) + r8;
+            uint32_t off;
+            if (tsel < 2) off = (uint32_t)(((hh * XT_TP) + kt * FA_KT + rowb) * 128 + ch * 16);
+            else off = (uint32_t)(((hh * XT_HD + rowb) * XT_TP + kt * FA_KT) * 2 + ch * 16);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(tsel < 2 ? rk : rv, (lds_void *)(st + 1024 * seg), 16, (int)off, 0,
+                                                     0, 0);
+        }
+    };
+
+    // Q fragments (B operand of S^T): query q0 + l32, dims 16 step + 8 g .. + 8
+    v8bf qf[4];
+    {
+        const int qrow = active ? q0 + l32 : 0;
+        const uint16_t *qp = q + ((size_t)b * XT_NH + head) * XT_TP * XT_HD + (size_t)qrow * XT_HD + 8 * g;
+#pragma unroll
+        for (int s = 0; s < 4; s++) qf[s] = __builtin_bit_cast(v8bf, *(const uint4 *)(qp + 16 * s));
+    }
+    const int jrow = 16 * ((l32 >> 3) >> 1) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);  // pi(l32)
+
+    v16f o[2];
+    o[0] = v16f{};
+    o[1] = v16f{};
+    float mrun = -INFINITY, lsum = 0.f;
+
+    issue(smem, 0);
+    for (int kt = 0; kt < FA_NKT; kt++) {
+        uint8_t *st = smem + (kt & 1) * FA_STAGE;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (kt + 1 < FA_NKT) issue(smem + ((kt + 1) & 1) * FA_STAGE, kt + 1);
+        if (active) {
+            const uint8_t *tk = st + hsel * FA_TILE, *tv = st + (2 + hsel) * FA_TILE;
+            v16f s[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                s[u] = v16f{};
+#pragma unroll
+                for (int step = 0; step < 4; step++)
+                    s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tk, 32 * u + jrow, 2 * step + g), qf[step],
+                                                                  s[u], 0, 0, 0);
+            }
+            if (kt == FA_NKT - 1) {  // keys past 1024 are padding
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int j = e >> 2, i = e & 3;
+                        const int key = kt * FA_KT + 32 * u + 16 * (j >> 1) + 8 * g + 4 * (j & 1) + i;
+                        if (key >= XT_T) s[u][e] = -INFINITY;
+                    }
+            }
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) tmax = __builtin_fmaxf(tmax, s[u][e]);
+            tmax = __builtin_fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            if (__builtin_amdgcn_ballot_w64(tmax > mrun + FA_RESCALE) != 0) {  // wave-uniform lazy rescale
+                const float mnew = __builtin_fmaxf(mrun, tmax);
+                const float sc = __builtin_amdgcn_exp2f(mrun - mnew);
+                lsum *= sc;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    o[0][e] *= sc;
+                    o[1][e] *= sc;
+                }
+                mrun = mnew;
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const float p = __builtin_amdgcn_exp2f(s[u][e] - mrun);
+                    s[u][e] = p;
+                    lsum += p;
+                }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int sp = 0; sp < 2; sp++) {
+                    const v8bf pf = pack_p(s[u], 8 * sp);
+#pragma unroll
+                    for (int dt = 0; dt < 2; dt++)
+                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tv, 32 * dt + l32, 4 * u + 2 * sp + g),
+                                                                       pf, o[dt], 0, 0, 0);
+                }
+        }
+    }
+
+    // normalise, then E4M3 with one scale per (query, 128 columns = this head pair)
+    float amax = 0.f, inv_l = 0.f;
+    if (active) {
+        lsum += __shfl_xor(lsum, 32, 64);
+        inv_l = 1.0f / lsum;
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                o[dt][e] *= inv_l;
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(o[dt][e]));
+            }
+        amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, 64));
+    }
+    if (lane < 32) xamax[w * 32 + lane] = amax;
+    __syncthreads();
+    if (!active) return;
+    amax = __builtin_fmaxf(amax, xamax[(w ^ 4) * 32 + l32]);
+    const float sc = block_scale(amax), inv = 1.0f / sc;
+    const int query = q0 + l32;
+    if (query >= XT_T) return;
+    const size_t m = (size_t)b * XT_T + query;
+    uint8_t *dst = o8 + m * XT_D + head * XT_HD;
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int d = 32 * dt + 8 * j + 4 * g;
+            *(uint32_t *)(dst + d) = e4_pack4(o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv, o[dt][4 * j + 2] * inv,
+                                              o[dt][4 * j + 3] * inv);
+            if (DBG) {
+                float *dd = o32 + m * XT_D + head * XT_HD + d;
+                *(float4 *)dd = make_float4(o[dt][4 * j], o[dt][4 * j + 1], o[dt][4 * j + 2], o[dt][4 * j + 3]);
+            }
+        }
+    if (hsel == 0 && g == 0) os[(size_t)blockIdx.y * lds + m] = sc;
+}
+
+extern "C" int eva_k_flash(const void *q, const void *k, const void *vt, void *o8, float *os, int lds, int nb,
+                           float *o32, void *stream)
+{
+    if (nb <= 0 || lds < nb * XT_T) return xt_fail("eva_k_flash", "bad shape (nb > 0, lds >= nb * 1025)");
+    if ((((uintptr_t)q) | ((uintptr_t)k) | ((uintptr_t)vt) | ((uintptr_t)o8)) & 15)
+        return xt_fail("eva_k_flash", "q, k, vt, o8 must be 16-byte aligned");
+    const dim3 grid((XT_T + FA_QB - 1) / FA_QB, XT_NH / 2, nb);
+    if (o32)
+        hipLaunchKernelGGL(k_flash<1>, grid, dim3(512), 0, (hipStream_t)stream, (const uint16_t *)q, (const uint16_t *)k,
+                           (const uint16_t *)vt, (uint8_t *)o8, os, lds, o32);
+    else
+        hipLaunchKernelGGL(k_flash<0>, grid, dim3(512), 0, (hipStream_t)stream, (const uint16_t *)q, (const uint16_t *)k,
+                           (const uint16_t *)vt, (uint8_t *)o8, os, lds, o32);
+    return xt_check("eva_k_flash");
+}

@@ -1,0 +1,443 @@
+// engine.cpp - the wd / EVA02-L engine behind the reference's C host API (src/engine/eva.h:573-745), on HIP for one
+// MI355X. eva_open returns at once; the bring-up (device, weights, packing, buffers, graph capture) runs on its own
+// thread and eva_ready joins it. One forward = one replay of a HIP graph captured once for nb inputs (eva.h:531-536).
+#include <hip/hip_runtime.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "xt_abi.h"
+#include "xtag_eva.h"
+
+extern "C" {
+int eva_k_ln(const void *x, const float *g, const float *b, void *q, float *s, int rows, int lds, void *stream);
+int eva_k_qkv(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *cs, void *q, void *k,
+              void *vt, int rows, void *stream);
+int eva_k_flash(const void *q, const void *k, const void *vt, void *o8, float *os, int lds, int nb, float *o32,
+                void *stream);
+int eva_k_oproj(const void *a8, const float *as, int lds, const void *w, const float *ws, void *x, int rows, void *stream);
+int eva_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8, float *ms, float *stat,
+              int rows, void *stream);
+int eva_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *stat, const float *cn,
+              const float *dn, void *x, int rows, void *stream);
+int eva_k_head(const void *pq, const float *ps, int lds, const void *w, const float *ws, const float *hb, float *out,
+               int nb, int nt, void *stream);
+int eva_k_pe(const void *in, const void *pe, const float *pos, void *x, int nb, void *stream);
+int eva_k_pool(const void *x, float *p, int nb, void *stream);
+int eva_k_lnh(const float *p, const float *g, const float *b, void *pn, void *q, float *s, int rows, int lds,
+              void *stream);
+int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_out, int perm, const float *colscale,
+                 float *scratch, void *q, float *s, void *stream);
+int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const float *beta, float *c, float *d,
+                  void *stream);
+}
+
+#define V2_HIDP 2736          // hidden padding of the reference's v2 blob (export_eva.py:19)
+#define EVA_CHUNK (32u << 20) // weight streaming chunk (eva.h:59)
+#define EVA_HB_OFF (-16.0f)   // bias of an extra head row nothing has written (eva.h:69)
+
+struct Layer {
+    const float *ln1w, *ln1b, *ln2w, *ln2b, *mlnw, *mlnb;  // in the blob
+    const uint16_t *wqkv16, *wo16, *w1216, *w216;          // fp16 block weights in the blob
+    uint8_t *wqkv, *wo, *w12, *w2;                         // packed E4M3
+    float *sqkv, *so, *s12, *s2, *cn, *dn;
+};
+
+struct eva_impl {
+    int devno, bstatus, up, booted;
+    pthread_t boot;
+    char *path;                                            // own copy of the weights path
+    size_t wbytes;
+    uint32_t nb, M, Mp;                                    // inputs per launch, token rows, rows padded to 256
+    hipStream_t st;
+    uint8_t *blob;                                         // the file's tensors, resident
+    const uint16_t *pe;
+    const float *pos, *cs, *fnw, *fnb, *hb0;
+    const uint16_t *hw0;
+    Layer L[EVA_NL];
+    uint16_t *hmaster;                                     // head fp16 [nt][1024] (file rows, then extra rows)
+    float *hb;                                             // [nt]
+    uint8_t *hq;                                           // head E4M3 [ceil(nt/128)*128][1024]
+    float *hs;                                             // [ceil(nt/128)][8]
+    float *scratch;
+    // activations
+    uint16_t *in, *x, *q, *k, *vt, *pn;
+    uint8_t *h8, *m8, *pq;
+    float *sh, *sm, *stat, *pool, *ps, *out;
+    hipGraphExec_t graph;
+    hipEvent_t done[EVA_NBUF];
+    uint16_t *stage;                                       // pinned staging for inputs (nb inputs)
+    std::vector<void *> allocs;
+};
+
+static int ev_alloc(eva_impl *E, void **p, size_t bytes, bool zero)
+{
+    if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) return xt_fail("hipMalloc", "out of device memory");
+    E->allocs.push_back(*p);
+    if (zero && hipMemset(*p, 0, bytes) != hipSuccess) return xt_fail("hipMemset", "failed");
+    return 0;
+}
+#define EV_ALLOC(E, p, bytes, zero)                                    \
+    do {                                                               \
+        void *tmp_;                                                    \
+        if (ev_alloc((E), &tmp_, (bytes), (zero))) return -1;          \
+        (p) = (decltype(p))tmp_;                                       \
+    } while (0)
+#define EV_CK(call)                                                    \
+    do {                                                               \
+        if ((call)) return -1;                                         \
+    } while (0)
+
+// Blob layout of export_eva.py v2 (eva.h:380-430 with EVA_VER 2): every tensor on a 256-byte boundary.
+static int ev_layout(eva_impl *E, uint32_t ntp)
+{
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> uint8_t * {
+        off = (off + 255) & ~(size_t)255;
+        uint8_t *p = E->blob + off;
+        off += bytes;
+        return p;
+    };
+    E->pe = (const uint16_t *)take((size_t)EVA_D * EVA_K0P * 2);
+    E->pos = (const float *)take((size_t)EVA_T * EVA_D * 4);
+    E->cs = (const float *)take((size_t)EVA_NP * 32 * 2 * 4);
+    for (int i = 0; i < EVA_NL; i++) {
+        Layer &L = E->L[i];
+        L.ln1w = (const float *)take(EVA_D * 4);
+        L.ln1b = (const float *)take(EVA_D * 4);
+        L.wqkv16 = (const uint16_t *)take((size_t)3 * EVA_D * EVA_D * 2);
+        L.wo16 = (const uint16_t *)take((size_t)EVA_D * EVA_D * 2);
+        L.ln2w = (const float *)take(EVA_D * 4);
+        L.ln2b = (const float *)take(EVA_D * 4);
+        L.w1216 = (const uint16_t *)take((size_t)2 * V2_HIDP * EVA_D * 2);
+        L.mlnw = (const float *)take(V2_HIDP * 4);
+        L.mlnb = (const float *)take(V2_HIDP * 4);
+        L.w216 = (const uint16_t *)take((size_t)EVA_D * V2_HIDP * 2);
+    }
+    E->fnw = (const float *)take(EVA_D * 4);
+    E->fnb = (const float *)take(EVA_D * 4);
+    E->hw0 = (const uint16_t *)take((size_t)ntp * EVA_D * 2);
+    E->hb0 = (const float *)take((size_t)ntp * 4);
+    if (off != E->wbytes) {
+        fprintf(stderr, "eva: weight layout mismatch (%zu vs %zu bytes)\n", off, E->wbytes);
+        return -1;
+    }
+    return 0;
+}
+
+// file bytes [256, 256 + wbytes) -> device, through two pinned chunks (eva.h:343-376)
+static int ev_stream_weights(eva_impl *E)
+{
+    FILE *f = fopen(E->path, "rb");
+    void *buf[2] = {NULL, NULL};
+    hipEvent_t ev[2] = {NULL, NULL};
+    size_t off = 0, n;
+    int i = 0, rc = -1;
+
+    if (!f) return xt_fail("weights", "cannot open");
+    if (fseek(f, 256, SEEK_SET)) goto out;
+    for (int j = 0; j < 2; j++)
+        if (hipHostMalloc(&buf[j], EVA_CHUNK, hipHostMallocDefault) != hipSuccess || hipEventCreate(&ev[j]) != hipSuccess)
+            goto out;
+    for (off = 0; off < E->wbytes; off += n, i ^= 1) {
+        n = E->wbytes - off < EVA_CHUNK ? E->wbytes - off : EVA_CHUNK;
+        if (hipEventSynchronize(ev[i]) != hipSuccess || fread(buf[i], 1, n, f) != n) goto out;
+        if (hipMemcpyAsync(E->blob + off, buf[i], n, hipMemcpyHostToDevice, E->st) != hipSuccess) goto out;
+        if (hipEventRecord(ev[i], E->st) != hipSuccess) goto out;
+    }
+    if (hipStreamSynchronize(E->st) == hipSuccess) rc = 0;
+out:
+    (void)hipStreamSynchronize(E->st);
+    for (int j = 0; j < 2; j++) {
+        if (ev[j]) (void)hipEventDestroy(ev[j]);
+        if (buf[j]) (void)hipHostFree(buf[j]);
+    }
+    fclose(f);
+    if (rc) fprintf(stderr, "eva: cannot stream weights from %s\n", E->path);
+    return rc;
+}
+
+// The whole forward for nb inputs on E->st (captured once into E->graph), eva.h:227-310.
+static int ev_forward(eva *e)
+{
+    eva_impl *E = e->impl;
+    void *st = (void *)E->st;
+    const int M = (int)E->M, lds = (int)E->Mp, nb = (int)E->nb;
+
+    EV_CK(eva_k_pe(E->in, E->pe, E->pos, E->x, nb, st));
+    for (int i = 0; i < EVA_NL; i++) {
+        const Layer &L = E->L[i];
+        EV_CK(eva_k_ln(E->x, L.ln1w, L.ln1b, E->h8, E->sh, M, lds, st));
+        EV_CK(eva_k_qkv(E->h8, E->sh, lds, L.wqkv, L.sqkv, E->cs, E->q, E->k, E->vt, M, st));
+        EV_CK(eva_k_flash(E->q, E->k, E->vt, E->h8, E->sh, lds, nb, NULL, st));
+        EV_CK(eva_k_oproj(E->h8, E->sh, lds, L.wo, L.so, E->x, M, st));
+        EV_CK(eva_k_ln(E->x, L.ln2w, L.ln2b, E->h8, E->sh, M, lds, st));
+        EV_CK(eva_k_fc1(E->h8, E->sh, lds, L.w12, L.s12, E->m8, E->sm, E->stat, M, st));
+        EV_CK(eva_k_fc2(E->m8, E->sm, lds, L.w2, L.s2, E->stat, L.cn, L.dn, E->x, M, st));
+    }
+    EV_CK(eva_k_pool(E->x, E->pool, nb, st));
+    EV_CK(eva_k_lnh(E->pool, E->fnw, E->fnb, E->pn, E->pq, E->ps, nb, nb, st));
+    EV_CK(eva_k_head(E->pq, E->ps, nb, E->hq, E->hs, E->hb, E->out, nb, (int)e->nt, st));
+    return 0;
+}
+
+// pack one 128-row block of the head from the fp16 master
+static int ev_pack_head_block(eva *e, uint32_t blk)
+{
+    eva_impl *E = e->impl;
+    const uint32_t r0 = blk * 128, n = e->nt - r0 < 128 ? e->nt - r0 : 128;
+    return eva_k_prep_w(E->hmaster + (size_t)r0 * EVA_D, EVA_D, (int)n, EVA_D, 128, EVA_D, 0, NULL, E->scratch,
+                        E->hq + (size_t)r0 * EVA_D, E->hs + (size_t)blk * 8, (void *)E->st);
+}
+
+static int ev_up(eva *e)
+{
+    eva_impl *E = e->impl;
+    const uint32_t ntp = (e->nt0 + 7) & ~7u, nt = e->nt, nblk = (nt + 127) / 128;
+    void *st;
+
+    XT_HIP(hipSetDevice(E->devno));
+    XT_HIP(hipStreamCreateWithFlags(&E->st, hipStreamNonBlocking));
+    st = (void *)E->st;
+    EV_ALLOC(E, E->blob, E->wbytes, false);
+    if (ev_stream_weights(E) || ev_layout(E, ntp)) return -1;
+
+    // packed weights (bring-up packing on the GPU)
+    EV_ALLOC(E, E->scratch, (size_t)2 * EVA_HIDP * EVA_D * 4, false);
+    for (int i = 0; i < EVA_NL; i++) {
+        Layer &L = E->L[i];
+        EV_ALLOC(E, L.wqkv, (size_t)3 * EVA_D * EVA_D, false);
+        EV_ALLOC(E, L.sqkv, 24 * 8 * 4, false);
+        EV_ALLOC(E, L.wo, (size_t)EVA_D * EVA_D, false);
+        EV_ALLOC(E, L.so, 8 * 8 * 4, false);
+        EV_ALLOC(E, L.w12, (size_t)2 * EVA_HIDP * EVA_D, false);
+        EV_ALLOC(E, L.s12, 44 * 8 * 4, false);
+        EV_ALLOC(E, L.w2, (size_t)EVA_D * EVA_HIDP, false);
+        EV_ALLOC(E, L.s2, 8 * 22 * 4, false);
+        EV_ALLOC(E, L.cn, EVA_D * 4, false);
+        EV_ALLOC(E, L.dn, EVA_D * 4, false);
+        EV_CK(eva_k_prep_w(L.wqkv16, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, NULL, E->scratch, L.wqkv, L.sqkv, st));
+        EV_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
+        EV_CK(eva_k_prep_w(L.w1216, EVA_D, 2 * V2_HIDP, EVA_D, 2 * EVA_HIDP, EVA_D, 0, NULL, E->scratch, L.w12, L.s12, st));
+        EV_CK(eva_k_prep_w(L.w216, V2_HIDP, EVA_D, EVA_HID, EVA_D, EVA_HIDP, 0, L.mlnw, E->scratch, L.w2, L.s2, st));
+        EV_CK(eva_k_fold_cd(L.w2, L.s2, L.w216, V2_HIDP, L.mlnb, L.cn, L.dn, st));
+    }
+    // head: fp16 master (file rows, then zero extra rows with bias -16), packed per 128-row block
+    EV_ALLOC(E, E->hmaster, (size_t)nt * EVA_D * 2, true);
+    EV_ALLOC(E, E->hb, (size_t)nt * 4, false);
+    EV_ALLOC(E, E->hq, (size_t)nblk * 128 * EVA_D, false);
+    EV_ALLOC(E, E->hs, (size_t)nblk * 8 * 4, false);
+    XT_HIP(hipMemcpyAsync(E->hmaster, E->hw0, (size_t)e->nt0 * EVA_D * 2, hipMemcpyDeviceToDevice, E->st));
+    XT_HIP(hipMemcpyAsync(E->hb, E->hb0, (size_t)e->nt0 * 4, hipMemcpyDeviceToDevice, E->st));
+    if (nt > e->nt0) {
+        std::vector<float> nb16(nt - e->nt0, EVA_HB_OFF);
+        XT_HIP(hipMemcpy(E->hb + e->nt0, nb16.data(), nb16.size() * 4, hipMemcpyHostToDevice));
+    }
+    for (uint32_t b = 0; b < nblk; b++) EV_CK(ev_pack_head_block(e, b));
+
+    // activations
+    const size_t M = E->M, Mp = E->Mp, nb = E->nb;
+    const size_t qkvb = nb * EVA_NH * 1088 * 64 * 2;
+    EV_ALLOC(E, E->in, nb * EVA_IN * 2, true);
+    EV_ALLOC(E, E->x, Mp * EVA_D * 2, true);
+    EV_ALLOC(E, E->h8, Mp * EVA_D, true);
+    EV_ALLOC(E, E->sh, 8 * Mp * 4, true);
+    EV_ALLOC(E, E->q, qkvb, true);                      // padded attention rows stay zero forever
+    EV_ALLOC(E, E->k, qkvb, true);
+    EV_ALLOC(E, E->vt, qkvb, true);
+    EV_ALLOC(E, E->m8, Mp * EVA_HIDP, true);
+    EV_ALLOC(E, E->sm, 22 * Mp * 4, true);
+    EV_ALLOC(E, E->stat, 22 * Mp * 8, true);
+    EV_ALLOC(E, E->pool, nb * EVA_D * 4, true);
+    EV_ALLOC(E, E->pn, nb * EVA_D * 2, true);
+    EV_ALLOC(E, E->pq, nb * EVA_D, true);
+    EV_ALLOC(E, E->ps, 8 * nb * 4, true);
+    EV_ALLOC(E, E->out, nb * nt * 4, true);
+    (void)M;
+    XT_HIP(hipHostMalloc((void **)&E->stage, nb * EVA_IN * 2, hipHostMallocDefault));
+    for (int s = 0; s < EVA_NBUF; s++) {
+        XT_HIP(hipHostMalloc((void **)&e->hout[s], nb * nt * 4, hipHostMallocDefault));
+        if (nt > e->nt0) XT_HIP(hipHostMalloc((void **)&e->hpn[s], nb * EVA_D * 2, hipHostMallocDefault));
+        XT_HIP(hipEventCreateWithFlags(&E->done[s], hipEventDisableTiming));
+    }
+    XT_HIP(hipStreamSynchronize(E->st));
+
+    // graph capture of the forward
+    hipGraph_t g;
+    XT_HIP(hipStreamBeginCapture(E->st, hipStreamCaptureModeThreadLocal));
+    if (ev_forward(e)) {
+        (void)hipStreamEndCapture(E->st, &g);
+        return -1;
+    }
+    XT_HIP(hipStreamEndCapture(E->st, &g));
+    XT_HIP(hipGraphInstantiate(&E->graph, g, NULL, NULL, 0));
+    XT_HIP(hipGraphDestroy(g));
+    XT_HIP(hipGraphUpload(E->graph, E->st));
+    XT_HIP(hipStreamSynchronize(E->st));
+    return 0;
+}
+
+static void *ev_boot(void *arg)
+{
+    eva *e = (eva *)arg;
+    e->impl->bstatus = ev_up(e);
+    return NULL;
+}
+
+extern "C" int eva_open_nb(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra, uint32_t nb)
+{
+    uint32_t hdr[4];
+    FILE *f;
+
+    (void)pool;
+    (void)poolb;
+    memset(e, 0, sizeof(*e));
+    if (nb < 1 || nb > EVA_NBMAX) return xt_fail("eva_open", "batch must be 1..EVA_NBMAX");
+    f = fopen(weights, "rb");
+    if (!f || fread(hdr, 4, 4, f) != 4 || memcmp(hdr, "EVA2", 4) || hdr[1] != 2) {
+        fprintf(stderr, "eva: %s is not an eva02.bin v2 (run export_eva.py without a calibration file)\n", weights);
+        if (f) fclose(f);
+        return -1;
+    }
+    fclose(f);
+    eva_impl *E = new eva_impl();
+    e->impl = E;
+    E->path = strdup(weights);
+    if (!E->path) return xt_fail("eva_open", "out of memory");
+    E->devno = device;
+    E->wbytes = hdr[3];
+    E->nb = nb;
+    E->M = nb * EVA_T;
+    E->Mp = (E->M + 255) & ~255u;
+    e->nt0 = hdr[2];
+    e->nt = hdr[2] + extra;
+    e->ntp = (hdr[2] + 7) & ~7u;
+    e->nb = nb;
+    E->bstatus = -1;
+    if (pthread_create(&E->boot, NULL, ev_boot, e)) return xt_fail("eva_open", "cannot start the bring-up thread");
+    E->booted = 1;
+    return 0;
+}
+
+extern "C" int eva_open(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra)
+{
+    return eva_open_nb(e, weights, device, pool, poolb, extra, EVA_NB);
+}
+
+extern "C" int eva_ready(eva *e)
+{
+    eva_impl *E = e->impl;
+    if (!E) return -1;
+    if (E->up) return 0;
+    if (E->booted) {
+        pthread_join(E->boot, NULL);
+        E->booted = 0;
+    }
+    if (E->bstatus) return -1;
+    XT_HIP(hipSetDevice(E->devno));
+    E->up = 1;
+    return 0;
+}
+
+extern "C" int eva_poll(eva *e)
+{
+    eva_impl *E = e->impl;
+    if (!E) return 0;
+    if (E->up) return 1;
+    return E->booted ? pthread_tryjoin_np(E->boot, NULL) == 0 ? (E->booted = 0, 1) : 0 : 1;
+}
+
+extern "C" int eva_submit(eva *e, uint32_t buf, uint16_t *const *in, uint32_t n)
+{
+    if (eva_ready(e)) return -1;
+    eva_impl *E = e->impl;
+    if (buf >= EVA_NBUF || n > E->nb) return xt_fail("eva_submit", "buf >= EVA_NBUF or n > nb");
+    // inputs staged into engine-owned pinned memory (this platform does not page-lock caller memory in place)
+    XT_HIP(hipStreamSynchronize(E->st));
+    for (uint32_t i = 0; i < n; i++) memcpy(E->stage + (size_t)i * EVA_IN, in[i], EVA_IN * 2);
+    if (n) XT_HIP(hipMemcpyAsync(E->in, E->stage, (size_t)n * EVA_IN * 2, hipMemcpyHostToDevice, E->st));
+    XT_HIP(hipGraphLaunch(E->graph, E->st));
+    if (n) XT_HIP(hipMemcpyAsync(e->hout[buf], E->out, (size_t)n * e->nt * 4, hipMemcpyDeviceToHost, E->st));
+    if (e->hpn[buf] && n) XT_HIP(hipMemcpyAsync(e->hpn[buf], E->pn, (size_t)n * EVA_D * 2, hipMemcpyDeviceToHost, E->st));
+    XT_HIP(hipEventRecord(E->done[buf], E->st));
+    return 0;
+}
+
+extern "C" int eva_query(eva *e, uint32_t buf)
+{
+    eva_impl *E = e->impl;
+    if (!E || !E->up || buf >= EVA_NBUF) return 1;
+    return hipEventQuery(E->done[buf]) != hipErrorNotReady;
+}
+
+extern "C" const float *eva_wait(eva *e, uint32_t buf)
+{
+    eva_impl *E = e->impl;
+    if (!E || !E->up || buf >= EVA_NBUF) return NULL;
+    return hipEventSynchronize(E->done[buf]) == hipSuccess ? e->hout[buf] : NULL;
+}
+
+extern "C" int eva_head_put(eva *e, uint32_t j, const uint16_t *w, float bias)
+{
+    if (eva_ready(e)) return -1;
+    eva_impl *E = e->impl;
+    if (j >= e->nt) return xt_fail("eva_head_put", "row past nt");
+    XT_HIP(hipMemcpyAsync(E->hmaster + (size_t)j * EVA_D, w, EVA_D * 2, hipMemcpyHostToDevice, E->st));
+    XT_HIP(hipMemcpyAsync(E->hb + j, &bias, 4, hipMemcpyHostToDevice, E->st));
+    XT_HIP(hipStreamSynchronize(E->st));  // bias and row are pageable: copied before the call returns
+    return ev_pack_head_block(e, j / 128);
+}
+
+extern "C" int eva_head_get(eva *e, uint16_t *w, float *bias)
+{
+    if (eva_ready(e)) return -1;
+    eva_impl *E = e->impl;
+    XT_HIP(hipStreamSynchronize(E->st));
+    XT_HIP(hipMemcpy(w, E->hw0, (size_t)e->nt0 * EVA_D * 2, hipMemcpyDeviceToHost));
+    XT_HIP(hipMemcpy(bias, E->hb0, (size_t)e->nt0 * 4, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+extern "C" void eva_close(eva *e)
+{
+    eva_impl *E = e->impl;
+    if (!E) return;
+    if (E->booted) {
+        pthread_join(E->boot, NULL);
+        E->booted = 0;
+    }
+    (void)hipSetDevice(E->devno);
+    if (E->st) (void)hipStreamSynchronize(E->st);
+    if (E->graph) (void)hipGraphExecDestroy(E->graph);
+    for (int s = 0; s < EVA_NBUF; s++) {
+        if (E->done[s]) (void)hipEventDestroy(E->done[s]);
+        if (e->hout[s]) (void)hipHostFree(e->hout[s]);
+        if (e->hpn[s]) (void)hipHostFree(e->hpn[s]);
+    }
+    if (E->stage) (void)hipHostFree(E->stage);
+    for (void *p : E->allocs) (void)hipFree(p);
+    if (E->st) (void)hipStreamDestroy(E->st);
+    free(E->path);
+    delete E;
+    memset(e, 0, sizeof(*e));
+}
+
+extern "C" void *eva_dev_input(eva *e) { return eva_ready(e) ? NULL : (void *)e->impl->in; }
+extern "C" const float *eva_dev_output(eva *e) { return eva_ready(e) ? NULL : e->impl->out; }
+extern "C" void *eva_stream_handle(eva *e) { return eva_ready(e) ? NULL : (void *)e->impl->st; }
+extern "C" int eva_run(eva *e)
+{
+    if (eva_ready(e)) return -1;
+    XT_HIP(hipGraphLaunch(e->impl->graph, e->impl->st));
+    return 0;
+}
+extern "C" int eva_sync(eva *e)
+{
+    if (eva_ready(e)) return -1;
+    XT_HIP(hipStreamSynchronize(e->impl->st));
+    return 0;
+}

@@ -1,0 +1,429 @@
+// layer.hip - the EVA02-L block GEMMs with their fused epilogues, all on the block-scaled main loop (gemm_core.h),
+// plus the fp16 patch embedding. Reference roles (src/engine/eva_kernels.cu): k_qkv (41-114), k_oproj (134-162),
+// k_fc1 (211-279), k_fc2 (286-334), k_pe + k_embed (126-130, 21-33), and the head k_headmv
+// (src/engine/kern_common.cuh:679-727) as a block-scaled FP8 GEMM.
+//
+// Token rows: m = 1025 b + t for image b, token t (t = 0 is cls). Activations E4M3 [rows][K] with 1x128 scale
+// planes [K/128][lds]; residual x fp16 [rows][1024].
+#include "gemm_core.h"
+#include "xt_abi.h"
+
+typedef BsCfg<128, 256, 2, 4, 3> LayerCfg;  // 8 waves of 64 x 64: one head (qkv) or 32 SwiGLU units (fc1) per wave
+typedef BsCfg<64, 128, 1, 2, 3> HeadCfg;    // head: few rows, 10861 columns
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b)
+{
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), b2));
+}
+
+template <class C>
+__device__ __forceinline__ void layer_tile(int M, int N, int &m0, int &n0)
+{
+    int tm, tn;
+    tile_of_block((M + C::BM - 1) / C::BM, (N + C::BN - 1) / C::BN, tm, tn);
+    m0 = tm * C::BM;
+    n0 = tn * C::BN;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// k_qkv: h8 [rows][1024] x Wqkv [3072][1024] -> q, k bf16 [nb][16][1088][64] (RoPE on patch tokens), vt bf16
+// [nb][16][64][1088]. A 256-column block is 4 heads of one of q | k | v; each wave owns one head. The weight rows of
+// q and k heads are stored pair-split (see eva_prep_qkv): column tile 2p holds dims 2i and tile 2p+1 dims 2i+1 of
+// pair i = 16p + (lane & 15), so a rotary pair meets in one lane. q rows carry log2(e)/8 (export_eva.py:71).
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
+                                                     int lds, const uint8_t *__restrict__ w,
+                                                     const float *__restrict__ ws, const float *__restrict__ cs,
+                                                     uint16_t *__restrict__ q, uint16_t *__restrict__ k,
+                                                     uint16_t *__restrict__ vt, int rows)
+{
+    using C = LayerCfg;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    v4f acc[C::TM][C::TN];
+    int m0, n0, wm0, wn0;
+    layer_tile<C>(rows, 3 * XT_D, m0, n0);
+    bs_mainloop<C>(h8, XT_D, hs, lds, w, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, acc);
+    bs_wave_origin<C>(wm0, wn0);
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const int part = n0 >> 10, head = ((n0 & 1023) + wn0) >> 6;
+    if (part < 2) {
+        uint16_t *dst = part ? k : q;
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm0 + 16 * i + 4 * g + r;
+                if (m >= rows) continue;
+                const int b = m / XT_T, t = m - b * XT_T;
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    const int pi = 16 * p + c16;
+                    float f0 = acc[i][2 * p][r], f1 = acc[i][2 * p + 1][r];
+                    if (t) {  // eva_kernels.cu:74-79
+                        const float2 a = *(const float2 *)(cs + ((size_t)(t - 1) * 32 + pi) * 2);
+                        const float g0 = f0 * a.x - f1 * a.y;
+                        f1 = f1 * a.x + f0 * a.y;
+                        f0 = g0;
+                    }
+                    *(uint32_t *)(dst + (((size_t)b * XT_NH + head) * XT_TP + t) * XT_HD + 2 * pi) = pk_bf16(f0, f1);
+                }
+            }
+        return;
+    }
+    // v: transpose the wave's 64 rows x 64 dims through LDS, then lanes walk rows (consecutive tokens)
+    uint16_t *tr = (uint16_t *)(smem + (threadIdx.x >> 6) * 64 * 66 * 2);  // [64 dims][66] bf16, padded rows
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int j = 0; j < C::TN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t two = pk_bf16(acc[i][j][r], 0.f);
+                tr[(16 * j + c16) * 66 + 16 * i + 4 * g + r] = (uint16_t)two;
+            }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int m = m0 + wm0 + lane;
+    if (m < rows) {
+        const int b = m / XT_T, t = m - b * XT_T;
+        uint16_t *dst = vt + ((size_t)b * XT_NH + head) * XT_HD * XT_TP + t;
+#pragma unroll 8
+        for (int d = 0; d < XT_HD; d++) dst[(size_t)d * XT_TP] = tr[d * 66 + lane];
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// k_oproj: x [rows][1024] = f16(x + attn_out . Wo^T) (eva_kernels.cu:150-160, alpha folded into the block scales)
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restrict__ a8, const float *__restrict__ as,
+                                                       int lds, const uint8_t *__restrict__ w,
+                                                       const float *__restrict__ ws, uint16_t *__restrict__ x, int rows)
+{
+    using C = LayerCfg;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    v4f acc[C::TM][C::TN];
+    int m0, n0, wm0, wn0;
+    layer_tile<C>(rows, XT_D, m0, n0);
+    bs_mainloop<C>(a8, XT_D, as, lds, w, ws, rows, XT_D, XT_D, m0, n0, smem, acc);
+    bs_wave_origin<C>(wm0, wn0);
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = m0 + wm0 + 16 * i + 4 * g + r;
+            if (m >= rows) continue;
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                uint16_t *p = x + (size_t)m * XT_D + n0 + wn0 + 16 * j + c16;
+                *p = f2h(h2f(*p) + acc[i][j][r]);
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// k_fc1: h8 [rows][1024] x W12 [5632][1024] -> SwiGLU h = silu(g) x (silu(g) = g / (1 + e^-g)), packed to
+// m8 [rows][2816] E4M3 with 1x128 scales ms [22][lds], and per-(row, block) (sum h, sum h^2) of the unpacked h in
+// stat [22][lds][2] for the folded MLP LayerNorm (eva_kernels.cu:211-279). W12 rows hold g and x of 16 units in
+// alternate 16-row chunks (export_eva.py:60-62), so column tile 2c is g and 2c+1 is x of the same 16 units: a
+// 256-column block is one 128-unit block of h, whose |max| and sums meet through LDS across the 4 column waves.
+// Each (row, block) partial has one writer: no atomics, deterministic.
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
+                                                     int lds, const uint8_t *__restrict__ w,
+                                                     const float *__restrict__ ws, uint8_t *__restrict__ m8,
+                                                     float *__restrict__ ms, float *__restrict__ stat, int rows)
+{
+    using C = LayerCfg;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    v4f acc[C::TM][C::TN];
+    int m0, n0, wm0, wn0;
+    layer_tile<C>(rows, 2 * XT_HIDP, m0, n0);
+    bs_mainloop<C>(h8, XT_D, hs, lds, w, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc);
+    bs_wave_origin<C>(wm0, wn0);
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const int wm = wm0 / C::WM, wn = wn0 / C::WN, ct = n0 >> 8;
+    float *red = (float *)smem;                          // [3][2 wm][4 wn][64 rows]: amax, sum, sum of squares
+    uint8_t *qt = smem + 3 * 2 * 4 * 64 * 4;             // [128 rows][128 units] E4M3 staging
+    float h[C::TM][2][4];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float amax = 0.f, s = 0.f, q = 0.f;
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const float gg = acc[i][2 * p][r], xx = acc[i][2 * p + 1][r];
+                const float e = __expf(-gg), den = 1.0f + e, sg = gg / den;
+                const float v = sg * xx;
+                h[i][p][r] = v;
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
+                s += v;
+                q = __builtin_fmaf(v, v, q);
+            }
+            amax = group_max<16>(amax);
+            s = group_sum<16>(s);
+            q = group_sum<16>(q);
+            if (c16 == 0) {
+                const int rr = 16 * i + 4 * g + r;
+                red[((0 * 2 + wm) * 4 + wn) * 64 + rr] = amax;
+                red[((1 * 2 + wm) * 4 + wn) * 64 + rr] = s;
+                red[((2 * 2 + wm) * 4 + wn) * 64 + rr] = q;
+            }
+        }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rr = 16 * i + 4 * g + r;
+            float amax = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; u++) amax = __builtin_fmaxf(amax, red[((0 * 2 + wm) * 4 + u) * 64 + rr]);
+            const float sc = block_scale(amax), inv = 1.0f / sc;
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+                qt[(wm0 + rr) * 128 + 32 * wn + 16 * p + c16] = (uint8_t)e4_pack2(h[i][p][r] * inv, 0.f);
+        }
+    // one thread per block row: scale and the row sums (column waves added in order)
+    if (threadIdx.x < C::BM) {
+        const int rr = threadIdx.x, m = m0 + rr, wmr = rr >> 6, r64 = rr & 63;
+        float amax = 0.f, s = 0.f, q = 0.f;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            amax = __builtin_fmaxf(amax, red[((0 * 2 + wmr) * 4 + u) * 64 + r64]);
+            s += red[((1 * 2 + wmr) * 4 + u) * 64 + r64];
+            q += red[((2 * 2 + wmr) * 4 + u) * 64 + r64];
+        }
+        if (m < rows) {
+            ms[(size_t)ct * lds + m] = block_scale(amax);
+            *(float2 *)(stat + ((size_t)ct * lds + m) * 2) = make_float2(s, q);
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < C::BM * 8; idx += C::NT) {
+        const int rr = idx >> 3, ch = idx & 7, m = m0 + rr;
+        if (m < rows) *(uint4 *)(m8 + (size_t)m * XT_HIDP + ct * 128 + ch * 16) = *(const uint4 *)(qt + rr * 128 + ch * 16);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// k_fc2: x = f16(x + rstd (acc - mean c) + d) with acc = m8 . W~^T (W~ = W2 diag(gamma), c = W~ 1 from the packed
+// W~, d = W2 beta), mean / rstd of the SwiGLU row over 2730 units from k_fc1's 22 partials summed in block order:
+// mean = S / 2730, var = max(Q / 2730 - mean^2, 0), rstd = 1 / sqrt(var + 1e-6) (eva_kernels.cu:300-333).
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict__ m8, const float *__restrict__ ms,
+                                                     int lds, const uint8_t *__restrict__ w,
+                                                     const float *__restrict__ ws, const float *__restrict__ stat,
+                                                     const float *__restrict__ cn, const float *__restrict__ dn,
+                                                     uint16_t *__restrict__ x, int rows)
+{
+    using C = LayerCfg;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    v4f acc[C::TM][C::TN];
+    int m0, n0, wm0, wn0;
+    layer_tile<C>(rows, XT_D, m0, n0);
+    bs_mainloop<C>(m8, XT_HIDP, ms, lds, w, ws, rows, XT_D, XT_HIDP, m0, n0, smem, acc);
+    bs_wave_origin<C>(wm0, wn0);
+    float2 *rs = (float2 *)smem;  // [128 rows] (rstd, -mean * rstd)
+    if (threadIdx.x < C::BM) {
+        const int m = m0 + threadIdx.x;
+        float S = 0.f, Q = 0.f;
+        if (m < rows)
+            for (int blk = 0; blk < XT_HIDP / 128; blk++) {
+                const float2 p = *(const float2 *)(stat + ((size_t)blk * lds + m) * 2);
+                S += p.x;
+                Q += p.y;
+            }
+        const float mean = S / (float)XT_HID;
+        float var = Q / (float)XT_HID - mean * mean;
+        var = __builtin_fmaxf(var, 0.f);
+        const float rstd = 1.0f / __builtin_sqrtf(var + XT_EPS);
+        rs[threadIdx.x] = make_float2(rstd, -mean * rstd);
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rr = wm0 + 16 * i + 4 * g + r, m = m0 + rr;
+            if (m >= rows) continue;
+            const float2 st = rs[rr];
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                const int n = n0 + wn0 + 16 * j + c16;
+                const float y = __builtin_fmaf(st.x, acc[i][j][r], __builtin_fmaf(st.y, cn[n], dn[n]));
+                uint16_t *p = x + (size_t)m * XT_D + n;
+                *p = f2h(h2f(*p) + y);
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// k_head: out [nb][nt] = sigmoid(pq . Wh^T + hb) (kern_common.cuh:679-727 as a block-scaled FP8 GEMM)
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(HeadCfg::NT) k_head(const uint8_t *__restrict__ pq, const float *__restrict__ ps,
+                                                     int lds, const uint8_t *__restrict__ w,
+                                                     const float *__restrict__ ws, const float *__restrict__ hb,
+                                                     float *__restrict__ out, int nb, int nt)
+{
+    using C = HeadCfg;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    v4f acc[C::TM][C::TN];
+    int m0, n0, wm0, wn0;
+    layer_tile<C>(nb, nt, m0, n0);
+    bs_mainloop<C>(pq, XT_D, ps, lds, w, ws, nb, (nt + 127) & ~127, XT_D, m0, n0, smem, acc);
+    bs_wave_origin<C>(wm0, wn0);
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            const int n = n0 + wn0 + 16 * j + c16;
+            if (n >= nt) continue;
+            const float bias = hb[n];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm0 + 16 * i + 4 * g + r;
+                if (m < nb) out[(size_t)m * nt + n] = 1.0f / (1.0f + __expf(-(acc[i][j][r] + bias)));
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// k_pe: patch embedding in fp16 with fp32 accumulation (v_mfma_f32_16x16x32_f16) and the position add fused
+// (k_pe + k_embed, eva_kernels.cu:21-33, 126-130): x[1025 b + 1 + p] = f16(in[1024 b + p] . pe^T + pos[1 + p]),
+// x[1025 b] = f16(pos[0]) (pos carries cls and the conv bias, export_eva.py:76-80). Block 128 patches x 128
+// columns, 4 waves of 64 x 64, K = 592 in steps of 64 halves (the last step holds 16; the rest is zeroed).
+// ---------------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_pe(const uint16_t *__restrict__ in, const uint16_t *__restrict__ pe,
+                                            const float *__restrict__ pos, uint16_t *__restrict__ x, int nb)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 128 * 128];  // A | B tile of one K step
+    const int m0 = blockIdx.y * 128, n0 = blockIdx.x * 128, t = threadIdx.x;
+    const int lane = t & 63, w = t >> 6, g = lane >> 4, r16 = lane & 15;
+    const int wm0 = (w >> 1) * 64, wn0 = (w & 1) * 64;
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < XT_K0P; k0 += 64) {
+        // stage: 128 rows x 8 chunks of 8 halves for A and B; chunks past column 592 are zero
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const int idx = t + 256 * it, row = idx >> 3, ch = idx & 7, col = k0 + 8 * ch;
+            uint4 va = make_uint4(0, 0, 0, 0), vb = make_uint4(0, 0, 0, 0);
+            if (col < XT_K0P) {
+                va = *(const uint4 *)(in + (size_t)(m0 + row) * XT_K0P + col);
+                vb = *(const uint4 *)(pe + (size_t)(n0 + row) * XT_K0P + col);
+            }
+            *(uint4 *)(smem + swz(row, ch)) = va;
+            *(uint4 *)(smem + 128 * 128 + swz(row, ch)) = vb;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            v8h a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) a[i] = __builtin_bit_cast(v8h, *(const uint4 *)(smem + swz(wm0 + 16 * i + r16, 4 * s + g)));
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                b[j] = __builtin_bit_cast(v8h, *(const uint4 *)(smem + 128 * 128 + swz(wn0 + 16 * j + r16, 4 * s + g)));
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    const int c16 = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = m0 + wm0 + 16 * i + 4 * g + r, b = m >> 10, p = m & 1023;
+            uint16_t *xr = x + ((size_t)b * XT_T + 1 + p) * XT_D;
+            const float *pr = pos + (size_t)(1 + p) * XT_D;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int n = n0 + wn0 + 16 * j + c16;
+                xr[n] = f2h(acc[i][j][r] + pr[n]);
+            }
+        }
+    if ((m0 & 1023) == 0 && t < 128) {  // the first patch tile of an image also writes its cls row
+        const int b = m0 >> 10, n = n0 + t;
+        x[(size_t)b * XT_T * XT_D + n] = f2h(pos[n]);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// C-ABI launchers
+// ---------------------------------------------------------------------------------------------------------------
+static unsigned layer_grid(int rows, int N, int BM, int BN) { return (unsigned)(((rows + BM - 1) / BM) * ((N + BN - 1) / BN)); }
+
+#define XT_ALIGNED(p) ((((uintptr_t)(p)) & 15) == 0)
+
+extern "C" int eva_k_qkv(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *cs,
+                         void *q, void *k, void *vt, int rows, void *stream)
+{
+    if (rows <= 0 || lds < rows || rows % XT_T) return xt_fail("eva_k_qkv", "rows must be nb * 1025, lds >= rows");
+    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w)) return xt_fail("eva_k_qkv", "h8 and w must be 16-byte aligned");
+    hipLaunchKernelGGL(k_qkv, dim3(layer_grid(rows, 3 * XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w, ws, cs, (uint16_t *)q,
+                       (uint16_t *)k, (uint16_t *)vt, rows);
+    return xt_check("eva_k_qkv");
+}
+
+extern "C" int eva_k_oproj(const void *a8, const float *as, int lds, const void *w, const float *ws, void *x, int rows,
+                           void *stream)
+{
+    if (rows <= 0 || lds < rows) return xt_fail("eva_k_oproj", "bad shape (rows > 0, lds >= rows)");
+    if (!XT_ALIGNED(a8) || !XT_ALIGNED(w)) return xt_fail("eva_k_oproj", "a8 and w must be 16-byte aligned");
+    hipLaunchKernelGGL(k_oproj, dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)a8, as, lds, (const uint8_t *)w, ws, (uint16_t *)x, rows);
+    return xt_check("eva_k_oproj");
+}
+
+extern "C" int eva_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8, float *ms,
+                         float *stat, int rows, void *stream)
+{
+    if (rows <= 0 || lds < rows) return xt_fail("eva_k_fc1", "bad shape (rows > 0, lds >= rows)");
+    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || !XT_ALIGNED(m8)) return xt_fail("eva_k_fc1", "h8, w, m8 must be 16-byte aligned");
+    hipLaunchKernelGGL(k_fc1, dim3(layer_grid(rows, 2 * XT_HIDP, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w, ws, (uint8_t *)m8, ms,
+                       stat, rows);
+    return xt_check("eva_k_fc1");
+}
+
+extern "C" int eva_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *stat,
+                         const float *cn, const float *dn, void *x, int rows, void *stream)
+{
+    if (rows <= 0 || lds < rows) return xt_fail("eva_k_fc2", "bad shape (rows > 0, lds >= rows)");
+    if (!XT_ALIGNED(m8) || !XT_ALIGNED(w)) return xt_fail("eva_k_fc2", "m8 and w must be 16-byte aligned");
+    hipLaunchKernelGGL(k_fc2, dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)m8, ms, lds, (const uint8_t *)w, ws, stat, cn, dn,
+                       (uint16_t *)x, rows);
+    return xt_check("eva_k_fc2");
+}
+
+extern "C" int eva_k_head(const void *pq, const float *ps, int lds, const void *w, const float *ws, const float *hb,
+                          float *out, int nb, int nt, void *stream)
+{
+    if (nb <= 0 || nt <= 0 || lds < nb) return xt_fail("eva_k_head", "bad shape (nb > 0, nt > 0, lds >= nb)");
+    if (!XT_ALIGNED(pq) || !XT_ALIGNED(w)) return xt_fail("eva_k_head", "pq and w must be 16-byte aligned");
+    hipLaunchKernelGGL(k_head, dim3(layer_grid(nb, nt, HeadCfg::BM, HeadCfg::BN)), dim3(HeadCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)pq, ps, lds, (const uint8_t *)w, ws, hb, out, nb, nt);
+    return xt_check("eva_k_head");
+}
+
+extern "C" int eva_k_pe(const void *in, const void *pe, const float *pos, void *x, int nb, void *stream)
+{
+    if (nb <= 0) return xt_fail("eva_k_pe", "nb must be positive");
+    if (!XT_ALIGNED(in) || !XT_ALIGNED(pe)) return xt_fail("eva_k_pe", "in and pe must be 16-byte aligned");
+    hipLaunchKernelGGL(k_pe, dim3(XT_D / 128, nb * XT_NP / 128), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)in, (const uint16_t *)pe, pos, (uint16_t *)x, nb);
+    return xt_check("eva_k_pe");
+}

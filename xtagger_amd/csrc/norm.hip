@@ -1,0 +1,162 @@
+// norm.hip - bandwidth-bound kernels around the block GEMMs: LayerNorm -> E4M3 with 1x128 scales (k_ln,
+// src/engine/kern_common.cuh:147-186), the mean-pool over patch tokens (k_pool, src/engine/eva_kernels.cu:402-431)
+// and the final LayerNorm -> fp16 head input -> E4M3 (k_lnh, kern_common.cuh:188-192).
+//
+// One wave64 per 1024-wide row: lane l owns elements [8l, 8l+8) and [512+8l, 512+8l+8), so every load is a
+// 16-byte coalesced access and each 128-element scale block is 16 aligned lanes. Sums run per lane in element
+// order, then through an xor butterfly (32, 16, ..., 1), a fixed order the host restatement follows exactly.
+#include "xt_abi.h"
+#include "xt_common.h"
+
+// LayerNorm of one row held as v[16] (lane layout above), eps 1e-6, two-pass:
+// y = fma((x - mean) * rstd, gamma, beta), rstd = 1 / sqrt(var + eps) with IEEE sqrt and division.
+__device__ __forceinline__ void ln16(float *v, const float *__restrict__ g, const float *__restrict__ b, int lane)
+{
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) s += v[j];
+    const float mean = wave_sum(s) * (1.0f / 1024.0f);
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float d = v[j] - mean;
+        q = __builtin_fmaf(d, d, q);
+    }
+    const float var = wave_sum(q) * (1.0f / 1024.0f);
+    const float rstd = 1.0f / __builtin_sqrtf(var + XT_EPS);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int e0 = 512 * h + 8 * lane;
+        const float4 g0 = *(const float4 *)(g + e0), g1 = *(const float4 *)(g + e0 + 4);
+        const float4 b0 = *(const float4 *)(b + e0), b1 = *(const float4 *)(b + e0 + 4);
+        const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[8 * h + j] = __builtin_fmaf((v[8 * h + j] - mean) * rstd, gg[j], bb[j]);
+    }
+}
+
+// v[16] -> E4M3 bytes of the row at q (row-major, 1024 bytes) and its 8 scales at s[kb * lds + row]
+__device__ __forceinline__ void quant_row16(const float *v, uint8_t *__restrict__ q, float *__restrict__ s, int lds,
+                                            int row, int lane)
+{
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[8 * h + j]));
+        amax = group_max<16>(amax);
+        const float sc = block_scale(amax), inv = 1.0f / sc;
+        const float *w = v + 8 * h;
+        uint2 o;
+        o.x = e4_pack4(w[0] * inv, w[1] * inv, w[2] * inv, w[3] * inv);
+        o.y = e4_pack4(w[4] * inv, w[5] * inv, w[6] * inv, w[7] * inv);
+        *(uint2 *)(q + 512 * h + 8 * lane) = o;
+        if ((lane & 15) == 0) s[(size_t)(4 * h + (lane >> 4)) * lds + row] = sc;
+    }
+}
+
+__device__ __forceinline__ void load_row16_f16(const uint16_t *__restrict__ x, int lane, float *v)
+{
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint4 u = *(const uint4 *)(x + 512 * h + 8 * lane);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[8 * h + 2 * i] = h2f((uint16_t)(w[i] & 0xffffu));
+            v[8 * h + 2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+        }
+    }
+}
+
+// k_ln: x fp16 [rows][1024] -> q E4M3 [rows][1024] + s [8][lds]. 4 rows per 256-thread block.
+__global__ void __launch_bounds__(256) k_ln(const uint16_t *__restrict__ x, const float *__restrict__ g,
+                                            const float *__restrict__ b, uint8_t *__restrict__ q,
+                                            float *__restrict__ s, int rows, int lds)
+{
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    float v[16];
+    load_row16_f16(x + (size_t)row * XT_D, lane, v);
+    ln16(v, g, b, lane);
+    quant_row16(v, q + (size_t)row * XT_D, s, lds, row, lane);
+}
+
+// k_pool: mean over tokens 1..1024 of each image: x fp16 [nb * 1025][1024] -> p fp32 [nb][1024].
+// Grid (nb, 4), 128 threads, two columns per thread, tokens summed in order.
+__global__ void __launch_bounds__(128) k_pool(const uint16_t *__restrict__ x, float *__restrict__ p)
+{
+    const int c = blockIdx.y * 256 + 2 * threadIdx.x;
+    const uint16_t *xr = x + ((size_t)blockIdx.x * XT_T + 1) * XT_D + c;
+    float s0 = 0.f, s1 = 0.f;
+    for (int t = 0; t < XT_NP; t++) {
+        const uint32_t u = *(const uint32_t *)(xr + (size_t)t * XT_D);
+        s0 += h2f((uint16_t)(u & 0xffffu));
+        s1 += h2f((uint16_t)(u >> 16));
+    }
+    *(float2 *)(p + (size_t)blockIdx.x * XT_D + c) = make_float2(s0 * (1.0f / XT_NP), s1 * (1.0f / XT_NP));
+}
+
+// k_lnh: final LayerNorm of the pooled rows (fc_norm) -> fp16 head input pn [nb][1024] (the reference's head
+// operand, also read back as hpn), then E4M3 of those fp16 values with 1x128 scales for the FP8 head.
+__global__ void __launch_bounds__(256) k_lnh(const float *__restrict__ p, const float *__restrict__ g,
+                                             const float *__restrict__ b, uint16_t *__restrict__ pn,
+                                             uint8_t *__restrict__ q, float *__restrict__ s, int rows, int lds)
+{
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    float v[16];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const float4 a = *(const float4 *)(p + (size_t)row * XT_D + 512 * h + 8 * lane);
+        const float4 c = *(const float4 *)(p + (size_t)row * XT_D + 512 * h + 8 * lane + 4);
+        v[8 * h + 0] = a.x; v[8 * h + 1] = a.y; v[8 * h + 2] = a.z; v[8 * h + 3] = a.w;
+        v[8 * h + 4] = c.x; v[8 * h + 5] = c.y; v[8 * h + 6] = c.z; v[8 * h + 7] = c.w;
+    }
+    ln16(v, g, b, lane);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint16_t lo = f2h(v[8 * h + 2 * i]), hi = f2h(v[8 * h + 2 * i + 1]);
+            v[8 * h + 2 * i] = h2f(lo);
+            v[8 * h + 2 * i + 1] = h2f(hi);
+            w[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        *(uint4 *)(pn + (size_t)row * XT_D + 512 * h + 8 * lane) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    quant_row16(v, q + (size_t)row * XT_D, s, lds, row, lane);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+extern "C" int eva_k_ln(const void *x, const float *g, const float *b, void *q, float *s, int rows, int lds,
+                        void *stream)
+{
+    if (rows < 0 || lds < rows) return xt_fail("eva_k_ln", "bad shape (lds >= rows)");
+    if (((uintptr_t)x | (uintptr_t)g | (uintptr_t)b | (uintptr_t)q) & 15)
+        return xt_fail("eva_k_ln", "x, g, b, q must be 16-byte aligned");
+    if (!rows) return 0;
+    hipLaunchKernelGGL(k_ln, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x, g, b,
+                       (uint8_t *)q, s, rows, lds);
+    return xt_check("eva_k_ln");
+}
+
+extern "C" int eva_k_pool(const void *x, float *p, int nb, void *stream)
+{
+    if (nb <= 0) return xt_fail("eva_k_pool", "nb must be positive");
+    hipLaunchKernelGGL(k_pool, dim3(nb, 4), dim3(128), 0, (hipStream_t)stream, (const uint16_t *)x, p);
+    return xt_check("eva_k_pool");
+}
+
+extern "C" int eva_k_lnh(const float *p, const float *g, const float *b, void *pn, void *q, float *s, int rows,
+                         int lds, void *stream)
+{
+    if (rows <= 0 || lds < rows) return xt_fail("eva_k_lnh", "bad shape (rows > 0, lds >= rows)");
+    if (((uintptr_t)p | (uintptr_t)g | (uintptr_t)b | (uintptr_t)pn | (uintptr_t)q) & 15)
+        return xt_fail("eva_k_lnh", "p, g, b, pn, q must be 16-byte aligned");
+    hipLaunchKernelGGL(k_lnh, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, p, g, b, (uint16_t *)pn,
+                       (uint8_t *)q, s, rows, lds);
+    return xt_check("eva_k_lnh");
+}

@@ -95,35 +95,75 @@ __global__ void __launch_bounds__(256) k_e4m3_bits(uint32_t first, uint32_t coun
 }
 
 // ---- standalone block-scaled GEMM: C [M][ldc] = bf16 or fp32 of the block-scaled product ----
-template <int BM, int BN, int WM, int WN, int OUT>  // OUT 0: bf16, 1: fp32
-__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64) k_gemm(const uint8_t *__restrict__ A, int lda,
-                                                                  const float *__restrict__ sa, int lds,
-                                                                  const uint8_t *__restrict__ W,
-                                                                  const float *__restrict__ sw, void *__restrict__ Cp,
-                                                                  int ldc, int M, int N, int K)
+// bf16: each wave stages its WM x WN tile through LDS (the operand stages are free after the main loop) and writes
+// whole rows with 16-byte stores. fp32 (the parity build) stores straight from the accumulators.
+template <class C, int OUT>  // OUT 0: bf16, 1: fp32
+__global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
+                                               int lds, const uint8_t *__restrict__ W, const float *__restrict__ sw,
+                                               void *__restrict__ Cp, int ldc, int M, int N, int K)
 {
-    using C = BsCfg<BM, BN, WM, WN>;
     __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
     v4f acc[C::TM][C::TN];
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, lane = threadIdx.x & 63;
-    bs_mainloop<BM, BN, WM, WN>(A, lda, sa, lds, W, sw, M, K, m0, n0, smem, acc);
+    int tm, tn;
+    tile_of_block((M + C::BM - 1) / C::BM, (N + C::BN - 1) / C::BN, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * C::BN, lane = threadIdx.x & 63, g = lane >> 4;
+    const int Npad = (N + 127) & ~127;
+    bs_mainloop<C>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
     int wm0, wn0;
-    bs_wave_origin<BM, BN, WM, WN>(wm0, wn0);
+    bs_wave_origin<C>(wm0, wn0);
+    if (OUT == 1) {
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                const int col = n0 + wn0 + 16 * j + (lane & 15);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = m0 + wm0 + 16 * i + 4 * g + r;
+                    if (row < M && col < N) ((float *)Cp)[(size_t)row * ldc + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+    constexpr int RS = C::WN * 2 + 4;   // staged row stride in bytes (one pad dword spreads the banks)
+    static_assert(C::NW * C::WM * RS <= C::LDS, "bf16 staging must fit the shared memory");
+    uint8_t *wt = smem + (threadIdx.x >> 6) * C::WM * RS;
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
 #pragma unroll
-        for (int j = 0; j < C::TN; j++) {
-            const int col = n0 + wn0 + 16 * j + (lane & 15);
+        for (int j = 0; j < C::TN; j++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int row = m0 + wm0 + 16 * i + 4 * (lane >> 4) + r;
-                if (row < M && col < N) {
-                    if (OUT == 0) ((uint16_t *)Cp)[(size_t)row * ldc + col] = f2bf(acc[i][j][r]);
-                    else ((float *)Cp)[(size_t)row * ldc + col] = acc[i][j][r];
-                }
-            }
+            for (int r = 0; r < 4; r++)
+                *(uint16_t *)(wt + (16 * i + 4 * g + r) * RS + 2 * (16 * j + (lane & 15))) = f2bf(acc[i][j][r]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the staged tile is wave-private: no block barrier
+    constexpr int CPR = C::WN / 8;       // 16-byte chunks per staged row
+    const bool vec = (ldc % 8) == 0 && (((uintptr_t)Cp) & 15) == 0;
+    for (int idx = lane; idx < C::WM * CPR; idx += 64) {
+        const int rr = idx / CPR, cc = idx - rr * CPR;
+        const int row = m0 + wm0 + rr, col = n0 + wn0 + 8 * cc;
+        if (row >= M || col >= N) continue;
+        const uint4 v = *(const uint4 *)(wt + rr * RS + 16 * cc);
+        uint16_t *dst = (uint16_t *)Cp + (size_t)row * ldc + col;
+        if (vec && col + 8 <= N) {
+            *(uint4 *)dst = v;
+        } else {
+            const uint16_t *e = (const uint16_t *)&v;
+            for (int t = 0; t < 8 && col + t < N; t++) dst[t] = e[t];
         }
+    }
 }
+
+#ifndef XT_BIG
+#define XT_BIG 1
+#endif
+#if XT_BIG == 0
+typedef BsCfg<256, 256, 4, 2, 2> GemmBig;    // 8 waves of 64 x 128, 2 stages
+#elif XT_BIG == 1
+typedef BsCfg<128, 256, 2, 4, 3> GemmBig;    // 8 waves of 64 x 64, 3 stages
+#else
+typedef BsCfg<256, 128, 4, 2, 3> GemmBig;    // 8 waves of 64 x 64, 3 stages
+#endif
+typedef BsCfg<128, 256, 2, 4, 3> GemmMid;    // 8 waves of 64 x 64, 3 stages
 
 // ---------------------------------------------------------------------------------------------------------------
 // C-ABI launchers
@@ -177,12 +217,24 @@ extern "C" int eva_k_gemm(const void *qa, int lda, const float *sa, int lds, con
         return xt_fail("eva_k_gemm", "bad shape (K % 128, lda >= K and a multiple of 16, lds >= M, ldc >= N, out_kind 0 or 1)");
     if (((uintptr_t)qa | (uintptr_t)qw) & 15) return xt_fail("eva_k_gemm", "qa and qw must be 16-byte aligned");
     if (!M) return 0;
-    const dim3 grid((N + 127) / 128, (M + 127) / 128);
-    if (out_kind == 0)
-        hipLaunchKernelGGL((k_gemm<128, 128, 64, 64, 0>), grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t *)qa,
-                           lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
-    else
-        hipLaunchKernelGGL((k_gemm<128, 128, 64, 64, 1>), grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t *)qa,
-                           lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+    // big tiles once there are enough of them to fill the 256 CUs, else 128-row tiles
+    const long big = (long)((M + GemmBig::BM - 1) / GemmBig::BM) * ((N + GemmBig::BN - 1) / GemmBig::BN);
+    if (big >= 256) {
+        const dim3 grid((unsigned)big);
+        if (out_kind == 0)
+            hipLaunchKernelGGL((k_gemm<GemmBig, 0>), grid, dim3(GemmBig::NT), 0, (hipStream_t)stream,
+                               (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+        else
+            hipLaunchKernelGGL((k_gemm<GemmBig, 1>), grid, dim3(GemmBig::NT), 0, (hipStream_t)stream,
+                               (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+    } else {
+        const dim3 grid((unsigned)(((M + 127) / 128) * ((N + 255) / 256)));
+        if (out_kind == 0)
+            hipLaunchKernelGGL((k_gemm<GemmMid, 0>), grid, dim3(GemmMid::NT), 0, (hipStream_t)stream,
+                               (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+        else
+            hipLaunchKernelGGL((k_gemm<GemmMid, 1>), grid, dim3(GemmMid::NT), 0, (hipStream_t)stream,
+                               (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+    }
     return xt_check("eva_k_gemm");
 }

@@ -54,6 +54,7 @@ __device__ __forceinline__ uint16_t f2bf(float x)
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 __device__ __forceinline__ uint16_t f2h(float x)
 {
+    asm volatile("" : "+v"(x));  // keep x an fp32 value: no fused fp32-op + fp16-round (v_fma_mix*) single rounding
     _Float16 h = (_Float16)x;
     return __builtin_bit_cast(uint16_t, h);
 }

@@ -16,6 +16,33 @@ _SIGS = {
     "eva_k_quant_w": (_i, [_p, _i, _i, _p, _p, _p]),
     "eva_k_e4m3_bits": (_i, [_u32, _u32, _p, _p]),
     "eva_k_gemm": (_i, [_p, _i, _p, _i, _p, _p, _i, _i, _i, _p, _i, _i, _p]),
+    "eva_k_ln": (_i, [_p, _p, _p, _p, _p, _i, _i, _p]),
+    "eva_k_qkv": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
+    "eva_k_flash": (_i, [_p, _p, _p, _p, _p, _i, _i, _p, _p]),
+    "eva_k_oproj": (_i, [_p, _p, _i, _p, _p, _p, _i, _p]),
+    "eva_k_fc1": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _i, _p]),
+    "eva_k_fc2": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
+    "eva_k_head": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _p]),
+    "eva_k_pe": (_i, [_p, _p, _p, _p, _i, _p]),
+    "eva_k_pool": (_i, [_p, _p, _i, _p]),
+    "eva_k_lnh": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _p]),
+    "eva_k_prep_w": (_i, [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p]),
+    "eva_k_fold_cd": (_i, [_p, _p, _p, _i, _p, _p, _p, _p]),
+    "eva_open": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32]),
+    "eva_open_nb": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32, _u32]),
+    "eva_ready": (_i, [_p]),
+    "eva_poll": (_i, [_p]),
+    "eva_submit": (_i, [_p, _u32, _p, _u32]),
+    "eva_query": (_i, [_p, _u32]),
+    "eva_wait": (_p, [_p, _u32]),
+    "eva_head_put": (_i, [_p, _u32, _p, _f]),
+    "eva_head_get": (_i, [_p, _p, _p]),
+    "eva_close": (None, [_p]),
+    "eva_dev_input": (_p, [_p]),
+    "eva_run": (_i, [_p]),
+    "eva_dev_output": (_p, [_p]),
+    "eva_stream_handle": (_p, [_p]),
+    "eva_sync": (_i, [_p]),
 }
 
 for _name, (_res, _args) in _SIGS.items():
