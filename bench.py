@@ -183,6 +183,33 @@ def cpu_baseline(orc, M=T, rows=None):
     return total / secs / 1e12, thr, secs
 
 
+def measured_peaks(torch, L):
+    """Ceilings measured on this GPU: dense FP8 MFMA (TFLOP/s), HBM stream copy (GB/s), LDS reads (TB/s)."""
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream().cuda_stream
+    blocks, iters = 4096, 1000
+    out = torch.empty(blocks * 256, device=dev)
+    f = lambda: L.lib.eva_probe_mfma_fp8(blocks, iters, L.ptr(out), st)
+    time_launches(torch, f, 2)
+    ms = time_launches(torch, f, 5)
+    mfma = blocks * 4 * iters * 8 * 65536 / (ms * 1e-3) / 1e12
+    n = 2 << 30
+    a = torch.empty(n, dtype=torch.uint8, device=dev)
+    b = torch.empty(n, dtype=torch.uint8, device=dev)
+    g = lambda: L.lib.eva_probe_copy(L.ptr(a), L.ptr(b), n, st)
+    time_launches(torch, g, 2)
+    ms = time_launches(torch, g, 10)
+    copy = 2.0 * n / (ms * 1e-3) / 1e9
+    del a, b
+    lb, li = 1024, 2000
+    o2 = torch.empty(lb * 256, dtype=torch.int32, device=dev)
+    h = lambda: L.lib.eva_probe_lds(lb, li, L.ptr(o2), st)
+    time_launches(torch, h, 2)
+    ms = time_launches(torch, h, 5)
+    lds = lb * 256 * li * 16 * 16 / (ms * 1e-3) / 1e12
+    return {"fp8_mfma_tflops": round(mfma, 1), "hbm_copy_gbs": round(copy, 1), "lds_read_tbs": round(lds, 1)}
+
+
 def traffic_from_profiles():
     """HBM bytes per fc1 launch from the committed rocprofv3 PMC summary, if present."""
     p = os.path.join(ROOT, "profiles", "fc1_m8200_hbm_traffic.txt")
@@ -237,6 +264,7 @@ def main():
             "algorithmic_flops_per_launch": fl["fc1"]}
 
     cfg1, cfg1_ms = bench_cfg1(torch, L)
+    peaks = measured_peaks(torch, L)
     out = {"metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "e4m3 (fp32 accumulate)", "data": "synthetic",
@@ -246,7 +274,8 @@ def main():
                       "M": M, "gflop_per_step": round(step_flops / 1e9, 2)},
            "pct_fp8_peak": round(100 * tflops / PEAK_FP8, 2), "per_kernel": per,
            "cfg1_qkv_gemm_m1025": {"tflops": round(cfg1, 1), "us": round(cfg1_ms * 1e3, 2)},
-           "roofline": roof}
+           "roofline": roof, "measured_peaks": peaks,
+           "pct_measured_fp8_peak": round(100 * tflops / peaks["fp8_mfma_tflops"], 2)}
     if not args.no_forward:
         ips, fms = bench_forward(torch)
         out["forward_b32"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),

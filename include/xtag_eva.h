@@ -141,6 +141,15 @@ int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_
 int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const float *beta, float *c, float *d,
                   void *stream);
 
+/* ---- on-box ceilings (no reference counterpart; the roofline fractions use peaks measured on the same GPU) ---- */
+/* dense FP8 MFMA: blocks x 256 threads, each wave issuing iters x 8 v_mfma_f32_16x16x128_f8f6f4 on register operands
+ * (flops = blocks * 4 * iters * 8 * 65536); out [blocks * 256] keeps the result live */
+int eva_probe_mfma_fp8(int blocks, int iters, float *out, void *stream);
+/* HBM stream copy of bytes (16-byte multiple) from src to dst */
+int eva_probe_copy(const void *src, void *dst, size_t bytes, void *stream);
+/* LDS read bandwidth: blocks x 256 threads, each reading iters x 16 x 16 bytes conflict-free from a 64 KB array */
+int eva_probe_lds(int blocks, int iters, uint32_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

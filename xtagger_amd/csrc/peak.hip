@@ -1,0 +1,74 @@
+// peak.hip - on-box measurement of the ceilings the roofline fractions are taken against: dense FP8 MFMA
+// throughput (v_mfma_f32_16x16x128_f8f6f4 on register operands), HBM stream-copy bandwidth, and LDS read bandwidth
+// (ds_read_b128). No reference counterpart: the reference publishes no kernel-level numbers; these entry points exist
+// so every fraction reported beside a benchmark uses a peak measured on the same GPU.
+#include "xt_abi.h"
+#include "xt_common.h"
+
+// Each wave keeps 8 independent accumulator chains so back-to-back MFMAs never wait on each other.
+__global__ void __launch_bounds__(256) k_peak_mfma(int iters, float *__restrict__ out)
+{
+    const int lane = threadIdx.x & 63;
+    v8i a, b;
+    for (int i = 0; i < 8; i++) {
+        a[i] = 0x38383838 ^ (lane * 0x01010101 + i);   // finite E4M3 bytes, lane dependent
+        b[i] = 0x30303030 ^ (lane + i * 0x00010001);
+    }
+    v4f acc[8];
+    for (int c = 0; c < 8; c++) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            acc[c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[c], 0, 0, 0, 0, 0, 0);
+    }
+    float s = 0.f;
+    for (int c = 0; c < 8; c++) s += acc[c][0] + acc[c][1] + acc[c][2] + acc[c][3];
+    out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
+__global__ void __launch_bounds__(256) k_peak_copy(const uint4 *__restrict__ src, uint4 *__restrict__ dst, long n16)
+{
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n16; i += (long)gridDim.x * 256) dst[i] = src[i];
+}
+
+// 256 threads read 16 bytes each per step from a 64 KB LDS array, conflict-free (consecutive lanes, consecutive
+// 16-byte chunks), and fold the data so the reads stay live.
+__global__ void __launch_bounds__(256) k_peak_lds(int iters, uint32_t *__restrict__ out)
+{
+    __shared__ __attribute__((aligned(16))) uint4 buf[4096];
+    for (int i = threadIdx.x; i < 4096; i += 256) buf[i] = make_uint4(i, i * 3, i * 5, i * 7);
+    __syncthreads();
+    uint4 acc = make_uint4(0, 0, 0, 0);
+    int idx = threadIdx.x;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const uint4 v = buf[(idx + u * 256) & 4095];
+            acc.x ^= v.x; acc.y += v.y; acc.z ^= v.z; acc.w += v.w;
+        }
+        idx += 37;
+    }
+    out[blockIdx.x * 256 + threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
+}
+
+extern "C" int eva_probe_mfma_fp8(int blocks, int iters, float *out, void *stream)
+{
+    if (blocks <= 0 || iters <= 0) return xt_fail("eva_probe_mfma_fp8", "blocks and iters must be positive");
+    hipLaunchKernelGGL(k_peak_mfma, dim3(blocks), dim3(256), 0, (hipStream_t)stream, iters, out);
+    return xt_check("eva_probe_mfma_fp8");
+}
+
+extern "C" int eva_probe_copy(const void *src, void *dst, size_t bytes, void *stream)
+{
+    if (bytes % 16 || (((uintptr_t)src | (uintptr_t)dst) & 15)) return xt_fail("eva_probe_copy", "16-byte multiples");
+    hipLaunchKernelGGL(k_peak_copy, dim3(4096), dim3(256), 0, (hipStream_t)stream, (const uint4 *)src, (uint4 *)dst,
+                       (long)(bytes / 16));
+    return xt_check("eva_probe_copy");
+}
+
+extern "C" int eva_probe_lds(int blocks, int iters, uint32_t *out, void *stream)
+{
+    if (blocks <= 0 || iters <= 0) return xt_fail("eva_probe_lds", "blocks and iters must be positive");
+    hipLaunchKernelGGL(k_peak_lds, dim3(blocks), dim3(256), 0, (hipStream_t)stream, iters, out);
+    return xt_check("eva_probe_lds");
+}

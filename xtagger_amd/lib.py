@@ -43,6 +43,9 @@ _SIGS = {
     "eva_dev_output": (_p, [_p]),
     "eva_stream_handle": (_p, [_p]),
     "eva_sync": (_i, [_p]),
+    "eva_probe_mfma_fp8": (_i, [_i, _i, _p, _p]),
+    "eva_probe_copy": (_i, [_p, _p, C.c_size_t, _p]),
+    "eva_probe_lds": (_i, [_i, _i, _p, _p]),
 }
 
 for _name, (_res, _args) in _SIGS.items():
