@@ -27,6 +27,41 @@ __device__ __forceinline__ void layer_tile(int M, int N, int &m0, int &n0)
     n0 = tn * C::BN;
 }
 
+// Residual update x = f16(x + y) of a wave's 64 x 64 tile, y in the MFMA C layout. The wave parks y in its own LDS
+// slice (row stride 68 floats: the 64 lanes of one store hit 64 different banks), then each lane updates 8
+// consecutive halves with one 16-byte load and store, so one wave instruction covers 8 rows of 128 bytes.
+template <class C>
+__device__ __forceinline__ void residual_add(uint8_t *slices, v4f (&y)[C::TM][C::TN], uint16_t *__restrict__ x,
+                                             int mw, int nw, int rows)
+{
+    static_assert(C::TM == 4 && C::TN == 4, "64 x 64 wave tiles");
+    float *tr = (float *)slices + (threadIdx.x >> 6) * 64 * 68;
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) tr[(16 * i + 4 * g + r) * 68 + 16 * j + c16] = y[i][j][r];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
+    const int rs = lane >> 3, ch = lane & 7;
+#pragma unroll
+    for (int it = 0; it < 8; it++) {
+        const int rr = 8 * it + rs, m = mw + rr;
+        if (m >= rows) continue;
+        const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
+        uint4 *p = (uint4 *)(x + (size_t)m * XT_D + nw + 8 * ch);
+        const uint4 v = *p;
+        uint4 o;
+        o.x = f2h(h2f(v.x & 0xFFFF) + a.x) | (uint32_t)f2h(h2f(v.x >> 16) + a.y) << 16;
+        o.y = f2h(h2f(v.y & 0xFFFF) + a.z) | (uint32_t)f2h(h2f(v.y >> 16) + a.w) << 16;
+        o.z = f2h(h2f(v.z & 0xFFFF) + b.x) | (uint32_t)f2h(h2f(v.z >> 16) + b.y) << 16;
+        o.w = f2h(h2f(v.w & 0xFFFF) + b.z) | (uint32_t)f2h(h2f(v.w >> 16) + b.w) << 16;
+        *p = o;
+    }
+}
+static_assert(LayerCfg::LDS >= 1024 + LayerCfg::NW * 64 * 68 * 4, "residual slices (after 1 KB of row stats) fit");
+
 // ---------------------------------------------------------------------------------------------------------------
 // k_qkv: h8 [rows][1024] x Wqkv [3072][1024] -> q, k bf16 [nb][16][1088][64] (RoPE on patch tokens), vt bf16
 // [nb][16][64][1088]. A 256-column block is 4 heads of one of q | k | v; each wave owns one head. The weight rows of
@@ -107,23 +142,12 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
     layer_tile<C>(rows, XT_D, m0, n0);
     bs_mainloop<C>(a8, XT_D, as, lds, w, ws, rows, XT_D, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
-    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-#pragma unroll
-    for (int i = 0; i < C::TM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = m0 + wm0 + 16 * i + 4 * g + r;
-            if (m >= rows) continue;
-#pragma unroll
-            for (int j = 0; j < C::TN; j++) {
-                uint16_t *p = x + (size_t)m * XT_D + n0 + wn0 + 16 * j + c16;
-                *p = f2h(h2f(*p) + acc[i][j][r]);
-            }
-        }
+    residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// k_fc1: h8 [rows][1024] x W12 [5632][1024] -> SwiGLU h = silu(g) x (silu(g) = g / (1 + e^-g)), packed to
+// k_fc1: h8 [rows][1024] x W12 [5632][1024] -> SwiGLU h = silu(g) x (silu(g) = g / (1 + e^-g), the quotient by the
+// hardware reciprocal, within 1 ulp), packed to
 // m8 [rows][2816] E4M3 with 1x128 scales ms [22][lds], and per-(row, block) (sum h, sum h^2) of the unpacked h in
 // stat [22][lds][2] for the folded MLP LayerNorm (eva_kernels.cu:211-279). W12 rows hold g and x of 16 units in
 // alternate 16-row chunks (export_eva.py:60-62), so column tile 2c is g and 2c+1 is x of the same 16 units: a
@@ -145,7 +169,8 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int wm = wm0 / C::WM, wn = wn0 / C::WN, ct = n0 >> 8;
     float *red = (float *)smem;                          // [3][2 wm][4 wn][64 rows]: amax, sum, sum of squares
-    uint8_t *qt = smem + 3 * 2 * 4 * 64 * 4;             // [128 rows][128 units] E4M3 staging
+    float *rinv = red + 3 * 2 * 4 * 64;                  // [128 rows] 1 / block scale
+    uint8_t *qt = smem + (3 * 2 * 4 * 64 + 128) * 4;     // [128 rows][128 units] E4M3 staging
     float h[C::TM][2][4];
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
@@ -155,16 +180,16 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
 #pragma unroll
             for (int p = 0; p < 2; p++) {
                 const float gg = acc[i][2 * p][r], xx = acc[i][2 * p + 1][r];
-                const float e = __expf(-gg), den = 1.0f + e, sg = gg / den;
-                const float v = sg * xx;
+                const float e = __expf(-gg), den = 1.0f + e;
+                const float v = (gg * __builtin_amdgcn_rcpf(den)) * xx;  // silu(g) x, hardware reciprocal (1 ulp)
                 h[i][p][r] = v;
                 amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
                 s += v;
                 q = __builtin_fmaf(v, v, q);
             }
-            amax = group_max<16>(amax);
-            s = group_sum<16>(s);
-            q = group_sum<16>(q);
+            amax = row16_max(amax);
+            s = row16_sum(s);
+            q = row16_sum(q);
             if (c16 == 0) {
                 const int rr = 16 * i + 4 * g + r;
                 red[((0 * 2 + wm) * 4 + wn) * 64 + rr] = amax;
@@ -173,20 +198,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
             }
         }
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < C::TM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int rr = 16 * i + 4 * g + r;
-            float amax = 0.f;
-#pragma unroll
-            for (int u = 0; u < 4; u++) amax = __builtin_fmaxf(amax, red[((0 * 2 + wm) * 4 + u) * 64 + rr]);
-            const float sc = block_scale(amax), inv = 1.0f / sc;
-#pragma unroll
-            for (int p = 0; p < 2; p++)
-                qt[(wm0 + rr) * 128 + 32 * wn + 16 * p + c16] = (uint8_t)e4_pack2(h[i][p][r] * inv, 0.f);
-        }
-    // one thread per block row: scale and the row sums (column waves added in order)
+    // one thread per block row: the block scale (IEEE divisions, once per row) and the row sums (column waves in order)
     if (threadIdx.x < C::BM) {
         const int rr = threadIdx.x, m = m0 + rr, wmr = rr >> 6, r64 = rr & 63;
         float amax = 0.f, s = 0.f, q = 0.f;
@@ -196,11 +208,24 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
             s += red[((1 * 2 + wmr) * 4 + u) * 64 + r64];
             q += red[((2 * 2 + wmr) * 4 + u) * 64 + r64];
         }
+        const float sc = block_scale(amax);
+        rinv[rr] = 1.0f / sc;
         if (m < rows) {
-            ms[(size_t)ct * lds + m] = block_scale(amax);
+            ms[(size_t)ct * lds + m] = sc;
             *(float2 *)(stat + ((size_t)ct * lds + m) * 2) = make_float2(s, q);
         }
     }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rr = wm0 + 16 * i + 4 * g + r;
+            const float inv = rinv[rr];
+            const uint32_t two = e4_pack2(h[i][0][r] * inv, h[i][1][r] * inv);
+            qt[rr * 128 + 32 * wn + c16] = (uint8_t)two;
+            qt[rr * 128 + 32 * wn + 16 + c16] = (uint8_t)(two >> 8);
+        }
     __syncthreads();
     for (int idx = threadIdx.x; idx < C::BM * 8; idx += C::NT) {
         const int rr = idx >> 3, ch = idx & 7, m = m0 + rr;
@@ -244,21 +269,22 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    float cj[C::TN], dj[C::TN];
+#pragma unroll
+    for (int j = 0; j < C::TN; j++) {
+        cj[j] = cn[n0 + wn0 + 16 * j + c16];
+        dj[j] = dn[n0 + wn0 + 16 * j + c16];
+    }
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int rr = wm0 + 16 * i + 4 * g + r, m = m0 + rr;
-            if (m >= rows) continue;
-            const float2 st = rs[rr];
+            const float2 st = rs[wm0 + 16 * i + 4 * g + r];
 #pragma unroll
-            for (int j = 0; j < C::TN; j++) {
-                const int n = n0 + wn0 + 16 * j + c16;
-                const float y = __builtin_fmaf(st.x, acc[i][j][r], __builtin_fmaf(st.y, cn[n], dn[n]));
-                uint16_t *p = x + (size_t)m * XT_D + n;
-                *p = f2h(h2f(*p) + y);
-            }
+            for (int j = 0; j < C::TN; j++)
+                acc[i][j][r] = __builtin_fmaf(st.x, acc[i][j][r], __builtin_fmaf(st.y, cj[j], dj[j]));
         }
+    residual_add<C>(smem + 1024, acc, x, m0 + wm0, n0 + wn0, rows);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -89,6 +89,30 @@ __device__ __forceinline__ float group_sum(float v)
     return v;
 }
 
+// 16-lane (one DPP row) reductions without LDS traffic: quad_perm xor 1, xor 2, then half-row and row mirrors;
+// after each step every lane of the group holds the same partial, so all 16 lanes end with the full result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v)
+{
+    v = __builtin_fmaxf(v, dpp_f<0xB1>(v));
+    v = __builtin_fmaxf(v, dpp_f<0x4E>(v));
+    v = __builtin_fmaxf(v, dpp_f<0x141>(v));
+    v = __builtin_fmaxf(v, dpp_f<0x140>(v));
+    return v;
+}
+
 __device__ __forceinline__ v4f mfma_e4m3_16x16x128(v8i a, v8i b)
 {
     v4f z = {0.f, 0.f, 0.f, 0.f};
