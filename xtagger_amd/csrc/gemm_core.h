@@ -9,23 +9,27 @@
 // CDNA4 mapping:
 //  - one K step = one 128-wide scale block = one v_mfma_f32_16x16x128_f8f6f4 per 16x16 output tile, so the block
 //    partial leaves the matrix core whole and is promoted with one fma per accumulator: acc = fma(p, sa*sw, acc);
-//  - operands go HBM/L2 -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging): each wave instruction fills 1 KB
-//    of LDS = 8 rows of 128 bytes; the XOR swizzle (16-byte chunk c of row r at chunk c ^ (r & 7)) is applied on the
-//    global side by choosing which chunk each lane fetches. Buffer descriptors bound A and W, so rows past M (or past
-//    the padded N) read as zero without a branch;
-//  - two LDS stages, one barrier per K step; the next step's loads are in flight during this step's MFMAs;
+//  - operands go HBM/L2 -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging), 1 KB = 8 rows x 128 bytes (whole
+//    cache lines) per wave instruction. The loads are issued from inline assembly: the compiler then does not track
+//    them, and its conservative "wait for every LDS DMA before any LDS read" rule (which would drain the whole
+//    prefetch pipeline every K step) is replaced by exact vmcnt waits below;
+//  - LDS tiles are row-major, 128 bytes per row, with 16-byte chunk c of row r rotated to chunk (c + r) & 7. Lane
+//    (g, r) of an operand fragment holds chunks g and g + 4 of its row; both ds_read_b128 of a fragment then run at
+//    the full LDS rate on gfx950 (measured: an XOR swizzle of the same reads runs at half of it). The rotation is
+//    applied on the global side, by choosing which chunk of its row each DMA lane fetches;
+//  - every row offset is in the per-lane VGPR offset and only the K step in the SGPR offset, so rows past M (or past
+//    the padded N) fail the buffer range check and load as zero whether or not the SGPR offset is range-checked;
+//  - NS LDS stages, one barrier per K step; the next NS - 1 steps' loads are in flight during this step's MFMAs;
 //  - waves are laid out NWM x NWN, each owning a WM x WN sub-tile (WN inside one 128-column weight block). A wave
-//    holds its TM A fragments and streams its TN B fragments.
+//    holds its TM A fragments and streams its TN B fragments one column tile ahead.
 #pragma once
 #include "xt_common.h"
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 #ifndef XT_LAG
 #define XT_LAG 2      // MFMA -> promotion distance of the main-loop software pipeline
-#endif
-#ifndef XT_SGB
-#define XT_SGB 1      // interleave hints (sched_group_barrier) in the main loop
 #endif
 #ifndef XT_GM
 #define XT_GM 8       // grouped raster: row tiles walked together
@@ -40,19 +44,23 @@ struct BsCfg {
     static constexpr int TM = WM / 16, TN = WN / 16;
     static constexpr int A_BYTES = BM * 128;
     static constexpr int B_BYTES = BN * 128;
-    static constexpr int S_BYTES = BM * 4;
-    static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    static constexpr int S_BYTES = BM * 4;     // activation scales of the BM rows
+    static constexpr int SW_BYTES = 256;       // weight scales of the BN / 128 column blocks (one 64-lane dword load)
+    static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES + SW_BYTES;
     static constexpr int LDS = NS * STAGE;
-    static constexpr int LA = BM / (8 * NW);  // 1 KB A loads per wave per stage
+    static constexpr int LA = BM / (8 * NW);  // 1 KB A loads (8 rows) per wave per stage
     static constexpr int LB = BN / (8 * NW);  // 1 KB B loads per wave per stage
-    static constexpr int LPS = LA + LB + 1;   // buffer loads per wave per stage (every wave loads one scale chunk)
+    static constexpr int SL = BM / 64;        // 256-byte activation-scale loads per stage (waves 0 .. SL-1)
+    static constexpr int LPS = LA + LB + 1;   // loads per wave per stage: every wave issues one dword load
     static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile must be whole 16x16 MFMA tiles");
     static_assert(WN <= 128 && 128 % WN == 0, "a wave's columns must sit in one weight block");
     static_assert(LA * 8 * NW == BM && LB * 8 * NW == BN, "tile rows must split evenly over the waves");
-    static_assert(BM % 64 == 0 && BM / 64 <= NW, "one 256-byte scale load per wave");
+    static_assert(BM % 64 == 0 && SL < NW, "scale loads: one wave per 64 rows plus one for the weight scales");
+    static_assert(BN / 128 <= 64, "weight-scale load covers at most 64 column blocks");
     static_assert(NS >= 2 && LDS <= 160 * 1024, "the stages must fit the 160 KB LDS");
 };
 
+// 16-byte chunk swizzle of the attention and patch-embedding tiles (chunk c of row r at c ^ (r & 7))
 __device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 128 + ((chunk ^ (row & 7)) << 4)); }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes)
@@ -60,14 +68,30 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-// 16 bytes per lane from rsrc + voff into LDS at lds + 16 * lane (lds wave-uniform)
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff)
+// Raw buffer descriptor (base, stride 0, num_records = bytes, 32-bit dword format) in SGPRs.
+__device__ __forceinline__ v4i buf_desc(const void *p, uint32_t bytes)
 {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, (int)voff, 0, 0, 0);
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    v4i r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+    r[3] = 0x00020000;
+    return r;
 }
-__device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, uint8_t *lds, uint32_t voff)
+
+// LDS address (byte offset in the workgroup's LDS) of a shared-memory pointer
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(lds_void *)p; }
+
+// buffer_load ... lds: lane l's 16 (4) bytes from rsrc + voff + soff land at LDS m0 + 16 l (4 l). m0 and soff are
+// wave-uniform. Not visible to the compiler's wait-count tracking: callers wait with wait_vmem*.
+__device__ __forceinline__ void dma16(v4i r, uint32_t m0, uint32_t voff, uint32_t soff)
 {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, (int)voff, 0, 0, 0);
+    asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(m0), "v"(voff), "s"(r), "s"(soff) : "memory");
+}
+__device__ __forceinline__ void dma4(v4i r, uint32_t m0, uint32_t voff, uint32_t soff)
+{
+    asm volatile("buffer_load_dword %1, %2, %3 offen lds" ::"{m0}"(m0), "v"(voff), "s"(r), "s"(soff) : "memory");
 }
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -77,57 +101,77 @@ __device__ __forceinline__ void wait_vmem_n()
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// block barrier after this wave's LDS reads have returned; no fence (the LDS DMA waits are explicit)
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// 32 bytes of swizzled LDS row `row` for lane group g (logical chunks 2g, 2g+1) as an MFMA operand. A and B use
-// the same (lane group, byte) -> k map, so the product sums every k of the block exactly once.
-__device__ __forceinline__ v8i ld_frag(const uint8_t *tile, int row, int g)
+// MFMA operand fragment of the 16-row tile starting at tile row r0 (a multiple of 16): lane (g, r) gets chunks g
+// and g + 4 of row r0 + r. A and B use the same (lane group, byte) -> k map, so the product sums every k of the
+// 128-wide block exactly once.
+__device__ __forceinline__ v8i ld_frag(const uint8_t *tile, int r0)
 {
-    const uint4 lo = *(const uint4 *)(tile + swz(row, 2 * g));
-    const uint4 hi = *(const uint4 *)(tile + swz(row, 2 * g + 1));
+    const int lane = threadIdx.x & 63, g = lane >> 4, r = lane & 15;
+    const uint8_t *p = tile + (r0 + r) * 128;
+    const uint4 lo = *(const uint4 *)(p + (((g + r) & 7) << 4));
+    const uint4 hi = *(const uint4 *)(p + (((g + 4 + r) & 7) << 4));
     v8i v;
     v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
     v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
     return v;
 }
 
+#define XT_OOR 0x80000000u  // a buffer offset past every range used here: the load returns zero
+
 template <class C>
 struct BsOperands {
-    // Per-lane parts of the load offsets live in one VGPR per operand; the wave-uniform parts (segment rows, K step)
-    // go in the SGPR soffset of each buffer load.
-    __amdgpu_buffer_rsrc_t ra, rw, rs;
-    uint32_t a_lane, w_lane, s_lane;
-    uint32_t a_seg, w_seg, s_plane;  // uniform: bytes between this wave's 8-row segments, scale plane bytes
+    v4i ra, rw, rs;                 // A, W and the scale source of this wave's dword load (sa or sw)
+    uint32_t a_off[C::LA], w_off[C::LB], s_off;
+    uint32_t s_step;                // SGPR offset of one K step for the dword load (sa plane or one sw float)
+    uint32_t m0_a, m0_b, m0_s;      // LDS byte offsets of this wave's slots inside a stage
 
     __device__ __forceinline__ void init(const uint8_t *A, int lda, const float *sa, int lds, const uint8_t *W,
-                                         int K, int M, int Npad, int m0, int n0)
+                                         const float *sw, int K, int M, int Npad, int m0, int n0)
     {
-        ra = buf_rsrc(A, (uint32_t)M * (uint32_t)lda);
-        rw = buf_rsrc(W, (uint32_t)Npad * (uint32_t)K);
-        rs = buf_rsrc(sa, (uint32_t)(K >> 7) * (uint32_t)lds * 4u);
+        const int KB = K >> 7;
+        ra = buf_desc(A, (uint32_t)M * (uint32_t)lda);
+        rw = buf_desc(W, (uint32_t)Npad * (uint32_t)K);
         const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-        const int r8 = lane >> 3, c = (lane & 7) ^ r8;  // every segment starts on a multiple of 8 rows
-        a_lane = (uint32_t)(m0 + 8 * w * C::LA + r8) * lda + c * 16;
-        w_lane = (uint32_t)(n0 + 8 * w * C::LB + r8) * K + c * 16;
-        s_lane = (uint32_t)(m0 + 64 * (w % (C::BM / 64)) + lane) * 4u;
-        a_seg = 8u * lda;
-        w_seg = 8u * K;
-        s_plane = (uint32_t)lds * 4u;
+        const int r8 = lane >> 3, p = lane & 7;
+#pragma unroll
+        for (int i = 0; i < C::LA; i++) {  // 1 KB block q = tile rows 8q .. 8q+7; lane slot p holds chunk (p - row) & 7
+            const int rl = 8 * (w * C::LA + i) + r8, m = m0 + rl;
+            a_off[i] = m < M ? (uint32_t)m * (uint32_t)lda + (uint32_t)(((p - rl) & 7) << 4) : XT_OOR;
+        }
+#pragma unroll
+        for (int i = 0; i < C::LB; i++) {
+            const int rl = 8 * (w * C::LB + i) + r8, n = n0 + rl;
+            w_off[i] = n < Npad ? (uint32_t)n * (uint32_t)K + (uint32_t)(((p - rl) & 7) << 4) : XT_OOR;
+        }
+        m0_a = (uint32_t)(1024 * w * C::LA);
+        m0_b = (uint32_t)(C::A_BYTES + 1024 * w * C::LB);
+        if (w < C::SL) {            // activation scales of rows m0 + 64 w + lane, plane kb
+            rs = buf_desc(sa, (uint32_t)KB * (uint32_t)lds * 4u);
+            const int m = m0 + 64 * w + lane;
+            s_off = m < lds ? (uint32_t)m * 4u : XT_OOR;
+            s_step = (uint32_t)lds * 4u;
+            m0_s = (uint32_t)(C::A_BYTES + C::B_BYTES + 256 * w);
+        } else {                    // weight scales of column blocks n0 / 128 + lane (the last waves repeat it)
+            const int nbt = Npad >> 7, nb = (n0 >> 7) + lane;
+            rs = buf_desc(sw, (uint32_t)nbt * (uint32_t)KB * 4u);
+            s_off = (lane < C::BN / 128 && nb < nbt) ? (uint32_t)(nb * KB) * 4u : XT_OOR;
+            s_step = 4u;
+            m0_s = (uint32_t)(C::A_BYTES + C::B_BYTES + C::S_BYTES);
+        }
     }
 
-    __device__ __forceinline__ void issue(uint8_t *stage, int kb) const
+    // all LPS loads of K step kb into the stage at LDS byte offset stage
+    __device__ __forceinline__ void issue(uint32_t stage, int kb) const
     {
-        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const uint32_t koff = (uint32_t)kb * 128u;
 #pragma unroll
-        for (int i = 0; i < C::LA; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(stage + 1024 * (w * C::LA + i)), 16, (int)a_lane,
-                                                     (int)(i * a_seg + kb * 128), 0, 0);
+        for (int i = 0; i < C::LA; i++) dma16(ra, stage + m0_a + 1024u * i, a_off[i], koff);
 #pragma unroll
-        for (int i = 0; i < C::LB; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void *)(stage + C::A_BYTES + 1024 * (w * C::LB + i)), 16,
-                                                     (int)w_lane, (int)(i * w_seg + kb * 128), 0, 0);
-        // waves past BM / 64 repeat a scale chunk (same bytes to the same place) so every wave issues LPS loads
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(stage + C::A_BYTES + C::B_BYTES + 256 * (w % (C::BM / 64))),
-                                                 4, (int)s_lane, (int)(kb * s_plane), 0, 0);
+        for (int i = 0; i < C::LB; i++) dma16(rw, stage + m0_b + 1024u * i, w_off[i], koff);
+        dma4(rs, stage + m0_s, s_off, (uint32_t)kb * s_step);
     }
 };
 
@@ -139,22 +183,70 @@ __device__ __forceinline__ void bs_wave_origin(int &wm0, int &wn0)
     wn0 = (w % C::NWN) * C::WN;
 }
 
-// Main loop. On return acc[i][j][r] holds output row m0 + wm0 + 16 i + 4 (lane >> 4) + r, column
-// n0 + wn0 + 16 j + (lane & 15), where (wm0, wn0) = bs_wave_origin(). The block is synchronised and the whole
-// shared memory is free for the epilogue.
+// One K step on a resident stage: TM x TN MFMAs, each block partial promoted into acc.
 template <class C>
+__device__ __forceinline__ void bs_step(const uint8_t *st, int wm0, int wn0, v4f (&acc)[C::TM][C::TN])
+{
+    const int lane = threadIdx.x & 63, g = lane >> 4;
+    const uint8_t *ta = st, *tb = st + C::A_BYTES;
+    const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
+    const float swv = *(const float *)(st + C::A_BYTES + C::B_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
+    v8i a[C::TM];
+    v4f sc[C::TM];
+    v8i bcur = ld_frag(tb, wn0), bnext = bcur;
+#pragma unroll
+    for (int i = 0; i < C::TM; i++) a[i] = ld_frag(ta, wm0 + 16 * i);
+#pragma unroll
+    for (int i = 0; i < C::TM; i++) {
+        const float4 s4 = *(const float4 *)(ts + wm0 + 16 * i + 4 * g);
+        sc[i] = v4f{s4.x * swv, s4.y * swv, s4.z * swv, s4.w * swv};
+    }
+    // Software pipeline over the TN x TM MFMAs: MFMA number t is issued, then the four promotion fmas of MFMA
+    // t - LAG, whose result has had LAG MFMA slots to land; B fragments are read one column tile ahead.
+    constexpr int NS = C::TN * C::TM, LAG = XT_LAG;
+    v4f pr[LAG + 1];
+#pragma unroll
+    for (int t = 0; t < NS + LAG; t++) {
+        if (t < NS) {
+            const int j = t / C::TM, i = t % C::TM;
+            if (i == 0 && j + 1 < C::TN) bnext = ld_frag(tb, wn0 + 16 * (j + 1));
+            pr[t % (LAG + 1)] = mfma_e4m3_16x16x128(a[i], bcur);
+            if (i == C::TM - 1) bcur = bnext;
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        }
+        if (t >= LAG) {
+            const int u = t - LAG, j = u / C::TM, i = u % C::TM;
+            const v4f p = pr[u % (LAG + 1)];
+            acc[i][j][0] = __builtin_fmaf(p[0], sc[i][0], acc[i][j][0]);
+            acc[i][j][1] = __builtin_fmaf(p[1], sc[i][1], acc[i][j][1]);
+            acc[i][j][2] = __builtin_fmaf(p[2], sc[i][2], acc[i][j][2]);
+            acc[i][j][3] = __builtin_fmaf(p[3], sc[i][3], acc[i][j][3]);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then 4 VALU
+        }
+    }
+}
+
+struct BsNoPre {
+    __device__ __forceinline__ void operator()() const {}
+};
+
+// Main loop. On return acc[i][j][r] holds output row m0 + wm0 + 16 i + 4 (lane >> 4) + r, column
+// n0 + wn0 + 16 j + (lane & 15), where (wm0, wn0) = bs_wave_origin(). The block is synchronised, no load is in
+// flight and the whole shared memory is free for the epilogue. pre() runs once the first stages' loads are issued
+// (epilogue inputs can be fetched there, under the prologue's memory latency); it may write shared memory only past
+// C::LDS.
+template <class C, class Pre = BsNoPre>
 __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
                                             int lds, const uint8_t *__restrict__ W, const float *__restrict__ sw,
                                             int M, int Npad, int K, int m0, int n0, uint8_t *smem,
-                                            v4f (&acc)[C::TM][C::TN])
+                                            v4f (&acc)[C::TM][C::TN], Pre pre = Pre())
 {
     BsOperands<C> op;
-    const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
     const int KB = K >> 7;
     int wm0, wn0;
     bs_wave_origin<C>(wm0, wn0);
-    const float *swp = sw + (size_t)__builtin_amdgcn_readfirstlane((n0 + wn0) >> 7) * KB;
-    op.init(A, lda, sa, lds, W, K, M, Npad, m0, n0);
+    op.init(A, lda, sa, lds, W, sw, K, M, Npad, m0, n0);
+    const uint32_t base = lds_addr(smem);
 
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
@@ -163,63 +255,25 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
 
 #pragma unroll
     for (int s = 0; s < C::NS - 1; s++)
-        if (s < KB) op.issue(smem + s * C::STAGE, s);
-    if (KB >= C::NS - 1) wait_vmem_n<(C::NS - 2) * C::LPS>();
-    else wait_vmem();
-    __syncthreads();
+        if (s < KB) op.issue(base + s * C::STAGE, s);
+    pre();
     int cs = 0, is = C::NS - 1;  // stage computed now, stage issued now
     for (int kb = 0; kb < KB; kb++) {
-        const uint8_t *st = smem + cs * C::STAGE;
-        const bool more = kb + C::NS - 1 < KB;
-        if (more) op.issue(smem + is * C::STAGE, kb + C::NS - 1);
-        const float swv = swp[kb];  // wave-uniform pointer: a scalar load, off the vector-memory counter
-        const uint8_t *ta = st, *tb = st + C::A_BYTES;
-        const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
-        v8i a[C::TM];
-        v4f sc[C::TM];
-#pragma unroll
-        for (int i = 0; i < C::TM; i++) {
-            a[i] = ld_frag(ta, wm0 + 16 * i + r16, g);
-            const float4 s4 = *(const float4 *)(ts + wm0 + 16 * i + 4 * g);
-            sc[i] = v4f{s4.x * swv, s4.y * swv, s4.z * swv, s4.w * swv};
-        }
-        // Software pipeline over the TN x TM MFMAs of this K step: MFMA number t is issued, then the four
-        // promotion fmas of MFMA t - 2, whose result has had two MFMA slots to land. One wave thus keeps the matrix
-        // core busy while its VALU promotes; B fragments are read one column tile ahead.
-        constexpr int NS = C::TN * C::TM, LAG = XT_LAG;
-        v4f pr[LAG + 1];
-        v8i bcur = ld_frag(tb, wn0 + r16, g), bnext = bcur;
-#pragma unroll
-        for (int t = 0; t < NS + LAG; t++) {
-            if (t < NS) {
-                const int j = t / C::TM, i = t % C::TM;
-                if (i == 0 && j + 1 < C::TN) bnext = ld_frag(tb, wn0 + 16 * (j + 1) + r16, g);
-                pr[t % (LAG + 1)] = mfma_e4m3_16x16x128(a[i], bcur);
-                if (i == C::TM - 1) bcur = bnext;
-                if (XT_SGB) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-            }
-            if (t >= LAG) {
-                const int u = t - LAG, j = u / C::TM, i = u % C::TM;
-                const v4f p = pr[u % (LAG + 1)];
-                acc[i][j][0] = __builtin_fmaf(p[0], sc[i][0], acc[i][j][0]);
-                acc[i][j][1] = __builtin_fmaf(p[1], sc[i][1], acc[i][j][1]);
-                acc[i][j][2] = __builtin_fmaf(p[2], sc[i][2], acc[i][j][2]);
-                acc[i][j][3] = __builtin_fmaf(p[3], sc[i][3], acc[i][j][3]);
-                if (XT_SGB) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then 4 VALU
-            }
-        }
-        // stage kb + 1 must be resident: the NS - 2 stages issued after it may stay in flight
-        if (more) wait_vmem_n<(C::NS - 2) * C::LPS>();
+        // stage kb must be resident; the min(NS - 2, KB - 1 - kb) stages issued after it may stay in flight
+        if (kb + C::NS - 2 < KB) wait_vmem_n<(C::NS - 2) * C::LPS>();
         else wait_vmem();
-        __syncthreads();
+        lds_barrier();  // every wave's part of stage kb landed; every wave finished reading stage kb - 1
+        if (kb + C::NS - 1 < KB) op.issue(base + is * C::STAGE, kb + C::NS - 1);
+        bs_step<C>(smem + cs * C::STAGE, wm0, wn0, acc);
         cs = cs == C::NS - 1 ? 0 : cs + 1;
         is = is == C::NS - 1 ? 0 : is + 1;
     }
+    lds_barrier();
 }
 
 // XCD-aware tile order for a 1-D grid of T = tiles_m * tiles_n blocks. Blocks are dispatched to the 8 XCDs round
 // robin (block b -> XCD b % 8), so XCD x is given a contiguous run of a grouped raster (XT_GM row tiles walked
-// together across all column tiles): the ~32 blocks an XCD runs at once share a few A row tiles and W column tiles
+// together across all column tiles): the blocks an XCD runs at once share a few A row tiles and W column tiles
 // in that XCD's L2.
 __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int &tm, int &tn)
 {

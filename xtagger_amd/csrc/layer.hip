@@ -8,8 +8,18 @@
 #include "gemm_core.h"
 #include "xt_abi.h"
 
-typedef BsCfg<128, 256, 2, 4, 3> LayerCfg;  // 8 waves of 64 x 64: one head (qkv) or 32 SwiGLU units (fc1) per wave
+typedef BsCfg<256, 256, 4, 2, 2> LayerCfg;  // 8 waves of 64 x 128: two heads (qkv) or 64 SwiGLU units (fc1) per wave
 typedef BsCfg<64, 128, 1, 2, 3> HeadCfg;    // head: few rows, 10861 columns
+
+// Shared memory of the layer kernels: the main-loop stages, reused by the epilogues (one 64 x 68 fp32 residual slice
+// per wave, one [128][66] bf16 transpose slice per wave, or the fc1 h tile), then 2 KB of per-row statistics that
+// k_fc2 fills while its first stages load.
+constexpr int LAYER_RES_SLICE = 64 * 68 * 4;
+constexpr int LAYER_ROWSTAT = LayerCfg::NW * LAYER_RES_SLICE;  // byte offset of the per-row statistics
+constexpr int LAYER_SMEM = LAYER_ROWSTAT + 2048;
+static_assert(LAYER_ROWSTAT >= LayerCfg::LDS, "row statistics sit past the main-loop stages");
+static_assert(LAYER_SMEM <= 160 * 1024, "layer kernels fit the LDS");
+static_assert(LayerCfg::NW * 128 * 66 * 2 <= LAYER_ROWSTAT, "v transpose slices fit");
 
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b)
 {
@@ -27,46 +37,68 @@ __device__ __forceinline__ void layer_tile(int M, int N, int &m0, int &n0)
     n0 = tn * C::BN;
 }
 
-// Residual update x = f16(x + y) of a wave's 64 x 64 tile, y in the MFMA C layout. The wave parks y in its own LDS
-// slice (row stride 68 floats: the 64 lanes of one store hit 64 different banks), then each lane updates 8
-// consecutive halves with one 16-byte load and store, so one wave instruction covers 8 rows of 128 bytes.
-template <class C>
+// Residual update x = f16(x + y) of a wave's 64 x (16 TN) tile, y in the MFMA C layout, in passes of 64 columns.
+// The wave parks 64 x 64 of y in its own LDS slice (row stride 68 floats: the 64 lanes of one store hit 64 different
+// banks), then each lane updates 8 consecutive halves with one 16-byte load and store, so one wave instruction
+// covers 8 rows of 128 bytes. Every x load of the tile is issued before the first store (one memory round trip for
+// the whole update), through a buffer descriptor that ends at row `rows`: rows past it load zero and their stores
+// are dropped, with no branch between the loads.
+struct ResIdentity {
+    __device__ __forceinline__ float operator()(int, int, int, float v) const { return v; }
+};
+
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// f(i, j, r, y) maps each accumulator to the value added (row m0 + mw + 16 i + 4 (lane >> 4) + r, column tile j).
+template <class C, class F = ResIdentity>
 __device__ __forceinline__ void residual_add(uint8_t *slices, v4f (&y)[C::TM][C::TN], uint16_t *__restrict__ x,
-                                             int mw, int nw, int rows)
+                                             int mw, int nw, int rows, F f = F())
 {
-    static_assert(C::TM == 4 && C::TN == 4, "64 x 64 wave tiles");
-    float *tr = (float *)slices + (threadIdx.x >> 6) * 64 * 68;
+    static_assert(C::TM == 4 && C::TN % 4 == 0, "64-row wave tiles, whole 64-column passes");
+    constexpr int NP = C::TN / 4;
+    float *tr = (float *)(slices + (threadIdx.x >> 6) * LAYER_RES_SLICE);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) tr[(16 * i + 4 * g + r) * 68 + 16 * j + c16] = y[i][j][r];
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
     const int rs = lane >> 3, ch = lane & 7;
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, (uint32_t)rows * XT_D * 2u);
+    const uint32_t off0 = (uint32_t)(((mw + rs) * XT_D + nw + 8 * ch) * 2);
+    v4u xv[NP][8];
 #pragma unroll
-    for (int it = 0; it < 8; it++) {
-        const int rr = 8 * it + rs, m = mw + rr;
-        if (m >= rows) continue;
-        const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
-        uint4 *p = (uint4 *)(x + (size_t)m * XT_D + nw + 8 * ch);
-        const uint4 v = *p;
-        uint4 o;
-        o.x = f2h(h2f(v.x & 0xFFFF) + a.x) | (uint32_t)f2h(h2f(v.x >> 16) + a.y) << 16;
-        o.y = f2h(h2f(v.y & 0xFFFF) + a.z) | (uint32_t)f2h(h2f(v.y >> 16) + a.w) << 16;
-        o.z = f2h(h2f(v.z & 0xFFFF) + b.x) | (uint32_t)f2h(h2f(v.z >> 16) + b.y) << 16;
-        o.w = f2h(h2f(v.w & 0xFFFF) + b.z) | (uint32_t)f2h(h2f(v.w >> 16) + b.w) << 16;
-        *p = o;
+    for (int pass = 0; pass < NP; pass++)
+#pragma unroll
+        for (int it = 0; it < 8; it++)
+            xv[pass][it] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
+#pragma unroll
+    for (int pass = 0; pass < NP; pass++) {
+        if (pass) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous pass's slice reads are done
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    tr[(16 * i + 4 * g + r) * 68 + 16 * j + c16] = f(i, 4 * pass + j, r, y[i][4 * pass + j][r]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const int rr = 8 * it + rs;
+            const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
+            const v4u v = xv[pass][it];
+            v4u o;
+            o[0] = f2h(h2f(v[0] & 0xFFFF) + a.x) | (uint32_t)f2h(h2f(v[0] >> 16) + a.y) << 16;
+            o[1] = f2h(h2f(v[1] & 0xFFFF) + a.z) | (uint32_t)f2h(h2f(v[1] >> 16) + a.w) << 16;
+            o[2] = f2h(h2f(v[2] & 0xFFFF) + b.x) | (uint32_t)f2h(h2f(v[2] >> 16) + b.y) << 16;
+            o[3] = f2h(h2f(v[3] & 0xFFFF) + b.z) | (uint32_t)f2h(h2f(v[3] >> 16) + b.w) << 16;
+            __builtin_amdgcn_raw_buffer_store_b128(o, rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
+        }
     }
 }
-static_assert(LayerCfg::LDS >= 1024 + LayerCfg::NW * 64 * 68 * 4, "residual slices (after 1 KB of row stats) fit");
 
 // ---------------------------------------------------------------------------------------------------------------
 // k_qkv: h8 [rows][1024] x Wqkv [3072][1024] -> q, k bf16 [nb][16][1088][64] (RoPE on patch tokens), vt bf16
-// [nb][16][64][1088]. A 256-column block is 4 heads of one of q | k | v; each wave owns one head. The weight rows of
-// q and k heads are stored pair-split (see eva_prep_qkv): column tile 2p holds dims 2i and tile 2p+1 dims 2i+1 of
-// pair i = 16p + (lane & 15), so a rotary pair meets in one lane. q rows carry log2(e)/8 (export_eva.py:71).
+// [nb][16][64][1088]. A 256-column block is 4 heads of one of q | k | v; each wave owns two heads. The weight rows
+// of q and k heads are stored pair-split (see eva_prep_qkv): within a head, column tile 2p holds dims 2i and tile
+// 2p+1 dims 2i+1 of pair i = 16p + (lane & 15), so a rotary pair meets in one lane. q rows carry log2(e)/8
+// (export_eva.py:71).
 // ---------------------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
                                                      int lds, const uint8_t *__restrict__ w,
@@ -75,40 +107,62 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
                                                      uint16_t *__restrict__ vt, int rows)
 {
     using C = LayerCfg;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[LAYER_SMEM];
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 3 * XT_D, m0, n0);
     bs_mainloop<C>(h8, XT_D, hs, lds, w, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-    const int part = n0 >> 10, head = ((n0 & 1023) + wn0) >> 6;
+    const int part = n0 >> 10, head0 = ((n0 & 1023) + wn0) >> 6;
     if (part < 2) {
-        uint16_t *dst = part ? k : q;
+        // every (cos, sin) pair of the tile is loaded before the first store: one memory round trip. Patch token t of
+        // image b uses row t - 1 of the table (eva_kernels.cu:74-79); cls rows (t = 0) load an out-of-range offset
+        // (zero) and are not rotated. Stores go through a descriptor that ends at image nb: rows past `rows` are
+        // dropped without a branch.
+        const int nbi = rows / XT_T;
+        const __amdgpu_buffer_rsrc_t rc = buf_rsrc(cs, 1024u * 32u * 8u);
+        const __amdgpu_buffer_rsrc_t rd = buf_rsrc(part ? k : q, (uint32_t)nbi * XT_NH * XT_TP * XT_HD * 2u);
+        typedef float v2f __attribute__((ext_vector_type(2)));
+        v2f rot[C::TM][4][2];
+        int tok[C::TM][4], img[C::TM][4];
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm0 + 16 * i + 4 * g + r;
-                if (m >= rows) continue;
-                const int b = m / XT_T, t = m - b * XT_T;
+                const int m = m0 + wm0 + 16 * i + 4 * g + r, b = m / XT_T, t = m - b * XT_T;
+                img[i][r] = b;
+                tok[i][r] = t;
 #pragma unroll
-                for (int p = 0; p < 2; p++) {
-                    const int pi = 16 * p + c16;
-                    float f0 = acc[i][2 * p][r], f1 = acc[i][2 * p + 1][r];
-                    if (t) {  // eva_kernels.cu:74-79
-                        const float2 a = *(const float2 *)(cs + ((size_t)(t - 1) * 32 + pi) * 2);
-                        const float g0 = f0 * a.x - f1 * a.y;
-                        f1 = f1 * a.x + f0 * a.y;
-                        f0 = g0;
+                for (int p = 0; p < 2; p++)
+                    rot[i][r][p] = __builtin_bit_cast(
+                        v2f, __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(((uint32_t)(t - 1) * 32u + 16 * p + c16) * 8u), 0, 0));
+            }
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int b = img[i][r], t = tok[i][r];
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                    for (int p = 0; p < 2; p++) {
+                        const int pi = 16 * p + c16;
+                        float f0 = acc[i][4 * hh + 2 * p][r], f1 = acc[i][4 * hh + 2 * p + 1][r];
+                        if (t) {
+                            const v2f a = rot[i][r][p];
+                            const float g0 = f0 * a.x - f1 * a.y;
+                            f1 = f1 * a.x + f0 * a.y;
+                            f0 = g0;
+                        }
+                        const uint32_t off = (uint32_t)((((size_t)b * XT_NH + head0 + hh) * XT_TP + t) * XT_HD + 2 * pi) * 2u;
+                        __builtin_amdgcn_raw_buffer_store_b32(pk_bf16(f0, f1), rd, (int)off, 0, 0);
                     }
-                    *(uint32_t *)(dst + (((size_t)b * XT_NH + head) * XT_TP + t) * XT_HD + 2 * pi) = pk_bf16(f0, f1);
-                }
             }
         return;
     }
-    // v: transpose the wave's 64 rows x 64 dims through LDS, then lanes walk rows (consecutive tokens)
-    uint16_t *tr = (uint16_t *)(smem + (threadIdx.x >> 6) * 64 * 66 * 2);  // [64 dims][66] bf16, padded rows
+    // v: transpose the wave's 64 rows x 128 dims (two heads) through LDS, then lanes walk rows (consecutive tokens)
+    uint16_t *tr = (uint16_t *)(smem + (threadIdx.x >> 6) * 128 * 66 * 2);  // [128 dims][66] bf16, padded rows
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
 #pragma unroll
@@ -122,9 +176,12 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
     const int m = m0 + wm0 + lane;
     if (m < rows) {
         const int b = m / XT_T, t = m - b * XT_T;
-        uint16_t *dst = vt + ((size_t)b * XT_NH + head) * XT_HD * XT_TP + t;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            uint16_t *dst = vt + ((size_t)b * XT_NH + head0 + hh) * XT_HD * XT_TP + t;
 #pragma unroll 8
-        for (int d = 0; d < XT_HD; d++) dst[(size_t)d * XT_TP] = tr[d * 66 + lane];
+            for (int d = 0; d < XT_HD; d++) dst[(size_t)d * XT_TP] = tr[(64 * hh + d) * 66 + lane];
+        }
     }
 }
 
@@ -136,7 +193,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
                                                        const float *__restrict__ ws, uint16_t *__restrict__ x, int rows)
 {
     using C = LayerCfg;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[LAYER_SMEM];
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, XT_D, m0, n0);
@@ -151,7 +208,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
 // m8 [rows][2816] E4M3 with 1x128 scales ms [22][lds], and per-(row, block) (sum h, sum h^2) of the unpacked h in
 // stat [22][lds][2] for the folded MLP LayerNorm (eva_kernels.cu:211-279). W12 rows hold g and x of 16 units in
 // alternate 16-row chunks (export_eva.py:60-62), so column tile 2c is g and 2c+1 is x of the same 16 units: a
-// 256-column block is one 128-unit block of h, whose |max| and sums meet through LDS across the 4 column waves.
+// 256-column block is one 128-unit block of h, whose |max| and sums meet through LDS across the 2 column waves.
 // Each (row, block) partial has one writer: no atomics, deterministic.
 // ---------------------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
@@ -160,7 +217,9 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
                                                      float *__restrict__ ms, float *__restrict__ stat, int rows)
 {
     using C = LayerCfg;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    constexpr int NP = C::TN / 2;                        // SwiGLU tile pairs per wave (16 units each)
+    __shared__ __attribute__((aligned(16))) uint8_t smem[LAYER_SMEM];
+    static_assert(C::BM * 8 % C::NT == 0, "packing items split evenly over the threads");
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 2 * XT_HIDP, m0, n0);
@@ -168,21 +227,24 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int wm = wm0 / C::WM, wn = wn0 / C::WN, ct = n0 >> 8;
-    float *red = (float *)smem;                          // [3][2 wm][4 wn][64 rows]: amax, sum, sum of squares
-    float *rinv = red + 3 * 2 * 4 * 64;                  // [128 rows] 1 / block scale
-    uint8_t *qt = smem + (3 * 2 * 4 * 64 + 128) * 4;     // [128 rows][128 units] E4M3 staging
-    float h[C::TM][2][4];
+    // h tile [BM rows][128 units] fp32, 16-byte chunk c of row r at chunk c ^ (r & 7); then the statistics
+    float *ht = (float *)smem;
+    float *red = ht + C::BM * 128;                       // [3][NWM][NWN][64 rows]: amax, sum, sum of squares
+    float *rinv = red + 3 * C::NWM * C::NWN * 64;        // [BM rows] 1 / block scale
+    static_assert((C::BM * 128 + 3 * C::NWM * C::NWN * 64 + C::BM) * 4 <= LAYER_SMEM, "fc1 staging fits");
+    auto hix = [](int row, int unit) { return row * 128 + ((((unit >> 2) ^ row) & 7) | ((unit >> 2) & ~7)) * 4 + (unit & 3); };
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
+            const int rr = 16 * i + 4 * g + r;
             float amax = 0.f, s = 0.f, q = 0.f;
 #pragma unroll
-            for (int p = 0; p < 2; p++) {
+            for (int p = 0; p < NP; p++) {
                 const float gg = acc[i][2 * p][r], xx = acc[i][2 * p + 1][r];
                 const float e = __expf(-gg), den = 1.0f + e;
                 const float v = (gg * __builtin_amdgcn_rcpf(den)) * xx;  // silu(g) x, hardware reciprocal (1 ulp)
-                h[i][p][r] = v;
+                ht[hix(wm0 + rr, 16 * NP * wn + 16 * p + c16)] = v;
                 amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
                 s += v;
                 q = __builtin_fmaf(v, v, q);
@@ -191,10 +253,9 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
             s = row16_sum(s);
             q = row16_sum(q);
             if (c16 == 0) {
-                const int rr = 16 * i + 4 * g + r;
-                red[((0 * 2 + wm) * 4 + wn) * 64 + rr] = amax;
-                red[((1 * 2 + wm) * 4 + wn) * 64 + rr] = s;
-                red[((2 * 2 + wm) * 4 + wn) * 64 + rr] = q;
+                red[((0 * C::NWM + wm) * C::NWN + wn) * 64 + rr] = amax;
+                red[((1 * C::NWM + wm) * C::NWN + wn) * 64 + rr] = s;
+                red[((2 * C::NWM + wm) * C::NWN + wn) * 64 + rr] = q;
             }
         }
     __syncthreads();
@@ -203,10 +264,10 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
         const int rr = threadIdx.x, m = m0 + rr, wmr = rr >> 6, r64 = rr & 63;
         float amax = 0.f, s = 0.f, q = 0.f;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            amax = __builtin_fmaxf(amax, red[((0 * 2 + wmr) * 4 + u) * 64 + r64]);
-            s += red[((1 * 2 + wmr) * 4 + u) * 64 + r64];
-            q += red[((2 * 2 + wmr) * 4 + u) * 64 + r64];
+        for (int u = 0; u < C::NWN; u++) {
+            amax = __builtin_fmaxf(amax, red[((0 * C::NWM + wmr) * C::NWN + u) * 64 + r64]);
+            s += red[((1 * C::NWM + wmr) * C::NWN + u) * 64 + r64];
+            q += red[((2 * C::NWM + wmr) * C::NWN + u) * 64 + r64];
         }
         const float sc = block_scale(amax);
         rinv[rr] = 1.0f / sc;
@@ -216,20 +277,20 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
         }
     }
     __syncthreads();
+    // 16 consecutive units of one row per item: 64 bytes of h -> 16 E4M3 bytes, one 16-byte store
+    const __amdgpu_buffer_rsrc_t rm = buf_rsrc(m8, (uint32_t)rows * XT_HIDP);
 #pragma unroll
-    for (int i = 0; i < C::TM; i++)
+    for (int it = 0; it < C::BM * 8 / C::NT; it++) {
+        const int idx = threadIdx.x + it * C::NT, rr = idx >> 3, u0 = (idx & 7) * 16;
+        const float inv = rinv[rr];
+        uint32_t w[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int rr = wm0 + 16 * i + 4 * g + r;
-            const float inv = rinv[rr];
-            const uint32_t two = e4_pack2(h[i][0][r] * inv, h[i][1][r] * inv);
-            qt[rr * 128 + 32 * wn + c16] = (uint8_t)two;
-            qt[rr * 128 + 32 * wn + 16 + c16] = (uint8_t)(two >> 8);
+        for (int c = 0; c < 4; c++) {
+            const float4 v = *(const float4 *)(ht + hix(rr, u0 + 4 * c));
+            w[c] = e4_pack4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
         }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < C::BM * 8; idx += C::NT) {
-        const int rr = idx >> 3, ch = idx & 7, m = m0 + rr;
-        if (m < rows) *(uint4 *)(m8 + (size_t)m * XT_HIDP + ct * 128 + ch * 16) = *(const uint4 *)(qt + rr * 128 + ch * 16);
+        const v4u o = {w[0], w[1], w[2], w[3]};
+        __builtin_amdgcn_raw_buffer_store_b128(o, rm, (int)((uint32_t)(m0 + rr) * XT_HIDP + ct * 128 + u0), 0, 0);
     }
 }
 
@@ -245,46 +306,42 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
                                                      uint16_t *__restrict__ x, int rows)
 {
     using C = LayerCfg;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[LAYER_SMEM];
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, XT_D, m0, n0);
-    bs_mainloop<C>(m8, XT_HIDP, ms, lds, w, ws, rows, XT_D, XT_HIDP, m0, n0, smem, acc);
-    bs_wave_origin<C>(wm0, wn0);
-    float2 *rs = (float2 *)smem;  // [128 rows] (rstd, -mean * rstd)
-    if (threadIdx.x < C::BM) {
-        const int m = m0 + threadIdx.x;
-        float S = 0.f, Q = 0.f;
-        if (m < rows)
+    float2 *rs = (float2 *)(smem + LAYER_ROWSTAT);  // [BM rows] (rstd, -mean * rstd)
+    static_assert(C::BM * 8 <= 2048, "row statistics fit their 2 KB");
+    auto rowstats = [&]() {
+        if (threadIdx.x < C::BM) {
+            const int m = m0 + threadIdx.x;
+            float2 p[XT_HIDP / 128];
+#pragma unroll
+            for (int blk = 0; blk < XT_HIDP / 128; blk++)
+                p[blk] = m < rows ? *(const float2 *)(stat + ((size_t)blk * lds + m) * 2) : make_float2(0.f, 0.f);
+            float S = 0.f, Q = 0.f;
+#pragma unroll
             for (int blk = 0; blk < XT_HIDP / 128; blk++) {
-                const float2 p = *(const float2 *)(stat + ((size_t)blk * lds + m) * 2);
-                S += p.x;
-                Q += p.y;
+                S += p[blk].x;
+                Q += p[blk].y;
             }
-        const float mean = S / (float)XT_HID;
-        float var = Q / (float)XT_HID - mean * mean;
-        var = __builtin_fmaxf(var, 0.f);
-        const float rstd = 1.0f / __builtin_sqrtf(var + XT_EPS);
-        rs[threadIdx.x] = make_float2(rstd, -mean * rstd);
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-    float cj[C::TN], dj[C::TN];
-#pragma unroll
-    for (int j = 0; j < C::TN; j++) {
-        cj[j] = cn[n0 + wn0 + 16 * j + c16];
-        dj[j] = dn[n0 + wn0 + 16 * j + c16];
-    }
-#pragma unroll
-    for (int i = 0; i < C::TM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float2 st = rs[wm0 + 16 * i + 4 * g + r];
-#pragma unroll
-            for (int j = 0; j < C::TN; j++)
-                acc[i][j][r] = __builtin_fmaf(st.x, acc[i][j][r], __builtin_fmaf(st.y, cj[j], dj[j]));
+            const float mean = S / (float)XT_HID;
+            float var = Q / (float)XT_HID - mean * mean;
+            var = __builtin_fmaxf(var, 0.f);
+            const float rstd = 1.0f / __builtin_sqrtf(var + XT_EPS);
+            rs[threadIdx.x] = make_float2(rstd, -mean * rstd);
         }
-    residual_add<C>(smem + 1024, acc, x, m0 + wm0, n0 + wn0, rows);
+    };
+    bs_mainloop<C>(m8, XT_HIDP, ms, lds, w, ws, rows, XT_D, XT_HIDP, m0, n0, smem, acc, rowstats);
+    bs_wave_origin<C>(wm0, wn0);
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const float *cw = cn + n0 + wn0 + c16, *dw = dn + n0 + wn0 + c16;
+    const float2 *rw = rs + wm0 + 4 * g;
+    auto fold = [&](int i, int j, int r, float v) {
+        const float2 st = rw[16 * i + r];
+        return __builtin_fmaf(st.x, v, __builtin_fmaf(st.y, cw[16 * j], dw[16 * j]));
+    };
+    residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows, fold);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

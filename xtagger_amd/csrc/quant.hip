@@ -153,17 +153,8 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
     }
 }
 
-#ifndef XT_BIG
-#define XT_BIG 1
-#endif
-#if XT_BIG == 0
-typedef BsCfg<256, 256, 4, 2, 2> GemmBig;    // 8 waves of 64 x 128, 2 stages
-#elif XT_BIG == 1
-typedef BsCfg<128, 256, 2, 4, 3> GemmBig;    // 8 waves of 64 x 64, 3 stages
-#else
-typedef BsCfg<256, 128, 4, 2, 3> GemmBig;    // 8 waves of 64 x 64, 3 stages
-#endif
-typedef BsCfg<128, 256, 2, 4, 3> GemmMid;    // 8 waves of 64 x 64, 3 stages
+typedef BsCfg<256, 256, 4, 2, 2> GemmBig;    // 8 waves of 64 x 128, 2 stages: once the tiles fill the 256 CUs
+typedef BsCfg<128, 128, 2, 2, 2> GemmMid;    // 4 waves of 64 x 64, 2 stages, two blocks per CU: small M
 
 // ---------------------------------------------------------------------------------------------------------------
 // C-ABI launchers
@@ -228,7 +219,7 @@ extern "C" int eva_k_gemm(const void *qa, int lda, const float *sa, int lds, con
             hipLaunchKernelGGL((k_gemm<GemmBig, 1>), grid, dim3(GemmBig::NT), 0, (hipStream_t)stream,
                                (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
     } else {
-        const dim3 grid((unsigned)(((M + 127) / 128) * ((N + 255) / 256)));
+        const dim3 grid((unsigned)(((M + GemmMid::BM - 1) / GemmMid::BM) * ((N + GemmMid::BN - 1) / GemmMid::BN)));
         if (out_kind == 0)
             hipLaunchKernelGGL((k_gemm<GemmMid, 0>), grid, dim3(GemmMid::NT), 0, (hipStream_t)stream,
                                (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
