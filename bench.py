@@ -37,7 +37,6 @@ class LayerStep:
         dev = torch.device("cuda:0")
         self.torch, self.L, self.M = torch, L, M
         self.nb = M // T
-        self.st = torch.cuda.current_stream().cuda_stream
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
         self.lds = lds = (M + 255) // 256 * 256
@@ -79,6 +78,11 @@ class LayerStep:
         self.fc1_stat = t(22, lds, 2, dt=torch.float32)
         torch.cuda.synchronize()
 
+    @property
+    def st(self):
+        # the launch stream is read at call time, so the launches also land in a graph being captured
+        return self.torch.cuda.current_stream().cuda_stream
+
     def qkv(self):
         L = self.L
         return L.lib.eva_k_qkv(L.ptr(self.a8), L.ptr(self.as_), self.lds, L.ptr(self.wqkv), L.ptr(self.sqkv),
@@ -104,6 +108,14 @@ class LayerStep:
             if f() != 0:
                 raise RuntimeError("layer GEMM launch failed")
 
+    def kernel_graph(self, name, reps):
+        f = getattr(self, name)
+
+        def run():
+            if f() != 0:
+                raise RuntimeError(name)
+        return capture(self.torch, run, reps)
+
 
 def time_launches(torch, fn, iters):
     """Average duration of `iters` back-to-back launches, HIP events on the launch stream."""
@@ -116,6 +128,34 @@ def time_launches(torch, fn, iters):
     e1.record(st)
     e1.synchronize()
     return e0.elapsed_time(e1) / iters
+
+
+def capture(torch, fn, reps):
+    """A HIP graph of `reps` back-to-back calls of fn (each call launches on the current stream)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, replays):
+    """Average duration of one replay of g over `replays` back-to-back replays, HIP events on the replay stream."""
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(replays):
+        g.replay()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / replays
 
 
 def bench_cfg1(torch, L, iters=50):
@@ -132,9 +172,13 @@ def bench_cfg1(torch, L, iters=50):
     c = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     L.check(L.lib.eva_k_quant_act(L.ptr(x), 0, K, M, K, L.ptr(qa), K, L.ptr(sa), M, st), "qa")
     L.check(L.lib.eva_k_quant_w(L.ptr(w), N, K, L.ptr(qw), L.ptr(sw), st), "qw")
-    f = lambda: L.lib.eva_k_gemm(L.ptr(qa), K, L.ptr(sa), M, L.ptr(qw), L.ptr(sw), M, N, K, L.ptr(c), N, 0, st)
-    time_launches(torch, f, 5)
-    ms = time_launches(torch, f, iters)
+    def f():
+        if L.lib.eva_k_gemm(L.ptr(qa), K, L.ptr(sa), M, L.ptr(qw), L.ptr(sw), M, N, K, L.ptr(c), N, 0,
+                            torch.cuda.current_stream().cuda_stream) != 0:
+            raise RuntimeError("eva_k_gemm")
+    g = capture(torch, f, iters)
+    time_graph(torch, g, 20)
+    ms = time_graph(torch, g, 20) / iters
     return 2.0 * M * N * K / ms / 1e9, ms
 
 
@@ -247,8 +291,8 @@ def profile_kernels(torch, L, M, launches=5, copy_bytes=1 << 30):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-forward", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-kernels", action="store_true",
@@ -269,21 +313,24 @@ def main():
     st = LayerStep(torch, L, M)
     fl = gemm_flops(M)
     step_flops = sum(fl.values())
+    # one step = the four kernels, replayed as one HIP graph (no host launch gaps between the kernels)
+    gstep = capture(torch, st.step, 1)
     for _ in range(args.warmup):
-        st.step()
+        gstep.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        st.step()
+        gstep.replay()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     tflops = step_flops / (ms * 1e-3) / 1e12
 
     per = {}
     for name in ("qkv", "oproj", "fc1", "fc2"):
-        f = getattr(st, name)
-        time_launches(torch, f, 3)
-        kms = time_launches(torch, f, max(args.steps, 20))
+        reps = 20
+        g = st.kernel_graph(name, reps)
+        time_graph(torch, g, 5)
+        kms = time_graph(torch, g, 10) / reps
         per[name] = {"us": round(kms * 1e3, 2), "tflops": round(fl[name] / (kms * 1e-3) / 1e12, 1)}
     fc1_ms = per["fc1"]["us"] * 1e-3
     achieved = fl["fc1"] / (fc1_ms * 1e-3) / 1e12

@@ -12,11 +12,11 @@ typedef BsCfg<256, 256, 4, 2, 2> LayerCfg;  // 8 waves of 64 x 128: two heads (q
 typedef BsCfg<64, 128, 1, 2, 3> HeadCfg;    // head: few rows, 10861 columns
 
 // Shared memory of the layer kernels: the main-loop stages, reused by the epilogues (one 64 x 68 fp32 residual slice
-// per wave, one [128][66] bf16 transpose slice per wave, or the fc1 h tile), then 2 KB of per-row statistics that
-// k_fc2 fills while its first stages load.
+// per wave, one [128][66] bf16 transpose slice per wave, or the fc1 h tile), then 2 KB of per-row statistics and
+// 2 KB of per-column fold terms that k_fc2 fills while its first stages load.
 constexpr int LAYER_RES_SLICE = 64 * 68 * 4;
 constexpr int LAYER_ROWSTAT = LayerCfg::NW * LAYER_RES_SLICE;  // byte offset of the per-row statistics
-constexpr int LAYER_SMEM = LAYER_ROWSTAT + 2048;
+constexpr int LAYER_SMEM = LAYER_ROWSTAT + 4096;                 // 2 KB row statistics + 2 KB column terms
 static_assert(LAYER_ROWSTAT >= LayerCfg::LDS, "row statistics sit past the main-loop stages");
 static_assert(LAYER_SMEM <= 160 * 1024, "layer kernels fit the LDS");
 static_assert(LayerCfg::NW * 128 * 66 * 2 <= LAYER_ROWSTAT, "v transpose slices fit");
@@ -310,8 +310,9 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, XT_D, m0, n0);
-    float2 *rs = (float2 *)(smem + LAYER_ROWSTAT);  // [BM rows] (rstd, -mean * rstd)
-    static_assert(C::BM * 8 <= 2048, "row statistics fit their 2 KB");
+    float2 *rs = (float2 *)(smem + LAYER_ROWSTAT);         // [BM rows] (rstd, -mean * rstd)
+    float2 *cd = (float2 *)(smem + LAYER_ROWSTAT + 2048);  // [BN columns] (c, d)
+    static_assert(C::BM * 8 <= 2048 && C::BN * 8 <= 2048, "row statistics and column terms fit their 2 KB each");
     auto rowstats = [&]() {
         if (threadIdx.x < C::BM) {
             const int m = m0 + threadIdx.x;
@@ -330,18 +331,36 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
             var = __builtin_fmaxf(var, 0.f);
             const float rstd = 1.0f / __builtin_sqrtf(var + XT_EPS);
             rs[threadIdx.x] = make_float2(rstd, -mean * rstd);
+        } else if (threadIdx.x < C::BM + C::BN) {
+            const int n = n0 + threadIdx.x - C::BM;
+            cd[threadIdx.x - C::BM] = make_float2(cn[n], dn[n]);
         }
     };
     bs_mainloop<C>(m8, XT_HIDP, ms, lds, w, ws, rows, XT_D, XT_HIDP, m0, n0, smem, acc, rowstats);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-    const float *cw = cn + n0 + wn0 + c16, *dw = dn + n0 + wn0 + c16;
-    const float2 *rw = rs + wm0 + 4 * g;
-    auto fold = [&](int i, int j, int r, float v) {
-        const float2 st = rw[16 * i + r];
-        return __builtin_fmaf(st.x, v, __builtin_fmaf(st.y, cw[16 * j], dw[16 * j]));
-    };
-    residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows, fold);
+    // fold in registers: the lane's column terms and 16 row statistics read from shared memory in one batch
+    static_assert(C::BM + C::BN <= C::NT, "one thread per row statistic and per column term");
+    float cj[C::TN], dj[C::TN];
+#pragma unroll
+    for (int j = 0; j < C::TN; j++) {
+        const float2 t = cd[wn0 + 16 * j + c16];
+        cj[j] = t.x;
+        dj[j] = t.y;
+    }
+    float2 st[C::TM][4];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) st[i][r] = rs[wm0 + 16 * i + 4 * g + r];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int j = 0; j < C::TN; j++)
+                acc[i][j][r] = __builtin_fmaf(st[i][r].x, acc[i][j][r], __builtin_fmaf(st[i][r].y, cj[j], dj[j]));
+    residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

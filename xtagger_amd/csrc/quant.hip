@@ -95,18 +95,27 @@ __global__ void __launch_bounds__(256) k_e4m3_bits(uint32_t first, uint32_t coun
 }
 
 // ---- standalone block-scaled GEMM: C [M][ldc] = bf16 or fp32 of the block-scaled product ----
-// bf16: each wave stages its WM x WN tile through LDS (the operand stages are free after the main loop) and writes
-// whole rows with 16-byte stores. fp32 (the parity build) stores straight from the accumulators.
+// bf16: each wave parks 64 x 64 fp32 of its tile in its own LDS slice (row stride 68 floats, conflict-free), then
+// every lane rounds 8 consecutive columns to bf16 (RNE) and writes them with one 16-byte store through a descriptor
+// that ends at row M (rows past it are dropped). ldc and N multiples of 8 and a 16-byte aligned C take that path; other
+// shapes store element by element. fp32 (the parity build) stores straight from the accumulators.
+constexpr int GEMM_SLICE = 64 * 68 * 4;
+template <class C>
+constexpr int gemm_smem() { return C::LDS > C::NW * GEMM_SLICE ? C::LDS : C::NW * GEMM_SLICE; }
+
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
 template <class C, int OUT>  // OUT 0: bf16, 1: fp32
 __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
                                                int lds, const uint8_t *__restrict__ W, const float *__restrict__ sw,
                                                void *__restrict__ Cp, int ldc, int M, int N, int K)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+    static_assert(C::TM == 4 && C::TN % 4 == 0, "64-row wave tiles, whole 64-column passes");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[gemm_smem<C>()];
     v4f acc[C::TM][C::TN];
     int tm, tn;
     tile_of_block((M + C::BM - 1) / C::BM, (N + C::BN - 1) / C::BN, tm, tn);
-    const int m0 = tm * C::BM, n0 = tn * C::BN, lane = threadIdx.x & 63, g = lane >> 4;
+    const int m0 = tm * C::BM, n0 = tn * C::BN, lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int Npad = (N + 127) & ~127;
     bs_mainloop<C>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
     int wm0, wn0;
@@ -116,7 +125,7 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
             for (int j = 0; j < C::TN; j++) {
-                const int col = n0 + wn0 + 16 * j + (lane & 15);
+                const int col = n0 + wn0 + 16 * j + c16;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int row = m0 + wm0 + 16 * i + 4 * g + r;
@@ -125,30 +134,43 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
             }
         return;
     }
-    constexpr int RS = C::WN * 2 + 4;   // staged row stride in bytes (one pad dword spreads the banks)
-    static_assert(C::NW * C::WM * RS <= C::LDS, "bf16 staging must fit the shared memory");
-    uint8_t *wt = smem + (threadIdx.x >> 6) * C::WM * RS;
+    uint16_t *Cb = (uint16_t *)Cp;
+    if ((ldc | N) % 8 != 0 || (((uintptr_t)Cp) & 15)) {  // general shapes: one element per store
 #pragma unroll
-    for (int i = 0; i < C::TM; i++)
+        for (int i = 0; i < C::TM; i++)
 #pragma unroll
-        for (int j = 0; j < C::TN; j++)
+            for (int j = 0; j < C::TN; j++) {
+                const int col = n0 + wn0 + 16 * j + c16;
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                *(uint16_t *)(wt + (16 * i + 4 * g + r) * RS + 2 * (16 * j + (lane & 15))) = f2bf(acc[i][j][r]);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the staged tile is wave-private: no block barrier
-    constexpr int CPR = C::WN / 8;       // 16-byte chunks per staged row
-    const bool vec = (ldc % 8) == 0 && (((uintptr_t)Cp) & 15) == 0;
-    for (int idx = lane; idx < C::WM * CPR; idx += 64) {
-        const int rr = idx / CPR, cc = idx - rr * CPR;
-        const int row = m0 + wm0 + rr, col = n0 + wn0 + 8 * cc;
-        if (row >= M || col >= N) continue;
-        const uint4 v = *(const uint4 *)(wt + rr * RS + 16 * cc);
-        uint16_t *dst = (uint16_t *)Cp + (size_t)row * ldc + col;
-        if (vec && col + 8 <= N) {
-            *(uint4 *)dst = v;
-        } else {
-            const uint16_t *e = (const uint16_t *)&v;
-            for (int t = 0; t < 8 && col + t < N; t++) dst[t] = e[t];
+                for (int r = 0; r < 4; r++) {
+                    const int row = m0 + wm0 + 16 * i + 4 * g + r;
+                    if (row < M && col < N) Cb[(size_t)row * ldc + col] = f2bf(acc[i][j][r]);
+                }
+            }
+        return;
+    }
+    float *tr = (float *)(smem + (threadIdx.x >> 6) * GEMM_SLICE);
+    const __amdgpu_buffer_rsrc_t rc = buf_rsrc(Cp, (uint32_t)M * (uint32_t)ldc * 2u);
+    const int rs = lane >> 3, ch = lane & 7;
+#pragma unroll
+    for (int pass = 0; pass < C::TN / 4; pass++) {
+        if (pass) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous pass's slice reads are done
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) tr[(16 * i + 4 * g + r) * 68 + 16 * j + c16] = acc[i][4 * pass + j][r];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
+        const int col = n0 + wn0 + 64 * pass + 8 * ch;
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const int rr = 8 * it + rs;
+            const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
+            const v4u o = {f2bf(a.x) | (uint32_t)f2bf(a.y) << 16, f2bf(a.z) | (uint32_t)f2bf(a.w) << 16,
+                           f2bf(b.x) | (uint32_t)f2bf(b.y) << 16, f2bf(b.z) | (uint32_t)f2bf(b.w) << 16};
+            if (col < N)
+                __builtin_amdgcn_raw_buffer_store_b128(o, rc, (int)(((uint32_t)(m0 + wm0 + rr) * (uint32_t)ldc + col) * 2u), 0, 0);
         }
     }
 }
