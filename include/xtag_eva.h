@@ -141,6 +141,30 @@ int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_
 int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const float *beta, float *c, float *d,
                   void *stream);
 
+/* ---- 2:4 structured-sparse weights (src/tools/prune24.py:43-56 prunes, mma.sp named at
+ * prune24.py:1 is never used there) ---- */
+/* In every group of 4 consecutive k of each row of the E4M3 weights w [N][K] (in place), zero the 2 smallest
+ * |values| (prune24.py "mag" rule); ties drop the lower k first. K % 4 == 0. */
+int eva_k_prune24(void *w, int N, int K, void *stream);
+/* Compressed layout of 2:4 weights w [N][K] (N % 16 == 0, K % 128 == 0): vals [N/16][K/128][64][16] (lane l = 16 g
+ * + r: row 16 t + r, dense k [128 kb + 32 g, +32), the 2 kept bytes of each group of 4 in k order), idx
+ * [N/16][K/128][64] u32 (nibble j = p0 | p1 << 2). bad (may be NULL, device int) counts groups with more than 2
+ * nonzero bytes (those pack wrongly). */
+int eva_k_pack24(const void *w, int N, int K, void *vals, void *idx, int *bad, void *stream);
+/* eva_k_gemm with 2:4-sparse weights (v_smfmac_f32_16x16x128_fp8_fp8): vals, idx from eva_k_pack24, sw the dense
+ * weights' 128x128 block scales. N % 16 == 0. */
+int eva_k_gemm_sp(const void *qa, int lda, const float *sa, int lds, const void *vals, const void *idx, const float *sw,
+                  int M, int N, int K, void *c, int ldc, int out_kind, void *stream);
+/* The layer kernels with 2:4-sparse weights (vals, idx of eva_k_pack24 in place of w; same epilogues). */
+int eva_k_qkv_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx, const float *ws,
+                 const float *cs, void *q, void *k, void *vt, int rows, void *stream);
+int eva_k_oproj_sp(const void *a8, const float *as, int lds, const void *vals, const void *idx, const float *ws,
+                   void *x, int rows, void *stream);
+int eva_k_fc1_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx, const float *ws,
+                 void *m8, float *ms, float *stat, int rows, void *stream);
+int eva_k_fc2_sp(const void *m8, const float *ms, int lds, const void *vals, const void *idx, const float *ws,
+                 const float *stat, const float *cn, const float *dn, void *x, int rows, void *stream);
+
 /* ---- on-box ceilings (no reference counterpart; the roofline fractions use peaks measured on the same GPU) ---- */
 /* dense FP8 MFMA: blocks x 256 threads, each wave issuing iters x 8 v_mfma_f32_16x16x128_f8f6f4 on register operands
  * (flops = blocks * 4 * iters * 8 * 65536); out [blocks * 256] keeps the result live */

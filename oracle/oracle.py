@@ -49,6 +49,8 @@ _SIGS = {
     "xo_fold_w2": (None, [_p, _i, _p, _p, _p, _p]),
     "xo_fold_c": (None, [_p, _p, _p]),
     "xo_forward": (_i, [_p, _p, _i, _i, _p, _p, _i]),
+    "xo_prune24": (None, [_p, _i, _i, _i]),
+    "xo_pack24": (_i, [_p, _i, _i, _p, _p]),
     "xo_lcg_frand": (None, [_p, C.c_size_t, _p]),
     "xo_lcg_e4m3": (None, [_p, C.c_size_t, _p]),
 }
@@ -286,11 +288,33 @@ class _Model(C.Structure):
                 ("ln1w", C.c_void_p * 24), ("ln1b", C.c_void_p * 24), ("ln2w", C.c_void_p * 24),
                 ("ln2b", C.c_void_p * 24), ("mlnw", C.c_void_p * 24), ("mlnb", C.c_void_p * 24),
                 ("wqkv", C.c_void_p * 24), ("wo", C.c_void_p * 24), ("w12", C.c_void_p * 24), ("w2", C.c_void_p * 24),
-                ("fnw", C.c_void_p), ("fnb", C.c_void_p), ("hw", C.c_void_p), ("hb", C.c_void_p), ("nt", C.c_int)]
+                ("fnw", C.c_void_p), ("fnb", C.c_void_p), ("hw", C.c_void_p), ("hb", C.c_void_p), ("nt", C.c_int),
+                ("sparse", C.c_int)]
 
 
-def forward(m, inp16, nl=24, threads=0):
-    """Full oracle forward from model tensors m (xtagger_amd.blob layout) on fp16 inputs [nb][1024][592]."""
+def prune24(q, wanda=False):
+    """2:4 pruning of E4M3 weights q [N][K] along K (a copy; see xo_prune24)."""
+    _done()
+    q = np.array(q, dtype=np.uint8, order="C", copy=True)
+    lib.xo_prune24(_ptr(q), q.shape[0], q.shape[1], 1 if wanda else 0)
+    return q
+
+
+def pack24(q):
+    """Compressed 2:4 layout (vals [N/16][K/128][64][16] u8, idx [N/16][K/128][64] u32) of pruned E4M3 q [N][K]."""
+    _done()
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    N, K = q.shape
+    vals = np.empty((N // 16, K // 128, 64, 16), np.uint8)
+    idx = np.empty((N // 16, K // 128, 64), np.uint32)
+    if lib.xo_pack24(_ptr(q), N, K, _ptr(vals), _ptr(idx)) != 0:
+        raise ValueError("a group of 4 holds more than 2 nonzero bytes")
+    return vals, idx
+
+
+def forward(m, inp16, nl=24, threads=0, sparse=False):
+    """Full oracle forward from model tensors m (xtagger_amd.blob layout) on fp16 inputs [nb][1024][592];
+    sparse: the layer GEMM weights are 2:4-pruned (magnitude) after packing."""
     _done()
     keep = []
 
@@ -310,6 +334,7 @@ def forward(m, inp16, nl=24, threads=0):
     md.fnw, md.fnb = P(m["fnw"], np.float32), P(m["fnb"], np.float32)
     md.hw, md.hb = P(m["hw"].view(np.uint16), np.uint16), P(m["hb"], np.float32)
     md.nt = m["nt"]
+    md.sparse = 1 if sparse else 0
     x = np.ascontiguousarray(inp16, dtype=np.float16).view(np.uint16)
     nb = x.shape[0]
     out = np.empty((nb, m["nt"]), np.float32)

@@ -703,6 +703,73 @@ void xo_fold_c(const uint8_t *q, const float *s, float *c)
     }
 }
 
+void xo_prune24(uint8_t *q, int N, int K, int wanda)
+{
+    float *colmax = NULL;
+    int n, k;
+
+    e4lut_init();
+    if (wanda) {
+        colmax = (float *)calloc((size_t)K, sizeof(float));
+        for (n = 0; n < N; n++)
+            for (k = 0; k < K; k++) {
+                const float v = fabsf(E4LUT[q[(size_t)n * K + k]]);
+                if (v > colmax[k]) colmax[k] = v;
+            }
+    }
+    for (n = 0; n < N; n++)
+        for (k = 0; k < K; k += 4) {
+            uint8_t *g = q + (size_t)n * K + k;
+            float sc[4];
+            int i, j, drop[4] = {0, 0, 0, 0}, nd = 0;
+            for (i = 0; i < 4; i++) sc[i] = fabsf(E4LUT[g[i]]) * (wanda ? colmax[k + i] : 1.0f);
+            /* the 2 lowest scores in ascending (score, k) order: a stable ascending sort's first two */
+            while (nd < 2) {
+                int best = -1;
+                for (j = 0; j < 4; j++)
+                    if (!drop[j] && (best < 0 || sc[j] < sc[best])) best = j;
+                drop[best] = 1;
+                nd++;
+            }
+            for (i = 0; i < 4; i++)
+                if (drop[i]) g[i] = 0;
+        }
+    free(colmax);
+}
+
+int xo_pack24(const uint8_t *q, int N, int K, uint8_t *vals, uint32_t *idx)
+{
+    const int KB = K / 128;
+    int t, kb, l, j;
+
+    e4lut_init();
+    for (t = 0; t < N / 16; t++)
+        for (kb = 0; kb < KB; kb++)
+            for (l = 0; l < 64; l++) {
+                const int g = l >> 4, r = l & 15;
+                const uint8_t *row = q + (size_t)(16 * t + r) * K + 128 * kb + 32 * g;
+                uint8_t *v = vals + (((size_t)t * KB + kb) * 64 + l) * 16;
+                uint32_t w = 0;
+                for (j = 0; j < 8; j++) {
+                    const uint8_t *grp = row + 4 * j;
+                    int pos[2], np = 0, i;
+                    for (i = 0; i < 4 && np < 3; i++)
+                        if (grp[i] != 0) {
+                            if (np == 2) return -1;
+                            pos[np++] = i;
+                        }
+                    for (i = 0; i < 4 && np < 2; i++)  /* complete with the lowest-k zero positions */
+                        if (grp[i] == 0 && !(np == 1 && pos[0] == i)) pos[np++] = i;
+                    if (pos[0] > pos[1]) { i = pos[0]; pos[0] = pos[1]; pos[1] = i; }
+                    v[2 * j] = grp[pos[0]];
+                    v[2 * j + 1] = grp[pos[1]];
+                    w |= (uint32_t)(pos[0] | pos[1] << 2) << (4 * j);
+                }
+                idx[((size_t)t * KB + kb) * 64 + l] = w;
+            }
+    return 0;
+}
+
 /* fp16 [rows][ld] (first cols columns) -> fp32 [rows_out][cols_out], zero padded */
 static float *f16_to_f32_pad(const uint16_t *w, int rows, int cols, int ld, int rows_out, int cols_out)
 {
@@ -746,6 +813,7 @@ int xo_forward(const xo_model *md, const uint16_t *in, int nb, int nl, float *ou
         wf = f16_to_f32_pad(md->wqkv[i], 3072, XO_D, XO_D, 3072, XO_D);
         xo_quant_w(wf, 3072, XO_D, wq, ws);
         free(wf);
+        if (md->sparse) xo_prune24(wq, 3072, XO_D, 0);
         xo_gemm_bs_f32(h8, XO_D, hs, M, wq, ws, 3072, XO_D, 0, M, acc, NULL, 3072, threads, avx);
         xo_qkv_epi(acc, nb, md->cs, q, k, vt);
         xo_attention(q, k, vt, nb, o, threads);
@@ -754,6 +822,7 @@ int xo_forward(const xo_model *md, const uint16_t *in, int nb, int nl, float *ou
         wf = f16_to_f32_pad(md->wo[i], XO_D, XO_D, XO_D, XO_D, XO_D);
         xo_quant_w(wf, XO_D, XO_D, wq, ws);
         free(wf);
+        if (md->sparse) xo_prune24(wq, XO_D, XO_D, 0);
         xo_gemm_bs_f32(h8, XO_D, hs, M, wq, ws, XO_D, XO_D, 0, M, acc, NULL, XO_D, threads, avx);
         xo_oproj_epi(acc, M, x);
         /* MLP */
@@ -761,6 +830,7 @@ int xo_forward(const xo_model *md, const uint16_t *in, int nb, int nl, float *ou
         wf = f16_to_f32_pad(md->w12[i], 2 * 2736, XO_D, XO_D, 2 * XO_HIDP, XO_D);
         xo_quant_w(wf, 2 * XO_HIDP, XO_D, wq, ws);
         free(wf);
+        if (md->sparse) xo_prune24(wq, 2 * XO_HIDP, XO_D, 0);
         xo_gemm_bs_f32(h8, XO_D, hs, M, wq, ws, 2 * XO_HIDP, XO_D, 0, M, acc, NULL, 2 * XO_HIDP, threads, avx);
         xo_fc1_epi(acc, M, hf, stat);
         xo_quant_act(hf, M, XO_HIDP, XO_HIDP, h8, XO_HIDP, hs, M);
@@ -768,6 +838,7 @@ int xo_forward(const xo_model *md, const uint16_t *in, int nb, int nl, float *ou
         xo_fold_w2(md->w2[i], 2736, md->mlnw[i], md->mlnb[i], wf, dfold);
         xo_quant_w(wf, XO_D, XO_HIDP, wq, ws);
         free(wf);
+        if (md->sparse) xo_prune24(wq, XO_D, XO_HIDP, 0);
         xo_fold_c(wq, ws, cfold);
         xo_gemm_bs_f32(h8, XO_HIDP, hs, M, wq, ws, XO_D, XO_HIDP, 0, M, acc, NULL, XO_D, threads, avx);
         xo_fc2_epi(acc, M, stat, cfold, dfold, x);

@@ -94,6 +94,20 @@ void xo_fold_w2(const uint16_t *w2, int ldw2, const float *gamma, const float *b
 /* c[n] = sum_k dec(q[n][k]) * s[n/128][k/128] over [1024][2816] (fp32, in k order) */
 void xo_fold_c(const uint8_t *q, const float *s, float *c);
 
+/* ---- 2:4 structured sparsity of the block weights ---- */
+/* 2:4 pruning along K of E4M3 weights (src/tools/prune24.py:43-56): in every group of 4 consecutive k of each row,
+ * the 2 lowest scores are zeroed. Score |dec(q)| (the "mag" rule) or, with wanda != 0, |dec(q)| * max_n |dec(q[n][k])|
+ * (prune24.py:50). Ties drop the lower k first (prune24.py's argsort order is unspecified for ties).
+ * q [N][K] bytes in place, K % 4 == 0. */
+void xo_prune24(uint8_t *q, int N, int K, int wanda);
+/* Compressed 2:4 layout read by the sparse GEMM. For 16-row tile t and 128-wide K block kb, lane l = 16 g + r
+ * (g = 0..3, r = 0..15) holds row 16 t + r, dense k in [128 kb + 32 g, +32) as 8 groups of 4:
+ *   vals [N/16][K/128][64][16]: group j's two kept bytes at 2j, 2j + 1, in k order;
+ *   idx  [N/16][K/128][64] u32: nibble j = p0 | p1 << 2, the positions (0..3, p0 < p1) of those bytes in the group.
+ * Kept positions: the group's nonzero bytes, completed with its lowest-k zero positions. N % 16 == 0, K % 128 == 0.
+ * Returns -1 (and packs nothing further) if a group holds more than 2 nonzero bytes. */
+int xo_pack24(const uint8_t *q, int N, int K, uint8_t *vals, uint32_t *idx);
+
 /* Full wd forward (eva.h:227-310) from the reference's v2 blob tensors (export_eva.py layout, fp16 block weights,
  * HIDP 2736). Weights are packed here with xo_quant_w exactly as the device does. nl layers (24 for the model);
  * out [nb][nt] sigmoid scores, pn [nb][1024] fp16 head inputs. */
@@ -109,6 +123,8 @@ typedef struct {
     const uint16_t *hw;          /* [ntp][1024] */
     const float *hb;             /* [ntp] */
     int nt;
+    int sparse;                  /* != 0: the four layer GEMMs' E4M3 weights are 2:4-pruned (xo_prune24, magnitude)
+                                    after packing; fc2's fold term c is taken from the pruned W~ */
 } xo_model;
 int xo_forward(const xo_model *m, const uint16_t *in, int nb, int nl, float *out, uint16_t *pn, int threads);
 

@@ -58,6 +58,13 @@ struct BsCfg {
     static_assert(BM % 64 == 0 && SL < NW, "scale loads: one wave per 64 rows plus one for the weight scales");
     static_assert(BN / 128 <= 64, "weight-scale load covers at most 64 column blocks");
     static_assert(NS >= 2 && LDS <= 160 * 1024, "the stages must fit the 160 KB LDS");
+    // 2:4-sparse weights (bs_mainloop_sp): per stage BN / 16 compressed 1 KB value blocks and 256-byte index blocks
+    static constexpr int LV = BN / (16 * NW);   // value (and index) blocks per wave per stage
+    static constexpr int V_BYTES = BN * 64;
+    static constexpr int X_BYTES = BN * 16;
+    static constexpr int STAGE_SP = A_BYTES + V_BYTES + X_BYTES + S_BYTES + SW_BYTES;
+    static constexpr int LDS_SP = NS * STAGE_SP;
+    static constexpr int LPS_SP = LA + 2 * LV + 1;
 };
 
 // 16-byte chunk swizzle of the attention and patch-embedding tiles (chunk c of row r at c ^ (r & 7))
@@ -268,6 +275,190 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
         cs = cs == C::NS - 1 ? 0 : cs + 1;
         is = is == C::NS - 1 ? 0 : is + 1;
     }
+    lds_barrier();
+}
+
+// ---- 2:4-sparse weights ----------------------------------------------------------------------------------------
+// W is stored compressed (xtagger_amd pack24 layout): for 16-row tile t and K block kb, 64 lanes l = 16 g + r hold
+// row 16 t + r, dense k in [128 kb + 32 g, +32) as 16 value bytes (2 of every 4) in vals [N/16][K/128][64][16] and one
+// index word (nibble j = p0 | p1 << 2 for group j) in idx [N/16][K/128][64]. v_smfmac_f32_16x16x128_fp8_fp8 takes the
+// sparse operand as A with exactly that lane layout, and the dense operand (the activations) as B in the layout
+// ld_frag reads: lane group g of B holds chunks g and g + 4 of its row, which makes sparse lane group g cover dense k
+// [32 g, 32 g + 32) of the same 128-wide block (measured on gfx950 for every group and index pattern). Each 1 KB value
+// block and 256-byte index block is contiguous in memory and in LDS, read lane-linear.
+// A wave computes the transposed tile D'[n][m] (weight rows as MFMA rows), promoted per K block with the activation
+// scale of its column m and the weight-block scale; bs_sp_to_dense then moves it into the dense accumulator layout.
+
+template <class C>
+struct BsSpOperands {
+    v4i ra, rv, rx, rs;
+    uint32_t a_off[C::LA], v_off[C::LV], x_off[C::LV], s_off;
+    uint32_t s_step;
+    uint32_t m0_a, m0_v, m0_x, m0_s;
+
+    __device__ __forceinline__ void init(const uint8_t *A, int lda, const float *sa, int lds, const uint8_t *V,
+                                         const uint32_t *X, const float *sw, int K, int M, int Npad, int m0, int n0)
+    {
+        const int KB = K >> 7, NT16 = Npad >> 4;
+        ra = buf_desc(A, (uint32_t)M * (uint32_t)lda);
+        rv = buf_desc(V, (uint32_t)NT16 * (uint32_t)KB * 1024u);
+        rx = buf_desc(X, (uint32_t)NT16 * (uint32_t)KB * 256u);
+        const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+        const int r8 = lane >> 3, p = lane & 7;
+#pragma unroll
+        for (int i = 0; i < C::LA; i++) {
+            const int rl = 8 * (w * C::LA + i) + r8, m = m0 + rl;
+            a_off[i] = m < M ? (uint32_t)m * (uint32_t)lda + (uint32_t)(((p - rl) & 7) << 4) : XT_OOR;
+        }
+#pragma unroll
+        for (int i = 0; i < C::LV; i++) {
+            const int t = (n0 >> 4) + w * C::LV + i;
+            v_off[i] = t < NT16 ? (uint32_t)t * (uint32_t)KB * 1024u + 16u * lane : XT_OOR;
+            x_off[i] = t < NT16 ? (uint32_t)t * (uint32_t)KB * 256u + 4u * lane : XT_OOR;
+        }
+        m0_a = (uint32_t)(1024 * w * C::LA);
+        m0_v = (uint32_t)(C::A_BYTES + 1024 * w * C::LV);
+        m0_x = (uint32_t)(C::A_BYTES + C::V_BYTES + 256 * w * C::LV);
+        if (w < C::SL) {
+            rs = buf_desc(sa, (uint32_t)KB * (uint32_t)lds * 4u);
+            const int m = m0 + 64 * w + lane;
+            s_off = m < lds ? (uint32_t)m * 4u : XT_OOR;
+            s_step = (uint32_t)lds * 4u;
+            m0_s = (uint32_t)(C::A_BYTES + C::V_BYTES + C::X_BYTES + 256 * w);
+        } else {
+            const int nbt = Npad >> 7, nb = (n0 >> 7) + lane;
+            rs = buf_desc(sw, (uint32_t)nbt * (uint32_t)KB * 4u);
+            s_off = (lane < C::BN / 128 && nb < nbt) ? (uint32_t)(nb * KB) * 4u : XT_OOR;
+            s_step = 4u;
+            m0_s = (uint32_t)(C::A_BYTES + C::V_BYTES + C::X_BYTES + C::S_BYTES);
+        }
+    }
+
+    __device__ __forceinline__ void issue(uint32_t stage, int kb) const
+    {
+#pragma unroll
+        for (int i = 0; i < C::LA; i++) dma16(ra, stage + m0_a + 1024u * i, a_off[i], (uint32_t)kb * 128u);
+#pragma unroll
+        for (int i = 0; i < C::LV; i++) dma16(rv, stage + m0_v + 1024u * i, v_off[i], (uint32_t)kb * 1024u);
+#pragma unroll
+        for (int i = 0; i < C::LV; i++) dma4(rx, stage + m0_x + 256u * i, x_off[i], (uint32_t)kb * 256u);
+        dma4(rs, stage + m0_s, s_off, (uint32_t)kb * s_step);
+    }
+};
+
+// One K step: TN x TM sparse MFMAs into the transposed accumulators accT[n tile][m tile].
+template <class C>
+__device__ __forceinline__ void bs_step_sp(const uint8_t *st, int wm0, int wn0, v4f (&accT)[C::TN][C::TM])
+{
+    const int lane = threadIdx.x & 63, c16 = lane & 15;
+    const uint8_t *ta = st, *tv = st + C::A_BYTES, *tx = st + C::A_BYTES + C::V_BYTES;
+    const float *ts = (const float *)(st + C::A_BYTES + C::V_BYTES + C::X_BYTES);
+    const float swv = *(const float *)(st + C::A_BYTES + C::V_BYTES + C::X_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
+    v8i xa[C::TM];
+    float sc[C::TM];
+#pragma unroll
+    for (int j = 0; j < C::TM; j++) xa[j] = ld_frag(ta, wm0 + 16 * j);
+#pragma unroll
+    for (int j = 0; j < C::TM; j++) sc[j] = ts[wm0 + 16 * j + c16] * swv;
+    const int t0 = wn0 >> 4;
+    v4i vcur = *(const v4i *)(tv + t0 * 1024 + 16 * lane), vnext = vcur;
+    int xcur = *(const int *)(tx + t0 * 256 + 4 * lane), xnext = xcur;
+    constexpr int NS = C::TN * C::TM, LAG = XT_LAG;
+    v4f pr[LAG + 1];
+#pragma unroll
+    for (int t = 0; t < NS + LAG; t++) {
+        if (t < NS) {
+            const int i = t / C::TM, j = t % C::TM;
+            if (j == 0 && i + 1 < C::TN) {
+                vnext = *(const v4i *)(tv + (t0 + i + 1) * 1024 + 16 * lane);
+                xnext = *(const int *)(tx + (t0 + i + 1) * 256 + 4 * lane);
+            }
+            pr[t % (LAG + 1)] = __builtin_amdgcn_smfmac_f32_16x16x128_fp8_fp8(vcur, xa[j], v4f{0.f, 0.f, 0.f, 0.f},
+                                                                               xcur, 0, 0);
+            if (j == C::TM - 1) {
+                vcur = vnext;
+                xcur = xnext;
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        }
+        if (t >= LAG) {
+            const int u = t - LAG, i = u / C::TM, j = u % C::TM;
+            const v4f p = pr[u % (LAG + 1)];
+            accT[i][j][0] = __builtin_fmaf(p[0], sc[j], accT[i][j][0]);
+            accT[i][j][1] = __builtin_fmaf(p[1], sc[j], accT[i][j][1]);
+            accT[i][j][2] = __builtin_fmaf(p[2], sc[j], accT[i][j][2]);
+            accT[i][j][3] = __builtin_fmaf(p[3], sc[j], accT[i][j][3]);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then 4 VALU
+        }
+    }
+}
+
+// The transposed wave tile (accT[n tile][m tile][r]: n = wn0 + 16 i + 4 (lane >> 4) + r, m = wm0 + 16 j + (lane & 15))
+// to the dense accumulator layout of bs_mainloop, through the wave's own 64 x 68 fp32 slice of shared memory
+// (slices at `slices` + wave * 17408 bytes), 64 columns per pass.
+template <class C>
+__device__ __forceinline__ void bs_sp_to_dense(uint8_t *slices, v4f (&accT)[C::TN][C::TM], v4f (&acc)[C::TM][C::TN])
+{
+    static_assert(C::TM == 4 && C::TN % 4 == 0, "64-row wave tiles, whole 64-column passes");
+    float *tr = (float *)(slices + (threadIdx.x >> 6) * (64 * 68 * 4));
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int pass = 0; pass < C::TN / 4; pass++) {
+        if (pass) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                *(float4 *)(tr + (16 * j + c16) * 68 + 16 * i + 4 * g) =
+                    make_float4(accT[4 * pass + i][j][0], accT[4 * pass + i][j][1], accT[4 * pass + i][j][2],
+                                accT[4 * pass + i][j][3]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[i][4 * pass + j][r] = tr[(16 * i + 4 * g + r) * 68 + 16 * j + c16];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// Sparse main loop: the same contract as bs_mainloop (dense accumulator layout on return, block synchronised, no load
+// in flight, shared memory free), with the weights given as pack24 values V and indices X plus the dense 128 x 128
+// block scales sw. Uses NW * 17408 bytes of shared memory at the end for the transposition.
+template <class C, class Pre = BsNoPre>
+__device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
+                                               int lds, const uint8_t *__restrict__ V, const uint32_t *__restrict__ X,
+                                               const float *__restrict__ sw, int M, int Npad, int K, int m0, int n0,
+                                               uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre())
+{
+    BsSpOperands<C> op;
+    const int KB = K >> 7;
+    int wm0, wn0;
+    bs_wave_origin<C>(wm0, wn0);
+    op.init(A, lda, sa, lds, V, X, sw, K, M, Npad, m0, n0);
+    const uint32_t base = lds_addr(smem);
+    v4f accT[C::TN][C::TM];
+#pragma unroll
+    for (int i = 0; i < C::TN; i++)
+#pragma unroll
+        for (int j = 0; j < C::TM; j++) accT[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < C::NS - 1; s++)
+        if (s < KB) op.issue(base + s * C::STAGE_SP, s);
+    pre();
+    int cs = 0, is = C::NS - 1;
+    for (int kb = 0; kb < KB; kb++) {
+        if (kb + C::NS - 2 < KB) wait_vmem_n<(C::NS - 2) * C::LPS_SP>();
+        else wait_vmem();
+        lds_barrier();
+        if (kb + C::NS - 1 < KB) op.issue(base + is * C::STAGE_SP, kb + C::NS - 1);
+        bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT);
+        cs = cs == C::NS - 1 ? 0 : cs + 1;
+        is = is == C::NS - 1 ? 0 : is + 1;
+    }
+    lds_barrier();
+    bs_sp_to_dense<C>(smem, accT, acc);
     lds_barrier();
 }
 

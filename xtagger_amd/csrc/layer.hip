@@ -28,6 +28,17 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b)
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), b2));
 }
 
+// The layer kernels take their weights dense (w, wx unused) or 2:4-sparse (SP: w = pack24 values, wx = indices).
+template <class C, bool SP, class Pre = BsNoPre>
+__device__ __forceinline__ void layer_mainloop(const uint8_t *A, int lda, const float *sa, int lds, const uint8_t *w,
+                                               const uint32_t *wx, const float *ws, int rows, int Npad, int K, int m0,
+                                               int n0, uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre())
+{
+    static_assert(!SP || C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
+    if constexpr (SP) bs_mainloop_sp<C>(A, lda, sa, lds, w, wx, ws, rows, Npad, K, m0, n0, smem, acc, pre);
+    else bs_mainloop<C>(A, lda, sa, lds, w, ws, rows, Npad, K, m0, n0, smem, acc, pre);
+}
+
 template <class C>
 __device__ __forceinline__ void layer_tile(int M, int N, int &m0, int &n0)
 {
@@ -100,8 +111,10 @@ __device__ __forceinline__ void residual_add(uint8_t *slices, v4f (&y)[C::TM][C:
 // 2p+1 dims 2i+1 of pair i = 16p + (lane & 15), so a rotary pair meets in one lane. q rows carry log2(e)/8
 // (export_eva.py:71).
 // ---------------------------------------------------------------------------------------------------------------
+template <bool SP>
 __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
                                                      int lds, const uint8_t *__restrict__ w,
+                                                     const uint32_t *__restrict__ wx,
                                                      const float *__restrict__ ws, const float *__restrict__ cs,
                                                      uint16_t *__restrict__ q, uint16_t *__restrict__ k,
                                                      uint16_t *__restrict__ vt, int rows)
@@ -111,7 +124,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 3 * XT_D, m0, n0);
-    bs_mainloop<C>(h8, XT_D, hs, lds, w, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, acc);
+    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int part = n0 >> 10, head0 = ((n0 & 1023) + wn0) >> 6;
@@ -188,8 +201,10 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
 // ---------------------------------------------------------------------------------------------------------------
 // k_oproj: x [rows][1024] = f16(x + attn_out . Wo^T) (eva_kernels.cu:150-160, alpha folded into the block scales)
 // ---------------------------------------------------------------------------------------------------------------
+template <bool SP>
 __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restrict__ a8, const float *__restrict__ as,
                                                        int lds, const uint8_t *__restrict__ w,
+                                                       const uint32_t *__restrict__ wx,
                                                        const float *__restrict__ ws, uint16_t *__restrict__ x, int rows)
 {
     using C = LayerCfg;
@@ -197,7 +212,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, XT_D, m0, n0);
-    bs_mainloop<C>(a8, XT_D, as, lds, w, ws, rows, XT_D, XT_D, m0, n0, smem, acc);
+    layer_mainloop<C, SP>(a8, XT_D, as, lds, w, wx, ws, rows, XT_D, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows);
 }
@@ -211,8 +226,10 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
 // 256-column block is one 128-unit block of h, whose |max| and sums meet through LDS across the 2 column waves.
 // Each (row, block) partial has one writer: no atomics, deterministic.
 // ---------------------------------------------------------------------------------------------------------------
+template <bool SP>
 __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
                                                      int lds, const uint8_t *__restrict__ w,
+                                                     const uint32_t *__restrict__ wx,
                                                      const float *__restrict__ ws, uint8_t *__restrict__ m8,
                                                      float *__restrict__ ms, float *__restrict__ stat, int rows)
 {
@@ -223,7 +240,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 2 * XT_HIDP, m0, n0);
-    bs_mainloop<C>(h8, XT_D, hs, lds, w, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc);
+    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int wm = wm0 / C::WM, wn = wn0 / C::WN, ct = n0 >> 8;
@@ -299,8 +316,10 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
 // W~, d = W2 beta), mean / rstd of the SwiGLU row over 2730 units from k_fc1's 22 partials summed in block order:
 // mean = S / 2730, var = max(Q / 2730 - mean^2, 0), rstd = 1 / sqrt(var + 1e-6) (eva_kernels.cu:300-333).
 // ---------------------------------------------------------------------------------------------------------------
+template <bool SP>
 __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict__ m8, const float *__restrict__ ms,
                                                      int lds, const uint8_t *__restrict__ w,
+                                                     const uint32_t *__restrict__ wx,
                                                      const float *__restrict__ ws, const float *__restrict__ stat,
                                                      const float *__restrict__ cn, const float *__restrict__ dn,
                                                      uint16_t *__restrict__ x, int rows)
@@ -336,7 +355,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
             cd[threadIdx.x - C::BM] = make_float2(cn[n], dn[n]);
         }
     };
-    bs_mainloop<C>(m8, XT_HIDP, ms, lds, w, ws, rows, XT_D, XT_HIDP, m0, n0, smem, acc, rowstats);
+    layer_mainloop<C, SP>(m8, XT_HIDP, ms, lds, w, wx, ws, rows, XT_D, XT_HIDP, m0, n0, smem, acc, rowstats);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     // fold in registers: the lane's column terms and 16 row statistics read from shared memory in one batch
@@ -468,47 +487,103 @@ static unsigned layer_grid(int rows, int N, int BM, int BN) { return (unsigned)(
 
 #define XT_ALIGNED(p) ((((uintptr_t)(p)) & 15) == 0)
 
+template <bool SP>
+static int qkv_launch(const char *what, const void *h8, const float *hs, int lds, const void *w, const void *wx,
+                      const float *ws, const float *cs, void *q, void *k, void *vt, int rows, void *stream)
+{
+    if (rows <= 0 || lds < rows || rows % XT_T) return xt_fail(what, "rows must be nb * 1025, lds >= rows");
+    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || (SP && !wx)) return xt_fail(what, "h8 and w must be 16-byte aligned");
+    hipLaunchKernelGGL(k_qkv<SP>, dim3(layer_grid(rows, 3 * XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w, (const uint32_t *)wx, ws,
+                       cs, (uint16_t *)q, (uint16_t *)k, (uint16_t *)vt, rows);
+    return xt_check(what);
+}
+
+template <bool SP>
+static int oproj_launch(const char *what, const void *a8, const float *as, int lds, const void *w, const void *wx,
+                        const float *ws, void *x, int rows, void *stream)
+{
+    if (rows <= 0 || lds < rows) return xt_fail(what, "bad shape (rows > 0, lds >= rows)");
+    if (!XT_ALIGNED(a8) || !XT_ALIGNED(w) || (SP && !wx)) return xt_fail(what, "a8 and w must be 16-byte aligned");
+    hipLaunchKernelGGL(k_oproj<SP>, dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)a8, as, lds, (const uint8_t *)w, (const uint32_t *)wx, ws,
+                       (uint16_t *)x, rows);
+    return xt_check(what);
+}
+
+template <bool SP>
+static int fc1_launch(const char *what, const void *h8, const float *hs, int lds, const void *w, const void *wx,
+                      const float *ws, void *m8, float *ms, float *stat, int rows, void *stream)
+{
+    if (rows <= 0 || lds < rows) return xt_fail(what, "bad shape (rows > 0, lds >= rows)");
+    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || !XT_ALIGNED(m8) || (SP && !wx))
+        return xt_fail(what, "h8, w, m8 must be 16-byte aligned");
+    hipLaunchKernelGGL(k_fc1<SP>, dim3(layer_grid(rows, 2 * XT_HIDP, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w, (const uint32_t *)wx, ws,
+                       (uint8_t *)m8, ms, stat, rows);
+    return xt_check(what);
+}
+
+template <bool SP>
+static int fc2_launch(const char *what, const void *m8, const float *ms, int lds, const void *w, const void *wx,
+                      const float *ws, const float *stat, const float *cn, const float *dn, void *x, int rows,
+                      void *stream)
+{
+    if (rows <= 0 || lds < rows) return xt_fail(what, "bad shape (rows > 0, lds >= rows)");
+    if (!XT_ALIGNED(m8) || !XT_ALIGNED(w) || (SP && !wx)) return xt_fail(what, "m8 and w must be 16-byte aligned");
+    hipLaunchKernelGGL(k_fc2<SP>, dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)m8, ms, lds, (const uint8_t *)w, (const uint32_t *)wx, ws,
+                       stat, cn, dn, (uint16_t *)x, rows);
+    return xt_check(what);
+}
+
 extern "C" int eva_k_qkv(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *cs,
                          void *q, void *k, void *vt, int rows, void *stream)
 {
-    if (rows <= 0 || lds < rows || rows % XT_T) return xt_fail("eva_k_qkv", "rows must be nb * 1025, lds >= rows");
-    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w)) return xt_fail("eva_k_qkv", "h8 and w must be 16-byte aligned");
-    hipLaunchKernelGGL(k_qkv, dim3(layer_grid(rows, 3 * XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
-                       (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w, ws, cs, (uint16_t *)q,
-                       (uint16_t *)k, (uint16_t *)vt, rows);
-    return xt_check("eva_k_qkv");
+    return qkv_launch<false>("eva_k_qkv", h8, hs, lds, w, nullptr, ws, cs, q, k, vt, rows, stream);
 }
 
 extern "C" int eva_k_oproj(const void *a8, const float *as, int lds, const void *w, const float *ws, void *x, int rows,
                            void *stream)
 {
-    if (rows <= 0 || lds < rows) return xt_fail("eva_k_oproj", "bad shape (rows > 0, lds >= rows)");
-    if (!XT_ALIGNED(a8) || !XT_ALIGNED(w)) return xt_fail("eva_k_oproj", "a8 and w must be 16-byte aligned");
-    hipLaunchKernelGGL(k_oproj, dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
-                       (hipStream_t)stream, (const uint8_t *)a8, as, lds, (const uint8_t *)w, ws, (uint16_t *)x, rows);
-    return xt_check("eva_k_oproj");
+    return oproj_launch<false>("eva_k_oproj", a8, as, lds, w, nullptr, ws, x, rows, stream);
 }
 
 extern "C" int eva_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8, float *ms,
                          float *stat, int rows, void *stream)
 {
-    if (rows <= 0 || lds < rows) return xt_fail("eva_k_fc1", "bad shape (rows > 0, lds >= rows)");
-    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || !XT_ALIGNED(m8)) return xt_fail("eva_k_fc1", "h8, w, m8 must be 16-byte aligned");
-    hipLaunchKernelGGL(k_fc1, dim3(layer_grid(rows, 2 * XT_HIDP, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
-                       (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w, ws, (uint8_t *)m8, ms,
-                       stat, rows);
-    return xt_check("eva_k_fc1");
+    return fc1_launch<false>("eva_k_fc1", h8, hs, lds, w, nullptr, ws, m8, ms, stat, rows, stream);
 }
 
 extern "C" int eva_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *stat,
                          const float *cn, const float *dn, void *x, int rows, void *stream)
 {
-    if (rows <= 0 || lds < rows) return xt_fail("eva_k_fc2", "bad shape (rows > 0, lds >= rows)");
-    if (!XT_ALIGNED(m8) || !XT_ALIGNED(w)) return xt_fail("eva_k_fc2", "m8 and w must be 16-byte aligned");
-    hipLaunchKernelGGL(k_fc2, dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
-                       (hipStream_t)stream, (const uint8_t *)m8, ms, lds, (const uint8_t *)w, ws, stat, cn, dn,
-                       (uint16_t *)x, rows);
-    return xt_check("eva_k_fc2");
+    return fc2_launch<false>("eva_k_fc2", m8, ms, lds, w, nullptr, ws, stat, cn, dn, x, rows, stream);
+}
+
+extern "C" int eva_k_qkv_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx,
+                            const float *ws, const float *cs, void *q, void *k, void *vt, int rows, void *stream)
+{
+    return qkv_launch<true>("eva_k_qkv_sp", h8, hs, lds, vals, idx, ws, cs, q, k, vt, rows, stream);
+}
+
+extern "C" int eva_k_oproj_sp(const void *a8, const float *as, int lds, const void *vals, const void *idx,
+                              const float *ws, void *x, int rows, void *stream)
+{
+    return oproj_launch<true>("eva_k_oproj_sp", a8, as, lds, vals, idx, ws, x, rows, stream);
+}
+
+extern "C" int eva_k_fc1_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx,
+                            const float *ws, void *m8, float *ms, float *stat, int rows, void *stream)
+{
+    return fc1_launch<true>("eva_k_fc1_sp", h8, hs, lds, vals, idx, ws, m8, ms, stat, rows, stream);
+}
+
+extern "C" int eva_k_fc2_sp(const void *m8, const float *ms, int lds, const void *vals, const void *idx,
+                            const float *ws, const float *stat, const float *cn, const float *dn, void *x, int rows,
+                            void *stream)
+{
+    return fc2_launch<true>("eva_k_fc2_sp", m8, ms, lds, vals, idx, ws, stat, cn, dn, x, rows, stream);
 }
 
 extern "C" int eva_k_head(const void *pq, const float *ps, int lds, const void *w, const float *ws, const float *hb,

@@ -101,14 +101,20 @@ __global__ void __launch_bounds__(256) k_e4m3_bits(uint32_t first, uint32_t coun
 // shapes store element by element. fp32 (the parity build) stores straight from the accumulators.
 constexpr int GEMM_SLICE = 64 * 68 * 4;
 template <class C>
-constexpr int gemm_smem() { return C::LDS > C::NW * GEMM_SLICE ? C::LDS : C::NW * GEMM_SLICE; }
+constexpr int gemm_smem()
+{
+    return C::LDS > C::NW * GEMM_SLICE ? (C::LDS > C::LDS_SP ? C::LDS : C::LDS_SP)
+                                       : (C::NW * GEMM_SLICE > C::LDS_SP ? C::NW * GEMM_SLICE : C::LDS_SP);
+}
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
-template <class C, int OUT>  // OUT 0: bf16, 1: fp32
+// SP: W holds the 2:4 values and WX the indices of the pack24 layout (bs_mainloop_sp); otherwise W is dense, WX unused.
+template <class C, int OUT, bool SP>  // OUT 0: bf16, 1: fp32
 __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
-                                               int lds, const uint8_t *__restrict__ W, const float *__restrict__ sw,
-                                               void *__restrict__ Cp, int ldc, int M, int N, int K)
+                                               int lds, const uint8_t *__restrict__ W, const uint32_t *__restrict__ WX,
+                                               const float *__restrict__ sw, void *__restrict__ Cp, int ldc, int M,
+                                               int N, int K)
 {
     static_assert(C::TM == 4 && C::TN % 4 == 0, "64-row wave tiles, whole 64-column passes");
     __shared__ __attribute__((aligned(16))) uint8_t smem[gemm_smem<C>()];
@@ -117,7 +123,8 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
     tile_of_block((M + C::BM - 1) / C::BM, (N + C::BN - 1) / C::BN, tm, tn);
     const int m0 = tm * C::BM, n0 = tn * C::BN, lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int Npad = (N + 127) & ~127;
-    bs_mainloop<C>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
+    if constexpr (SP) bs_mainloop_sp<C>(A, lda, sa, lds, W, WX, sw, M, Npad, K, m0, n0, smem, acc);
+    else bs_mainloop<C>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
     int wm0, wn0;
     bs_wave_origin<C>(wm0, wn0);
     if (OUT == 1) {
@@ -222,32 +229,50 @@ extern "C" int eva_k_e4m3_bits(uint32_t first, uint32_t count, void *out, void *
     return xt_check("eva_k_e4m3_bits");
 }
 
-extern "C" int eva_k_gemm(const void *qa, int lda, const float *sa, int lds, const void *qw, const float *sw, int M,
-                          int N, int K, void *c, int ldc, int out_kind, void *stream)
+template <bool SP>
+static int gemm_launch(const char *what, const void *qa, int lda, const float *sa, int lds, const void *qw,
+                       const void *qx, const float *sw, int M, int N, int K, void *c, int ldc, int out_kind,
+                       void *stream)
 {
     if (M < 0 || N <= 0 || K <= 0 || K % 128 || lda < K || lda % 16 || lds < M || ldc < N ||
         (out_kind != 0 && out_kind != 1))
-        return xt_fail("eva_k_gemm", "bad shape (K % 128, lda >= K and a multiple of 16, lds >= M, ldc >= N, out_kind 0 or 1)");
-    if (((uintptr_t)qa | (uintptr_t)qw) & 15) return xt_fail("eva_k_gemm", "qa and qw must be 16-byte aligned");
+        return xt_fail(what, "bad shape (K % 128, lda >= K and a multiple of 16, lds >= M, ldc >= N, out_kind 0 or 1)");
+    if (((uintptr_t)qa | (uintptr_t)qw) & 15) return xt_fail(what, "qa and qw must be 16-byte aligned");
+    if (SP && (N % 16 || !qx || ((uintptr_t)qx & 3))) return xt_fail(what, "sparse weights: N % 16 == 0, 4-byte aligned indices");
     if (!M) return 0;
-    // big tiles once there are enough of them to fill the 256 CUs, else 128-row tiles
+    const uint8_t *A = (const uint8_t *)qa, *W = (const uint8_t *)qw;
+    const uint32_t *X = (const uint32_t *)qx;
+    hipStream_t st = (hipStream_t)stream;
+    // big tiles once there are enough of them to fill the 256 CUs, else 128 x 128 tiles (two blocks per CU)
     const long big = (long)((M + GemmBig::BM - 1) / GemmBig::BM) * ((N + GemmBig::BN - 1) / GemmBig::BN);
     if (big >= 256) {
         const dim3 grid((unsigned)big);
         if (out_kind == 0)
-            hipLaunchKernelGGL((k_gemm<GemmBig, 0>), grid, dim3(GemmBig::NT), 0, (hipStream_t)stream,
-                               (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+            hipLaunchKernelGGL((k_gemm<GemmBig, 0, SP>), grid, dim3(GemmBig::NT), 0, st, A, lda, sa, lds, W, X, sw, c,
+                               ldc, M, N, K);
         else
-            hipLaunchKernelGGL((k_gemm<GemmBig, 1>), grid, dim3(GemmBig::NT), 0, (hipStream_t)stream,
-                               (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+            hipLaunchKernelGGL((k_gemm<GemmBig, 1, SP>), grid, dim3(GemmBig::NT), 0, st, A, lda, sa, lds, W, X, sw, c,
+                               ldc, M, N, K);
     } else {
         const dim3 grid((unsigned)(((M + GemmMid::BM - 1) / GemmMid::BM) * ((N + GemmMid::BN - 1) / GemmMid::BN)));
         if (out_kind == 0)
-            hipLaunchKernelGGL((k_gemm<GemmMid, 0>), grid, dim3(GemmMid::NT), 0, (hipStream_t)stream,
-                               (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+            hipLaunchKernelGGL((k_gemm<GemmMid, 0, SP>), grid, dim3(GemmMid::NT), 0, st, A, lda, sa, lds, W, X, sw, c,
+                               ldc, M, N, K);
         else
-            hipLaunchKernelGGL((k_gemm<GemmMid, 1>), grid, dim3(GemmMid::NT), 0, (hipStream_t)stream,
-                               (const uint8_t *)qa, lda, sa, lds, (const uint8_t *)qw, sw, c, ldc, M, N, K);
+            hipLaunchKernelGGL((k_gemm<GemmMid, 1, SP>), grid, dim3(GemmMid::NT), 0, st, A, lda, sa, lds, W, X, sw, c,
+                               ldc, M, N, K);
     }
-    return xt_check("eva_k_gemm");
+    return xt_check(what);
+}
+
+extern "C" int eva_k_gemm(const void *qa, int lda, const float *sa, int lds, const void *qw, const float *sw, int M,
+                          int N, int K, void *c, int ldc, int out_kind, void *stream)
+{
+    return gemm_launch<false>("eva_k_gemm", qa, lda, sa, lds, qw, nullptr, sw, M, N, K, c, ldc, out_kind, stream);
+}
+
+extern "C" int eva_k_gemm_sp(const void *qa, int lda, const float *sa, int lds, const void *vals, const void *idx,
+                             const float *sw, int M, int N, int K, void *c, int ldc, int out_kind, void *stream)
+{
+    return gemm_launch<true>("eva_k_gemm_sp", qa, lda, sa, lds, vals, idx, sw, M, N, K, c, ldc, out_kind, stream);
 }

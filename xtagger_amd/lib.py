@@ -28,6 +28,13 @@ _SIGS = {
     "eva_k_lnh": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _p]),
     "eva_k_prep_w": (_i, [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p]),
     "eva_k_fold_cd": (_i, [_p, _p, _p, _i, _p, _p, _p, _p]),
+    "eva_k_prune24": (_i, [_p, _i, _i, _p]),
+    "eva_k_pack24": (_i, [_p, _i, _i, _p, _p, _p, _p]),
+    "eva_k_gemm_sp": (_i, [_p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _p, _i, _i, _p]),
+    "eva_k_qkv_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _p]),
+    "eva_k_oproj_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _p]),
+    "eva_k_fc1_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
+    "eva_k_fc2_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _p]),
     "eva_open": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32]),
     "eva_open_nb": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32, _u32]),
     "eva_ready": (_i, [_p]),
