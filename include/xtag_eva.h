@@ -62,6 +62,12 @@ typedef struct {
 int eva_open(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra);
 /* eva_open with the batch (model inputs per launch, 1..EVA_NBMAX) as a runtime parameter */
 int eva_open_nb(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra, uint32_t nb);
+/* eva_open_nb with flags. EVA_SPARSE24: the bring-up 2:4-prunes the four layer GEMMs' E4M3 weights (magnitude, as
+ * src/tools/prune24.py "mag" does to a v3 blob) and the forward runs them on the sparse matrix cores. No reference
+ * counterpart as an API (the reference prunes offline with prune24.py and has no sparse kernel). */
+#define EVA_SPARSE24 1u
+int eva_open_ex(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra, uint32_t nb,
+                uint32_t flags);
 int eva_ready(eva *e);                                              /* eva.h:607 */
 int eva_poll(eva *e);                                               /* eva.h:620 */
 /* eva.h:627. n <= nb inputs, each an fp16 [1024][592] patch operand (BGR in [-1,1], element c*196 + ky*14 + kx,

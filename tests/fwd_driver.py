@@ -18,8 +18,11 @@ T, D, TP, HIDP, HID = 1025, 1024, 1088, 2816, 2730
 
 
 class StepForward:
-    def __init__(self, xt, m, nb, dev):
-        self.xt, self.m, self.nb, self.dev = xt, m, nb, dev
+    """sparse: the four layer GEMMs' packed weights are 2:4-pruned and packed (eva_k_prune24 / eva_k_pack24) and the
+    sparse kernels run, as the engine does with EVA_SPARSE24."""
+
+    def __init__(self, xt, m, nb, dev, sparse=False):
+        self.xt, self.m, self.nb, self.dev, self.sparse = xt, m, nb, dev, sparse
         self.M = nb * T
         self.lds = (self.M + 255) // 256 * 256
         self.st = torch.cuda.current_stream().cuda_stream
@@ -46,6 +49,12 @@ class StepForward:
                               st))
             ck(L.eva_k_prep_w(P(w16["w2"]), 2736, D, HID, D, HIDP, 0, P(d["mlnw"]), P(scratch), P(d["w2"]), P(d["s2"]),
                               st))
+            if sparse:
+                for k, n, kk in (("wqkv", 3 * D, D), ("wo", D, D), ("w12", 2 * HIDP, D), ("w2", D, HIDP)):
+                    ck(L.eva_k_prune24(P(d[k]), n, kk, st))
+                    d[k + "_v"] = z8(n // 16, kk // 128, 64, 16)
+                    d[k + "_x"] = torch.zeros(n // 16, kk // 128, 64, dtype=torch.int32, device=dev)
+                    ck(L.eva_k_pack24(P(d[k]), n, kk, P(d[k + "_v"]), P(d[k + "_x"]), None, st))
             ck(L.eva_k_fold_cd(P(d["w2"]), P(d["s2"]), P(w16["w2"]), 2736, P(d["mlnb"]), P(d["cn"]), P(d["dn"]), st))
             torch.cuda.synchronize()
             self.layers.append(d)
@@ -96,8 +105,12 @@ class StepForward:
             if check:
                 check("ln1", i, {"x": x0, "h8": h(self.h8[:M]), "sh": h(self.sh[:, :M])})
                 a8, as_ = h(self.h8[:M]), h(self.sh[:, :M])
-            xt.check(L.eva_k_qkv(P(self.h8), P(self.sh), lds, P(W["wqkv"]), P(W["sqkv"]), P(self.cs), P(self.q),
-                                 P(self.k), P(self.vt), M, st), "qkv")
+            if self.sparse:
+                xt.check(L.eva_k_qkv_sp(P(self.h8), P(self.sh), lds, P(W["wqkv_v"]), P(W["wqkv_x"]), P(W["sqkv"]),
+                                        P(self.cs), P(self.q), P(self.k), P(self.vt), M, st), "qkv")
+            else:
+                xt.check(L.eva_k_qkv(P(self.h8), P(self.sh), lds, P(W["wqkv"]), P(W["sqkv"]), P(self.cs), P(self.q),
+                                     P(self.k), P(self.vt), M, st), "qkv")
             sync()
             if check:
                 check("qkv", i, {"h8": a8, "sh": as_, "q": h(self.q), "k": h(self.k), "vt": h(self.vt)})
@@ -108,7 +121,11 @@ class StepForward:
                 check("flash", i, {"q": h(self.q), "k": h(self.k), "vt": h(self.vt), "o32": h(self.o32),
                                    "h8": h(self.h8[:M]), "sh": h(self.sh[:, :M])})
                 a8, as_, x1 = h(self.h8[:M]), h(self.sh[:, :M]), h(self.x[:M])
-            xt.check(L.eva_k_oproj(P(self.h8), P(self.sh), lds, P(W["wo"]), P(W["so"]), P(self.x), M, st), "oproj")
+            if self.sparse:
+                xt.check(L.eva_k_oproj_sp(P(self.h8), P(self.sh), lds, P(W["wo_v"]), P(W["wo_x"]), P(W["so"]),
+                                          P(self.x), M, st), "oproj")
+            else:
+                xt.check(L.eva_k_oproj(P(self.h8), P(self.sh), lds, P(W["wo"]), P(W["so"]), P(self.x), M, st), "oproj")
             sync()
             if check:
                 check("oproj", i, {"h8": a8, "sh": as_, "x_in": x1, "x": h(self.x[:M])})
@@ -118,15 +135,23 @@ class StepForward:
             if check:
                 check("ln2", i, {"x": x2, "h8": h(self.h8[:M]), "sh": h(self.sh[:, :M])})
                 a8, as_ = h(self.h8[:M]), h(self.sh[:, :M])
-            xt.check(L.eva_k_fc1(P(self.h8), P(self.sh), lds, P(W["w12"]), P(W["s12"]), P(self.m8), P(self.sm),
-                                 P(self.stat), M, st), "fc1")
+            if self.sparse:
+                xt.check(L.eva_k_fc1_sp(P(self.h8), P(self.sh), lds, P(W["w12_v"]), P(W["w12_x"]), P(W["s12"]),
+                                        P(self.m8), P(self.sm), P(self.stat), M, st), "fc1")
+            else:
+                xt.check(L.eva_k_fc1(P(self.h8), P(self.sh), lds, P(W["w12"]), P(W["s12"]), P(self.m8), P(self.sm),
+                                     P(self.stat), M, st), "fc1")
             sync()
             if check:
                 check("fc1", i, {"h8": a8, "sh": as_, "m8": h(self.m8[:M]), "sm": h(self.sm[:, :M]),
                                  "stat": h(self.stat[:, :M])})
                 m8, ms, stt, x3 = h(self.m8[:M]), h(self.sm[:, :M]), h(self.stat[:, :M]), h(self.x[:M])
-            xt.check(L.eva_k_fc2(P(self.m8), P(self.sm), lds, P(W["w2"]), P(W["s2"]), P(self.stat), P(W["cn"]),
-                                 P(W["dn"]), P(self.x), M, st), "fc2")
+            if self.sparse:
+                xt.check(L.eva_k_fc2_sp(P(self.m8), P(self.sm), lds, P(W["w2_v"]), P(W["w2_x"]), P(W["s2"]),
+                                        P(self.stat), P(W["cn"]), P(W["dn"]), P(self.x), M, st), "fc2")
+            else:
+                xt.check(L.eva_k_fc2(P(self.m8), P(self.sm), lds, P(W["w2"]), P(W["s2"]), P(self.stat), P(W["cn"]),
+                                     P(W["dn"]), P(self.x), M, st), "fc2")
             sync()
             if check:
                 check("fc2", i, {"m8": m8, "sm": ms, "stat": stt, "x_in": x3, "x": h(self.x[:M])})

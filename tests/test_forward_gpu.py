@@ -5,6 +5,8 @@
    GEMM-fed epilogues within one output rounding unit plus 2e-4 of the terms; attention within 4e-3; the head's
    sigmoid scores within 1e-4 (the contract asks 2e-3) with identical top-50 tag sets.
 2. The engine (eva_open .. eva_wait, one HIP graph replay) returns exactly the scores of that validated sequence.
+   With 2:4-sparse weights (EVA_SPARSE24) the same holds against the oracle with the same pruned
+   weights (its "dense-decoded reference"), and the sparse engine's graph returns that validated sequence's bits.
 3. Free running, the GPU and the oracle drift apart through the per-layer E4M3 re-quantization exactly as the oracle
    drifts from itself when only its fp32 summation order changes (tests/golden/forward_self_divergence.json); the
    GPU's drift is held to 3x that envelope. The strict 2e-3 bound cannot hold free running for any implementation
@@ -48,8 +50,8 @@ def _bf16(u):
 class OracleCheck:
     """Recomputes each step with the oracle from the GPU's inputs; records the worst error / bound per step kind."""
 
-    def __init__(self, orc, m, inp, nb):
-        self.orc, self.m, self.inp, self.nb = orc, m, inp, nb
+    def __init__(self, orc, m, inp, nb, sparse=False):
+        self.orc, self.m, self.inp, self.nb, self.sparse = orc, m, inp, nb, sparse
         self.M = nb * T
         self.worst = defaultdict(float)
         self._w = (None, None)
@@ -59,13 +61,14 @@ class OracleCheck:
             return self._w[1]
         orc, L = self.orc, self.m["layers"][i]
         W = {}
-        W["qkv"] = orc.quant_w(L["wqkv"].astype(np.float32))
-        W["wo"] = orc.quant_w(L["wo"].astype(np.float32))
+        pr = (lambda qs: (orc.prune24(qs[0]), qs[1])) if self.sparse else (lambda qs: qs)
+        W["qkv"] = pr(orc.quant_w(L["wqkv"].astype(np.float32)))
+        W["wo"] = pr(orc.quant_w(L["wo"].astype(np.float32)))
         w12 = np.zeros((2 * HIDP, D), np.float32)
         w12[:2 * 2736] = L["w12"].astype(np.float32)
-        W["w12"] = orc.quant_w(w12)
+        W["w12"] = pr(orc.quant_w(w12))
         wt, dd = orc.fold_w2(L["w2"].view(np.uint16), L["mlnw"], L["mlnb"])
-        W["w2"] = orc.quant_w(wt)
+        W["w2"] = pr(orc.quant_w(wt))
         W["c"], W["d"] = orc.fold_c(*W["w2"]), dd
         self._w = (i, W)
         return W
@@ -181,6 +184,28 @@ def test_forward_teacher_forced_and_engine(dev, xt, orc, synth_blob):
     e.close()
     assert np.array_equal(got, out), "the engine's graph differs from the validated kernel sequence"
     np.save(os.path.join(os.environ.get("TMPDIR", "/tmp"), "xtag_gpu_forward_seed1.npy"), got)
+
+
+def test_forward_sparse_teacher_forced_and_engine(dev, xt, orc, synth_blob):
+    from tests.fwd_driver import StepForward
+    from xtagger_amd import blob
+    from xtagger_amd.engine import Engine
+    path, m = synth_blob
+    nb = 1
+    inp = blob.synth_inputs(nb, seed=2)
+    _say("sparse step driver: packing, pruning and compressing weights")
+    drv = StepForward(xt, m, nb, dev, sparse=True)
+    chk = OracleCheck(orc, m, inp, nb, sparse=True)
+    out = drv.run(inp, check=chk)
+    for k, v in sorted(chk.worst.items()):
+        _say(f"  worst {k}: {v:.3g}")
+    _say("sparse engine forward")
+    e = Engine(path, device=0, nb=nb, sparse=True)
+    e.ready()
+    e.submit(0, inp)
+    got = e.wait(0, nb)
+    e.close()
+    assert np.array_equal(got, out), "the sparse engine's graph differs from the validated kernel sequence"
 
 
 def test_forward_free_running_envelope(dev, orc, synth_blob):

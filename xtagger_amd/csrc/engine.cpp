@@ -34,6 +34,16 @@ int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_
                  float *scratch, void *q, float *s, void *stream);
 int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const float *beta, float *c, float *d,
                   void *stream);
+int eva_k_prune24(void *w, int N, int K, void *stream);
+int eva_k_pack24(const void *w, int N, int K, void *vals, void *idx, int *bad, void *stream);
+int eva_k_qkv_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx, const float *ws,
+                 const float *cs, void *q, void *k, void *vt, int rows, void *stream);
+int eva_k_oproj_sp(const void *a8, const float *as, int lds, const void *vals, const void *idx, const float *ws,
+                   void *x, int rows, void *stream);
+int eva_k_fc1_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx, const float *ws,
+                 void *m8, float *ms, float *stat, int rows, void *stream);
+int eva_k_fc2_sp(const void *m8, const float *ms, int lds, const void *vals, const void *idx, const float *ws,
+                 const float *stat, const float *cn, const float *dn, void *x, int rows, void *stream);
 }
 
 #define V2_HIDP 2736          // hidden padding of the reference's v2 blob (export_eva.py:19)
@@ -43,12 +53,15 @@ int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const
 struct Layer {
     const float *ln1w, *ln1b, *ln2w, *ln2b, *mlnw, *mlnb;  // in the blob
     const uint16_t *wqkv16, *wo16, *w1216, *w216;          // fp16 block weights in the blob
-    uint8_t *wqkv, *wo, *w12, *w2;                         // packed E4M3
+    uint8_t *wqkv, *wo, *w12, *w2;                         // packed E4M3 (2:4-pruned with EVA_SPARSE24)
     float *sqkv, *so, *s12, *s2, *cn, *dn;
+    uint8_t *vqkv, *vo, *v12, *v2;                         // EVA_SPARSE24: pack24 values of the pruned weights
+    uint32_t *xqkv, *xo, *x12, *x2;                        // and their indices
 };
 
 struct eva_impl {
     int devno, bstatus, up, booted;
+    uint32_t flags;                                        // EVA_SPARSE24
     pthread_t boot;
     char *path;                                            // own copy of the weights path
     size_t wbytes;
@@ -171,13 +184,18 @@ static int ev_forward(eva *e)
     EV_CK(eva_k_pe(E->in, E->pe, E->pos, E->x, nb, st));
     for (int i = 0; i < EVA_NL; i++) {
         const Layer &L = E->L[i];
+        const bool sp = E->flags & EVA_SPARSE24;
         EV_CK(eva_k_ln(E->x, L.ln1w, L.ln1b, E->h8, E->sh, M, lds, st));
-        EV_CK(eva_k_qkv(E->h8, E->sh, lds, L.wqkv, L.sqkv, E->cs, E->q, E->k, E->vt, M, st));
+        if (sp) EV_CK(eva_k_qkv_sp(E->h8, E->sh, lds, L.vqkv, L.xqkv, L.sqkv, E->cs, E->q, E->k, E->vt, M, st));
+        else EV_CK(eva_k_qkv(E->h8, E->sh, lds, L.wqkv, L.sqkv, E->cs, E->q, E->k, E->vt, M, st));
         EV_CK(eva_k_flash(E->q, E->k, E->vt, E->h8, E->sh, lds, nb, NULL, st));
-        EV_CK(eva_k_oproj(E->h8, E->sh, lds, L.wo, L.so, E->x, M, st));
+        if (sp) EV_CK(eva_k_oproj_sp(E->h8, E->sh, lds, L.vo, L.xo, L.so, E->x, M, st));
+        else EV_CK(eva_k_oproj(E->h8, E->sh, lds, L.wo, L.so, E->x, M, st));
         EV_CK(eva_k_ln(E->x, L.ln2w, L.ln2b, E->h8, E->sh, M, lds, st));
-        EV_CK(eva_k_fc1(E->h8, E->sh, lds, L.w12, L.s12, E->m8, E->sm, E->stat, M, st));
-        EV_CK(eva_k_fc2(E->m8, E->sm, lds, L.w2, L.s2, E->stat, L.cn, L.dn, E->x, M, st));
+        if (sp) EV_CK(eva_k_fc1_sp(E->h8, E->sh, lds, L.v12, L.x12, L.s12, E->m8, E->sm, E->stat, M, st));
+        else EV_CK(eva_k_fc1(E->h8, E->sh, lds, L.w12, L.s12, E->m8, E->sm, E->stat, M, st));
+        if (sp) EV_CK(eva_k_fc2_sp(E->m8, E->sm, lds, L.v2, L.x2, L.s2, E->stat, L.cn, L.dn, E->x, M, st));
+        else EV_CK(eva_k_fc2(E->m8, E->sm, lds, L.w2, L.s2, E->stat, L.cn, L.dn, E->x, M, st));
     }
     EV_CK(eva_k_pool(E->x, E->pool, nb, st));
     EV_CK(eva_k_lnh(E->pool, E->fnw, E->fnb, E->pn, E->pq, E->ps, nb, nb, st));
@@ -224,6 +242,19 @@ static int ev_up(eva *e)
         EV_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
         EV_CK(eva_k_prep_w(L.w1216, EVA_D, 2 * V2_HIDP, EVA_D, 2 * EVA_HIDP, EVA_D, 0, NULL, E->scratch, L.w12, L.s12, st));
         EV_CK(eva_k_prep_w(L.w216, V2_HIDP, EVA_D, EVA_HID, EVA_D, EVA_HIDP, 0, L.mlnw, E->scratch, L.w2, L.s2, st));
+        if (E->flags & EVA_SPARSE24) {
+            // 2:4 magnitude pruning of the packed E4M3 weights (prune24.py "mag"); the fold term c below then sums
+            // the pruned W~, which keeps the folded LayerNorm exact for the weights the GEMM uses
+            struct { uint8_t *w; int n, k; uint8_t **v; uint32_t **x; } sw[4] = {
+                {L.wqkv, 3 * EVA_D, EVA_D, &L.vqkv, &L.xqkv}, {L.wo, EVA_D, EVA_D, &L.vo, &L.xo},
+                {L.w12, 2 * EVA_HIDP, EVA_D, &L.v12, &L.x12}, {L.w2, EVA_D, EVA_HIDP, &L.v2, &L.x2}};
+            for (auto &t : sw) {
+                EV_CK(eva_k_prune24(t.w, t.n, t.k, st));
+                EV_ALLOC(E, *t.v, (size_t)t.n * t.k / 2, false);
+                EV_ALLOC(E, *t.x, (size_t)t.n * t.k / 8, false);
+                EV_CK(eva_k_pack24(t.w, t.n, t.k, *t.v, *t.x, NULL, st));
+            }
+        }
         EV_CK(eva_k_fold_cd(L.w2, L.s2, L.w216, V2_HIDP, L.mlnb, L.cn, L.dn, st));
     }
     // head: fp16 master (file rows, then zero extra rows with bias -16), packed per 128-row block
@@ -288,7 +319,8 @@ static void *ev_boot(void *arg)
     return NULL;
 }
 
-extern "C" int eva_open_nb(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra, uint32_t nb)
+extern "C" int eva_open_ex(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra, uint32_t nb,
+                           uint32_t flags)
 {
     uint32_t hdr[4];
     FILE *f;
@@ -309,6 +341,7 @@ extern "C" int eva_open_nb(eva *e, const char *weights, int device, void *pool, 
     E->path = strdup(weights);
     if (!E->path) return xt_fail("eva_open", "out of memory");
     E->devno = device;
+    E->flags = flags;
     E->wbytes = hdr[3];
     E->nb = nb;
     E->M = nb * EVA_T;
@@ -321,6 +354,11 @@ extern "C" int eva_open_nb(eva *e, const char *weights, int device, void *pool, 
     if (pthread_create(&E->boot, NULL, ev_boot, e)) return xt_fail("eva_open", "cannot start the bring-up thread");
     E->booted = 1;
     return 0;
+}
+
+extern "C" int eva_open_nb(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra, uint32_t nb)
+{
+    return eva_open_ex(e, weights, device, pool, poolb, extra, nb, 0);
 }
 
 extern "C" int eva_open(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra)

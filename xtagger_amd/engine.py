@@ -7,6 +7,7 @@ from .lib import lib
 
 EVA_NBUF = 8
 EVA_IN = 1024 * 592
+EVA_SPARSE24 = 1
 
 
 class EvaStruct(C.Structure):
@@ -16,12 +17,14 @@ class EvaStruct(C.Structure):
 
 
 class Engine:
-    """eva_open_nb .. eva_close. Errors raise RuntimeError (the C calls print "eva: ..." to stderr)."""
+    """eva_open_ex .. eva_close. Errors raise RuntimeError (the C calls print "eva: ..." to stderr).
+    sparse: 2:4-prune the layer GEMM weights at bring-up and run them on the sparse matrix cores (EVA_SPARSE24)."""
 
-    def __init__(self, weights, device=0, nb=8, extra=0):
+    def __init__(self, weights, device=0, nb=8, extra=0, sparse=False):
         self.e = EvaStruct()
         self.ref = C.byref(self.e)
-        if lib.eva_open_nb(self.ref, str(weights).encode(), device, None, 0, extra, nb) != 0:
+        flags = EVA_SPARSE24 if sparse else 0
+        if lib.eva_open_ex(self.ref, str(weights).encode(), device, None, 0, extra, nb, flags) != 0:
             raise RuntimeError("eva_open failed")
         self.open = True
 

@@ -37,6 +37,7 @@ _SIGS = {
     "eva_k_fc2_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _p]),
     "eva_open": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32]),
     "eva_open_nb": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32, _u32]),
+    "eva_open_ex": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32, _u32, _u32]),
     "eva_ready": (_i, [_p]),
     "eva_poll": (_i, [_p]),
     "eva_submit": (_i, [_p, _u32, _p, _u32]),
