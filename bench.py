@@ -108,6 +108,35 @@ class LayerStep:
             if f() != 0:
                 raise RuntimeError("layer GEMM launch failed")
 
+    def make_sparse(self):
+        """2:4-prune the four packed weights in place and pack them for the sparse kernels."""
+        L = self.L
+        self.sp = {}
+        for name, w, n, k in (("qkv", self.wqkv, 3 * D, D), ("oproj", self.wo, D, D), ("fc1", self.w12, 2 * HIDP, D),
+                              ("fc2", self.w2, D, HIDP)):
+            L.check(L.lib.eva_k_prune24(L.ptr(w), n, k, self.st), "prune")
+            v = self.torch.empty(n // 16, k // 128, 64, 16, dtype=self.torch.uint8, device=w.device)
+            x = self.torch.empty(n // 16, k // 128, 64, dtype=self.torch.int32, device=w.device)
+            L.check(L.lib.eva_k_pack24(L.ptr(w), n, k, L.ptr(v), L.ptr(x), None, self.st), "pack")
+            self.sp[name] = (v, x)
+        self.torch.cuda.synchronize()
+
+    def step_sp(self):
+        L, sp = self.L, self.sp
+        rcs = (L.lib.eva_k_qkv_sp(L.ptr(self.a8), L.ptr(self.as_), self.lds, L.ptr(sp["qkv"][0]), L.ptr(sp["qkv"][1]),
+                                  L.ptr(self.sqkv), L.ptr(self.cs), L.ptr(self.q), L.ptr(self.k), L.ptr(self.vt), self.M,
+                                  self.st),
+               L.lib.eva_k_oproj_sp(L.ptr(self.a8), L.ptr(self.as_), self.lds, L.ptr(sp["oproj"][0]),
+                                    L.ptr(sp["oproj"][1]), L.ptr(self.so), L.ptr(self.x), self.M, self.st),
+               L.lib.eva_k_fc1_sp(L.ptr(self.a8), L.ptr(self.as_), self.lds, L.ptr(sp["fc1"][0]), L.ptr(sp["fc1"][1]),
+                                  L.ptr(self.s12), L.ptr(self.fc1_out8), L.ptr(self.fc1_ms), L.ptr(self.fc1_stat),
+                                  self.M, self.st),
+               L.lib.eva_k_fc2_sp(L.ptr(self.m8), L.ptr(self.ms), self.lds, L.ptr(sp["fc2"][0]), L.ptr(sp["fc2"][1]),
+                                  L.ptr(self.s2), L.ptr(self.stat), L.ptr(self.cn), L.ptr(self.dn), L.ptr(self.x),
+                                  self.M, self.st))
+        if any(rcs):
+            raise RuntimeError("sparse layer GEMM launch failed")
+
     def kernel_graph(self, name, reps):
         f = getattr(self, name)
 
@@ -182,14 +211,15 @@ def bench_cfg1(torch, L, iters=50):
     return 2.0 * M * N * K / ms / 1e9, ms
 
 
-def bench_forward(torch, nb=32, iters=5):
-    """Full wd forward (24 blocks + head 10861) at batch nb on a synthetic v2 blob: images/s with inputs resident."""
+def bench_forward(torch, nb=32, iters=5, extra=0, sparse=False):
+    """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
+    resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores."""
     from xtagger_amd import blob
     from xtagger_amd.engine import Engine
     path = os.path.join(os.environ.get("TMPDIR", "/tmp"), "xtag_bench_eva02_v2.bin")
     if not os.path.exists(path):
         blob.write_v2(path, blob.synth_model(seed=0, nt=10861))
-    e = Engine(path, device=0, nb=nb)
+    e = Engine(path, device=0, nb=nb, extra=extra, sparse=sparse)
     e.ready()
     inp = blob.synth_inputs(nb, seed=7)
     e.submit(0, inp)                       # inputs land in the device buffer; later replays reuse them
@@ -351,10 +381,25 @@ def main():
            "cfg1_qkv_gemm_m1025": {"tflops": round(cfg1, 1), "us": round(cfg1_ms * 1e3, 2)},
            "roofline": roof, "measured_peaks": peaks,
            "pct_measured_fp8_peak": round(100 * tflops / peaks["fp8_mfma_tflops"], 2)}
+    # 2:4-sparse weights (config 5): the same step on pruned weights, dense-equivalent FLOPs
+    st.make_sparse()
+    gsp = capture(torch, st.step_sp, 1)
+    time_graph(torch, gsp, args.warmup)
+    sp_ms = time_graph(torch, gsp, args.steps)
+    out["sparse24_step"] = {"tflops_dense_equivalent": round(step_flops / (sp_ms * 1e-3) / 1e12, 1),
+                            "ms_per_step": round(sp_ms, 4)}
     if not args.no_forward:
         ips, fms = bench_forward(torch)
         out["forward_b32"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
                               "tflops": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1)}
+        ips, fms = bench_forward(torch, sparse=True)
+        out["forward_b32_sparse24"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
+                                       "tflops_dense_equivalent": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1)}
+        # config 4: 64 sequences of 1025 tokens (16 images x (1 full view + crops)) and a 13461-row head
+        ips, fms = bench_forward(torch, nb=64, extra=13461 - 10861)
+        out["forward_ragged64_head13461"] = {"sequences_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
+                                             "tflops": round((64 * 723.5e9 + 2 * 64 * 13461 * 1024)
+                                                             / (fms * 1e-3) / 1e12, 1)}
     if not args.no_cpu:
         from oracle import oracle as O
         cpu_tf, thr, secs, reps = cpu_baseline(O)
