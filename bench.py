@@ -300,8 +300,8 @@ def traffic_from_profiles():
 
 
 def profile_kernels(torch, L, M, launches=5, copy_bytes=1 << 30):
-    """Dispatches for hardware-counter passes: each layer kernel `launches` times at M rows, then `launches` stream
-    copies of copy_bytes (copy_bytes read + copy_bytes written per dispatch), the calibration of the byte counters."""
+    """Dispatches for hardware-counter passes: each layer kernel `launches` times at M rows, the four 2:4-sparse
+    layer kernels `launches` times each (on the pruned weights), then `launches` stream copies of copy_bytes (copy_bytes read + copy_bytes written per dispatch), the calibration of the byte counters."""
     st = LayerStep(torch, L, M)
     for name in ("qkv", "oproj", "fc1", "fc2"):
         f = getattr(st, name)
@@ -309,6 +309,10 @@ def profile_kernels(torch, L, M, launches=5, copy_bytes=1 << 30):
             if f() != 0:
                 raise RuntimeError(name)
         torch.cuda.synchronize()
+    st.make_sparse()
+    for _ in range(launches):
+        st.step_sp()
+    torch.cuda.synchronize()
     dev = torch.device("cuda:0")
     a = torch.ones(copy_bytes, dtype=torch.uint8, device=dev)
     b = torch.empty(copy_bytes, dtype=torch.uint8, device=dev)
