@@ -180,6 +180,14 @@ struct BsOperands {
         for (int i = 0; i < C::LB; i++) dma16(rw, stage + m0_b + 1024u * i, w_off[i], koff);
         dma4(rs, stage + m0_s, s_off, (uint32_t)kb * s_step);
     }
+    // load q (0 .. LPS - 1) of K step kb: the same loads as issue(), one at a time
+    __device__ __forceinline__ void issue_one(int q, uint32_t stage, int kb) const
+    {
+        const uint32_t koff = (uint32_t)kb * 128u;
+        if (q < C::LA) dma16(ra, stage + m0_a + 1024u * q, a_off[q], koff);
+        else if (q < C::LA + C::LB) dma16(rw, stage + m0_b + 1024u * (q - C::LA), w_off[q - C::LA], koff);
+        else dma4(rs, stage + m0_s, s_off, (uint32_t)kb * s_step);
+    }
 };
 
 template <class C>
@@ -233,6 +241,74 @@ __device__ __forceinline__ void bs_step(const uint8_t *st, int wm0, int wn0, v4f
     }
 }
 
+// The same K step for 64 x 128 wave tiles (TM = 4, TN = 8) in a fixed issue order. The matrix-core instructions and
+// the promotion fmas are single-instruction asm statements, and every LDS read sits between them, so the compiler
+// keeps the written order (it still allocates registers and places the LDS waits):
+//  - scales, A fragments and B fragments 0 and 1 are read first; the first MFMA waits only for A 0 and B 0;
+//  - B fragment j + 2 is read right after MFMA (j, 0), into the slot B fragment j - 1 has left (3-slot ring);
+//  - the promotion of MFMA t - 3 follows MFMA t. In steady state 15 instructions separate an MFMA from the first
+//    VALU read of its result (an 8-pass XDL result needs 11); the first promotion of a step is preceded by s_nop 7;
+//  - the LPS loads of K step dkb (dkb < 0: none) go out one per MFMA from MFMA 1 on, not in a burst that would stall
+//    this wave's issue behind the vector-memory queue.
+__device__ __forceinline__ void mfma_asm(v4f &p, const v8i &a, const v8i &b)
+{
+    asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %1, %2, 0" : "=&v"(p) : "v"(a), "v"(b) : "memory");
+}
+__device__ __forceinline__ void fmac_asm(float &acc, float p, float s)
+{
+    asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(acc) : "v"(p), "v"(s) : "memory");
+}
+
+template <class C>
+__device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn0, v4f (&acc)[C::TM][C::TN],
+                                              const BsOperands<C> &op, uint32_t dstage, int dkb)
+{
+    static_assert(C::TM == 4 && C::TN == 8 && C::LPS < 32, "schedule written for 64 x 128 wave tiles");
+    constexpr int LAG = 3;
+    const int lane = threadIdx.x & 63, g = lane >> 4;
+    const uint8_t *ta = st, *tb = st + C::A_BYTES;
+    const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
+    const float swv = *(const float *)(st + C::A_BYTES + C::B_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
+    float4 s4[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) s4[i] = *(const float4 *)(ts + wm0 + 16 * i + 4 * g);
+    v8i a[4], b[3];
+    b[0] = ld_frag(tb, wn0);
+    a[0] = ld_frag(ta, wm0);
+    asm volatile("" ::: "memory");
+    a[1] = ld_frag(ta, wm0 + 16);
+    a[2] = ld_frag(ta, wm0 + 32);
+    a[3] = ld_frag(ta, wm0 + 48);
+    b[1] = ld_frag(tb, wn0 + 16);
+    asm volatile("" ::: "memory");
+    float sc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        sc[i][0] = s4[i].x * swv; sc[i][1] = s4[i].y * swv; sc[i][2] = s4[i].z * swv; sc[i][3] = s4[i].w * swv;
+    }
+    v4f pr[LAG + 1];
+#pragma unroll
+    for (int t = 0; t < 32 + LAG; t++) {
+        if (t < 32) {
+            const int j = t >> 2, i = t & 3;
+            mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
+            if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
+            if (t >= 1 && t <= C::LPS && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
+        }
+        if (t == LAG) asm volatile("s_nop 7" ::: "memory");
+        if (t >= LAG) {
+            const int u = t - LAG, j = u >> 2, i = u & 3;
+            const v4f p = pr[u % (LAG + 1)];
+            float x0 = acc[i][j][0], x1 = acc[i][j][1], x2 = acc[i][j][2], x3 = acc[i][j][3];
+            fmac_asm(x0, p[0], sc[i][0]);
+            fmac_asm(x1, p[1], sc[i][1]);
+            fmac_asm(x2, p[2], sc[i][2]);
+            fmac_asm(x3, p[3], sc[i][3]);
+            acc[i][j] = v4f{x0, x1, x2, x3};
+        }
+    }
+}
+
 struct BsNoPre {
     __device__ __forceinline__ void operator()() const {}
 };
@@ -270,8 +346,13 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
         if (kb + C::NS - 2 < KB) wait_vmem_n<(C::NS - 2) * C::LPS>();
         else wait_vmem();
         lds_barrier();  // every wave's part of stage kb landed; every wave finished reading stage kb - 1
-        if (kb + C::NS - 1 < KB) op.issue(base + is * C::STAGE, kb + C::NS - 1);
-        bs_step<C>(smem + cs * C::STAGE, wm0, wn0, acc);
+        if constexpr (C::TM == 4 && C::TN == 8) {
+            bs_step_fixed<C>(smem + cs * C::STAGE, wm0, wn0, acc, op, base + is * C::STAGE,
+                             kb + C::NS - 1 < KB ? kb + C::NS - 1 : -1);
+        } else {
+            if (kb + C::NS - 1 < KB) op.issue(base + is * C::STAGE, kb + C::NS - 1);
+            bs_step<C>(smem + cs * C::STAGE, wm0, wn0, acc);
+        }
         cs = cs == C::NS - 1 ? 0 : cs + 1;
         is = is == C::NS - 1 ? 0 : is + 1;
     }

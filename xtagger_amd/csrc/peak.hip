@@ -4,6 +4,7 @@
 // so every fraction reported beside a benchmark uses a peak measured on the same GPU.
 #include "xt_abi.h"
 #include "xt_common.h"
+#include "gemm_core.h"
 
 // Each wave keeps 8 independent accumulator chains so back-to-back MFMAs never wait on each other.
 __global__ void __launch_bounds__(256) k_peak_mfma(int iters, float *__restrict__ out)
@@ -31,24 +32,24 @@ __global__ void __launch_bounds__(256) k_peak_copy(const uint4 *__restrict__ src
     for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n16; i += (long)gridDim.x * 256) dst[i] = src[i];
 }
 
-// 256 threads read 16 bytes each per step from a 64 KB LDS array, conflict-free (consecutive lanes, consecutive
-// 16-byte chunks), and fold the data so the reads stay live.
+// 256 threads issue 16 ds_read_b128 per iteration (lane-linear 1 KB rows, conflict-free) from inline assembly, so no
+// ALU work consumes the data and the loop is bound by the LDS read path alone.
 __global__ void __launch_bounds__(256) k_peak_lds(int iters, uint32_t *__restrict__ out)
 {
     __shared__ __attribute__((aligned(16))) uint4 buf[4096];
     for (int i = threadIdx.x; i < 4096; i += 256) buf[i] = make_uint4(i, i * 3, i * 5, i * 7);
     __syncthreads();
-    uint4 acc = make_uint4(0, 0, 0, 0);
-    int idx = threadIdx.x;
+    const uint32_t a = lds_addr(buf) + (uint32_t)((threadIdx.x >> 6) * 4096 + (threadIdx.x & 63) * 16);  // + 15 KB < 64 KB
+    v4i v0, v1;
     for (int it = 0; it < iters; it++) {
-#pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const uint4 v = buf[(idx + u * 256) & 4095];
-            acc.x ^= v.x; acc.y += v.y; acc.z ^= v.z; acc.w += v.w;
-        }
-        idx += 37;
+#define XT_RD2(o0, o1) asm volatile("ds_read_b128 %0, %2 offset:" #o0 "\n\tds_read_b128 %1, %2 offset:" #o1 \
+                                    : "=v"(v0), "=v"(v1) : "v"(a));
+        XT_RD2(0, 1024) XT_RD2(2048, 3072) XT_RD2(4096, 5120) XT_RD2(6144, 7168)
+        XT_RD2(8192, 9216) XT_RD2(10240, 11264) XT_RD2(12288, 13312) XT_RD2(14336, 15360)
+#undef XT_RD2
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    out[blockIdx.x * 256 + threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    out[blockIdx.x * 256 + threadIdx.x] = (uint32_t)(v0[0] ^ v1[3]);
 }
 
 extern "C" int eva_probe_mfma_fp8(int blocks, int iters, float *out, void *stream)
