@@ -223,7 +223,8 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
 // m8 [rows][2816] E4M3 with 1x128 scales ms [22][lds], and per-(row, block) (sum h, sum h^2) of the unpacked h in
 // stat [22][lds][2] for the folded MLP LayerNorm (eva_kernels.cu:211-279). W12 rows hold g and x of 16 units in
 // alternate 16-row chunks (export_eva.py:60-62), so column tile 2c is g and 2c+1 is x of the same 16 units: a
-// 256-column block is one 128-unit block of h, whose |max| and sums meet through LDS across the 2 column waves.
+// 256-column block is one 128-unit block of h; its rows are staged in LDS, where 8 threads per row take the |max|
+// and the sums.
 // Each (row, block) partial has one writer: no atomics, deterministic.
 // ---------------------------------------------------------------------------------------------------------------
 template <bool SP>
@@ -243,71 +244,59 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-    const int wm = wm0 / C::WM, wn = wn0 / C::WN, ct = n0 >> 8;
-    // h tile [BM rows][128 units] fp32, 16-byte chunk c of row r at chunk c ^ (r & 7); then the statistics
+    const int wn = wn0 / C::WN, ct = n0 >> 8;
+    // h tile [BM rows][128 units] fp32 in LDS, 16-byte chunk c of row r at chunk c ^ (r & 7)
     float *ht = (float *)smem;
-    float *red = ht + C::BM * 128;                       // [3][NWM][NWN][64 rows]: amax, sum, sum of squares
-    float *rinv = red + 3 * C::NWM * C::NWN * 64;        // [BM rows] 1 / block scale
-    static_assert((C::BM * 128 + 3 * C::NWM * C::NWN * 64 + C::BM) * 4 <= LAYER_SMEM, "fc1 staging fits");
+    static_assert(C::BM * 128 * 4 <= LAYER_SMEM, "fc1 staging fits");
     auto hix = [](int row, int unit) { return row * 128 + ((((unit >> 2) ^ row) & 7) | ((unit >> 2) & ~7)) * 4 + (unit & 3); };
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int rr = 16 * i + 4 * g + r;
-            float amax = 0.f, s = 0.f, q = 0.f;
 #pragma unroll
             for (int p = 0; p < NP; p++) {
                 const float gg = acc[i][2 * p][r], xx = acc[i][2 * p + 1][r];
                 const float e = __expf(-gg), den = 1.0f + e;
                 const float v = (gg * __builtin_amdgcn_rcpf(den)) * xx;  // silu(g) x, hardware reciprocal (1 ulp)
                 ht[hix(wm0 + rr, 16 * NP * wn + 16 * p + c16)] = v;
-                amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
-                s += v;
-                q = __builtin_fmaf(v, v, q);
-            }
-            amax = row16_max(amax);
-            s = row16_sum(s);
-            q = row16_sum(q);
-            if (c16 == 0) {
-                red[((0 * C::NWM + wm) * C::NWN + wn) * 64 + rr] = amax;
-                red[((1 * C::NWM + wm) * C::NWN + wn) * 64 + rr] = s;
-                red[((2 * C::NWM + wm) * C::NWN + wn) * 64 + rr] = q;
             }
         }
     __syncthreads();
-    // one thread per block row: the block scale (IEEE divisions, once per row) and the row sums (column waves in order)
-    if (threadIdx.x < C::BM) {
-        const int rr = threadIdx.x, m = m0 + rr, wmr = rr >> 6, r64 = rr & 63;
-        float amax = 0.f, s = 0.f, q = 0.f;
-#pragma unroll
-        for (int u = 0; u < C::NWN; u++) {
-            amax = __builtin_fmaxf(amax, red[((0 * C::NWM + wmr) * C::NWN + u) * 64 + r64]);
-            s += red[((1 * C::NWM + wmr) * C::NWN + u) * 64 + r64];
-            q += red[((2 * C::NWM + wmr) * C::NWN + u) * 64 + r64];
-        }
-        const float sc = block_scale(amax);
-        rinv[rr] = 1.0f / sc;
-        if (m < rows) {
-            ms[(size_t)ct * lds + m] = sc;
-            *(float2 *)(stat + ((size_t)ct * lds + m) * 2) = make_float2(s, q);
-        }
-    }
-    __syncthreads();
-    // 16 consecutive units of one row per item: 64 bytes of h -> 16 E4M3 bytes, one 16-byte store
+    // 8 consecutive threads per row, 16 consecutive units each: the row's |max| and sums over its 128 units meet in
+    // a DPP tree over the 8 lanes; each thread packs its 16 units to E4M3 (one 16-byte store) and the first thread
+    // of the row writes the block scale (IEEE division) and the partial sums
     const __amdgpu_buffer_rsrc_t rm = buf_rsrc(m8, (uint32_t)rows * XT_HIDP);
 #pragma unroll
     for (int it = 0; it < C::BM * 8 / C::NT; it++) {
-        const int idx = threadIdx.x + it * C::NT, rr = idx >> 3, u0 = (idx & 7) * 16;
-        const float inv = rinv[rr];
-        uint32_t w[4];
+        const int idx = threadIdx.x + it * C::NT, rr = idx >> 3, u0 = (idx & 7) * 16, m = m0 + rr;
+        float4 v[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = *(const float4 *)(ht + hix(rr, u0 + 4 * c));
+        float amax = 0.f, s = 0.f, q = 0.f;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const float4 v = *(const float4 *)(ht + hix(rr, u0 + 4 * c));
-            w[c] = e4_pack4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+            amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v[c].x), __builtin_fabsf(v[c].y)),
+                                                         __builtin_fmaxf(__builtin_fabsf(v[c].z), __builtin_fabsf(v[c].w))));
+            s += (v[c].x + v[c].y) + (v[c].z + v[c].w);
+            q = __builtin_fmaf(v[c].x, v[c].x, q);
+            q = __builtin_fmaf(v[c].y, v[c].y, q);
+            q = __builtin_fmaf(v[c].z, v[c].z, q);
+            q = __builtin_fmaf(v[c].w, v[c].w, q);
         }
-        const v4u o = {w[0], w[1], w[2], w[3]};
-        __builtin_amdgcn_raw_buffer_store_b128(o, rm, (int)((uint32_t)(m0 + rr) * XT_HIDP + ct * 128 + u0), 0, 0);
+        amax = row8_max(amax);
+        s = row8_sum(s);
+        q = row8_sum(q);
+        const float sc = block_scale(amax), inv = 1.0f / sc;
+        uint32_t w4[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) w4[c] = e4_pack4(v[c].x * inv, v[c].y * inv, v[c].z * inv, v[c].w * inv);
+        const v4u o = {w4[0], w4[1], w4[2], w4[3]};
+        __builtin_amdgcn_raw_buffer_store_b128(o, rm, (int)((uint32_t)m * XT_HIDP + ct * 128 + u0), 0, 0);
+        if ((idx & 7) == 0 && m < rows) {
+            ms[(size_t)ct * lds + m] = sc;
+            *(float2 *)(stat + ((size_t)ct * lds + m) * 2) = make_float2(s, q);
+        }
     }
 }
 

@@ -104,6 +104,21 @@ __device__ __forceinline__ float row16_sum(float v)
     v += dpp_f<0x140>(v);  // row_mirror
     return v;
 }
+// the same over aligned groups of 8 lanes (the first three steps)
+__device__ __forceinline__ float row8_sum(float v)
+{
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    return v;
+}
+__device__ __forceinline__ float row8_max(float v)
+{
+    v = __builtin_fmaxf(v, dpp_f<0xB1>(v));
+    v = __builtin_fmaxf(v, dpp_f<0x4E>(v));
+    v = __builtin_fmaxf(v, dpp_f<0x141>(v));
+    return v;
+}
 __device__ __forceinline__ float row16_max(float v)
 {
     v = __builtin_fmaxf(v, dpp_f<0xB1>(v));
