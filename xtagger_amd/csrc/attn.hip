@@ -89,10 +89,15 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
         if (kt + 1 < FA_NKT) issue(smem + ((kt + 1) & 1) * FA_STAGE, kt + 1);
         if (active) {
             const uint8_t *tk = st + hsel * FA_TILE, *tv = st + (2 + hsel) * FA_TILE;
+            // the scores start from -mb (mb = the running max, 0 before the first tile): after the first tile they
+            // come out of the matrix core already relative to the running max, and the common no-rescale path
+            // feeds them to exp2 as they are
+            const float mb = kt == 0 ? 0.f : mrun;
             v16f s[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                s[u] = v16f{};
+#pragma unroll
+                for (int e = 0; e < 16; e++) s[u][e] = -mb;
 #pragma unroll
                 for (int step = 0; step < 4; step++)
                     s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tk, 32 * u + jrow, 2 * step + g), qf[step],
@@ -108,28 +113,33 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
                         if (key >= XT_T) s[u][e] = -INFINITY;
                     }
             }
-            float tmax = -INFINITY;
+            float tmax = -INFINITY;  // relative to mb
 #pragma unroll
             for (int u = 0; u < 2; u++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) tmax = __builtin_fmaxf(tmax, s[u][e]);
             tmax = __builtin_fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-            if (__builtin_amdgcn_ballot_w64(tmax > mrun + FA_RESCALE) != 0) {  // wave-uniform lazy rescale
-                const float mnew = __builtin_fmaxf(mrun, tmax);
-                const float sc = __builtin_amdgcn_exp2f(mrun - mnew);
+            const float mref = mrun - mb;  // the running max relative to mb: -inf on the first tile, 0 after it
+            if (__builtin_amdgcn_ballot_w64(tmax > mref + FA_RESCALE) != 0) {  // wave-uniform lazy rescale
+                const float mnew = __builtin_fmaxf(mref, tmax);
+                const float sc = __builtin_amdgcn_exp2f(mref - mnew);
                 lsum *= sc;
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     o[0][e] *= sc;
                     o[1][e] *= sc;
                 }
-                mrun = mnew;
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) s[u][e] -= mnew;
+                mrun = mb + mnew;
             }
 #pragma unroll
             for (int u = 0; u < 2; u++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
-                    const float p = __builtin_amdgcn_exp2f(s[u][e] - mrun);
+                    const float p = __builtin_amdgcn_exp2f(s[u][e]);
                     s[u][e] = p;
                     lsum += p;
                 }
