@@ -244,7 +244,7 @@ __device__ __forceinline__ void bs_step(const uint8_t *st, int wm0, int wn0, v4f
 // The same K step for 64 x 128 wave tiles (TM = 4, TN = 8) in a fixed issue order. The matrix-core instructions and
 // the promotion fmas are single-instruction asm statements, and every LDS read sits between them, so the compiler
 // keeps the written order (it still allocates registers and places the LDS waits):
-//  - scales, A fragments and B fragments 0 and 1 are read first; the first MFMA waits only for A 0 and B 0;
+//  - A 0 and B 0 are read first, then the scales, then A 1-3 and B 1: the first MFMA waits for four reads only;
 //  - B fragment j + 2 is read right after MFMA (j, 0), into the slot B fragment j - 1 has left (3-slot ring);
 //  - the promotion of MFMA t - 3 follows MFMA t. In steady state 15 instructions separate an MFMA from the first
 //    VALU read of its result (an 8-pass XDL result needs 11); the first promotion of a step is preceded by s_nop 7;
@@ -268,13 +268,14 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
     const int lane = threadIdx.x & 63, g = lane >> 4;
     const uint8_t *ta = st, *tb = st + C::A_BYTES;
     const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
+    v8i a[4], b[3];
+    b[0] = ld_frag(tb, wn0);
+    a[0] = ld_frag(ta, wm0);
+    asm volatile("" ::: "memory");  // the first MFMA waits for these four reads only
     const float swv = *(const float *)(st + C::A_BYTES + C::B_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
     float4 s4[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) s4[i] = *(const float4 *)(ts + wm0 + 16 * i + 4 * g);
-    v8i a[4], b[3];
-    b[0] = ld_frag(tb, wn0);
-    a[0] = ld_frag(ta, wm0);
     asm volatile("" ::: "memory");
     a[1] = ld_frag(ta, wm0 + 16);
     a[2] = ld_frag(ta, wm0 + 32);
