@@ -211,6 +211,24 @@ def bench_cfg1(torch, L, iters=50):
     return 2.0 * M * N * K / ms / 1e9, ms
 
 
+def bench_ln(torch, L, M=32 * T):
+    """k_ln (LayerNorm + E4M3 1x128 pack) at M rows: bytes = M x 1024 x (2 read + 1 write) + 8 scales per row x 4."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(M, D, generator=g, device=dev).half()
+    ga = torch.randn(D, generator=g, device=dev) * 0.1 + 1.0
+    be = torch.randn(D, generator=g, device=dev) * 0.1
+    q = torch.empty(M, D, dtype=torch.uint8, device=dev)
+    sc = torch.empty(8, M, dtype=torch.float32, device=dev)
+    fn = lambda: L.check(L.lib.eva_k_ln(L.ptr(x), L.ptr(ga), L.ptr(be), L.ptr(q), L.ptr(sc), M, M,
+                                        torch.cuda.current_stream().cuda_stream), "eva_k_ln")
+    gr = capture(torch, fn, 20)
+    time_graph(torch, gr, 3)
+    us = time_graph(torch, gr, 10) * 1e3 / 20
+    nbytes = M * D * 3 + M * 8 * 4
+    return us, nbytes / (us * 1e-6) / 1e9
+
+
 def bench_forward(torch, nb=32, iters=5, extra=0, sparse=False):
     """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
     resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores."""
@@ -392,6 +410,9 @@ def main():
     sp_ms = time_graph(torch, gsp, args.steps)
     out["sparse24_step"] = {"tflops_dense_equivalent": round(step_flops / (sp_ms * 1e-3) / 1e12, 1),
                             "ms_per_step": round(sp_ms, 4)}
+    ln_us, ln_gbs = bench_ln(torch, L)
+    out["ln_m32800"] = {"us": round(ln_us, 2), "gbs": round(ln_gbs, 1), "frac_hbm_peak": round(ln_gbs / 8000.0, 3),
+                        "bytes": 32 * T * D * 3 + 32 * T * 8 * 4}
     if not args.no_forward:
         ips, fms = bench_forward(torch)
         out["forward_b32"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
