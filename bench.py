@@ -211,6 +211,28 @@ def bench_cfg1(torch, L, iters=50):
     return 2.0 * M * N * K / ms / 1e9, ms
 
 
+def bench_vendor(torch, M=8 * T):
+    """The same GEMM shapes through hipBLASLt (torch._scaled_mm): FP8 E4M3 with one per-tensor scale per operand, bf16
+    out, no block scales and no fused epilogues. A vendor reference point on the same GPU, not the metric."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    one = torch.tensor(1.0, device=dev)
+    res = {}
+    for name, m, n, k in (("qkv", M, 3 * D, D), ("oproj", M, D, D), ("fc1", M, 2 * HIDP, D), ("fc2", M, D, HIDP),
+                          ("cfg1_qkv_m1025", T, 3 * D, D)):
+        a = torch.randn(m, k, generator=g, device=dev).to(torch.float8_e4m3fn)
+        b = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.float8_e4m3fn)
+        fn = lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+        gr = capture(torch, fn, 20)
+        time_graph(torch, gr, 3)
+        res[name] = {"us": round(time_graph(torch, gr, 10) * 1e3 / 20, 2)}
+    step_us = sum(res[k]["us"] for k in ("qkv", "oproj", "fc1", "fc2"))
+    step_flops = 2.0 * M * D * (3 * D + D + 2 * HID + HID)  # unpadded, as the metric
+    res["step_tflops"] = round(step_flops / (step_us * 1e-6) / 1e12, 1)
+    res["step_us"] = round(step_us, 2)
+    return res
+
+
 def bench_ln(torch, L, M=32 * T):
     """k_ln (LayerNorm + E4M3 1x128 pack) at M rows: bytes = M x 1024 x (2 read + 1 write) + 8 scales per row x 4."""
     dev = torch.device("cuda:0")
@@ -410,6 +432,10 @@ def main():
     sp_ms = time_graph(torch, gsp, args.steps)
     out["sparse24_step"] = {"tflops_dense_equivalent": round(step_flops / (sp_ms * 1e-3) / 1e12, 1),
                             "ms_per_step": round(sp_ms, 4)}
+    try:
+        out["hipblaslt_fp8_per_tensor"] = bench_vendor(torch)
+    except Exception as ex:  # the vendor path is only a reference point
+        out["hipblaslt_fp8_per_tensor"] = {"error": str(ex)[:200]}
     ln_us, ln_gbs = bench_ln(torch, L)
     out["ln_m32800"] = {"us": round(ln_us, 2), "gbs": round(ln_gbs, 1), "frac_hbm_peak": round(ln_gbs / 8000.0, 3),
                         "bytes": 32 * T * D * 3 + 32 * T * 8 * 4}
