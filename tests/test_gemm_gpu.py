@@ -123,7 +123,9 @@ def _check_gemm(c, ref):
 
 
 @pytest.mark.parametrize("M,N,K", [(1025, 3072, 1024), (1, 128, 128), (17, 384, 256), (255, 1024, 2816),
-                                   (129, 10861, 1024)])
+                                   (129, 10861, 1024),
+                                   # 256 x 256 tiles (>= 256 tiles): one, three and an odd number of K blocks, ragged M
+                                   (4100, 4096, 128), (4096, 4096, 384), (4000, 4224, 640)])
 def test_gemm_parity(dev, xt, orc, M, N, K):
     _say(f"gemm M={M} N={N} K={K}")
     x, w = _packed(M, N, K, seed=M * 7 + N)
