@@ -245,39 +245,55 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int wn = wn0 / C::WN, ct = n0 >> 8;
-    // h tile [BM rows][128 units] fp32 in LDS, 16-byte chunk c of row r at chunk c ^ (r & 7)
+    // h tile [BM rows][128 units] fp32 in LDS, 16-byte chunk c of row r at chunk c ^ (r & 7). Every address is a
+    // per-lane base plus an immediate: rows wm0 + 16 i + 4 g + r have row & 7 = (4 g + r) & 7, and unit
+    // 64 wn + 16 p + (lane & 15) sits in chunk 16 wn + 8 (p >> 1) + (4 (p & 1) + (lane & 15) / 4), whose low three
+    // bits depend on p & 1 only; so element (i, r, p) is at wb[r][p & 1] + 2048 i + 32 (p >> 1) words.
     float *ht = (float *)smem;
     static_assert(C::BM * 128 * 4 <= LAYER_SMEM, "fc1 staging fits");
-    auto hix = [](int row, int unit) { return row * 128 + ((((unit >> 2) ^ row) & 7) | ((unit >> 2) & ~7)) * 4 + (unit & 3); };
+    static_assert(NP == 4, "two chunk pairs per 64-unit half");
+    const int cq = c16 >> 2;
+    uint32_t wb[4][2];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int ph = 0; ph < 2; ph++) {
+            const int rr = wm0 + 4 * g + r, lo = (4 * ph + cq) ^ ((4 * g + r) & 7);
+            wb[r][ph] = (uint32_t)(rr * 128 + (16 * wn + lo) * 4 + (c16 & 3));
+        }
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int rr = 16 * i + 4 * g + r;
 #pragma unroll
             for (int p = 0; p < NP; p++) {
                 const float gg = acc[i][2 * p][r], xx = acc[i][2 * p + 1][r];
                 const float e = __expf(-gg), den = 1.0f + e;
                 const float v = (gg * __builtin_amdgcn_rcpf(den)) * xx;  // silu(g) x, hardware reciprocal (1 ulp)
-                ht[hix(wm0 + rr, 16 * NP * wn + 16 * p + c16)] = v;
+                ht[wb[r][p & 1] + 2048 * i + 32 * (p >> 1)] = v;
             }
         }
     __syncthreads();
     // 8 consecutive threads per row, 16 consecutive units each: the row's |max| and sums over its 128 units meet in
     // a DPP tree over the 8 lanes; each thread packs its 16 units to E4M3 (one 16-byte store) and the first thread
-    // of the row writes the block scale (IEEE division) and the partial sums
+    // of the row writes the block scale (IEEE division) and the partial sums. Item it of a thread reads row
+    // (tid >> 3) + 64 it, whose row & 7 does not depend on it: the four chunk addresses are bases plus 8192 it words.
     const __amdgpu_buffer_rsrc_t rm = buf_rsrc(m8, (uint32_t)rows * XT_HIDP);
+    const int k8 = threadIdx.x & 7, r0 = threadIdx.x >> 3;
+    uint32_t rb[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) rb[c] = (uint32_t)(r0 * 128 + (((4 * k8 + c) ^ r0) & 7 | ((4 * k8 + c) & ~7)) * 4);
 #pragma unroll
     for (int it = 0; it < C::BM * 8 / C::NT; it++) {
         const int idx = threadIdx.x + it * C::NT, rr = idx >> 3, u0 = (idx & 7) * 16, m = m0 + rr;
         float4 v[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = *(const float4 *)(ht + hix(rr, u0 + 4 * c));
+        for (int c = 0; c < 4; c++) v[c] = *(const float4 *)(ht + rb[c] + 128 * (C::NT / 8) * it);
         float amax = 0.f, s = 0.f, q = 0.f;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v[c].x), __builtin_fabsf(v[c].y)),
-                                                         __builtin_fmaxf(__builtin_fabsf(v[c].z), __builtin_fabsf(v[c].w))));
+            amax = __builtin_fmaxf(__builtin_fmaxf(amax, __builtin_fabsf(v[c].x)), __builtin_fabsf(v[c].y));  // v_max3
+            amax = __builtin_fmaxf(__builtin_fmaxf(amax, __builtin_fabsf(v[c].z)), __builtin_fabsf(v[c].w));
             s += (v[c].x + v[c].y) + (v[c].z + v[c].w);
             q = __builtin_fmaf(v[c].x, v[c].x, q);
             q = __builtin_fmaf(v[c].y, v[c].y, q);
@@ -290,7 +306,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
         const float sc = block_scale(amax), inv = 1.0f / sc;
         uint32_t w4[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) w4[c] = e4_pack4(v[c].x * inv, v[c].y * inv, v[c].z * inv, v[c].w * inv);
+        for (int c = 0; c < 4; c++) w4[c] = e4_pack4_scaled(v[c].x * inv, v[c].y * inv, v[c].z * inv, v[c].w * inv);
         const v4u o = {w4[0], w4[1], w4[2], w4[3]};
         __builtin_amdgcn_raw_buffer_store_b128(o, rm, (int)((uint32_t)m * XT_HIDP + ct * 128 + u0), 0, 0);
         if ((idx & 7) == 0 && m < rows) {

@@ -41,6 +41,15 @@ __device__ __forceinline__ uint32_t e4_pack4(float a, float b, float c, float d)
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(e4_clamp(c), e4_clamp(d), w, true);
 }
 
+// e4_pack4 without the clamp, for values already scaled by 1 / block_scale(|max| of their block): |x| <= |max| / (|max|
+// / 448) <= 448 (1 + 2^-22), which rounds to 448 (the next code up, 480, is past the format and the midpoint is 464),
+// so the clamp cannot change a code.
+__device__ __forceinline__ uint32_t e4_pack4_scaled(float a, float b, float c, float d)
+{
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+}
+
 // Block scale from a block |max|: amax / 448 (IEEE division), 1 for a zero block (|max| < 2^-116).
 __device__ __forceinline__ float block_scale(float amax) { return amax < 0x1p-116f ? 1.0f : amax / XT_E4MAX; }
 
