@@ -23,6 +23,14 @@ lib = C.CDLL(SO)
 
 _p, _i, _u32, _f, _u8, _u16 = C.c_void_p, C.c_int, C.c_uint32, C.c_float, C.c_uint8, C.c_uint16
 _SIGS = {
+    "xo_img_over_white": (None, [_p, C.c_size_t, _p, C.c_size_t, _u32, _u32]),
+    "xo_img_half": (None, [_p, C.c_size_t, _p, C.c_size_t, _u32, _u32]),
+    "xo_img_levels": (_u32, [_u32, _u32, _u32, _p, _p]),
+    "xo_img_level": (_u32, [_u32, _u32, _u32]),
+    "xo_img_lsrc": (None, [_u32, _p, _p, _p, _p, _p, _p]),
+    "xo_img_mt": (_u32, [_u32, _u32]),
+    "xo_img_axis": (None, [_u32, _u32, _u32, _u32, _u32, _f, _f, _p, _p, _p, _p]),
+    "xo_img_prep": (None, [_p, C.c_size_t, _u32, _u32, _u32, _p]),
     "xo_e4m3_encode": (_u8, [_f]),
     "xo_e4m3_decode": (_f, [_u8]),
     "xo_e4m3_encode_bits": (None, [_u32, _u32, _p, _i]),
@@ -341,3 +349,53 @@ def forward(m, inp16, nl=24, threads=0, sparse=False):
     pn = np.empty((nb, 1024), np.uint16)
     lib.xo_forward(C.byref(md), _ptr(x), nb, nl, _ptr(out), _ptr(pn), threads)
     return out, pn
+
+
+# ---- patch-operand producer (src/core/procimg.h; xt_img.c) ----
+def img_over_white(rgba):
+    """RGBA uint8 [h][w][4] -> RGBX over white (pi_row_rgbx with alpha)."""
+    rgba = np.ascontiguousarray(rgba, np.uint8)
+    h, w = rgba.shape[:2]
+    out = np.empty_like(rgba)
+    lib.xo_img_over_white(_ptr(out), w * 4, _ptr(rgba), w * 4, w, h)
+    return out
+
+
+def img_pyramid(rgbx, S=448):
+    """Levels 0.. of pi_pyramid: a list of RGBX uint8 [lh][lw][4] arrays (level 0 is the input)."""
+    rgbx = np.ascontiguousarray(rgbx, np.uint8)
+    h, w = rgbx.shape[:2]
+    lw, lh = np.zeros(12, np.uint32), np.zeros(12, np.uint32)
+    n = lib.xo_img_levels(w, h, S, _ptr(lw), _ptr(lh))
+    lv = [rgbx]
+    for L in range(1, n):
+        d = np.empty((int(lh[L]), int(lw[L]), 4), np.uint8)
+        s = lv[L - 1]
+        lib.xo_img_half(_ptr(d), int(lw[L]) * 4, _ptr(s), s.shape[1] * 4, int(lw[L]), int(lh[L]))
+        lv.append(d)
+    return lv
+
+
+def img_prep(levels, x0, y0, cw, ch, S=448):
+    """pi_prep of the level-0 rect (x0, y0, cw, ch): the level choice, the rect on that level, the resample (or the
+    identity at side == S) -> fp16 bits [(S/14)^2][592]. Also returns (level, x0, y0, cw, ch) on that level."""
+    lw = np.array([l.shape[1] for l in levels] + [0] * (12 - len(levels)), np.uint32)
+    lh = np.array([l.shape[0] for l in levels] + [0] * (12 - len(levels)), np.uint32)
+    L = lib.xo_img_level(len(levels), max(cw, ch), S)
+    r = [C.c_uint32(v) for v in (x0, y0, cw, ch)]
+    lib.xo_img_lsrc(L, _ptr(lw), _ptr(lh), C.byref(r[0]), C.byref(r[1]), C.byref(r[2]), C.byref(r[3]))
+    x0, y0, cw, ch = (v.value for v in r)
+    src = levels[L]
+    out = np.empty(((S // 14) ** 2, 592), np.uint16)
+    lib.xo_img_prep(C.c_void_p(src.ctypes.data + (y0 * src.shape[1] + x0) * 4), src.shape[1] * 4, cw, ch, S, _ptr(out))
+    return out, (L, x0, y0, cw, ch)
+
+
+def img_axis(S, side, off, length, sc, add):
+    """pi_axis: weights [S][mt], first tap s [S], taps n [S], constant k [S]."""
+    mt = lib.xo_img_mt(side, S)
+    w = np.zeros((S, mt), np.float32)
+    s, n = np.zeros(S, np.int32), np.zeros(S, np.int32)
+    k = np.zeros(S, np.float32)
+    lib.xo_img_axis(S, side, off, length, mt, sc, add, _ptr(w), _ptr(s), _ptr(n), _ptr(k))
+    return w, s, n, k

@@ -133,6 +133,21 @@ int xo_forward(const xo_model *m, const uint16_t *in, int nb, int nl, float *out
 void xo_lcg_frand(uint32_t *rs, size_t n, float *out);
 void xo_lcg_e4m3(uint32_t *rs, size_t n, uint8_t *out);
 
+/* ---- patch-operand producer (src/core/procimg.h; xt_img.c) ---- */
+/* rows of RGBA -> RGBX over white (pi_row_rgbx with alpha, 592-630) */
+void xo_img_over_white(uint8_t *d, size_t ds, const uint8_t *s, size_t ss, uint32_t w, uint32_t h);
+/* pyramid level: wn x hn pixels from the level above (pi_half, 636-661) */
+void xo_img_half(uint8_t *d, size_t ds, const uint8_t *s, size_t ss, uint32_t wn, uint32_t hn);
+uint32_t xo_img_levels(uint32_t w, uint32_t h, uint32_t S, uint32_t *lw, uint32_t *lh); /* pi_pyramid sizes */
+uint32_t xo_img_level(uint32_t nlv, uint32_t side, uint32_t S);                          /* pi_level */
+void xo_img_lsrc(uint32_t L, const uint32_t *lw, const uint32_t *lh, uint32_t *x0, uint32_t *y0, uint32_t *cw,
+                 uint32_t *ch);                                                          /* pi_lsrc */
+uint32_t xo_img_mt(uint32_t side, uint32_t S);
+void xo_img_axis(uint32_t S, uint32_t side, uint32_t off, uint32_t len, uint32_t mt, float sc, float add, float *w,
+                 int32_t *s, int32_t *n, float *k);                                      /* pi_axis */
+/* pi_prep (926-969) from the level rect: out [(S/14)^2][592] fp16, BGR planes, white pad */
+void xo_img_prep(const uint8_t *src, size_t stride, uint32_t cw, uint32_t ch, uint32_t S, uint16_t *out);
+
 #ifdef __cplusplus
 }
 #endif
