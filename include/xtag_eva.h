@@ -171,6 +171,31 @@ int eva_k_fc1_sp(const void *h8, const float *hs, int lds, const void *vals, con
 int eva_k_fc2_sp(const void *m8, const float *ms, int lds, const void *vals, const void *idx, const float *ws,
                  const float *stat, const float *cn, const float *dn, void *x, int rows, void *stream);
 
+/* ---- patch-operand producer on the GPU (src/core/procimg.h:592-969: pi_row_rgbx, pi_pyramid, pi_level / pi_lsrc,
+ * pi_prep for the wd model). A decoded image already in device memory becomes the fp16 patch operand the engine
+ * reads (eva_dev_input), bit-identical to the reference's CPU producer. ---- */
+#define EVA_PYR_LV 12
+typedef struct {                     /* pi_pyr (procimg.h:468-472) with device levels */
+    uint8_t *lv[EVA_PYR_LV];         /* RGBX levels; lv[0] (lw[0], lh[0], ls[0]) is the caller's decoded image */
+    size_t ls[EVA_PYR_LV];           /* row strides in bytes (multiples of 4) */
+    uint32_t lw[EVA_PYR_LV], lh[EVA_PYR_LV], nlv;
+} eva_pyr;
+/* pi_row_rgbx with alpha (procimg.h:592-630), in place: RGBA -> RGBX over white, X = 255 */
+int eva_img_over_white(void *rgba, size_t stride, uint32_t w, uint32_t h, void *stream);
+/* Device bytes of levels 1.. of pi_pyramid (procimg.h:665-688) for a w x h image at model side S (0: EVA_S). */
+size_t eva_img_pyramid_bytes(uint32_t w, uint32_t h, uint32_t S);
+/* pi_pyramid: levels 1.. of p into `levels` (32-byte aligned, eva_img_pyramid_bytes), 2x2 boxes of pi_half
+ * (procimg.h:636-661); sets p->nlv and the level fields. */
+int eva_img_pyramid(eva_pyr *p, void *levels, size_t bytes, uint32_t S, void *stream);
+/* Scratch bytes of eva_img_prep for crops whose long side on the chosen level is at most max_side (4 S - 1 covers
+ * every crop of a full pyramid). */
+size_t eva_img_prep_bytes(uint32_t S, uint32_t max_side);
+/* pi_prep (procimg.h:926-969): the level-0 rect (x0, y0, cw, ch) -> out fp16 [(S/14)^2][592] (EVA_IN halves at
+ * S = 448; 16-byte aligned), resampled (bicubic onto the white square, [-1, 1], BGR planes) from the level pi_level
+ * picks, or normalised as is when the rect's long side on that level is S. The 4 pad halves of each patch row are 0. */
+int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S, void *scratch,
+                 size_t bytes, void *out, void *stream);
+
 /* ---- on-box ceilings (no reference counterpart; the roofline fractions use peaks measured on the same GPU) ---- */
 /* dense FP8 MFMA: blocks x 256 threads, each wave issuing iters x 8 v_mfma_f32_16x16x128_f8f6f4 on register operands
  * (flops = blocks * 4 * iters * 8 * 65536); out [blocks * 256] keeps the result live */

@@ -51,6 +51,11 @@ _SIGS = {
     "eva_dev_output": (_p, [_p]),
     "eva_stream_handle": (_p, [_p]),
     "eva_sync": (_i, [_p]),
+    "eva_img_over_white": (_i, [_p, C.c_size_t, _u32, _u32, _p]),
+    "eva_img_pyramid_bytes": (C.c_size_t, [_u32, _u32, _u32]),
+    "eva_img_pyramid": (_i, [_p, _p, C.c_size_t, _u32, _p]),
+    "eva_img_prep_bytes": (C.c_size_t, [_u32, _u32]),
+    "eva_img_prep": (_i, [_p, _u32, _u32, _u32, _u32, _u32, _p, C.c_size_t, _p, _p]),
     "eva_probe_mfma_fp8": (_i, [_i, _i, _p, _p]),
     "eva_probe_copy": (_i, [_p, _p, C.c_size_t, _p]),
     "eva_probe_lds": (_i, [_i, _i, _p, _p]),
@@ -74,3 +79,9 @@ def ptr(t):
 def check(rc, what):
     if rc != 0:
         raise RuntimeError(f"{what} failed (see stderr)")
+
+
+class EvaPyr(C.Structure):
+    """eva_pyr of include/xtag_eva.h: device RGBX levels of an image (pi_pyr, src/core/procimg.h:468-472)."""
+    _fields_ = [("lv", C.c_void_p * 12), ("ls", C.c_size_t * 12), ("lw", C.c_uint32 * 12), ("lh", C.c_uint32 * 12),
+                ("nlv", C.c_uint32)]
