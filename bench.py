@@ -251,6 +251,51 @@ def bench_ln(torch, L, M=32 * T):
     return us, nbytes / (us * 1e-6) / 1e9
 
 
+def bench_prep(torch, L, h=2048, w=3072, reps=20):
+    """The GPU patch-operand producer (eva_img_*) on a w x h RGBX image resident in HBM: the pyramid (levels 1..), the
+    full view (level 1, a 1536 x 1024 rect resampled to 448) and a 900 x 900 crop (level 0, factor 2.0), each timed as
+    graph replays. The oracle's scalar C restatement of the same full view is timed on one host core beside it."""
+    import ctypes as C
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    stride = w * 4
+    l0 = torch.randint(0, 256, (h, stride), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    p = L.EvaPyr()
+    p.lv[0], p.ls[0], p.lw[0], p.lh[0] = l0.data_ptr(), stride, w, h
+    nbl = L.lib.eva_img_pyramid_bytes(w, h, 448)
+    levels = torch.empty(nbl, dtype=torch.uint8, device=dev)
+    nbs = L.lib.eva_img_prep_bytes(448, 4 * 448 - 1)
+    scratch = torch.empty(nbs, dtype=torch.uint8, device=dev)
+    out = torch.empty(1024 * 592, dtype=torch.int16, device=dev)
+    st = lambda: torch.cuda.current_stream().cuda_stream
+    pyr = lambda: L.check(L.lib.eva_img_pyramid(C.byref(p), L.ptr(levels), nbl, 448, st()), "eva_img_pyramid")
+    pyr()
+    torch.cuda.synchronize()
+
+    def prep(rect):
+        return lambda: L.check(L.lib.eva_img_prep(C.byref(p), *rect, 448, L.ptr(scratch), nbs, L.ptr(out), st()),
+                               "eva_img_prep")
+    res = {}
+    for name, fn in (("pyramid_us", pyr), ("full_view_us", prep((0, 0, w, h))), ("crop900_us", prep((300, 200, 900, 900)))):
+        gr = capture(torch, fn, reps)
+        time_graph(torch, gr, 3)
+        res[name] = round(time_graph(torch, gr, 10) * 1e3 / reps, 2)
+    res["images_per_s"] = round(1e6 / (res["pyramid_us"] + res["full_view_us"]), 1)
+    # CPU: the oracle's scalar restatement of the same full view (level 1 rect), one core
+    from oracle import oracle as O
+    img = l0.cpu().numpy().reshape(h, w, 4)
+    lv = O.img_pyramid(img, 448)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < 2.0:
+        O.img_prep(lv, 0, 0, w, h, 448)
+        n += 1
+    res["cpu_full_view_us"] = round((time.perf_counter() - t0) / n * 1e6, 1)
+    res["cpu_cores"] = 1
+    res["cpu_kind"] = "port (scalar C restatement)"
+    return res
+
+
 def bench_forward(torch, nb=32, iters=5, extra=0, sparse=False):
     """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
     resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores."""
@@ -436,6 +481,7 @@ def main():
         out["hipblaslt_fp8_per_tensor"] = bench_vendor(torch)
     except Exception as ex:  # the vendor path is only a reference point
         out["hipblaslt_fp8_per_tensor"] = {"error": str(ex)[:200]}
+    out["prep_image_3072x2048"] = bench_prep(torch, L)
     ln_us, ln_gbs = bench_ln(torch, L)
     out["ln_m32800"] = {"us": round(ln_us, 2), "gbs": round(ln_gbs, 1), "frac_hbm_peak": round(ln_gbs / 8000.0, 3),
                         "bytes": 32 * T * D * 3 + 32 * T * 8 * 4}

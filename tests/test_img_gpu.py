@@ -100,3 +100,34 @@ def test_prep_bitexact(dev, xt, orc, h, w, crop):
     got = out.cpu().numpy().view(np.uint16)
     diff = got != ref
     assert not diff.any(), f"{diff.sum()} halves differ, first at {np.argwhere(diff)[0]}"
+
+
+def test_prep_feeds_engine(dev, xt, orc, tmp_path):
+    """Crops produced on the GPU straight into the engine's device input buffer (eva_dev_input) give the same scores
+    as the same crops produced by the oracle on the CPU and submitted through eva_submit (the reference's path)."""
+    from xtagger_amd import blob
+    from xtagger_amd.engine import Engine
+    path = str(tmp_path / "eva02_synth_v2.bin")
+    blob.write_v2(path, blob.synth_model(seed=0, nt=10861))
+    img = _img(2000, 3100, 4)
+    crops = [(0, 0, 3100, 2000), (900, 400, 1000, 1000)]
+    lv = orc.img_pyramid(img, S)
+    host = np.stack([orc.img_prep(lv, *c, S=S)[0] for c in crops]).view(np.float16)
+    e = Engine(path, device=0, nb=2)
+    e.ready()
+    e.submit(0, host)
+    ref = e.wait(0, 2)
+    di = DevImage(xt, dev, img)
+    nb = xt.lib.eva_img_prep_bytes(S, 4 * S - 1)
+    scratch = torch.empty(nb, dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    din, st = e.dev_input(), e.stream()
+    for k, c in enumerate(crops):   # on the engine's stream, ahead of its forward
+        assert xt.lib.eva_img_prep(C.byref(di.p), *c, S, xt.ptr(scratch), nb, C.c_void_p(din + k * 1024 * 592 * 2), st) == 0
+    e.run()
+    e.sync()
+    hip = C.CDLL("libamdhip64.so")
+    got = np.empty((2, e.nt), np.float32)
+    assert hip.hipMemcpy(C.c_void_p(got.ctypes.data), C.c_void_p(e.dev_output()), C.c_size_t(got.nbytes), 2) == 0
+    e.close()
+    assert np.array_equal(got, ref)

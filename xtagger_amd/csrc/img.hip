@@ -8,15 +8,16 @@
 // round-to-nearest-even. The outputs are therefore bit-identical to the reference's.
 //
 // Data flow of one crop (eva_img_prep): the host picks the level and the rect on it (pi_level / pi_lsrc, scalar), then
-//   k_img_axis  the two axes' tap tables (pi_axis) into the scratch;
 //   k_img_vpass tmp [S][cw * 4] fp32: output row i over the rect's columns, all RGBX channels (pi_vrow);
-//   k_img_hpass one 14-row band of 8 patches per block: each output pixel's B, G, R over its horizontal taps (pi_hrow),
+//   k_img_hpass one 14-row band of 2 patches per block: each output pixel's B, G, R over its horizontal taps (pi_hrow),
 //               staged in shared memory in the operand's own layout and written out as contiguous 16-byte stores.
+// Each block builds the tap tables it needs (pi_axis) in shared memory: every tap weight in parallel, each output's sum
+// over its taps in the reference's order by one thread.
 // A rect whose long side is S skips the resample (pi_idrow): k_img_ident normalises and white-pads the band directly.
 #include "xt_abi.h"
 #include "xtag_eva.h"
 
-#define IMG_BAND_P 8                        // patches per k_img_hpass block (8 x 592 halves = 9472 contiguous bytes)
+#define IMG_BAND_P 2                        // patches per band block (2 x 592 halves = 2368 contiguous bytes)
 #define IMG_PATCH 592                       // halves per patch row of the operand (588 + 4 zero pad)
 
 // ---- pi_row_rgbx with alpha (procimg.h:592-630): c -> (c a + 255 (255 - a)) / 255 rounded, X = 255, in place
@@ -55,62 +56,105 @@ __global__ void __launch_bounds__(256) k_img_half(uint8_t *__restrict__ d, size_
     *(uint32_t *)(d + (size_t)y * ds + 4 * (size_t)x) = o;
 }
 
-// ---- pi_cubic / pi_axis (procimg.h:750-790): one thread per output index of one axis
+// ---- pi_cubic / pi_axis (procimg.h:750-790), built per block in shared memory
 __device__ __forceinline__ float img_cubic(float x)
 {
     x = x < 0 ? -x : x;
     return x < 1.0f ? (1.5f * x - 2.5f) * x * x + 1.0f : x < 2.0f ? ((-0.5f * x + 2.5f) * x - 4.0f) * x + 2.0f : 0.0f;
 }
 
-struct ImgAxis {   // one axis' tap table in the scratch
-    float *w;      // [S][mt], taps inside the content, scaled by sc / (sum of all taps)
-    int32_t *s;    // first content pixel of output i
-    int32_t *n;    // content taps of output i
-    float *k;      // 255 x (white taps' weight) + add
+// One axis: output index i of S over a virtual square of `side` with the content at [off, off + len); the weights
+// come out scaled by sc, the constant offset by add (the x axis folds the [-1, 1] normalisation in).
+struct ImgGeom {
+    float scale, ss, support, sc, add;
+    int32_t side, off, end;
 };
 
-__global__ void __launch_bounds__(256) k_img_axis(ImgAxis ax, ImgAxis ay, uint32_t S, uint32_t side, uint32_t mt,
-                                                  uint32_t offx, uint32_t lenx, uint32_t offy, uint32_t leny)
+__device__ __forceinline__ ImgGeom img_geom(uint32_t S, uint32_t side, uint32_t off, uint32_t len, float sc, float add)
 {
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= S) return;
-    const bool isx = blockIdx.y == 0;
-    const ImgAxis t = isx ? ax : ay;
-    const uint32_t off = isx ? offx : offy, len = isx ? lenx : leny;
-    const float sc = isx ? 1.0f / 127.5f : 1.0f, add = isx ? -1.0f : 0.0f;
-    const float scale = (float)side / (float)S, fs = scale > 1.0f ? scale : 1.0f, support = 2.0f * fs, ss = 1.0f / fs;
-    const int32_t end = (int32_t)(off + len);
-    const float center = ((float)i + 0.5f) * scale;
-    int32_t lo = (int32_t)(center - support + 0.5f), hi = (int32_t)(center + support + 0.5f);
-    lo = lo < 0 ? 0 : lo;
-    hi = hi > (int32_t)side ? (int32_t)side : hi;
-    const int32_t a = lo > (int32_t)off ? lo : (int32_t)off;
-    int32_t b = hi < end ? hi : end;
-    b = b < a ? a : b;
-    float sum = 0.0f, white = 0.0f;
-    for (int32_t j = lo; j < hi; j++) {  // every tap, in order: the sums of the reference's single loop
-        const float wt = img_cubic(((float)j - center + 0.5f) * ss);
-        sum += wt;
-        white += j < a || j >= b ? wt : 0.0f;
-    }
-    sum = sc / sum;
-    float *wi = t.w + (size_t)i * mt;
-    for (int32_t j = a; j < b; j++) wi[j - a] = img_cubic(((float)j - center + 0.5f) * ss) * sum;
-    t.s[i] = a - (int32_t)off;
-    t.n[i] = b - a;
-    t.k[i] = 255.0f * white * sum + add;
+    ImgGeom g;
+    g.scale = (float)side / (float)S;
+    const float fs = g.scale > 1.0f ? g.scale : 1.0f;
+    g.support = 2.0f * fs;
+    g.ss = 1.0f / fs;
+    g.sc = sc;
+    g.add = add;
+    g.side = (int32_t)side;
+    g.off = (int32_t)off;
+    g.end = (int32_t)(off + len);
+    return g;
 }
 
-// ---- pi_vrow (procimg.h:800-836): tmp[i][4 x + c] = k + sum_j w[j] * src(s + j)[x].c, one RGBX pixel per thread
-__global__ void __launch_bounds__(256) k_img_vpass(const uint8_t *__restrict__ src, size_t stride, uint32_t cw,
-                                                   ImgAxis ay, uint32_t mt, float4 *__restrict__ tmp)
+// the taps [lo, hi) of output i and the content part [a, b) of them (pi_axis's integer bounds)
+__device__ __forceinline__ void img_bounds(const ImgGeom &g, int32_t i, float &center, int32_t &lo, int32_t &hi,
+                                           int32_t &a, int32_t &b)
 {
-    const uint32_t x = blockIdx.x * 256 + threadIdx.x, i = blockIdx.y;
+    center = ((float)i + 0.5f) * g.scale;
+    lo = (int32_t)(center - g.support + 0.5f);
+    hi = (int32_t)(center + g.support + 0.5f);
+    lo = lo < 0 ? 0 : lo;
+    hi = hi > g.side ? g.side : hi;
+    a = lo > g.off ? lo : g.off;
+    b = hi < g.end ? hi : g.end;
+    b = b < a ? a : b;
+}
+
+// Tap tables of `cnt` consecutive outputs i0 .. i0 + cnt - 1 into shared memory: every tap weight in parallel (the same
+// float expression as the reference), then one thread per output sums its taps in tap order (the reference's loop),
+// then the content taps are scaled. w [cnt][mt] holds the content taps; s, n, k per output. Ends synchronised.
+__device__ __forceinline__ void img_taps(const ImgGeom &g, int32_t i0, int32_t cnt, int32_t mt, float *w, int32_t *s,
+                                         int32_t *n, float *k, float *sum)
+{
+    for (int32_t e = threadIdx.x; e < cnt * mt; e += blockDim.x) {
+        const int32_t c = e / mt, t = e - c * mt;
+        float center;
+        int32_t lo, hi, a, b;
+        img_bounds(g, i0 + c, center, lo, hi, a, b);
+        w[e] = lo + t < hi ? img_cubic(((float)(lo + t) - center + 0.5f) * g.ss) : 0.0f;
+    }
+    __syncthreads();
+    for (int32_t c = threadIdx.x; c < cnt; c += blockDim.x) {
+        float center, sm = 0.0f, white = 0.0f;
+        int32_t lo, hi, a, b;
+        img_bounds(g, i0 + c, center, lo, hi, a, b);
+        for (int32_t j = lo; j < hi; j++) {
+            const float wt = w[c * mt + (j - lo)];
+            sm += wt;
+            white += j < a || j >= b ? wt : 0.0f;
+        }
+        sm = g.sc / sm;
+        sum[c] = sm;
+        s[c] = a - g.off;
+        n[c] = b - a;
+        k[c] = 255.0f * white * sm + g.add;
+    }
+    __syncthreads();
+    // content taps to the front of the row, scaled (pi_axis's memmove and wi[j] *= sum), in place: each thread moves
+    // the taps of one output so no row is read after another thread overwrote it
+    for (int32_t c = threadIdx.x; c < cnt; c += blockDim.x) {
+        float center;
+        int32_t lo, hi, a, b;
+        img_bounds(g, i0 + c, center, lo, hi, a, b);
+        for (int32_t q = 0; q < b - a; q++) w[c * mt + q] = w[c * mt + (a - lo) + q] * sum[c];
+    }
+    __syncthreads();
+}
+
+#define IMG_MT_MAX 24                       // taps per output up to a resample factor of 5 (mt = 2 (int)(2 f + 1) + 2)
+
+// ---- pi_vrow (procimg.h:800-836): tmp[i][4 x + c] = k + sum_j w[j] * src(s + j)[x].c, one RGBX pixel per thread;
+// block (blockIdx.x, i = blockIdx.y) builds the y tap table of output row i
+__global__ void __launch_bounds__(256) k_img_vpass(const uint8_t *__restrict__ src, size_t stride, uint32_t cw,
+                                                   uint32_t ch, uint32_t S, uint32_t side, uint32_t mt,
+                                                   float4 *__restrict__ tmp)
+{
+    __shared__ float w[IMG_MT_MAX], sum[1], k[1];
+    __shared__ int32_t sn[2];
+    const uint32_t i = blockIdx.y, x = blockIdx.x * 256 + threadIdx.x;
+    img_taps(img_geom(S, side, (side - ch) >> 1, ch, 1.0f, 0.0f), (int32_t)i, 1, (int32_t)mt, w, sn, sn + 1, k, sum);
     if (x >= cw) return;
-    const int32_t s = ay.s[i], n = ay.n[i];
-    const float k = ay.k[i];
-    const float *w = ay.w + (size_t)i * mt;
-    float a0 = k, a1 = k, a2 = k, a3 = k;
+    const int32_t s = sn[0], n = sn[1];
+    float a0 = k[0], a1 = a0, a2 = a0, a3 = a0;
     const uint8_t *p = src + (size_t)s * stride + 4 * (size_t)x;
     for (int32_t j = 0; j < n; j++, p += stride) {
         const uint32_t v = *(const uint32_t *)p;
@@ -128,8 +172,8 @@ __device__ __forceinline__ uint16_t img_f16(float v)
     return __builtin_bit_cast(uint16_t, (_Float16)v);  // v_cvt_f16_f32: round to nearest even
 }
 
-// Band staging: 14 rows x IMG_BAND_P patches of the operand, [patch][592] halves, pad halves zero; written out with
-// 16-byte stores (the band's patches are contiguous in the operand).
+// Band staging: 14 rows x np patches of the operand, [patch][592] halves, pad halves zero; written out with 16-byte
+// stores (the band's patches are contiguous in the operand).
 __device__ __forceinline__ void img_band_store(uint16_t *band, uint16_t *__restrict__ out, uint32_t S, uint32_t np)
 {
     __syncthreads();
@@ -139,25 +183,31 @@ __device__ __forceinline__ void img_band_store(uint16_t *band, uint16_t *__restr
     for (uint32_t q = threadIdx.x; q < np * IMG_PATCH / 8; q += blockDim.x) dst[q] = sb[q];
 }
 
-// ---- pi_hrow (procimg.h:843-868): output pixels of band blockIdx.y, patches blockIdx.x * 8 .. + 7
-__global__ void __launch_bounds__(256) k_img_hpass(const float4 *__restrict__ tmp, uint32_t cw, ImgAxis ax,
-                                                   uint32_t mt, uint32_t S, uint16_t *__restrict__ out)
+// ---- pi_hrow (procimg.h:843-868): band blockIdx.y, patches blockIdx.x * IMG_BAND_P ..; one output pixel per
+// thread; the block builds the x tap tables of its 14 IMG_BAND_P columns
+__global__ void __launch_bounds__(14 * 14 * IMG_BAND_P) k_img_hpass(const float4 *__restrict__ tmp, uint32_t cw,
+                                                                  uint32_t S, uint32_t side, uint32_t mt,
+                                                                  uint16_t *__restrict__ out)
 {
     __shared__ __attribute__((aligned(16))) uint16_t band[IMG_BAND_P * IMG_PATCH];
+    __shared__ float w[14 * IMG_BAND_P * IMG_MT_MAX], k[14 * IMG_BAND_P], sum[14 * IMG_BAND_P];
+    __shared__ int32_t ts[14 * IMG_BAND_P], tn[14 * IMG_BAND_P];
     const uint32_t pr = S / 14, pc0 = blockIdx.x * IMG_BAND_P;
     const uint32_t np = pr - pc0 < IMG_BAND_P ? pr - pc0 : IMG_BAND_P;
-    for (uint32_t q = threadIdx.x; q < np; q += blockDim.x) *(uint2 *)(band + q * IMG_PATCH + 588) = uint2{0u, 0u};
-    for (uint32_t e = threadIdx.x; e < 14 * 14 * np; e += blockDim.x) {
+    if (threadIdx.x < np) *(uint2 *)(band + threadIdx.x * IMG_PATCH + 588) = uint2{0u, 0u};
+    img_taps(img_geom(S, side, (side - cw) >> 1, cw, 1.0f / 127.5f, -1.0f), (int32_t)(pc0 * 14), (int32_t)(14 * np),
+             (int32_t)mt, w, ts, tn, k, sum);
+    const uint32_t e = threadIdx.x;
+    if (e < 14 * 14 * np) {
         const uint32_t ky = e / (14 * np), jj = e - ky * 14 * np;   // row in the band, column in the block
-        const uint32_t i = blockIdx.y * 14 + ky, j = pc0 * 14 + jj;
-        const int32_t s = ax.s[j], n = ax.n[j];
-        const float k = ax.k[j];
-        const float *w = ax.w + (size_t)j * mt;
-        const float4 *t = tmp + (size_t)i * cw + s;
-        float r = k, g = k, b = k;
+        const uint32_t i = blockIdx.y * 14 + ky;
+        const int32_t n = tn[jj];
+        const float *wj = w + jj * mt;
+        const float4 *t = tmp + (size_t)i * cw + ts[jj];
+        float r = k[jj], g = r, b = r;
         for (int32_t q = 0; q < n; q++) {
             const float4 v = t[q];
-            const float wq = w[q];
+            const float wq = wj[q];
             r = __builtin_fmaf(wq, v.x, r);
             g = __builtin_fmaf(wq, v.y, g);
             b = __builtin_fmaf(wq, v.z, b);
@@ -266,17 +316,13 @@ extern "C" int eva_img_pyramid(eva_pyr *p, void *levels, size_t bytes, uint32_t 
     return xt_check("eva_img_pyramid");
 }
 
-// scratch: two [S][mt] tables and their s / n / k arrays, then tmp [S][cw] float4
-static size_t img_scratch(uint32_t S, uint32_t side, uint32_t cw)
-{
-    const uint32_t mt = img_mt(side, S);
-    return img_a32((size_t)2 * S * mt * 4) + img_a32((size_t)6 * S * 4) + (size_t)S * cw * 16;
-}
+// scratch: tmp [S][cw] float4 of the vertical pass
+static size_t img_scratch(uint32_t S, uint32_t cw) { return (size_t)S * cw * 16; }
 
 extern "C" size_t eva_img_prep_bytes(uint32_t S, uint32_t max_side)
 {
     if (!S) S = EVA_S;
-    return img_scratch(S, max_side, max_side);
+    return img_scratch(S, max_side);
 }
 
 extern "C" int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S,
@@ -309,25 +355,13 @@ extern "C" int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t
         hipLaunchKernelGGL(k_img_ident, bands, dim3(256), 0, st, src, stride, cw, ch, S, (uint16_t *)out);
         return xt_check("eva_img_prep");
     }
-    if (!scratch || bytes < img_scratch(S, side, cw) || ((uintptr_t)scratch & 31))
-        return xt_fail("eva_img_prep", "scratch must be 32-byte aligned and hold eva_img_prep_bytes(S, side)");
     const uint32_t mt = img_mt(side, S);
-    uint8_t *sp = (uint8_t *)scratch;
-    ImgAxis ax, ay;
-    ax.w = (float *)sp;
-    ay.w = ax.w + (size_t)S * mt;
-    sp += img_a32((size_t)2 * S * mt * 4);
-    ax.s = (int32_t *)sp;
-    ax.n = ax.s + S;
-    ay.s = ax.n + S;
-    ay.n = ay.s + S;
-    ax.k = (float *)(ay.n + S);
-    ay.k = ax.k + S;
-    sp += img_a32((size_t)6 * S * 4);
-    float4 *tmp = (float4 *)sp;
-    hipLaunchKernelGGL(k_img_axis, dim3((S + 255) / 256, 2), dim3(256), 0, st, ax, ay, S, side, mt, (side - cw) >> 1, cw,
-                       (side - ch) >> 1, ch);
-    hipLaunchKernelGGL(k_img_vpass, dim3((cw + 255) / 256, S), dim3(256), 0, st, src, stride, cw, ay, mt, tmp);
-    hipLaunchKernelGGL(k_img_hpass, bands, dim3(256), 0, st, (const float4 *)tmp, cw, ax, mt, S, (uint16_t *)out);
+    if (mt > IMG_MT_MAX) return xt_fail("eva_img_prep", "rect more than 5x the model side on its level");
+    if (!scratch || bytes < img_scratch(S, cw) || ((uintptr_t)scratch & 15))
+        return xt_fail("eva_img_prep", "scratch must be 16-byte aligned and hold eva_img_prep_bytes(S, side)");
+    float4 *tmp = (float4 *)scratch;
+    hipLaunchKernelGGL(k_img_vpass, dim3((cw + 255) / 256, S), dim3(256), 0, st, src, stride, cw, ch, S, side, mt, tmp);
+    hipLaunchKernelGGL(k_img_hpass, bands, dim3(14 * 14 * IMG_BAND_P), 0, st, (const float4 *)tmp, cw, S, side, mt,
+                       (uint16_t *)out);
     return xt_check("eva_img_prep");
 }
