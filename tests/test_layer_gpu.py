@@ -258,6 +258,7 @@ def test_flash_parity(dev, xt, orc):
     _ok(xt.lib.eva_k_flash(xt.ptr(_d(q, dev)), xt.ptr(_d(k, dev)), xt.ptr(_d(vt, dev)), xt.ptr(d_o8), xt.ptr(d_os), lds,
                            nb, xt.ptr(d_o32), _st()), "eva_k_flash")
     ref = orc.attention(q.view(torch.int16).numpy(), k.view(torch.int16).numpy(), vt.view(torch.int16).numpy(), nb)
+    _say("  flash vs fp64 softmax:")
     o = d_o32.cpu().numpy().astype(np.float64)
     err = np.abs(o - ref)
     rel = err.max() / np.abs(ref).max()
@@ -288,7 +289,8 @@ def test_flash_row_sums_and_permutation(dev, xt, orc):
     _ok(xt.lib.eva_k_flash(xt.ptr(_d(q, dev)), xt.ptr(_d(k, dev)), xt.ptr(_d(vt1, dev)), xt.ptr(d_o8), xt.ptr(d_os), T,
                            nb, xt.ptr(d_o32), _st()), "flash ones")
     o = d_o32.cpu().numpy()
-    assert np.abs(o - 1.0).max() <= 4e-3                    # sum of bf16-rounded p over the fp32 sum of p
+    # l sums the same bf16 weights the PV product uses: rows of a V of ones come out 1 up to fp32 summation order
+    assert np.abs(o - 1.0).max() <= 1e-5
     perm = np.random.default_rng(5).permutation(T)
     kp, vp = k.clone(), vt.clone()
     kp[:, :, :T] = k[:, :, perm]

@@ -10,7 +10,8 @@
 // B operand of O^T += V^T P^T with V^T read as 16 contiguous bytes. No value moves between lanes.
 // Softmax runs in the exp2 domain (q carries log2(e)/8 from the weights) with the reference's lazy rescale: the
 // running max is refreshed only when some query of the wave grows past it by more than 8 (kern_common.cuh:480-493),
-// so p <= 2^8; l sums the fp32 p before their bf16 rounding (kern_common.cuh:505-506).
+// so p <= 2^8. l sums the bf16-rounded p that enter the PV product (the reference sums the fp32 p,
+// kern_common.cuh:505-506): the output's weights then sum to one exactly, and the row sum costs one v_dot2c per pair.
 // K and V^T tiles of 64 keys for both heads are double-buffered in LDS by buffer_load ... lds.
 #include "gemm_core.h"
 #include "xt_abi.h"
@@ -26,6 +27,9 @@ __device__ __forceinline__ v8bf frag_bf(const uint8_t *tile, int row, int chunk)
 {
     return __builtin_bit_cast(v8bf, *(const uint4 *)(tile + swz(row, chunk)));
 }
+
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+#define kOnes2 (v2bf{(__bf16)1.0f, (__bf16)1.0f})
 
 __device__ __forceinline__ v8bf pack_p(const v16f &s, int base)
 {
@@ -138,16 +142,17 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
 #pragma unroll
             for (int u = 0; u < 2; u++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const float p = __builtin_amdgcn_exp2f(s[u][e]);
-                    s[u][e] = p;
-                    lsum += p;
-                }
+                for (int e = 0; e < 16; e++) s[u][e] = __builtin_amdgcn_exp2f(s[u][e]);
 #pragma unroll
             for (int u = 0; u < 2; u++)
 #pragma unroll
                 for (int sp = 0; sp < 2; sp++) {
                     const v8bf pf = pack_p(s[u], 8 * sp);
+                    // l sums the bf16 weights the PV product uses, two per v_dot2c_f32_bf16
+                    lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 0, 1), kOnes2, lsum, false);
+                    lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 2, 3), kOnes2, lsum, false);
+                    lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 4, 5), kOnes2, lsum, false);
+                    lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 6, 7), kOnes2, lsum, false);
 #pragma unroll
                     for (int dt = 0; dt < 2; dt++)
                         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tv, 32 * dt + l32, 4 * u + 2 * sp + g),
