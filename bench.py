@@ -296,6 +296,27 @@ def bench_prep(torch, L, h=2048, w=3072, reps=20):
     return res
 
 
+def bench_attention_seq(torch, L, reps=10):
+    """eva_k_flash_seq at the PixAI engine's shapes (batch 4, px.h PX_NB): 36 windows of 576 tokens and 4 global
+    sequences of 5184, 16 heads of 64; FLOPs 4 T^2 64 16 per sequence (QK^T and PV)."""
+    dev = torch.device("cuda:0")
+    res = {}
+    for name, nseq, T in (("window_576_x36", 36, 576), ("global_5184_x4", 4, 5184)):
+        g = torch.Generator(device=dev).manual_seed(T)
+        q = (torch.randn(nseq, 16, T, 64, generator=g, device=dev) * 0.6).to(torch.bfloat16)
+        k = (torch.randn(nseq, 16, T, 64, generator=g, device=dev) * 0.6).to(torch.bfloat16)
+        vt = torch.randn(nseq, 16, 64, T, generator=g, device=dev).to(torch.bfloat16)
+        o8 = torch.empty(nseq * T, 1024, dtype=torch.uint8, device=dev)
+        os_ = torch.empty(8, nseq * T, dtype=torch.float32, device=dev)
+        fn = lambda: L.check(L.lib.eva_k_flash_seq(L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o8), L.ptr(os_), nseq * T, nseq,
+                                                   T, T, None, torch.cuda.current_stream().cuda_stream), "flash_seq")
+        gr = capture(torch, fn, reps)
+        time_graph(torch, gr, 2)
+        us = time_graph(torch, gr, 5) * 1e3 / reps
+        res[name] = {"us": round(us, 1), "tflops": round(4.0 * T * T * 64 * 16 * nseq / (us * 1e-6) / 1e12, 1)}
+    return res
+
+
 def bench_forward(torch, nb=32, iters=5, extra=0, sparse=False):
     """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
     resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores."""
@@ -482,6 +503,7 @@ def main():
     except Exception as ex:  # the vendor path is only a reference point
         out["hipblaslt_fp8_per_tensor"] = {"error": str(ex)[:200]}
     out["prep_image_3072x2048"] = bench_prep(torch, L)
+    out["attention_pixai_shapes"] = bench_attention_seq(torch, L)
     ln_us, ln_gbs = bench_ln(torch, L)
     out["ln_m32800"] = {"us": round(ln_us, 2), "gbs": round(ln_gbs, 1), "frac_hbm_peak": round(ln_gbs / 8000.0, 3),
                         "bytes": 32 * T * D * 3 + 32 * T * 8 * 4}

@@ -116,6 +116,11 @@ int eva_k_qkv(const void *h8, const float *hs, int lds, const void *w, const flo
  * scales os [8][lds]; o32 (may be NULL) receives the fp32 output before packing. */
 int eva_k_flash(const void *q, const void *k, const void *vt, void *o8, float *os, int lds, int nb, float *o32,
                 void *stream);
+/* eva_k_flash over nseq sequences of T tokens, q / k bf16 [nseq][16][TP][64], vt [nseq][16][64][TP] with TP >= T
+ * rounded up to 64 (padding rows finite; keys past T are masked): the PixAI engine's windowed (T = 576, 9 windows per
+ * image) and global (T = 5184) attention (px_kernels.cu:140-154, k_pflash_w / k_pflash_g), output rows s * T + t. */
+int eva_k_flash_seq(const void *q, const void *k, const void *vt, void *o8, float *os, int lds, int nseq, int T, int TP,
+                    float *o32, void *stream);
 /* Out-projection + residual (eva_kernels.cu:134-162 k_oproj): x fp16 [rows][1024] += a8 . Wo^T */
 int eva_k_oproj(const void *a8, const float *as, int lds, const void *w, const float *ws, void *x, int rows,
                 void *stream);

@@ -48,6 +48,7 @@ _SIGS = {
     "xo_ln_quant": (None, [_p, _p, _p, _i, _p, _p, _i, _p]),
     "xo_qkv_epi": (None, [_p, _i, _p, _p, _p, _p]),
     "xo_attention": (None, [_p, _p, _p, _i, _p, _i]),
+    "xo_attention_seq": (None, [_p, _p, _p, _i, _i, _i, _i, _p, _i]),
     "xo_fc1_epi": (None, [_p, _i, _p, _p]),
     "xo_fc2_epi": (None, [_p, _i, _p, _p, _p, _p]),
     "xo_oproj_epi": (None, [_p, _i, _p]),
@@ -219,6 +220,15 @@ def attention(q, k, vt, nb, threads=0):
     _done()
     o = np.empty((nb * 1025, 1024), np.float64)
     lib.xo_attention(_ptr(_c(q, np.uint16)), _ptr(_c(k, np.uint16)), _ptr(_c(vt, np.uint16)), nb, _ptr(o), threads)
+    return o
+
+
+def attention_seq(q, k, vt, nseq, T, TP, qstep=1, threads=0):
+    """fp64 softmax attention of nseq sequences of T tokens (padded to TP) -> o [nseq * T][1024] (rows t % qstep != 0
+    are NaN)."""
+    o = np.full((nseq * T, 1024), np.nan)
+    lib.xo_attention_seq(_ptr(np.ascontiguousarray(q)), _ptr(np.ascontiguousarray(k)), _ptr(np.ascontiguousarray(vt)),
+                         nseq, T, TP, qstep, _ptr(o), threads)
     return o
 
 

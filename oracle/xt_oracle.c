@@ -485,31 +485,33 @@ void xo_qkv_epi(const float *acc, int nb, const float *cs, uint16_t *q, uint16_t
     }
 }
 
-void xo_attention(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int nb, double *o, int threads)
+void xo_attention_seq(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int nseq, int T, int TP, int qstep,
+                      double *o, int threads)
 {
     int bh;
 
+    if (qstep < 1) qstep = 1;
 #ifdef _OPENMP
     if (threads <= 0) threads = omp_get_max_threads();
 #pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
 #else
     (void)threads;
 #endif
-    for (bh = 0; bh < nb * 16; bh++) {
+    for (bh = 0; bh < nseq * 16; bh++) {
         int b = bh / 16, h = bh % 16, t, j, d;
-        double *Q = (double *)malloc(sizeof(double) * XO_T * 64);
-        double *Kd = (double *)malloc(sizeof(double) * XO_T * 64);
-        double *V = (double *)malloc(sizeof(double) * XO_T * 64);
-        double *s = (double *)malloc(sizeof(double) * XO_T);
-        for (t = 0; t < XO_T; t++)
+        double *Q = (double *)malloc(sizeof(double) * T * 64);
+        double *Kd = (double *)malloc(sizeof(double) * T * 64);
+        double *V = (double *)malloc(sizeof(double) * T * 64);
+        double *s = (double *)malloc(sizeof(double) * T);
+        for (t = 0; t < T; t++)
             for (d = 0; d < 64; d++) {
-                Q[t * 64 + d] = xo_bf16_to_f32(q[((size_t)bh * XO_TP + t) * 64 + d]);
-                Kd[t * 64 + d] = xo_bf16_to_f32(k[((size_t)bh * XO_TP + t) * 64 + d]);
-                V[t * 64 + d] = xo_bf16_to_f32(vt[((size_t)bh * 64 + d) * XO_TP + t]);
+                Q[t * 64 + d] = xo_bf16_to_f32(q[((size_t)bh * TP + t) * 64 + d]);
+                Kd[t * 64 + d] = xo_bf16_to_f32(k[((size_t)bh * TP + t) * 64 + d]);
+                V[t * 64 + d] = xo_bf16_to_f32(vt[((size_t)bh * 64 + d) * TP + t]);
             }
-        for (t = 0; t < XO_T; t++) {
+        for (t = 0; t < T; t += qstep) {
             double mx = -INFINITY, l = 0.0, acc[64];
-            for (j = 0; j < XO_T; j++) {
+            for (j = 0; j < T; j++) {
                 double a0 = 0, a1 = 0, a2 = 0, a3 = 0;
                 for (d = 0; d < 64; d += 4) {
                     a0 += Q[t * 64 + d] * Kd[j * 64 + d];
@@ -521,18 +523,23 @@ void xo_attention(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int 
                 if (s[j] > mx) mx = s[j];
             }
             for (d = 0; d < 64; d++) acc[d] = 0.0;
-            for (j = 0; j < XO_T; j++) {
+            for (j = 0; j < T; j++) {
                 double p = exp2(s[j] - mx);
                 l += p;
                 for (d = 0; d < 64; d++) acc[d] += p * V[j * 64 + d];
             }
-            for (d = 0; d < 64; d++) o[((size_t)b * XO_T + t) * 1024 + h * 64 + d] = acc[d] / l;
+            for (d = 0; d < 64; d++) o[((size_t)b * T + t) * 1024 + h * 64 + d] = acc[d] / l;
         }
         free(Q);
         free(Kd);
         free(V);
         free(s);
     }
+}
+
+void xo_attention(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int nb, double *o, int threads)
+{
+    xo_attention_seq(q, k, vt, nb, XO_T, XO_TP, 1, o, threads);
 }
 
 void xo_fc1_epi(const float *acc, int M, float *h, float *stat)

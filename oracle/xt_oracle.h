@@ -70,6 +70,10 @@ void xo_qkv_epi(const float *acc, int nb, const float *cs, uint16_t *q, uint16_t
 /* softmax attention in fp64 (exp2 domain: scores already carry log2(e)/8), one output row per token:
  * o [nb * 1025][1024] at column h * 64 (flash8's math, kern_common.cuh:403-543, without its E4M3 roundings) */
 void xo_attention(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int nb, double *o, int threads);
+/* the same for nseq sequences of T tokens padded to TP (q, k [nseq][16][TP][64], vt [nseq][16][64][TP] bf16) ->
+ * o [nseq * T][1024]; only queries t % qstep == 0 are computed (others untouched) */
+void xo_attention_seq(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int nseq, int T, int TP, int qstep,
+                      double *o, int threads);
 /* fc1 epilogue (eva_kernels.cu:233-268): acc [M][5632] with g / x interleaved in 16-unit chunks
  * (export_eva.py:60-62) -> h = silu(g) * x, fp32 [M][2816] in unit order; stat [22][M][2] = (sum h, sum h^2) over
  * each 128-unit block. silu(g) = g / (1 + exp(-g)), exact form (the reference's tanh.approx is not restated). */

@@ -304,6 +304,42 @@ def test_flash_row_sums_and_permutation(dev, xt, orc):
     assert np.abs(a - b).max() <= 4e-3 * np.abs(a).max()
 
 
+@pytest.mark.parametrize("nseq,T,qstep", [(18, 576, 1), (1, 5184, 41), (3, 200, 1)])
+def test_flash_seq_parity(dev, xt, orc, nseq, T, qstep):
+    """Sequences of T tokens: the PixAI windows (9 per image x 2 images, L = 576) and its global attention (L = 5184,
+    every 41st query checked against fp64), plus a length that is not a multiple of 64 (masked keys)."""
+    TPad = (T + 63) // 64 * 64
+    _say(f"k_flash_seq nseq={nseq} T={T}")
+    r = np.random.default_rng(T)
+    qf = np.zeros((nseq, 16, TPad, 64), np.float32)
+    kf = np.zeros_like(qf)
+    vf = np.zeros((nseq, 16, 64, TPad), np.float32)
+    qf[:, :, :T] = r.standard_normal((nseq, 16, T, 64)) * 0.6
+    kf[:, :, :T] = r.standard_normal((nseq, 16, T, 64)) * 0.6
+    vf[..., :T] = r.standard_normal((nseq, 16, 64, T))
+    bf = lambda a: torch.from_numpy(a).to(torch.bfloat16)
+    q, k, vt = bf(qf), bf(kf), bf(vf)
+    M = nseq * T
+    lds = M + 5
+    d_o8 = torch.zeros((M, D), dtype=torch.uint8, device=dev)
+    d_os = torch.zeros((8, lds), dtype=torch.float32, device=dev)
+    d_o32 = torch.zeros((M, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_flash_seq(xt.ptr(_d(q, dev)), xt.ptr(_d(k, dev)), xt.ptr(_d(vt, dev)), xt.ptr(d_o8), xt.ptr(d_os),
+                               lds, nseq, T, TPad, xt.ptr(d_o32), _st()), "eva_k_flash_seq")
+    ref = orc.attention_seq(q.view(torch.int16).numpy(), k.view(torch.int16).numpy(), vt.view(torch.int16).numpy(),
+                            nseq, T, TPad, qstep)
+    rows = np.arange(M)[(np.arange(M) % T) % qstep == 0]
+    o = d_o32.cpu().numpy().astype(np.float64)[rows]
+    ref = ref[rows]
+    rel = np.abs(o - ref).max() / np.abs(ref).max()
+    _say(f"  o32 max err / max|ref| {rel:.3g}")
+    assert rel <= 4e-3
+    assert np.linalg.norm(o - ref) <= 2e-3 * np.linalg.norm(ref)
+    q8, s8 = orc.quant_act(d_o32.cpu().numpy(), lds=lds)     # output packing of the kernel's own fp32 output
+    assert (d_o8.cpu().numpy() == q8).all()
+    assert (d_os.cpu().numpy()[:, :M] == s8[:, :M]).all()
+
+
 def test_oproj_residual(dev, xt, orc):
     M = 2 * T
     _say("k_oproj")

@@ -18,7 +18,6 @@
 
 #define FA_QB 128                    // queries per block
 #define FA_KT 64                     // keys per LDS tile
-#define FA_NKT ((XT_T + FA_KT - 1) / FA_KT)  // 17 key tiles
 #define FA_TILE (FA_KT * 128)        // bytes of one K or V^T tile of one head
 #define FA_STAGE (4 * FA_TILE)       // K head 0 | K head 1 | V^T head 0 | V^T head 1
 #define FA_RESCALE 8.0f
@@ -38,10 +37,12 @@ __device__ __forceinline__ v8bf pack_p(const v16f &s, int base)
     return __builtin_convertvector(f, v8bf);
 }
 
+// One block per (query block of 128, head pair, sequence): sequences of T tokens, q / k rows and v^T columns padded to
+// TP >= T rounded up to 64 (rows past T read as data must be finite; keys past T are masked).
 template <int DBG>
 __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
                                                const uint16_t *__restrict__ vt, uint8_t *__restrict__ o8,
-                                               float *__restrict__ os, int lds, float *__restrict__ o32)
+                                               float *__restrict__ os, int lds, float *__restrict__ o32, int T, int TP)
 {
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * FA_STAGE + 8 * 32 * 4];
     float *xamax = (float *)(smem + 2 * FA_STAGE);
@@ -49,12 +50,13 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     const int hsel = w >> 2, qt = w & 3, b = blockIdx.z;
     const int head = 2 * blockIdx.y + hsel;
     const int q0 = blockIdx.x * FA_QB + 32 * qt;
-    const bool active = q0 < XT_T;
+    const bool active = q0 < T;
+    const int nkt = (T + FA_KT - 1) / FA_KT;
 
     // operand loads: per stage 32 x 1 KB, 4 per wave (K: 8 contiguous KB per head; V^T: 64 rows of 128 B, stride Tp)
-    const size_t hbase0 = ((size_t)b * XT_NH + 2 * blockIdx.y) * XT_TP * XT_HD;  // elements, head 2p
-    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(k + hbase0, 2u * XT_TP * XT_HD * 2u);
-    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vt + hbase0, 2u * XT_TP * XT_HD * 2u);
+    const size_t hbase0 = ((size_t)b * XT_NH + 2 * blockIdx.y) * TP * XT_HD;  // elements, head 2p
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(k + hbase0, 2u * (uint32_t)TP * XT_HD * 2u);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vt + hbase0, 2u * (uint32_t)TP * XT_HD * 2u);
     const int wu = __builtin_amdgcn_readfirstlane(w);
     const int r8 = lane >> 3, ch = (lane & 7) ^ r8;
     auto issue = [&](uint8_t *st, int kt) {
@@ -63,8 +65,8 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
             const int seg = wu * 4 + i;                 // 0..31: [K h0 | K h1 | V h0 | V h1] x 8 segments
             const int tsel = seg >> 3, hh = tsel & 1, rowb = 8 * (seg & 7) + r8;
             uint32_t off;
-            if (tsel < 2) off = (uint32_t)(((hh * XT_TP) + kt * FA_KT + rowb) * 128 + ch * 16);
-            else off = (uint32_t)(((hh * XT_HD + rowb) * XT_TP + kt * FA_KT) * 2 + ch * 16);
+            if (tsel < 2) off = (uint32_t)(((hh * TP) + kt * FA_KT + rowb) * 128 + ch * 16);
+            else off = (uint32_t)(((hh * XT_HD + rowb) * TP + kt * FA_KT) * 2 + ch * 16);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(tsel < 2 ? rk : rv, (lds_void *)(st + 1024 * seg), 16, (int)off, 0,
                                                      0, 0);
         }
@@ -74,7 +76,7 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     v8bf qf[4];
     {
         const int qrow = active ? q0 + l32 : 0;
-        const uint16_t *qp = q + ((size_t)b * XT_NH + head) * XT_TP * XT_HD + (size_t)qrow * XT_HD + 8 * g;
+        const uint16_t *qp = q + ((size_t)b * XT_NH + head) * TP * XT_HD + (size_t)qrow * XT_HD + 8 * g;
 #pragma unroll
         for (int s = 0; s < 4; s++) qf[s] = __builtin_bit_cast(v8bf, *(const uint4 *)(qp + 16 * s));
     }
@@ -86,11 +88,11 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     float mrun = -INFINITY, lsum = 0.f;
 
     issue(smem, 0);
-    for (int kt = 0; kt < FA_NKT; kt++) {
+    for (int kt = 0; kt < nkt; kt++) {
         uint8_t *st = smem + (kt & 1) * FA_STAGE;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (kt + 1 < FA_NKT) issue(smem + ((kt + 1) & 1) * FA_STAGE, kt + 1);
+        if (kt + 1 < nkt) issue(smem + ((kt + 1) & 1) * FA_STAGE, kt + 1);
         if (active) {
             const uint8_t *tk = st + hsel * FA_TILE, *tv = st + (2 + hsel) * FA_TILE;
             // the scores start from -mb (mb = the running max, 0 before the first tile): after the first tile they
@@ -107,14 +109,14 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
                     s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tk, 32 * u + jrow, 2 * step + g), qf[step],
                                                                   s[u], 0, 0, 0);
             }
-            if (kt == FA_NKT - 1) {  // keys past 1024 are padding
+            if (kt == nkt - 1 && (T & (FA_KT - 1))) {  // keys past T are padding
 #pragma unroll
                 for (int u = 0; u < 2; u++)
 #pragma unroll
                     for (int e = 0; e < 16; e++) {
                         const int j = e >> 2, i = e & 3;
                         const int key = kt * FA_KT + 32 * u + 16 * (j >> 1) + 8 * g + 4 * (j & 1) + i;
-                        if (key >= XT_T) s[u][e] = -INFINITY;
+                        if (key >= T) s[u][e] = -INFINITY;
                     }
             }
             float tmax = -INFINITY;  // relative to mb
@@ -181,8 +183,8 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     amax = __builtin_fmaxf(amax, xamax[(w ^ 4) * 32 + l32]);
     const float sc = block_scale(amax), inv = 1.0f / sc;
     const int query = q0 + l32;
-    if (query >= XT_T) return;
-    const size_t m = (size_t)b * XT_T + query;
+    if (query >= T) return;
+    const size_t m = (size_t)b * T + query;
     uint8_t *dst = o8 + m * XT_D + head * XT_HD;
 #pragma unroll
     for (int dt = 0; dt < 2; dt++)
@@ -199,18 +201,31 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     if (hsel == 0 && g == 0) os[(size_t)blockIdx.y * lds + m] = sc;
 }
 
+static int flash_launch(const char *what, const void *q, const void *k, const void *vt, void *o8, float *os, int lds,
+                        int nseq, int T, int TP, float *o32, void *stream)
+{
+    if (nseq <= 0 || T <= 0 || TP < (T + FA_KT - 1) / FA_KT * FA_KT || lds < nseq * T || (size_t)2 * TP * XT_HD * 2 > 0xFFFFFFFFu)
+        return xt_fail(what, "bad shape (nseq, T > 0; TP >= T rounded up to 64; lds >= nseq * T)");
+    if ((((uintptr_t)q) | ((uintptr_t)k) | ((uintptr_t)vt) | ((uintptr_t)o8)) & 15)
+        return xt_fail(what, "q, k, vt, o8 must be 16-byte aligned");
+    const dim3 grid((T + FA_QB - 1) / FA_QB, XT_NH / 2, nseq);
+    if (o32)
+        hipLaunchKernelGGL(k_flash<1>, grid, dim3(512), 0, (hipStream_t)stream, (const uint16_t *)q, (const uint16_t *)k,
+                           (const uint16_t *)vt, (uint8_t *)o8, os, lds, o32, T, TP);
+    else
+        hipLaunchKernelGGL(k_flash<0>, grid, dim3(512), 0, (hipStream_t)stream, (const uint16_t *)q, (const uint16_t *)k,
+                           (const uint16_t *)vt, (uint8_t *)o8, os, lds, o32, T, TP);
+    return xt_check(what);
+}
+
 extern "C" int eva_k_flash(const void *q, const void *k, const void *vt, void *o8, float *os, int lds, int nb,
                            float *o32, void *stream)
 {
-    if (nb <= 0 || lds < nb * XT_T) return xt_fail("eva_k_flash", "bad shape (nb > 0, lds >= nb * 1025)");
-    if ((((uintptr_t)q) | ((uintptr_t)k) | ((uintptr_t)vt) | ((uintptr_t)o8)) & 15)
-        return xt_fail("eva_k_flash", "q, k, vt, o8 must be 16-byte aligned");
-    const dim3 grid((XT_T + FA_QB - 1) / FA_QB, XT_NH / 2, nb);
-    if (o32)
-        hipLaunchKernelGGL(k_flash<1>, grid, dim3(512), 0, (hipStream_t)stream, (const uint16_t *)q, (const uint16_t *)k,
-                           (const uint16_t *)vt, (uint8_t *)o8, os, lds, o32);
-    else
-        hipLaunchKernelGGL(k_flash<0>, grid, dim3(512), 0, (hipStream_t)stream, (const uint16_t *)q, (const uint16_t *)k,
-                           (const uint16_t *)vt, (uint8_t *)o8, os, lds, o32);
-    return xt_check("eva_k_flash");
+    return flash_launch("eva_k_flash", q, k, vt, o8, os, lds, nb, XT_T, XT_TP, o32, stream);
+}
+
+extern "C" int eva_k_flash_seq(const void *q, const void *k, const void *vt, void *o8, float *os, int lds, int nseq,
+                               int T, int TP, float *o32, void *stream)
+{
+    return flash_launch("eva_k_flash_seq", q, k, vt, o8, os, lds, nseq, T, TP, o32, stream);
 }
