@@ -317,6 +317,78 @@ def bench_attention_seq(torch, L, reps=10):
     return res
 
 
+def bench_pixai_block(torch, L, nb=4, reps=10):
+    """The PixAI tagger's ViTDet-L block (px.h:130-156) at batch 4 (M = 4 x 5184 window-major token rows) on the
+    px_k_* kernels: the four block GEMMs with their epilogues (qkv 1024->3072 +bias +RoPE, proj 1024->1024 +bias
+    +residual, fc1 1024->4736 +bias +GELU +E4M3 repack, fc2 4736->1024 +bias +residual; 576.1 GFLOP), and whole
+    blocks (LN1, qkv, attention, proj, LN2, fc1, fc2) with windowed (36 x 576) and global (4 x 5184) attention."""
+    dev = torch.device("cuda:0")
+    M, PH = nb * 5184, 4736
+    g = torch.Generator(device=dev).manual_seed(7)
+    lds = M
+    t = lambda *s, dt=torch.uint8: torch.zeros(*s, dtype=dt, device=dev)
+    st = lambda: torch.cuda.current_stream().cuda_stream
+    scratch = torch.empty(PH * D, dtype=torch.float32, device=dev)
+
+    def packw(n, k, perm=0):
+        w16 = (torch.randn(n, k, generator=g, device=dev) * 0.02).half()
+        q, s = t(n, k), t(n // 128, k // 128, dt=torch.float32)
+        L.check(L.lib.eva_k_prep_w(L.ptr(w16), k, n, k, n, k, perm, None, L.ptr(scratch), L.ptr(q), L.ptr(s), st()),
+                "prep")
+        return q, s
+
+    wqkv, sqkv = packw(3 * D, D, 1)
+    wo, so = packw(D, D)
+    w1, s1 = packw(PH, D)
+    w2, s2 = packw(D, PH)
+    bqkv, bo = torch.randn(3 * D, generator=g, device=dev) * 0.1, torch.randn(D, generator=g, device=dev) * 0.1
+    b1, b2 = torch.randn(PH, generator=g, device=dev) * 0.1, torch.randn(D, generator=g, device=dev) * 0.1
+    lng, lnb = torch.ones(D, device=dev), torch.zeros(D, device=dev)
+    cs = {576: torch.rand(576, 32, 2, generator=g, device=dev), 5184: torch.rand(5184, 32, 2, generator=g, device=dev)}
+    x = torch.randn(M, D, generator=g, device=dev).half()
+    h8, hs = t(M, D), t(8, lds, dt=torch.float32)
+    q, k, vt = t(M * D, dt=torch.int16), t(M * D, dt=torch.int16), t(M * D, dt=torch.int16)
+    o8, os_ = t(M, D), t(8, lds, dt=torch.float32)
+    m8, ms = t(M, PH), t(PH // 128, lds, dt=torch.float32)
+    P = L.ptr
+    ln = lambda: L.lib.eva_k_ln(P(x), P(lng), P(lnb), P(h8), P(hs), M, lds, st())
+    qkv = lambda Ls=576: L.lib.px_k_qkv(P(h8), P(hs), lds, P(wqkv), P(sqkv), P(bqkv), P(cs[Ls]), Ls, P(q), P(k), P(vt),
+                                        M, st())
+    attn = lambda Ls: L.lib.eva_k_flash_seq(P(q), P(k), P(vt), P(o8), P(os_), lds, M // Ls, Ls, Ls, None, st())
+    proj = lambda: L.lib.px_k_proj(P(o8), P(os_), lds, P(wo), P(so), P(bo), P(x), M, st())
+    fc1 = lambda: L.lib.px_k_fc1(P(h8), P(hs), lds, P(w1), P(s1), P(b1), None, P(m8), P(ms), M, st())
+    fc2 = lambda: L.lib.px_k_fc2(P(m8), P(ms), lds, P(w2), P(s2), P(b2), P(x), M, st())
+
+    def run(*fs):
+        def f():
+            for fn in fs:
+                if fn() != 0:
+                    raise RuntimeError("PixAI block launch failed")
+        return f
+
+    run(ln, qkv, lambda: attn(576), fc1)()                     # real activations in h8, q / k / vt, o8, m8
+    torch.cuda.synchronize()
+    fl = {"qkv": 2.0 * M * 3 * D * D, "proj": 2.0 * M * D * D, "fc1": 2.0 * M * PH * D, "fc2": 2.0 * M * D * PH}
+    res = {"M": M, "gflop_gemms": round(sum(fl.values()) / 1e9, 1)}
+
+    def timed(fn, r=reps):
+        gr = capture(torch, fn, r)
+        time_graph(torch, gr, 2)
+        return time_graph(torch, gr, 5) * 1e3 / r                # us per call
+
+    us = timed(run(qkv, proj, fc1, fc2))
+    res["gemm_step"] = {"us": round(us, 1), "tflops": round(sum(fl.values()) / (us * 1e-6) / 1e12, 1)}
+    res["per_kernel"] = {}
+    for name, fn in (("qkv", qkv), ("proj", proj), ("fc1", fc1), ("fc2", fc2)):
+        kus = timed(run(fn), 20)
+        res["per_kernel"][name] = {"us": round(kus, 1), "tflops": round(fl[name] / (kus * 1e-6) / 1e12, 1)}
+    for name, Ls in (("block_windowed_us", 576), ("block_global_us", 5184)):
+        res[name] = round(timed(run(ln, lambda: qkv(Ls), lambda: attn(Ls), proj, ln, fc1, fc2)), 1)
+    # ViTDet-L: 32 blocks, global attention in 4 of them (px.h PX_GLOBAL)
+    res["blocks_32_ms"] = round((28 * res["block_windowed_us"] + 4 * res["block_global_us"]) / 1e3, 3)
+    return res
+
+
 def bench_forward(torch, nb=32, iters=5, extra=0, sparse=False):
     """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
     resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores."""
@@ -504,6 +576,7 @@ def main():
         out["hipblaslt_fp8_per_tensor"] = {"error": str(ex)[:200]}
     out["prep_image_3072x2048"] = bench_prep(torch, L)
     out["attention_pixai_shapes"] = bench_attention_seq(torch, L)
+    out["pixai_block_b4"] = bench_pixai_block(torch, L)
     ln_us, ln_gbs = bench_ln(torch, L)
     out["ln_m32800"] = {"us": round(ln_us, 2), "gbs": round(ln_gbs, 1), "frac_hbm_peak": round(ln_gbs / 8000.0, 3),
                         "bytes": 32 * T * D * 3 + 32 * T * 8 * 4}

@@ -201,6 +201,26 @@ size_t eva_img_prep_bytes(uint32_t S, uint32_t max_side);
 int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S, void *scratch,
                  size_t bytes, void *out, void *stream);
 
+/* ---- PixAI tagger (ViTDet-L) block kernels on the same block-scaled main loop (px_kernels.cu) ----
+ * Rows are window-major tokens (px_kernels.cu:1-4): sequence s = rows L s .. L s + L - 1 with L = 576 (windowed
+ * blocks, 9 windows per image) or 5184 (global blocks, one image); rows <= 2^19. LayerNorm is eva_k_ln, attention
+ * eva_k_flash_seq (T = TP = L). */
+/* px_kernels.cu:54-131 k_pqkv: q, k bf16 [rows/L][16][L][64] = RoPE(h8 . Wqkv^T + b) with table row m % L of
+ * cs [L][32][2] on every token, vt bf16 [rows/L][16][64][L] = (h8 . Wv^T + b)^T; w from eva_k_prep_w(perm 1), bias
+ * fp32 [3072] in natural order; q rows of w and bias carry log2(e)/8. */
+int px_k_qkv(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *bias,
+             const float *cs, int L, void *q, void *k, void *vt, int rows, void *stream);
+/* px_kernels.cu:156-190 k_pproj: x fp16 [rows][1024] = x + (a8 . Wo^T + bias) */
+int px_k_proj(const void *a8, const float *as, int lds, const void *w, const float *ws, const float *bias, void *x,
+              int rows, void *stream);
+/* px_kernels.cu:202-241 k_pfc1: m8 E4M3 [rows][4736], ms [37][lds] = block-packed rs * gelu(h8 . W1^T + b1), exact erf
+ * GELU; rs fp32 [4736] may be NULL (all ones). */
+int px_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *bias,
+             const float *rs, void *m8, float *ms, int rows, void *stream);
+/* px_kernels.cu:192-200 k_pfc2: x fp16 [rows][1024] = x + (m8 . W2^T + bias), W2 [1024][4736] */
+int px_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *bias, void *x,
+             int rows, void *stream);
+
 /* ---- on-box ceilings (no reference counterpart; the roofline fractions use peaks measured on the same GPU) ---- */
 /* dense FP8 MFMA: blocks x 256 threads, each wave issuing iters x 8 v_mfma_f32_16x16x128_f8f6f4 on register operands
  * (flops = blocks * 4 * iters * 8 * 65536); out [blocks * 256] keeps the result live */

@@ -599,6 +599,56 @@ void xo_oproj_epi(const float *acc, int M, uint16_t *x)
     for (i = 0; i < (size_t)M * XO_D; i++) x[i] = xo_f32_to_f16(f16f(x[i]) + acc[i]);
 }
 
+/* ---- PixAI (ViTDet-L) block epilogues, px_kernels.cu ---- */
+void xo_px_qkv_epi(const float *acc, int M, int L, const float *bias, const float *cs, uint16_t *q, uint16_t *k,
+                   uint16_t *vt)
+{
+    int m;
+
+#pragma omp parallel for schedule(static)
+    for (m = 0; m < M; m++) {
+        int s = m / L, t = m % L, part, h, i, d;
+        const float *a = acc + (size_t)m * 3072;
+        for (part = 0; part < 2; part++) {
+            uint16_t *dst = part ? k : q;
+            for (h = 0; h < 16; h++)
+                for (i = 0; i < 32; i++) {
+                    const int n = part * 1024 + h * 64 + 2 * i;
+                    const float f0 = a[n] + bias[n], f1 = a[n + 1] + bias[n + 1];
+                    const float c = cs[((size_t)t * 32 + i) * 2], sn = cs[((size_t)t * 32 + i) * 2 + 1];
+                    const float g0 = f0 * c - f1 * sn, g1 = f1 * c + f0 * sn;
+                    dst[(((size_t)s * 16 + h) * L + t) * 64 + 2 * i] = xo_f32_to_bf16(g0);
+                    dst[(((size_t)s * 16 + h) * L + t) * 64 + 2 * i + 1] = xo_f32_to_bf16(g1);
+                }
+        }
+        for (h = 0; h < 16; h++)
+            for (d = 0; d < 64; d++)
+                vt[(((size_t)s * 16 + h) * 64 + d) * L + t] = xo_f32_to_bf16(a[2048 + h * 64 + d] + bias[2048 + h * 64 + d]);
+    }
+}
+
+void xo_px_res_epi(const float *acc, int M, const float *bias, uint16_t *x)
+{
+    size_t i;
+
+    for (i = 0; i < (size_t)M * XO_D; i++) x[i] = xo_f32_to_f16(f16f(x[i]) + (acc[i] + bias[i % XO_D]));
+}
+
+void xo_px_fc1_epi(const float *acc, int M, const float *bias, const float *rs, float *h)
+{
+    int m;
+
+#pragma omp parallel for schedule(static)
+    for (m = 0; m < M; m++) {
+        int u;
+        for (u = 0; u < XO_PX_HID; u++) {
+            const float v = acc[(size_t)m * XO_PX_HID + u] + bias[u];
+            const float g = v * (0.5f * (1.0f + erff(v * 0.70710678f)));
+            h[(size_t)m * XO_PX_HID + u] = rs ? g * rs[u] : g;
+        }
+    }
+}
+
 void xo_embed(const uint16_t *in, const uint16_t *pe, const float *pos, int nb, uint16_t *x)
 {
     int r;

@@ -84,6 +84,18 @@ void xo_fc1_epi(const float *acc, int M, float *h, float *stat);
 void xo_fc2_epi(const float *acc, int M, const float *stat, const float *c, const float *d, uint16_t *x);
 /* out-projection epilogue (eva_kernels.cu:150-160): x = f16(x + acc) */
 void xo_oproj_epi(const float *acc, int M, uint16_t *x);
+/* ---- PixAI tagger (ViTDet-L) block epilogues (px_kernels.cu); rows are window-major tokens m = L s + t ---- */
+#define XO_PX_HID 4736
+/* k_pqkv (px_kernels.cu:82-131): acc fp32 [M][3072] natural columns, f = acc + bias (q's log2(e)/8 is in the weights and
+ * bias given), RoPE on every q, k token with pair (2i, 2i+1) and angle cs[(m % L) * 32 + i], bf16 (RNE);
+ * q, k [M/L][16][L][64], vt [M/L][16][64][L] */
+void xo_px_qkv_epi(const float *acc, int M, int L, const float *bias, const float *cs, uint16_t *q, uint16_t *k,
+                   uint16_t *vt);
+/* k_pproj / k_pfc2 (px_kernels.cu:170-182): x = f16(x + (acc + bias[n])), x fp16 [M][1024] in place */
+void xo_px_res_epi(const float *acc, int M, const float *bias, uint16_t *x);
+/* k_pfc1 (px_kernels.cu:222-233): h [M][4736] = (u (0.5 (1 + erff(u 0.70710678)))) rs[n], u = acc + bias[n] (libm erff;
+ * rs NULL = no multiply), fp32 */
+void xo_px_fc1_epi(const float *acc, int M, const float *bias, const float *rs, float *h);
 /* patch embedding + position (k_pe + k_embed, eva_kernels.cu:21-33, 126-130): in fp16 [nb*1024][592],
  * pe fp16 [1024][592], pos fp32 [1025][1024] -> x fp16 [nb*1025][1024]; x[b,0] = f16(pos[0]),
  * x[b,1+p] = f16((float)dot + pos[1+p]) with the dot in fp64 */

@@ -12,7 +12,7 @@ def declared_functions():
     for h in glob.glob(os.path.join(REPO_DIR, "include", "*.h")):
         src = open(h).read()
         src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(eva_\w+)\s*\(", src, flags=re.M):
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b((?:eva|px)_\w+)\s*\(", src, flags=re.M):
             names.add(m.group(1))
     return names
 
@@ -32,6 +32,18 @@ def test_bad_shapes_rejected_without_gpu():
     assert L.lib.eva_k_gemm(None, 100, None, 1, None, None, 1, 128, 100, None, 128, 0, None) == -1
     assert L.lib.eva_k_quant_act(None, 0, 100, 1, 100, None, 100, None, 1, None) == -1
     assert L.lib.eva_k_quant_w(None, 128, 100, None, None, None) == -1
+
+
+def test_px_bad_shapes_rejected_without_gpu():
+    """The PixAI block kernels check rows, L and lds before any HIP call (rows not a multiple of L, L not a multiple
+    of 64, lds < rows, rows past 2^19)."""
+    from xtagger_amd import lib as L
+    n = None
+    assert L.lib.px_k_qkv(n, n, 1152, n, n, n, n, 576, n, n, n, 1000, n) == -1
+    assert L.lib.px_k_qkv(n, n, 1152, n, n, n, n, 96, n, n, n, 1152, n) == -1
+    assert L.lib.px_k_proj(n, n, 10, n, n, n, n, 64, n) == -1
+    assert L.lib.px_k_fc1(n, n, 10, n, n, n, n, n, n, 64, n) == -1
+    assert L.lib.px_k_fc2(n, n, 1 << 20, n, n, n, n, (1 << 19) + 1, n) == -1
 
 
 def test_open_rejects_bad_header(tmp_path):

@@ -1,0 +1,244 @@
+"""GPU parity of the PixAI tagger (ViTDet-L) block kernels (px_k_qkv, px_k_proj, px_k_fc1, px_k_fc2; px_kernels.cu)
+against the oracle, through the C-ABI, at the real shapes: one image is 5184 window-major token rows, attention over
+9 windows of L = 576 or one global sequence of L = 5184.
+
+As for the wd kernels, the oracle applies each epilogue to the fp64 product of the same packed operands; the check
+is one rounding unit of the output type plus 2e-4 of the terms (the matrix core's summation order), and for the
+E4M3 repack of fc1: scales within 1e-4, codes equal except where a value sits on a rounding boundary.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+D, HID, T_IMG = 1024, 4736, 5184
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ok(rc, what):
+    assert rc == 0, f"{what} returned {rc}"
+    torch.cuda.synchronize()
+
+
+_KEEP = []
+
+
+@pytest.fixture(autouse=True)
+def _release_device_copies():
+    yield
+    _KEEP.clear()
+
+
+def _d(a, dev):
+    t = a.to(dev) if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    _KEEP.append(t)
+    return t
+
+
+def _bf16_f32(u16):
+    return (np.asarray(u16, np.uint32) << 16).view(np.float32)
+
+
+def _f16_f32(u16):
+    return np.asarray(u16, np.uint16).view(np.float16).astype(np.float32)
+
+
+def _check_close(name, got, ref, scale, unit):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    bound = unit * np.abs(ref) + 2e-4 * scale
+    worst = float((err / bound).max())
+    _say(f"  {name}: worst err / bound {worst:.3f}, elements differing {np.mean(err > 0):.2e}")
+    assert worst <= 1.0, name
+
+
+def _act(orc, M, K, seed, scale=1.0, lds=None):
+    x = (np.random.default_rng(seed).standard_normal((M, K)) * scale).astype(np.float32)
+    q, s = orc.quant_act(x, lds=lds)
+    return q, s
+
+
+def _w(orc, N, K, seed, std=0.02):
+    w = (np.random.default_rng(seed).standard_normal((N, K)) * std).astype(np.float32)
+    return orc.quant_w(w)
+
+
+def _acc(orc, qa, sa, qw, sw, N):
+    return orc.gemm_f64_rows(qa, sa, qw, sw, N, np.arange(qa.shape[0])).astype(np.float32)
+
+
+def _rope_table(L, seed):
+    ang = np.random.default_rng(seed).random((L, 32)) * 6.28
+    return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+
+
+def _run_qkv(dev, xt, qa, sa, lds, w16, bias, cs, L, M):
+    d_wq = torch.zeros((3 * D, D), dtype=torch.uint8, device=dev)
+    d_ws = torch.zeros((24, 8), dtype=torch.float32, device=dev)
+    scratch = torch.empty((3 * D, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_prep_w(xt.ptr(_d(w16, dev)), D, 3 * D, D, 3 * D, D, 1, None, xt.ptr(scratch), xt.ptr(d_wq),
+                            xt.ptr(d_ws), _st()), "prep")
+    S = M // L
+    q = torch.zeros((S, 16, L, 64), dtype=torch.int16, device=dev)
+    k = torch.zeros_like(q)
+    vt = torch.zeros((S, 16, 64, L), dtype=torch.int16, device=dev)
+    _ok(xt.lib.px_k_qkv(xt.ptr(qa), xt.ptr(sa), lds, xt.ptr(d_wq), xt.ptr(d_ws), xt.ptr(_d(bias, dev)),
+                        xt.ptr(_d(cs, dev)), L, xt.ptr(q), xt.ptr(k), xt.ptr(vt), M, _st()), "px_k_qkv")
+    return q, k, vt
+
+
+@pytest.mark.parametrize("L,S", [(576, 9), (5184, 1), (576, 2)])
+def test_px_qkv_bias_rope_layouts(dev, xt, orc, L, S):
+    M = L * S
+    _say(f"px_k_qkv L={L} S={S}")
+    qa, sa = _act(orc, M, D, 101)
+    r = np.random.default_rng(102)
+    w16 = (r.standard_normal((3 * D, D)) * 0.02).astype(np.float16)
+    bias = (r.standard_normal(3 * D) * 0.5).astype(np.float32)
+    cs = _rope_table(L, 103)
+    q, k, vt = _run_qkv(dev, xt, _d(qa, dev), _d(sa, dev), M, w16, bias, cs, L, M)
+    qw, sw = orc.quant_w(w16.astype(np.float32))
+    acc = _acc(orc, qa, sa, qw, sw, 3 * D)
+    rq, rk, rvt = orc.px_qkv_epi(acc, L, bias, cs)
+    scale = np.abs(acc + bias).max()
+    for name, got, ref in (("q", q, rq), ("k", k, rk), ("vt", vt, rvt)):
+        _check_close(name, _bf16_f32(got.cpu().numpy().view(np.uint16)), _bf16_f32(ref), scale, 2.0 ** -7)
+
+
+@pytest.mark.parametrize("K", [1024, 4736])
+def test_px_residual_bias(dev, xt, orc, K):
+    """px_k_proj (K = 1024) and px_k_fc2 (K = 4736): x = f16(x + (a8 . W^T + b)) over one image (5184 rows)."""
+    M = T_IMG
+    _say(f"px residual K={K}")
+    lds = M + 3
+    qa, sa = _act(orc, M, K, 111 + K, lds=lds)
+    qw, sw = _w(orc, D, K, 112)
+    r = np.random.default_rng(113)
+    bias = (r.standard_normal(D) * 0.3).astype(np.float32)
+    x = (r.standard_normal((M, D)) * 2).astype(np.float16)
+    d_x = _d(x, dev)
+    fn = xt.lib.px_k_proj if K == D else xt.lib.px_k_fc2
+    _ok(fn(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa, dev)), lds, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)),
+           xt.ptr(_d(bias, dev)), xt.ptr(d_x), M, _st()), "px residual")
+    acc = _acc(orc, qa, sa[:, :M], qw, sw, D)
+    ref = orc.px_res_epi(acc, bias, x.view(np.uint16))
+    _check_close("x", _f16_f32(d_x.cpu().numpy().view(np.uint16)), _f16_f32(ref), np.abs(acc + bias).max(), 2.0 ** -10)
+
+
+@pytest.mark.parametrize("with_rs", [False, True])
+def test_px_fc1_gelu_pack(dev, xt, orc, with_rs):
+    M = T_IMG
+    _say(f"px_k_fc1 rs={with_rs}")
+    lds = M + 5
+    qa, sa = _act(orc, M, D, 121, lds=lds)
+    qw, sw = _w(orc, HID, D, 122, std=0.04)
+    r = np.random.default_rng(123)
+    bias = (r.standard_normal(HID) * 0.5).astype(np.float32)
+    rs = (r.random(HID) * 1.5 + 0.25).astype(np.float32) if with_rs else None
+    d_m8 = torch.zeros((M, HID), dtype=torch.uint8, device=dev)
+    d_ms = torch.zeros((HID // 128, lds), dtype=torch.float32, device=dev)
+    _ok(xt.lib.px_k_fc1(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa, dev)), lds, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)),
+                        xt.ptr(_d(bias, dev)), None if rs is None else xt.ptr(_d(rs, dev)), xt.ptr(d_m8), xt.ptr(d_ms),
+                        M, _st()), "px_k_fc1")
+    h = orc.px_fc1_epi(_acc(orc, qa, sa[:, :M], qw, sw, HID), bias, rs)
+    q, s = orc.quant_act(h)
+    ms = d_ms.cpu().numpy()
+    assert (ms[:, M:] == 0).all()                             # nothing written past `rows`
+    ms = ms[:, :M]
+    assert np.abs(ms / s - 1).max() < 1e-4
+    m8 = d_m8.cpu().numpy()
+    diff = np.mean(m8 != q)
+    _say(f"  E4M3 codes differing: {diff:.2e}")
+    assert diff < 2e-3
+    dq = orc.e4m3_decode(m8) * np.repeat(ms.T, 128, 1)
+    assert np.abs(dq - h).max() <= 2.0 ** -3 * np.abs(h).max() + 1e-6
+
+
+def test_px_block_chain_windowed(dev, xt, orc):
+    """One ViTDet-L windowed block over one image, each kernel's input the previous kernel's GPU output
+    (px.h:130-156 order: LN1 -> qkv -> windowed attention -> proj -> LN2 -> fc1 -> fc2), every hand-off checked
+    against the oracle step applied to the same input."""
+    L, M = 576, T_IMG
+    S = M // L
+    _say("px block chain L=576")
+    r = np.random.default_rng(131)
+    x0 = (r.standard_normal((M, D)) * 1.5).astype(np.float16)
+    g1, b1 = (1 + 0.1 * r.standard_normal(D)).astype(np.float32), (0.1 * r.standard_normal(D)).astype(np.float32)
+    g2, b2 = (1 + 0.1 * r.standard_normal(D)).astype(np.float32), (0.1 * r.standard_normal(D)).astype(np.float32)
+    w16 = (r.standard_normal((3 * D, D)) * 0.03).astype(np.float16)
+    w16[:D] *= np.float16(np.log2(np.e) / 8)                  # q rows carry log2(e)/8
+    bqkv = (r.standard_normal(3 * D) * 0.1).astype(np.float32)
+    bqkv[:D] *= np.log2(np.e) / 8
+    cs = _rope_table(L, 132)
+    qwo, swo = _w(orc, D, D, 133)
+    qw1, sw1 = _w(orc, HID, D, 134, std=0.03)
+    qw2, sw2 = _w(orc, D, HID, 135)
+    bo = (r.standard_normal(D) * 0.1).astype(np.float32)
+    bf1 = (r.standard_normal(HID) * 0.2).astype(np.float32)
+    bf2 = (r.standard_normal(D) * 0.1).astype(np.float32)
+    lds = M
+    d_x = _d(x0, dev)
+    d_h8 = torch.zeros((M, D), dtype=torch.uint8, device=dev)
+    d_hs = torch.zeros((8, lds), dtype=torch.float32, device=dev)
+    # LN1
+    _ok(xt.lib.eva_k_ln(xt.ptr(d_x), xt.ptr(_d(g1, dev)), xt.ptr(_d(b1, dev)), xt.ptr(d_h8), xt.ptr(d_hs), M, lds,
+                        _st()), "ln1")
+    h8, hs, _ = orc.ln_quant(x0.view(np.uint16), g1, b1)
+    assert (d_h8.cpu().numpy() == h8).all() and (d_hs.cpu().numpy() == hs).all()
+    # qkv
+    q, k, vt = _run_qkv(dev, xt, d_h8, d_hs, lds, w16, bqkv, cs, L, M)
+    qw, sw = orc.quant_w(w16.astype(np.float32))
+    acc = _acc(orc, h8, hs, qw, sw, 3 * D)
+    rq, rk, rvt = orc.px_qkv_epi(acc, L, bqkv, cs)
+    for name, got, ref in (("q", q, rq), ("k", k, rk), ("vt", vt, rvt)):
+        _check_close(name, _bf16_f32(got.cpu().numpy().view(np.uint16)), _bf16_f32(ref), np.abs(acc + bqkv).max(),
+                     2.0 ** -7)
+    # windowed attention over the kernel's own q, k, vt
+    d_o8 = torch.zeros((M, D), dtype=torch.uint8, device=dev)
+    d_os = torch.zeros((8, lds), dtype=torch.float32, device=dev)
+    d_o32 = torch.zeros((M, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_flash_seq(xt.ptr(q), xt.ptr(k), xt.ptr(vt), xt.ptr(d_o8), xt.ptr(d_os), lds, S, L, L,
+                               xt.ptr(d_o32), _st()), "flash_seq")
+    ref = orc.attention_seq(q.cpu().numpy(), k.cpu().numpy(), vt.cpu().numpy(), S, L, L)
+    o = d_o32.cpu().numpy().astype(np.float64)
+    assert np.abs(o - ref).max() <= 4e-3 * np.abs(ref).max()
+    # proj
+    o8, os_ = d_o8.cpu().numpy(), d_os.cpu().numpy()
+    x1 = d_x.cpu().numpy().view(np.uint16).copy()
+    _ok(xt.lib.px_k_proj(xt.ptr(d_o8), xt.ptr(d_os), lds, xt.ptr(_d(qwo, dev)), xt.ptr(_d(swo, dev)),
+                         xt.ptr(_d(bo, dev)), xt.ptr(d_x), M, _st()), "proj")
+    acc = _acc(orc, o8, os_, qwo, swo, D)
+    x1r = orc.px_res_epi(acc, bo, x1)
+    x1g = d_x.cpu().numpy().view(np.uint16)
+    _check_close("x after proj", _f16_f32(x1g), _f16_f32(x1r), np.abs(acc + bo).max(), 2.0 ** -10)
+    # LN2 -> fc1
+    _ok(xt.lib.eva_k_ln(xt.ptr(d_x), xt.ptr(_d(g2, dev)), xt.ptr(_d(b2, dev)), xt.ptr(d_h8), xt.ptr(d_hs), M, lds,
+                        _st()), "ln2")
+    h8, hs, _ = orc.ln_quant(x1g, g2, b2)
+    assert (d_h8.cpu().numpy() == h8).all() and (d_hs.cpu().numpy() == hs).all()
+    d_m8 = torch.zeros((M, HID), dtype=torch.uint8, device=dev)
+    d_ms = torch.zeros((HID // 128, lds), dtype=torch.float32, device=dev)
+    _ok(xt.lib.px_k_fc1(xt.ptr(d_h8), xt.ptr(d_hs), lds, xt.ptr(_d(qw1, dev)), xt.ptr(_d(sw1, dev)),
+                        xt.ptr(_d(bf1, dev)), None, xt.ptr(d_m8), xt.ptr(d_ms), M, _st()), "fc1")
+    hh = orc.px_fc1_epi(_acc(orc, h8, hs, qw1, sw1, HID), bf1)
+    qh, sh = orc.quant_act(hh)
+    m8, ms = d_m8.cpu().numpy(), d_ms.cpu().numpy()
+    assert np.mean(m8 != qh) < 2e-3 and np.abs(ms / sh - 1).max() < 1e-4
+    # fc2 over the kernel's own packed hidden activations
+    x2 = x1g.copy()
+    _ok(xt.lib.px_k_fc2(xt.ptr(d_m8), xt.ptr(d_ms), lds, xt.ptr(_d(qw2, dev)), xt.ptr(_d(sw2, dev)),
+                        xt.ptr(_d(bf2, dev)), xt.ptr(d_x), M, _st()), "fc2")
+    acc = _acc(orc, m8, ms, qw2, sw2, D)
+    x2r = orc.px_res_epi(acc, bf2, x2)
+    _check_close("x after fc2", _f16_f32(d_x.cpu().numpy().view(np.uint16)), _f16_f32(x2r), np.abs(acc + bf2).max(),
+                 2.0 ** -10)
+

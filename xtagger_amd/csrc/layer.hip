@@ -5,104 +5,9 @@
 //
 // Token rows: m = 1025 b + t for image b, token t (t = 0 is cls). Activations E4M3 [rows][K] with 1x128 scale
 // planes [K/128][lds]; residual x fp16 [rows][1024].
-#include "gemm_core.h"
-#include "xt_abi.h"
+#include "layer_core.h"
 
-typedef BsCfg<256, 256, 4, 2, 2> LayerCfg;  // 8 waves of 64 x 128: two heads (qkv) or 64 SwiGLU units (fc1) per wave
 typedef BsCfg<64, 128, 1, 2, 3> HeadCfg;    // head: few rows, 10861 columns
-
-// Shared memory of the layer kernels: the main-loop stages, reused by the epilogues (one 64 x 68 fp32 residual slice
-// per wave, one [128][66] bf16 transpose slice per wave, or the fc1 h tile), then 2 KB of per-row statistics and
-// 2 KB of per-column fold terms that k_fc2 fills while its first stages load.
-constexpr int LAYER_RES_SLICE = 64 * 68 * 4;
-constexpr int LAYER_ROWSTAT = LayerCfg::NW * LAYER_RES_SLICE;  // byte offset of the per-row statistics
-constexpr int LAYER_SMEM = LAYER_ROWSTAT + 4096;                 // 2 KB row statistics + 2 KB column terms
-static_assert(LAYER_ROWSTAT >= LayerCfg::LDS, "row statistics sit past the main-loop stages");
-static_assert(LAYER_SMEM <= 160 * 1024, "layer kernels fit the LDS");
-static_assert(LayerCfg::NW * 128 * 66 * 2 <= LAYER_ROWSTAT, "v transpose slices fit");
-
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b)
-{
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), b2));
-}
-
-// The layer kernels take their weights dense (w, wx unused) or 2:4-sparse (SP: w = pack24 values, wx = indices).
-template <class C, bool SP, class Pre = BsNoPre>
-__device__ __forceinline__ void layer_mainloop(const uint8_t *A, int lda, const float *sa, int lds, const uint8_t *w,
-                                               const uint32_t *wx, const float *ws, int rows, int Npad, int K, int m0,
-                                               int n0, uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre())
-{
-    static_assert(!SP || C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
-    if constexpr (SP) bs_mainloop_sp<C>(A, lda, sa, lds, w, wx, ws, rows, Npad, K, m0, n0, smem, acc, pre);
-    else bs_mainloop<C>(A, lda, sa, lds, w, ws, rows, Npad, K, m0, n0, smem, acc, pre);
-}
-
-template <class C>
-__device__ __forceinline__ void layer_tile(int M, int N, int &m0, int &n0)
-{
-    int tm, tn;
-    tile_of_block((M + C::BM - 1) / C::BM, (N + C::BN - 1) / C::BN, tm, tn);
-    m0 = tm * C::BM;
-    n0 = tn * C::BN;
-}
-
-// Residual update x = f16(x + y) of a wave's 64 x (16 TN) tile, y in the MFMA C layout, in passes of 64 columns.
-// The wave parks 64 x 64 of y in its own LDS slice (row stride 68 floats: the 64 lanes of one store hit 64 different
-// banks), then each lane updates 8 consecutive halves with one 16-byte load and store, so one wave instruction
-// covers 8 rows of 128 bytes. Every x load of the tile is issued before the first store (one memory round trip for
-// the whole update), through a buffer descriptor that ends at row `rows`: rows past it load zero and their stores
-// are dropped, with no branch between the loads.
-struct ResIdentity {
-    __device__ __forceinline__ float operator()(int, int, int, float v) const { return v; }
-};
-
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-
-// f(i, j, r, y) maps each accumulator to the value added (row m0 + mw + 16 i + 4 (lane >> 4) + r, column tile j).
-template <class C, class F = ResIdentity>
-__device__ __forceinline__ void residual_add(uint8_t *slices, v4f (&y)[C::TM][C::TN], uint16_t *__restrict__ x,
-                                             int mw, int nw, int rows, F f = F())
-{
-    static_assert(C::TM == 4 && C::TN % 4 == 0, "64-row wave tiles, whole 64-column passes");
-    constexpr int NP = C::TN / 4;
-    float *tr = (float *)(slices + (threadIdx.x >> 6) * LAYER_RES_SLICE);
-    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-    const int rs = lane >> 3, ch = lane & 7;
-    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, (uint32_t)rows * XT_D * 2u);
-    const uint32_t off0 = (uint32_t)(((mw + rs) * XT_D + nw + 8 * ch) * 2);
-    v4u xv[NP][8];
-#pragma unroll
-    for (int pass = 0; pass < NP; pass++)
-#pragma unroll
-        for (int it = 0; it < 8; it++)
-            xv[pass][it] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
-#pragma unroll
-    for (int pass = 0; pass < NP; pass++) {
-        if (pass) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous pass's slice reads are done
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    tr[(16 * i + 4 * g + r) * 68 + 16 * j + c16] = f(i, 4 * pass + j, r, y[i][4 * pass + j][r]);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
-#pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int rr = 8 * it + rs;
-            const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
-            const v4u v = xv[pass][it];
-            v4u o;
-            o[0] = f2h(h2f(v[0] & 0xFFFF) + a.x) | (uint32_t)f2h(h2f(v[0] >> 16) + a.y) << 16;
-            o[1] = f2h(h2f(v[1] & 0xFFFF) + a.z) | (uint32_t)f2h(h2f(v[1] >> 16) + a.w) << 16;
-            o[2] = f2h(h2f(v[2] & 0xFFFF) + b.x) | (uint32_t)f2h(h2f(v[2] >> 16) + b.y) << 16;
-            o[3] = f2h(h2f(v[3] & 0xFFFF) + b.z) | (uint32_t)f2h(h2f(v[3] >> 16) + b.w) << 16;
-            __builtin_amdgcn_raw_buffer_store_b128(o, rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------------------------------------------
 // k_qkv: h8 [rows][1024] x Wqkv [3072][1024] -> q, k bf16 [nb][16][1088][64] (RoPE on patch tokens), vt bf16
@@ -282,7 +187,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     const int k8 = threadIdx.x & 7, r0 = threadIdx.x >> 3;
     uint32_t rb[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) rb[c] = (uint32_t)(r0 * 128 + (((4 * k8 + c) ^ r0) & 7 | ((4 * k8 + c) & ~7)) * 4);
+    for (int c = 0; c < 4; c++) rb[c] = (uint32_t)(r0 * 128 + ((((4 * k8 + c) ^ r0) & 7) | ((4 * k8 + c) & ~7)) * 4);
 #pragma unroll
     for (int it = 0; it < C::BM * 8 / C::NT; it++) {
         const int idx = threadIdx.x + it * C::NT, rr = idx >> 3, u0 = (idx & 7) * 16, m = m0 + rr;
@@ -488,10 +393,6 @@ __global__ void __launch_bounds__(256) k_pe(const uint16_t *__restrict__ in, con
 // ---------------------------------------------------------------------------------------------------------------
 // C-ABI launchers
 // ---------------------------------------------------------------------------------------------------------------
-static unsigned layer_grid(int rows, int N, int BM, int BN) { return (unsigned)(((rows + BM - 1) / BM) * ((N + BN - 1) / BN)); }
-
-#define XT_ALIGNED(p) ((((uintptr_t)(p)) & 15) == 0)
-
 template <bool SP>
 static int qkv_launch(const char *what, const void *h8, const float *hs, int lds, const void *w, const void *wx,
                       const float *ws, const float *cs, void *q, void *k, void *vt, int rows, void *stream)

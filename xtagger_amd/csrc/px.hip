@@ -1,0 +1,274 @@
+// px.hip - the ViTDet-L (PixAI tagger) block GEMMs on the block-scaled main loop, with the epilogues of
+// src/engine/px_kernels.cu: k_pqkv (54-131, bias + RoPE at table row m % L + the attention layouts), k_pproj / k_pfc2
+// (156-200, residual + bias) and k_pfc1 (202-241, bias + exact-erf GELU + per-unit multiplier, packed to E4M3).
+//
+// Tokens are window-major for the whole network (px_kernels.cu:1-4): image b's 72 x 72 patches are 9 windows of
+// 24 x 24, window w = rows 5184 b + 576 w .. + 575. A windowed block's attention runs over sequences of L = 576
+// rows, a global block's over L = 5184; both are row m = L s + t of sequence s, token t, so only L differs.
+// Activations E4M3 [rows][K] with 1x128 scale planes [K/128][lds]; residual x fp16 [rows][1024]; the reference's
+// per-tensor alpha and static quantization scales are the block scales here.
+#include "layer_core.h"
+
+#define PX_HID 4736  // MLP hidden units (37 blocks of 128)
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------------------------------------------
+// k_px_qkv: h8 [rows][1024] x Wqkv [3072][1024] + bias -> q, k bf16 [S][16][L][64] (RoPE on every token with table
+// row t = m % L, cs [L][32] (cos, sin) of pair i = dims 2i, 2i+1), vt bf16 [S][16][64][L]; rows = S L. Weight rows of
+// q and k are pair-split as for the wd model (column tile 2p of a head holds dims 2i, tile 2p+1 dims 2i+1 of pair
+// i = 16p + (lane & 15)); the bias stays in natural order. q rows of W and of the bias carry log2(e)/8 (the
+// reference's cq, px_kernels.cu:84).
+// ---------------------------------------------------------------------------------------------------------------
+template <bool SP>
+__global__ void __launch_bounds__(LayerCfg::NT) k_px_qkv(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
+                                                        int lds, const uint8_t *__restrict__ w,
+                                                        const uint32_t *__restrict__ wx, const float *__restrict__ ws,
+                                                        const float *__restrict__ bias, const float *__restrict__ cs,
+                                                        int L, uint16_t *__restrict__ q, uint16_t *__restrict__ k,
+                                                        uint16_t *__restrict__ vt, int rows)
+{
+    using C = LayerCfg;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[LAYER_SMEM];
+    v4f acc[C::TM][C::TN];
+    int m0, n0, wm0, wn0;
+    layer_tile<C>(rows, 3 * XT_D, m0, n0);
+    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, acc);
+    bs_wave_origin<C>(wm0, wn0);
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const int part = n0 >> 10, head0 = ((n0 & 1023) + wn0) >> 6;
+    if (part < 2) {
+        // every (cos, sin) pair of the tile is loaded before the first store. Stores go through a descriptor that ends
+        // at sequence S: rows past `rows` map to sequence S or later and are dropped without a branch.
+        const __amdgpu_buffer_rsrc_t rc = buf_rsrc(cs, (uint32_t)L * 32u * 8u);
+        const __amdgpu_buffer_rsrc_t rd = buf_rsrc(part ? k : q, (uint32_t)rows * XT_D * 2u);
+        v2f bq[2][2];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+                bq[hh][p] = *(const v2f *)(bias + part * XT_D + (head0 + hh) * XT_HD + 2 * (16 * p + c16));
+        v2f rot[C::TM][4][2];
+        uint32_t base[C::TM][4];  // element offset of (sequence, head head0, token), dims 0
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm0 + 16 * i + 4 * g + r, s = m / L, t = m - s * L;
+                base[i][r] = ((uint32_t)(s * XT_NH + head0) * (uint32_t)L + (uint32_t)t) * XT_HD;
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    rot[i][r][p] = __builtin_bit_cast(
+                        v2f, __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(((uint32_t)t * 32u + 16 * p + c16) * 8u), 0, 0));
+            }
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                    for (int p = 0; p < 2; p++) {
+                        const int pi = 16 * p + c16;
+                        const float f0 = acc[i][4 * hh + 2 * p][r] + bq[hh][p].x;
+                        const float f1 = acc[i][4 * hh + 2 * p + 1][r] + bq[hh][p].y;
+                        const v2f a = rot[i][r][p];
+                        const float g0 = f0 * a.x - f1 * a.y, g1 = f1 * a.x + f0 * a.y;
+                        const uint32_t off = (base[i][r] + (uint32_t)(hh * L * XT_HD + 2 * pi)) * 2u;
+                        __builtin_amdgcn_raw_buffer_store_b32(pk_bf16(g0, g1), rd, (int)off, 0, 0);
+                    }
+        return;
+    }
+    // v (+ bias): transpose the wave's 64 rows x 128 dims (two heads) through LDS, then lanes walk rows (consecutive
+    // tokens of one sequence: L is a multiple of 64 and the wave's 64 rows start on a multiple of 64)
+    float bv[C::TN];
+#pragma unroll
+    for (int j = 0; j < C::TN; j++) bv[j] = bias[n0 + wn0 + 16 * j + c16];
+    uint16_t *tr = (uint16_t *)(smem + (threadIdx.x >> 6) * 128 * 66 * 2);  // [128 dims][66] bf16, padded rows
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int j = 0; j < C::TN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                tr[(16 * j + c16) * 66 + 16 * i + 4 * g + r] = (uint16_t)pk_bf16(acc[i][j][r] + bv[j], 0.f);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int m = m0 + wm0 + lane;
+    if (m < rows) {
+        const int s = m / L, t = m - s * L;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            uint16_t *dst = vt + ((size_t)s * XT_NH + head0 + hh) * XT_HD * L + t;
+#pragma unroll 8
+            for (int d = 0; d < XT_HD; d++) dst[(size_t)d * L] = tr[(64 * hh + d) * 66 + lane];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// k_px_res: x [rows][1024] = f16(x + (a8 . W^T + bias)), K = 1024 (attention out-projection, k_pproj) or 4736 (fc2,
+// k_pfc2). The reference rounds (x + alpha acc) + b in fp32 (px_kernels.cu:178); here acc + b is formed first: the
+// two orders differ by at most one fp32 rounding before the fp16 store.
+// ---------------------------------------------------------------------------------------------------------------
+struct PxAddBias {
+    float b[LayerCfg::TN];  // the lane's column biases, held by value (registers)
+    __device__ __forceinline__ float operator()(int, int j, int, float v) const { return v + b[j]; }
+};
+
+template <bool SP, int K>
+__global__ void __launch_bounds__(LayerCfg::NT) k_px_res(const uint8_t *__restrict__ a8, const float *__restrict__ as,
+                                                        int lds, const uint8_t *__restrict__ w,
+                                                        const uint32_t *__restrict__ wx, const float *__restrict__ ws,
+                                                        const float *__restrict__ bias, uint16_t *__restrict__ x,
+                                                        int rows)
+{
+    using C = LayerCfg;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[LAYER_SMEM];
+    v4f acc[C::TM][C::TN];
+    int m0, n0, wm0, wn0;
+    layer_tile<C>(rows, XT_D, m0, n0);
+    layer_mainloop<C, SP>(a8, K, as, lds, w, wx, ws, rows, XT_D, K, m0, n0, smem, acc);
+    bs_wave_origin<C>(wm0, wn0);
+    const int c16 = threadIdx.x & 15;
+    PxAddBias f;
+#pragma unroll
+    for (int j = 0; j < C::TN; j++) f.b[j] = bias[n0 + wn0 + 16 * j + c16];
+    residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows, f);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// k_px_fc1: h8 [rows][1024] x W1 [4736][1024] -> h = rs (gelu(acc + b1)), gelu(u) = u (0.5 (1 + erf(u / sqrt 2)))
+// (exact erf, px_kernels.cu:228-231; rs may be NULL = 1), packed to m8 [rows][4736] E4M3 with 1x128 scales
+// ms [37][lds]. A wave's 128 columns are one scale block: each row's |max| meets in a 16-lane DPP reduction, the
+// values are scaled in registers, parked in the wave's own LDS slice 64 columns at a time and stored 8 consecutive
+// bytes per lane (8 rows of 64 bytes per wave instruction). The second half of the last column tile lies past
+// unit 4736 and stores nothing.
+// ---------------------------------------------------------------------------------------------------------------
+template <bool SP>
+__global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
+                                                        int lds, const uint8_t *__restrict__ w,
+                                                        const uint32_t *__restrict__ wx, const float *__restrict__ ws,
+                                                        const float *__restrict__ bias, const float *__restrict__ rs,
+                                                        uint8_t *__restrict__ m8, float *__restrict__ ms, int rows)
+{
+    using C = LayerCfg;
+    static_assert(C::TM == 4 && C::TN == 8 && C::WN == 128, "a wave tile is 64 rows x one 128-unit scale block");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[LAYER_SMEM];
+    v4f acc[C::TM][C::TN];
+    int m0, n0, wm0, wn0;
+    layer_tile<C>(rows, PX_HID, m0, n0);
+    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, PX_HID, XT_D, m0, n0, smem, acc);
+    bs_wave_origin<C>(wm0, wn0);
+    const int blk = (n0 + wn0) >> 7;
+    if (blk >= PX_HID / 128) return;  // no block barrier follows: the epilogue uses the wave's own slice only
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    float bj[C::TN], rj[C::TN];
+#pragma unroll
+    for (int j = 0; j < C::TN; j++) {
+        const int u = 128 * blk + 16 * j + c16;
+        bj[j] = bias[u];
+        rj[j] = rs ? rs[u] : 1.0f;
+    }
+    float inv[C::TM][4];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float amax = 0.f;
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                const float u = acc[i][j][r] + bj[j];
+                const float v = (u * (0.5f * (1.0f + erff(u * 0.70710678f)))) * rj[j];
+                acc[i][j][r] = v;
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
+            }
+            amax = row16_max(amax);
+            const float sc = block_scale(amax);
+            inv[i][r] = 1.0f / sc;
+            const int m = m0 + wm0 + 16 * i + 4 * g + r;
+            if (c16 == 0 && m < rows) ms[(size_t)blk * lds + m] = sc;
+        }
+    float *tr = (float *)(smem + (threadIdx.x >> 6) * LAYER_RES_SLICE);
+    const __amdgpu_buffer_rsrc_t rm = buf_rsrc(m8, (uint32_t)rows * PX_HID);
+    const int rsub = lane >> 3, ch = lane & 7;
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+        if (pass) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous pass's slice reads are done
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    tr[(16 * i + 4 * g + r) * 68 + 16 * jj + c16] = acc[i][4 * pass + jj][r] * inv[i][r];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const int rr = 8 * it + rsub;
+            const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
+            typedef unsigned v2u __attribute__((ext_vector_type(2)));
+            const v2u o = {e4_pack4_scaled(a.x, a.y, a.z, a.w), e4_pack4_scaled(b.x, b.y, b.z, b.w)};
+            const uint32_t off = (uint32_t)(m0 + wm0 + rr) * PX_HID + (uint32_t)(128 * blk + 64 * pass + 8 * ch);
+            __builtin_amdgcn_raw_buffer_store_b64(o, rm, (int)off, 0, 0);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// C-ABI launchers
+// ---------------------------------------------------------------------------------------------------------------
+static int px_rows_ok(const char *what, int rows, int lds)
+{
+    // every byte offset (rows x 4736 bytes of fc1's output and fc2's input, rows x 2048 of q / k) stays below 2^32
+    if (rows <= 0 || lds < rows || rows > (1 << 19)) return xt_fail(what, "bad shape (0 < rows <= 2^19, lds >= rows)");
+    return 0;
+}
+
+extern "C" int px_k_qkv(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *bias,
+                        const float *cs, int L, void *q, void *k, void *vt, int rows, void *stream)
+{
+    if (px_rows_ok("px_k_qkv", rows, lds)) return -1;
+    if (L <= 0 || L % 64 || rows % L) return xt_fail("px_k_qkv", "L must be a positive multiple of 64 dividing rows");
+    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || ((uintptr_t)bias & 7) || ((uintptr_t)cs & 7))
+        return xt_fail("px_k_qkv", "h8 and w must be 16-byte aligned, bias and cs 8-byte aligned");
+    hipLaunchKernelGGL(k_px_qkv<false>, dim3(layer_grid(rows, 3 * XT_D, LayerCfg::BM, LayerCfg::BN)),
+                       dim3(LayerCfg::NT), 0, (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w,
+                       (const uint32_t *)nullptr, ws, bias, cs, L, (uint16_t *)q, (uint16_t *)k, (uint16_t *)vt, rows);
+    return xt_check("px_k_qkv");
+}
+
+template <int K>
+static int px_res_launch(const char *what, const void *a8, const float *as, int lds, const void *w, const float *ws,
+                         const float *bias, void *x, int rows, void *stream)
+{
+    if (px_rows_ok(what, rows, lds)) return -1;
+    if (!XT_ALIGNED(a8) || !XT_ALIGNED(w)) return xt_fail(what, "a8 and w must be 16-byte aligned");
+    hipLaunchKernelGGL((k_px_res<false, K>), dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT),
+                       0, (hipStream_t)stream, (const uint8_t *)a8, as, lds, (const uint8_t *)w,
+                       (const uint32_t *)nullptr, ws, bias, (uint16_t *)x, rows);
+    return xt_check(what);
+}
+
+extern "C" int px_k_proj(const void *a8, const float *as, int lds, const void *w, const float *ws, const float *bias,
+                         void *x, int rows, void *stream)
+{
+    return px_res_launch<XT_D>("px_k_proj", a8, as, lds, w, ws, bias, x, rows, stream);
+}
+
+extern "C" int px_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *bias,
+                        void *x, int rows, void *stream)
+{
+    return px_res_launch<PX_HID>("px_k_fc2", m8, ms, lds, w, ws, bias, x, rows, stream);
+}
+
+extern "C" int px_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *bias,
+                        const float *rs, void *m8, float *ms, int rows, void *stream)
+{
+    if (px_rows_ok("px_k_fc1", rows, lds)) return -1;
+    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || ((uintptr_t)m8 & 7))
+        return xt_fail("px_k_fc1", "h8 and w must be 16-byte aligned, m8 8-byte aligned");
+    hipLaunchKernelGGL(k_px_fc1<false>, dim3(layer_grid(rows, PX_HID, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT),
+                       0, (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w,
+                       (const uint32_t *)nullptr, ws, bias, rs, (uint8_t *)m8, ms, rows);
+    return xt_check("px_k_fc1");
+}

@@ -21,6 +21,10 @@ _SIGS = {
     "eva_k_flash": (_i, [_p, _p, _p, _p, _p, _i, _i, _p, _p]),
     "eva_k_flash_seq": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p, _p]),
     "eva_k_oproj": (_i, [_p, _p, _i, _p, _p, _p, _i, _p]),
+    "px_k_qkv": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _p, _p, _p, _i, _p]),
+    "px_k_proj": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _p]),
+    "px_k_fc1": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
+    "px_k_fc2": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _p]),
     "eva_k_fc1": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _i, _p]),
     "eva_k_fc2": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
     "eva_k_head": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _p]),
