@@ -220,6 +220,8 @@ int px_k_fc1(const void *h8, const float *hs, int lds, const void *w, const floa
 /* px_kernels.cu:192-200 k_pfc2: x fp16 [rows][1024] = x + (m8 . W2^T + bias), W2 [1024][4736] */
 int px_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *bias, void *x,
              int rows, void *stream);
+/* g[i] = u[i] Phi(u[i]) for n fp32 values by px_k_fc1's GELU (px_kernels.cu:228-229), for testing its accuracy */
+int px_probe_gelu(const float *u, float *g, int n, void *stream);
 
 /* ---- on-box ceilings (no reference counterpart; the roofline fractions use peaks measured on the same GPU) ---- */
 /* dense FP8 MFMA: blocks x 256 threads, each wave issuing iters x 8 v_mfma_f32_16x16x128_f8f6f4 on register operands

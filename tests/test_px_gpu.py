@@ -134,6 +134,36 @@ def test_px_residual_bias(dev, xt, orc, K):
     _check_close("x", _f16_f32(d_x.cpu().numpy().view(np.uint16)), _f16_f32(ref), np.abs(acc + bias).max(), 2.0 ** -10)
 
 
+def test_px_gelu_accuracy(dev, xt, orc):
+    """px_k_fc1's GELU (u Phi(u), branch free) against float64 (scipy's ndtr) over a dense grid of [-14, 14] and random
+    values, and against the oracle's libm-erff restatement of the reference's formula."""
+    from scipy.special import ndtr
+    r = np.random.default_rng(141)
+    u = np.concatenate([np.linspace(-14, 14, 1 << 20), r.standard_normal(1 << 18) * 3,
+                        [0.0, -0.0, 1e-30, -1e-30, 1e-6, -1e-6, 40.0, -40.0]]).astype(np.float32)
+    d_g = torch.empty(u.size, dtype=torch.float32, device=dev)
+    _ok(xt.lib.px_probe_gelu(xt.ptr(_d(u, dev)), xt.ptr(d_g), u.size, _st()), "px_probe_gelu")
+    g = d_g.cpu().numpy().astype(np.float64)
+    uu = u.astype(np.float64)
+    ref = uu * ndtr(uu)                                       # float64 Phi without the 1 + erf cancellation
+    pos, mid, tail = uu >= 0, (uu < 0) & (uu >= -8), uu < -8
+    rel = np.abs(g - ref) / np.maximum(np.abs(ref), 1e-300)
+    _say(f"  u >= 0: max rel {rel[pos].max():.2e}; -8 <= u < 0: max rel {rel[mid].max():.2e}")
+    assert rel[pos].max() <= 8e-7                             # 1 - Phi(-t) to 1.7e-7 absolute + v_exp_f32, Phi(u) >= 1/2
+    assert rel[mid].max() <= 6e-6                             # Phi(-t) to 2.9e-6 relative
+    # past t = 8 the fit is held at its end: Phi(-t) < 6.3e-16 comes out too large by at most a factor t / 8
+    big = tail & (np.abs(ref) > 1e-30)                        # Phi(u) a normal fp32 value
+    ratio = g[big] / ref[big]
+    assert ratio.min() >= 1 - 1e-5 and np.all(ratio <= 1.05 * np.abs(uu[big]) / 8)
+    assert np.all(np.abs(g[tail & ~big]) <= 1e-29)
+    # against the oracle's formula with libm erff (u in [-10, 10]): 0.5 (1 + erf) carries an absolute error of about
+    # 2^-24 (it cancels to 0 below u = -5.4), so the bound adds 2^-23 |u|
+    sel = np.flatnonzero(np.abs(uu) <= 10)
+    sel = sel[:sel.size // 4736 * 4736]
+    h = orc.px_fc1_epi(u[sel].reshape(-1, 4736), np.zeros(4736, np.float32)).ravel()
+    assert np.all(np.abs(g[sel] - h) <= 1e-5 * np.abs(h) + 2.0 ** -23 * np.abs(uu[sel]))
+
+
 @pytest.mark.parametrize("with_rs", [False, True])
 def test_px_fc1_gelu_pack(dev, xt, orc, with_rs):
     M = T_IMG

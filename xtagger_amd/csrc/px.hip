@@ -13,6 +13,33 @@
 
 typedef float v2f __attribute__((ext_vector_type(2)));
 
+// GELU with the exact normal CDF, u Phi(u) (px_kernels.cu:228-229 computes Phi as 0.5 (1 + erf(u / sqrt 2))), branch
+// free: with t = |u|, Phi(-t) = 2^Q(t), Q(t) = -t^2 / (2 ln 2) + R(t), and R a degree-12 polynomial in s = t / 4 - 1
+// fitted to log2 Phi(-t) + t^2 / (2 ln 2) on [0, 8] (Chebyshev least squares reweighted toward minimax: |R error|
+// 1.6e-7); then Phi(u) = 2^Q for u < 0 and 1 - 2^Q otherwise, with no cancellation on either side. In fp32 against
+// float64: Phi(-t) within 2.9e-6 relative on [0, 8] (the rounding of Q), 1 - Phi(-t) within 1.7e-7 absolute. Past
+// t = 8 R is held at R(8): Phi(-t) < 6.3e-16 there and comes out within a factor t / 8. One v_exp_f32 and 17 fp32
+// operations per unit, where erff takes two divergent branches.
+__device__ __forceinline__ float gelu_erf(float u)
+{
+    const float t = __builtin_fabsf(u), s = __builtin_fmaf(__builtin_fminf(t, 8.0f), 0.25f, -1.0f);
+    float r = -1.352992957e-03f;
+    r = __builtin_fmaf(r, s, 2.075498225e-03f);
+    r = __builtin_fmaf(r, s, 1.706041396e-03f);
+    r = __builtin_fmaf(r, s, -4.959797952e-03f);
+    r = __builtin_fmaf(r, s, 6.737539079e-03f);
+    r = __builtin_fmaf(r, s, -1.677700505e-02f);
+    r = __builtin_fmaf(r, s, 3.916485980e-02f);
+    r = __builtin_fmaf(r, s, -7.741049677e-02f);
+    r = __builtin_fmaf(r, s, 1.462343782e-01f);
+    r = __builtin_fmaf(r, s, -2.747326195e-01f);
+    r = __builtin_fmaf(r, s, 5.386815071e-01f);
+    r = __builtin_fmaf(r, s, -1.301931143e+00f);
+    r = __builtin_fmaf(r, s, -3.404906750e+00f);
+    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(-0.72134752f, t * t, r));  // Phi(-t)
+    return u * (u < 0.0f ? e : 1.0f - e);
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // k_px_qkv: h8 [rows][1024] x Wqkv [3072][1024] + bias -> q, k bf16 [S][16][L][64] (RoPE on every token with table
 // row t = m % L, cs [L][32] (cos, sin) of pair i = dims 2i, 2i+1), vt bf16 [S][16][64][L]; rows = S L. Weight rows of
@@ -137,14 +164,14 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_res(const uint8_t *__restri
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// k_px_fc1: h8 [rows][1024] x W1 [4736][1024] -> h = rs (gelu(acc + b1)), gelu(u) = u (0.5 (1 + erf(u / sqrt 2)))
-// (exact erf, px_kernels.cu:228-231; rs may be NULL = 1), packed to m8 [rows][4736] E4M3 with 1x128 scales
+// k_px_fc1: h8 [rows][1024] x W1 [4736][1024] -> h = rs (gelu(acc + b1)), gelu(u) = u Phi(u) (exact normal CDF,
+// px_kernels.cu:228-231, by gelu_erf; rs may be NULL = 1), packed to m8 [rows][4736] E4M3 with 1x128 scales
 // ms [37][lds]. A wave's 128 columns are one scale block: each row's |max| meets in a 16-lane DPP reduction, the
 // values are scaled in registers, parked in the wave's own LDS slice 64 columns at a time and stored 8 consecutive
 // bytes per lane (8 rows of 64 bytes per wave instruction). The second half of the last column tile lies past
 // unit 4736 and stores nothing.
 // ---------------------------------------------------------------------------------------------------------------
-template <bool SP>
+template <bool SP, bool RS>
 __global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
                                                         int lds, const uint8_t *__restrict__ w,
                                                         const uint32_t *__restrict__ wx, const float *__restrict__ ws,
@@ -167,7 +194,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restri
     for (int j = 0; j < C::TN; j++) {
         const int u = 128 * blk + 16 * j + c16;
         bj[j] = bias[u];
-        rj[j] = rs ? rs[u] : 1.0f;
+        rj[j] = RS ? rs[u] : 1.0f;
     }
     float inv[C::TM][4];
 #pragma unroll
@@ -177,8 +204,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restri
             float amax = 0.f;
 #pragma unroll
             for (int j = 0; j < C::TN; j++) {
-                const float u = acc[i][j][r] + bj[j];
-                const float v = (u * (0.5f * (1.0f + erff(u * 0.70710678f)))) * rj[j];
+                const float g = gelu_erf(acc[i][j][r] + bj[j]), v = RS ? g * rj[j] : g;
                 acc[i][j][r] = v;
                 amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
             }
@@ -267,8 +293,23 @@ extern "C" int px_k_fc1(const void *h8, const float *hs, int lds, const void *w,
     if (px_rows_ok("px_k_fc1", rows, lds)) return -1;
     if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || ((uintptr_t)m8 & 7))
         return xt_fail("px_k_fc1", "h8 and w must be 16-byte aligned, m8 8-byte aligned");
-    hipLaunchKernelGGL(k_px_fc1<false>, dim3(layer_grid(rows, PX_HID, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT),
-                       0, (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w,
-                       (const uint32_t *)nullptr, ws, bias, rs, (uint8_t *)m8, ms, rows);
+    auto kern = rs ? k_px_fc1<false, true> : k_px_fc1<false, false>;  // the multiply only where rs is given
+    hipLaunchKernelGGL(kern, dim3(layer_grid(rows, PX_HID, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
+                       (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w, (const uint32_t *)nullptr,
+                       ws, bias, rs, (uint8_t *)m8, ms, rows);
     return xt_check("px_k_fc1");
+}
+
+// GELU of n fp32 values by the fc1 epilogue's gelu_erf (test hook: its accuracy is not visible through the E4M3 output)
+__global__ void __launch_bounds__(256) k_px_gelu(const float *__restrict__ u, float *__restrict__ g, int n)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) g[i] = gelu_erf(u[i]);
+}
+
+extern "C" int px_probe_gelu(const float *u, float *g, int n, void *stream)
+{
+    if (n <= 0) return xt_fail("px_probe_gelu", "n must be positive");
+    hipLaunchKernelGGL(k_px_gelu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, u, g, n);
+    return xt_check("px_probe_gelu");
 }
