@@ -328,13 +328,15 @@ def bench_pixai_block(torch, L, nb=4, reps=10):
     lds = M
     t = lambda *s, dt=torch.uint8: torch.zeros(*s, dtype=dt, device=dev)
     st = lambda: torch.cuda.current_stream().cuda_stream
-    scratch = torch.empty(PH * D, dtype=torch.float32, device=dev)
 
     def packw(n, k, perm=0):
+        # eva_k_prep_w writes its fp32 [n][k] staging into scratch: sized per call
         w16 = (torch.randn(n, k, generator=g, device=dev) * 0.02).half()
+        scratch = torch.empty(n * k, dtype=torch.float32, device=dev)
         q, s = t(n, k), t(n // 128, k // 128, dt=torch.float32)
         L.check(L.lib.eva_k_prep_w(L.ptr(w16), k, n, k, n, k, perm, None, L.ptr(scratch), L.ptr(q), L.ptr(s), st()),
                 "prep")
+        torch.cuda.synchronize()
         return q, s
 
     wqkv, sqkv = packw(3 * D, D, 1)
@@ -386,6 +388,23 @@ def bench_pixai_block(torch, L, nb=4, reps=10):
         res[name] = round(timed(run(ln, lambda: qkv(Ls), lambda: attn(Ls), proj, ln, fc1, fc2)), 1)
     # ViTDet-L: 32 blocks, global attention in 4 of them (px.h PX_GLOBAL)
     res["blocks_32_ms"] = round((28 * res["block_windowed_us"] + 4 * res["block_global_us"]) / 1e3, 3)
+    # attention-pool head (px.h:170-189) and a 13461-row tag head
+    nt, T5 = 13461, 5184
+    hpos = (torch.randn(T5, D, generator=g, device=dev) * 0.2).half()
+    U = torch.randn(16, D, generator=g, device=dev) * 0.05
+    wv = (torch.randn(D, D, generator=g, device=dev) * 0.03).half()
+    hw, hws = packw((nt + 127) // 128 * 128, D)
+    hb = torch.zeros(nt, device=dev)
+    y, s = t(M, D, dt=torch.int16), t(M, 16, dt=torch.float32)
+    Pm, part = t(nb, 16, T5, dt=torch.int16), t(nb, T5 // 144, 16, D, dt=torch.float32)
+    o, oq, oqs, out = t(nb, D, dt=torch.float32), t(nb, D), t(8, nb, dt=torch.float32), t(nb, nt, dt=torch.float32)
+    head = run(lambda: L.lib.px_k_hln(P(x), P(lng), P(lnb), P(hpos), T5, P(U), P(y), P(s), M, st()),
+               lambda: L.lib.px_k_hsoft(P(s), P(Pm), nb, T5, st()),
+               lambda: L.lib.px_k_hpool(P(Pm), P(y), P(part), nb, T5, st()),
+               lambda: L.lib.px_k_hv(P(part), T5 // 144, P(wv), P(o), nb, st()),
+               lambda: L.lib.eva_k_quant_act(P(o), 1, D, nb, D, P(oq), D, P(oqs), nb, st()),
+               lambda: L.lib.eva_k_head(P(oq), P(oqs), nb, P(hw), P(hws), P(hb), P(out), nb, nt, st()))
+    res["pool_head_us"] = round(timed(head), 1)
     return res
 
 

@@ -220,6 +220,18 @@ int px_k_fc1(const void *h8, const float *hs, int lds, const void *w, const floa
 /* px_kernels.cu:192-200 k_pfc2: x fp16 [rows][1024] = x + (m8 . W2^T + bias), W2 [1024][4736] */
 int px_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *bias, void *x,
              int rows, void *stream);
+/* Attention-pool head (px_kernels.cu:341-503; px.h:170-189), T = 5184 tokens per image, rows = nb * T:
+ * px_k_hln = k_phln + k_phscore: y fp16 [rows][1024] = f16(LN_1e-5(x) g + b + hpos[m % T]) (hpos fp16 [T][1024]),
+ * s fp32 [rows][16] = U y (U fp32 [16][1024], exp2 domain). */
+int px_k_hln(const void *x, const float *g, const float *b, const void *hpos, int T, const float *U, void *y, float *s,
+             int rows, void *stream);
+/* k_phsoft: P fp16 [nb][16][T] = softmax over the T tokens of each (image, head), exp2 domain */
+int px_k_hsoft(const float *s, void *P, int nb, int T, void *stream);
+/* k_phpool: part fp32 [nb][T/144][16][1024] = per 144-token chunk, sum_t P[b][h][t] y[b][t]; T % 144 == 0 */
+int px_k_hpool(const void *P, const void *y, float *part, int nb, int T, void *stream);
+/* k_phv: o [nb][1024] = f16(Wv[64 h + n] . pooled[b][h]) as fp32 values (pooled = the nch partials summed in order;
+ * Wv fp16 [1024][1024]); the tag head follows as eva_k_quant_act(o, fp32) + eva_k_head. */
+int px_k_hv(const float *part, int nch, const void *wv, float *o, int nb, void *stream);
 /* g[i] = u[i] Phi(u[i]) for n fp32 values by px_k_fc1's GELU (px_kernels.cu:228-229), for testing its accuracy */
 int px_probe_gelu(const float *u, float *g, int n, void *stream);
 

@@ -55,6 +55,9 @@ _SIGS = {
     "xo_px_qkv_epi": (None, [_p, _i, _i, _p, _p, _p, _p, _p]),
     "xo_px_res_epi": (None, [_p, _i, _p, _p]),
     "xo_px_fc1_epi": (None, [_p, _i, _p, _p, _p]),
+    "xo_px_hln": (None, [_p, _i, _i, _p, _p, _p, _p, _p, _p]),
+    "xo_px_hsoft": (None, [_p, _i, _i, _p]),
+    "xo_px_hpool_hv": (None, [_p, _p, _i, _i, _p, _p]),
     "xo_embed": (None, [_p, _p, _p, _i, _p]),
     "xo_pool": (None, [_p, _i, _p]),
     "xo_lnh": (None, [_p, _p, _p, _i, _p, _p, _p, _i]),
@@ -291,6 +294,32 @@ def px_fc1_epi(acc, bias, rs=None):
     lib.xo_px_fc1_epi(_ptr(acc), acc.shape[0], _ptr(_c(bias, np.float32)),
                       None if rs is None else _ptr(_c(rs, np.float32)), _ptr(h))
     return h
+
+
+def px_hln(x16, T, g, b, hpos16, U):
+    """PixAI pool head keys / scores: (y fp16 bits [M][1024], s float64 [M][16])."""
+    _done()
+    x16 = _c(x16, np.uint16)
+    M = x16.shape[0]
+    y = np.empty((M, 1024), np.uint16)
+    s = np.empty((M, 16), np.float64)
+    lib.xo_px_hln(_ptr(x16), M, T, _ptr(_c(g, np.float32)), _ptr(_c(b, np.float32)), _ptr(_c(hpos16, np.uint16)),
+                  _ptr(_c(U, np.float32)), _ptr(y), _ptr(s))
+    return y, s
+
+
+def px_hsoft(s, nb, T):
+    _done()
+    P = np.empty((nb, 16, T), np.float64)
+    lib.xo_px_hsoft(_ptr(_c(s, np.float32)), nb, T, _ptr(P))
+    return P
+
+
+def px_hpool_hv(P16, y16, nb, T, wv16):
+    _done()
+    o = np.empty((nb, 1024), np.float64)
+    lib.xo_px_hpool_hv(_ptr(_c(P16, np.uint16)), _ptr(_c(y16, np.uint16)), nb, T, _ptr(_c(wv16, np.uint16)), _ptr(o))
+    return o
 
 
 def embed(inp16, pe16, pos, nb):

@@ -649,6 +649,80 @@ void xo_px_fc1_epi(const float *acc, int M, const float *bias, const float *rs, 
     }
 }
 
+void xo_px_hln(const uint16_t *x, int M, int T, const float *g, const float *b, const uint16_t *hpos, const float *U,
+               uint16_t *y, double *s)
+{
+    int m;
+
+#pragma omp parallel for schedule(static)
+    for (m = 0; m < M; m++) {
+        float v[1024], ls[64], mean, var, rstd, d;
+        int l, j, e, h;
+
+        for (e = 0; e < 1024; e++) v[e] = xo_f16_to_f32(x[(size_t)m * 1024 + e]);
+        for (l = 0; l < 64; l++) {
+            ls[l] = 0.0f;
+            for (j = 0; j < 16; j++) ls[l] += v[ln_elem(l, j)];
+        }
+        mean = wave_sum64(ls) * (1.0f / 1024.0f);
+        for (l = 0; l < 64; l++) {
+            ls[l] = 0.0f;
+            for (j = 0; j < 16; j++) {
+                d = v[ln_elem(l, j)] - mean;
+                ls[l] = fmaf(d, d, ls[l]);
+            }
+        }
+        var = wave_sum64(ls) * (1.0f / 1024.0f);
+        rstd = 1.0f / sqrtf(var + 1e-5f);
+        for (e = 0; e < 1024; e++)
+            y[(size_t)m * 1024 + e] =
+                xo_f32_to_f16(fmaf((v[e] - mean) * rstd, g[e], b[e]) + xo_f16_to_f32(hpos[(size_t)(m % T) * 1024 + e]));
+        for (h = 0; h < 16; h++) {
+            double a = 0.0;
+            for (e = 0; e < 1024; e++) a += (double)U[h * 1024 + e] * xo_f16_to_f32(y[(size_t)m * 1024 + e]);
+            s[(size_t)m * 16 + h] = a;
+        }
+    }
+}
+
+void xo_px_hsoft(const float *s, int nb, int T, double *P)
+{
+    int bh;
+
+#pragma omp parallel for schedule(static)
+    for (bh = 0; bh < nb * 16; bh++) {
+        const int b = bh / 16, h = bh % 16;
+        double mx = -1e300, l = 0.0;
+        int t;
+        for (t = 0; t < T; t++) mx = fmax(mx, s[((size_t)b * T + t) * 16 + h]);
+        for (t = 0; t < T; t++) l += exp2(s[((size_t)b * T + t) * 16 + h] - mx);
+        for (t = 0; t < T; t++) P[(size_t)bh * T + t] = exp2(s[((size_t)b * T + t) * 16 + h] - mx) / l;
+    }
+}
+
+void xo_px_hpool_hv(const uint16_t *P, const uint16_t *y, int nb, int T, const uint16_t *wv, double *o)
+{
+    int bh;
+
+#pragma omp parallel for schedule(static)
+    for (bh = 0; bh < nb * 16; bh++) {
+        const int b = bh / 16, h = bh % 16;
+        double pooled[1024];
+        int t, d, n;
+        for (d = 0; d < 1024; d++) pooled[d] = 0.0;
+        for (t = 0; t < T; t++) {
+            const double p = xo_f16_to_f32(P[(size_t)bh * T + t]);
+            const uint16_t *yr = y + ((size_t)b * T + t) * 1024;
+            for (d = 0; d < 1024; d++) pooled[d] += p * xo_f16_to_f32(yr[d]);
+        }
+        for (n = 0; n < 64; n++) {
+            double a = 0.0;
+            for (d = 0; d < 1024; d++) a += (double)xo_f16_to_f32(wv[(size_t)(64 * h + n) * 1024 + d]) * pooled[d];
+            o[(size_t)b * 1024 + 64 * h + n] = a;
+        }
+    }
+}
+
 void xo_embed(const uint16_t *in, const uint16_t *pe, const float *pos, int nb, uint16_t *x)
 {
     int r;

@@ -96,6 +96,16 @@ void xo_px_res_epi(const float *acc, int M, const float *bias, uint16_t *x);
 /* k_pfc1 (px_kernels.cu:222-233): h [M][4736] = (u (0.5 (1 + erff(u 0.70710678)))) rs[n], u = acc + bias[n] (libm erff;
  * rs NULL = no multiply), fp32 */
 void xo_px_fc1_epi(const float *acc, int M, const float *bias, const float *rs, float *h);
+/* attention-pool head (px_kernels.cu:344-503). k_phln + k_phscore: y = f16(fma((x - mean) rstd, g, b) + hpos[m % T])
+ * with the LayerNorm (eps 1e-5, IEEE rstd) in the device's summation order (as xo_ln_quant), s [M][16] = U y in
+ * float64 from the fp16 y */
+void xo_px_hln(const uint16_t *x, int M, int T, const float *g, const float *b, const uint16_t *hpos, const float *U,
+               uint16_t *y, double *s);
+/* k_phsoft: P [nb][16][T] = 2^(s - max) / sum over the T tokens of each (image, head), float64 */
+void xo_px_hsoft(const float *s, int nb, int T, double *P);
+/* k_phpool + k_phv: pooled[b][h] = sum_t P[b][h][t] y[b][t], o [nb][1024] = Wv[64 h + n] . pooled[b][h], float64 from
+ * the fp16 P and y */
+void xo_px_hpool_hv(const uint16_t *P, const uint16_t *y, int nb, int T, const uint16_t *wv, double *o);
 /* patch embedding + position (k_pe + k_embed, eva_kernels.cu:21-33, 126-130): in fp16 [nb*1024][592],
  * pe fp16 [1024][592], pos fp32 [1025][1024] -> x fp16 [nb*1025][1024]; x[b,0] = f16(pos[0]),
  * x[b,1+p] = f16((float)dot + pos[1+p]) with the dot in fp64 */

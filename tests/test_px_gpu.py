@@ -272,3 +272,65 @@ def test_px_block_chain_windowed(dev, xt, orc):
     _check_close("x after fc2", _f16_f32(d_x.cpu().numpy().view(np.uint16)), _f16_f32(x2r), np.abs(acc + bf2).max(),
                  2.0 ** -10)
 
+
+
+def test_px_pool_head(dev, xt, orc):
+    """The attention-pool head (px_kernels.cu:341-503) over 2 images of 5184 tokens, each kernel fed the previous
+    kernel's GPU output: LN + position (bit-exact) and scores, softmax over the tokens, chunked pooling and the
+    per-head value projection, then the tag head as eva_k_quant_act + eva_k_head."""
+    nb, T = 2, T_IMG
+    M = nb * T
+    _say("px pool head nb=2")
+    r = np.random.default_rng(151)
+    x = (r.standard_normal((M, D)) * 1.5 + 0.2).astype(np.float16)
+    g = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    b = (0.1 * r.standard_normal(D)).astype(np.float32)
+    hpos = (r.standard_normal((T, D)) * 0.2).astype(np.float16)
+    U = (r.standard_normal((16, D)) * 0.05).astype(np.float32)
+    wv = (r.standard_normal((D, D)) * 0.03).astype(np.float16)
+    d_y = torch.zeros((M, D), dtype=torch.int16, device=dev)
+    d_s = torch.zeros((M, 16), dtype=torch.float32, device=dev)
+    _ok(xt.lib.px_k_hln(xt.ptr(_d(x, dev)), xt.ptr(_d(g, dev)), xt.ptr(_d(b, dev)), xt.ptr(_d(hpos, dev)), T,
+                        xt.ptr(_d(U, dev)), xt.ptr(d_y), xt.ptr(d_s), M, _st()), "px_k_hln")
+    y_ref, s_ref = orc.px_hln(x.view(np.uint16), T, g, b, hpos.view(np.uint16), U)
+    y = d_y.cpu().numpy().view(np.uint16)
+    assert (y == y_ref).all()
+    yf = y.view(np.float16).astype(np.float64)
+    s = d_s.cpu().numpy()
+    terms = np.abs(yf) @ np.abs(U.astype(np.float64)).T
+    assert np.all(np.abs(s - s_ref) <= 2e-6 * terms)
+    # softmax over the tokens, from the kernel's own scores
+    d_P = torch.zeros((nb, 16, T), dtype=torch.int16, device=dev)
+    _ok(xt.lib.px_k_hsoft(xt.ptr(d_s), xt.ptr(d_P), nb, T, _st()), "px_k_hsoft")
+    P = d_P.cpu().numpy().view(np.uint16)
+    Pf = P.view(np.float16).astype(np.float64)
+    P_ref = orc.px_hsoft(s, nb, T)
+    assert np.all(np.abs(Pf - P_ref) <= (2.0 ** -11 + 1e-5) * P_ref + 6e-8)
+    # pooling and the value projection, from the kernel's own P and y
+    nch = T // 144
+    d_part = torch.zeros((nb, nch, 16, D), dtype=torch.float32, device=dev)
+    d_o = torch.zeros((nb, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.px_k_hpool(xt.ptr(d_P), xt.ptr(d_y), xt.ptr(d_part), nb, T, _st()), "px_k_hpool")
+    _ok(xt.lib.px_k_hv(xt.ptr(d_part), nch, xt.ptr(_d(wv, dev)), xt.ptr(d_o), nb, _st()), "px_k_hv")
+    o = d_o.cpu().numpy()
+    assert (o.astype(np.float16).astype(np.float32) == o).all()         # fp16 values
+    o_ref = orc.px_hpool_hv(P, y, nb, T, wv.view(np.uint16))
+    pabs = np.matmul(Pf, np.abs(yf).reshape(nb, T, D))                      # sum_t P |y|, [nb][16][1024]
+    bnd = np.einsum("hnd,bhd->bhn", np.abs(wv.astype(np.float64)).reshape(16, 64, D), pabs).reshape(nb, D)
+    err = np.abs(o - o_ref)
+    _say(f"  o: worst err / bound {(err / (2.0 ** -11 * np.abs(o_ref) + 2e-5 * bnd)).max():.3f}")
+    assert np.all(err <= 2.0 ** -11 * np.abs(o_ref) + 2e-5 * bnd)
+    # tag head on the packed o (the block-scaled FP8 head, as the wd model's)
+    nt = 1000
+    qw, sw = _w(orc, nt, D, 152, std=0.05)
+    hb = (r.standard_normal(nt) * 0.1).astype(np.float32)
+    d_q = torch.zeros((nb, D), dtype=torch.uint8, device=dev)
+    d_qs = torch.zeros((8, nb), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_quant_act(xt.ptr(d_o), 1, D, nb, D, xt.ptr(d_q), D, xt.ptr(d_qs), nb, _st()), "quant o")
+    q_ref, qs_ref = orc.quant_act(o)
+    assert (d_q.cpu().numpy() == q_ref).all() and (d_qs.cpu().numpy() == qs_ref).all()
+    d_out = torch.zeros((nb, nt), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_head(xt.ptr(d_q), xt.ptr(d_qs), nb, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)), xt.ptr(_d(hb, dev)),
+                          xt.ptr(d_out), nb, nt, _st()), "eva_k_head")
+    logit = orc.gemm_f64_rows(q_ref, qs_ref, qw, sw, nt, np.arange(nb))
+    assert np.abs(d_out.cpu().numpy() - 1.0 / (1.0 + np.exp(-(logit + hb)))).max() < 1e-4

@@ -96,3 +96,57 @@ def test_px_res_epi_reduces_to_oproj_and_closed_form(orc):
     got = orc.px_res_epi(np.zeros_like(acc), bias, x).view(np.float16)
     ref = (x.view(np.float16).astype(np.float32) + bias).astype(np.float16)
     assert (got == ref).all()
+
+
+def _f16(a):
+    return np.asarray(a, np.float32).astype(np.float16)
+
+
+def test_px_hln_vs_float64_layernorm(orc):
+    """k_phln + k_phscore (px_kernels.cu:344-400): y = f16(LN_1e-5(x) g + b + hpos[m % T]) within one fp16 rounding of
+    the float64 formula, a constant row gives b + hpos, and s = U y of the fp16 y (numpy matmul)."""
+    r = np.random.default_rng(10)
+    T, M = 48, 96
+    x = _f16(r.standard_normal((M, 1024)) * 2 + 0.5)
+    x[5] = np.float16(1.25)
+    g = (1 + 0.1 * r.standard_normal(1024)).astype(np.float32)
+    b = (0.1 * r.standard_normal(1024)).astype(np.float32)
+    hpos = _f16(r.standard_normal((T, 1024)) * 0.2)
+    U = (r.standard_normal((16, 1024)) * 0.05).astype(np.float32)
+    y, s = orc.px_hln(x.view(np.uint16), T, g, b, hpos.view(np.uint16), U)
+    xf = x.astype(np.float64)
+    mean = xf.mean(1, keepdims=True)
+    var = ((xf - mean) ** 2).mean(1, keepdims=True)
+    ref = (xf - mean) / np.sqrt(var + 1e-5) * g + b + hpos[np.arange(M) % T].astype(np.float64)
+    yf = y.view(np.float16).astype(np.float64)
+    assert np.all(np.abs(yf - ref) <= 2.0 ** -10 * np.abs(ref) + 2.0 ** -24 + 1e-6 * np.abs(ref).max())
+    assert (y.view(np.float16)[5] == _f16(b + hpos[5].astype(np.float32))).all()
+    assert np.allclose(s, yf @ U.astype(np.float64).T, rtol=1e-12, atol=1e-12)
+
+
+def test_px_hsoft_vs_softmax(orc):
+    from scipy.special import softmax
+    r = np.random.default_rng(11)
+    nb, T = 2, 300
+    s = (np.round(r.standard_normal((nb * T, 16)) * 4 * 1024) / 1024).astype(np.float32)   # s + 3 stays exact
+    P = orc.px_hsoft(s, nb, T)
+    ref = softmax(s.astype(np.float64).reshape(nb, T, 16) * np.log(2.0), axis=1).transpose(0, 2, 1)
+    assert np.allclose(P, ref, rtol=1e-12, atol=0)
+    assert np.allclose(P.sum(2), 1.0, atol=1e-12)
+    assert np.allclose(orc.px_hsoft(s + np.float32(3.0), nb, T), P, rtol=1e-12)      # shift invariance
+
+
+def test_px_hpool_hv_vs_matmul(orc):
+    r = np.random.default_rng(12)
+    nb, T = 2, 144
+    P = _f16(r.random((nb, 16, T)) / T)
+    y = _f16(r.standard_normal((nb * T, 1024)))
+    wv = _f16(r.standard_normal((1024, 1024)) * 0.03)
+    o = orc.px_hpool_hv(P.view(np.uint16), y.view(np.uint16), nb, T, wv.view(np.uint16))
+    pooled = np.matmul(P.astype(np.float64), y.astype(np.float64).reshape(nb, T, 1024))      # [nb][16][1024]
+    w = wv.astype(np.float64).reshape(16, 64, 1024)
+    ref = np.einsum("hnd,bhd->bhn", w, pooled).reshape(nb, 1024)
+    assert np.allclose(o, ref, rtol=1e-12, atol=1e-12)
+    o2 = orc.px_hpool_hv((P.astype(np.float32) * 2).astype(np.float16).view(np.uint16), y.view(np.uint16), nb, T,
+                         wv.view(np.uint16))
+    assert np.allclose(o2, 2 * o, rtol=1e-12, atol=1e-12)                                   # linear in P

@@ -8,9 +8,10 @@
 #include "xt_abi.h"
 #include "xt_common.h"
 
-// LayerNorm of one row held as v[16] (lane layout above), eps 1e-6, two-pass:
+// LayerNorm of one row held as v[16] (lane layout above), eps 1e-6 (the blocks; 1e-5 for the PixAI head), two-pass:
 // y = fma((x - mean) * rstd, gamma, beta), rstd = 1 / sqrt(var + eps) with IEEE sqrt and division.
-__device__ __forceinline__ void ln16(float *v, const float *__restrict__ g, const float *__restrict__ b, int lane)
+__device__ __forceinline__ void ln16(float *v, const float *__restrict__ g, const float *__restrict__ b, int lane,
+                                     float eps = XT_EPS)
 {
     float s = 0.f;
 #pragma unroll
@@ -23,7 +24,7 @@ __device__ __forceinline__ void ln16(float *v, const float *__restrict__ g, cons
         q = __builtin_fmaf(d, d, q);
     }
     const float var = wave_sum(q) * (1.0f / 1024.0f);
-    const float rstd = 1.0f / __builtin_sqrtf(var + XT_EPS);
+    const float rstd = 1.0f / __builtin_sqrtf(var + eps);
 #pragma unroll
     for (int h = 0; h < 2; h++) {
         const int e0 = 512 * h + 8 * lane;
@@ -130,6 +131,59 @@ __global__ void __launch_bounds__(256) k_lnh(const float *__restrict__ p, const 
     quant_row16(v, q + (size_t)row * XT_D, s, lds, row, lane);
 }
 
+// k_px_hln: the PixAI attention-pool head's keys / values and scores (px_kernels.cu:344-400 k_phln + k_phscore,
+// fused): y = f16(LN_1e-5(x) + hpos[m % T]) fp16 [rows][1024] and s [rows][16] = U y of the fp16 y (exp2 domain, the
+// constant query folded into U). U [16][1024] fp32 sits in shared memory; each wave takes 16 rows in turn, and each
+// score is the lane's 16 products in element order (an fma chain) met in the xor butterfly.
+constexpr int PX_HLN_ROWS = 16;  // rows per wave
+__global__ void __launch_bounds__(256) k_px_hln(const uint16_t *__restrict__ x, const float *__restrict__ g,
+                                                const float *__restrict__ b, const uint16_t *__restrict__ hpos, int T,
+                                                const float *__restrict__ U, uint16_t *__restrict__ y,
+                                                float *__restrict__ s, int rows)
+{
+    __shared__ __attribute__((aligned(16))) float su[16 * XT_D];
+    for (int i = threadIdx.x; i < 16 * XT_D / 4; i += 256) ((float4 *)su)[i] = ((const float4 *)U)[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63, r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * PX_HLN_ROWS;
+    for (int rr = 0; rr < PX_HLN_ROWS; rr++) {
+        const int row = r0 + rr;
+        if (row >= rows) break;
+        float v[16], hp[16];
+        load_row16_f16(x + (size_t)row * XT_D, lane, v);
+        load_row16_f16(hpos + (size_t)(row % T) * XT_D, lane, hp);
+        ln16(v, g, b, lane, 1e-5f);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint16_t lo = f2h(v[8 * h + 2 * i] + hp[8 * h + 2 * i]);
+                const uint16_t hi = f2h(v[8 * h + 2 * i + 1] + hp[8 * h + 2 * i + 1]);
+                v[8 * h + 2 * i] = h2f(lo);
+                v[8 * h + 2 * i + 1] = h2f(hi);
+                w[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+            }
+            *(uint4 *)(y + (size_t)row * XT_D + 512 * h + 8 * lane) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        float mine = 0.f;
+#pragma unroll
+        for (int hd = 0; hd < 16; hd++) {
+            float a = 0.f;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float4 u0 = *(const float4 *)(su + hd * XT_D + 512 * h + 8 * lane);
+                const float4 u1 = *(const float4 *)(su + hd * XT_D + 512 * h + 8 * lane + 4);
+                const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) a = __builtin_fmaf(uu[j], v[8 * h + j], a);
+            }
+            a = wave_sum(a);
+            mine = lane == hd ? a : mine;
+        }
+        if (lane < 16) s[(size_t)row * 16 + lane] = mine;
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 extern "C" int eva_k_ln(const void *x, const float *g, const float *b, void *q, float *s, int rows, int lds,
                         void *stream)
@@ -159,4 +213,16 @@ extern "C" int eva_k_lnh(const float *p, const float *g, const float *b, void *p
     hipLaunchKernelGGL(k_lnh, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, p, g, b, (uint16_t *)pn,
                        (uint8_t *)q, s, rows, lds);
     return xt_check("eva_k_lnh");
+}
+
+extern "C" int px_k_hln(const void *x, const float *g, const float *b, const void *hpos, int T, const float *U, void *y,
+                        float *s, int rows, void *stream)
+{
+    if (rows <= 0 || T <= 0) return xt_fail("px_k_hln", "bad shape (rows > 0, T > 0)");
+    if (((uintptr_t)x | (uintptr_t)g | (uintptr_t)b | (uintptr_t)hpos | (uintptr_t)U | (uintptr_t)y) & 15)
+        return xt_fail("px_k_hln", "x, g, b, hpos, U, y must be 16-byte aligned");
+    const int per = 4 * PX_HLN_ROWS;
+    hipLaunchKernelGGL(k_px_hln, dim3((rows + per - 1) / per), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x,
+                       g, b, (const uint16_t *)hpos, T, U, (uint16_t *)y, s, rows);
+    return xt_check("px_k_hln");
 }

@@ -300,6 +300,145 @@ extern "C" int px_k_fc1(const void *h8, const float *hs, int lds, const void *w,
     return xt_check("px_k_fc1");
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Attention-pool head (px_kernels.cu:341-503): the scores s [nb T][16] of k_px_hln -> per (image, head) softmax over
+// the T tokens -> pooled = P y -> o = Wv pooled per head; the tag head is then eva_k_quant_act + eva_k_head.
+// ---------------------------------------------------------------------------------------------------------------
+#define PX_PCH 144  // tokens per pooling chunk (px_kernels.cu:446 PCH)
+
+// k_px_hsoft (k_phsoft, 406-440): P [nb][16][T] fp16 = 2^(s - max) / sum, one block of 256 threads per (image, head);
+// the maximum and the sum run per thread in token order, then through the wave butterfly and the 4 waves in order.
+__global__ void __launch_bounds__(256) k_px_hsoft(const float *__restrict__ s, uint16_t *__restrict__ P, int T)
+{
+    __shared__ float red[4];
+    const int b = blockIdx.x >> 4, h = blockIdx.x & 15, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const float *sb = s + (size_t)b * T * 16 + h;
+    float m = -3.0e38f;
+    for (int t = threadIdx.x; t < T; t += 256) m = __builtin_fmaxf(m, sb[(size_t)t * 16]);
+    m = wave_max(m);
+    if (lane == 0) red[w] = m;
+    __syncthreads();
+    m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    __syncthreads();
+    float l = 0.f;
+    for (int t = threadIdx.x; t < T; t += 256) l += __builtin_amdgcn_exp2f(sb[(size_t)t * 16] - m);
+    l = wave_sum(l);
+    if (lane == 0) red[w] = l;
+    __syncthreads();
+    const float inv = 1.0f / (((red[0] + red[1]) + red[2]) + red[3]);
+    for (int t = threadIdx.x; t < T; t += 256)
+        P[(size_t)blockIdx.x * T + t] = f2h(__builtin_amdgcn_exp2f(sb[(size_t)t * 16] - m) * inv);
+}
+
+// k_px_hpool (k_phpool, 447-473): part [nb][T/144][16][1024] fp32, the sum over one 144-token chunk of P[h][t] y[t][d],
+// tokens in order (fma chains); k_px_hv adds the chunks in order. Grid (nb, T/144, 2): 256 threads, two dims each,
+// all 16 heads at once, so y is read once; the chunk's P sits in shared memory as [token][head].
+__global__ void __launch_bounds__(256) k_px_hpool(const uint16_t *__restrict__ P, const uint16_t *__restrict__ y,
+                                                  float *__restrict__ part, int T)
+{
+    __shared__ __attribute__((aligned(16))) float sp[PX_PCH][16];
+    const int b = blockIdx.x, c = blockIdx.y, t0 = c * PX_PCH, d = 512 * blockIdx.z + 2 * threadIdx.x;
+    for (int i = threadIdx.x; i < PX_PCH * 16; i += 256) {
+        const int h = i / PX_PCH, t = i - h * PX_PCH;
+        sp[t][h] = h2f(P[((size_t)b * 16 + h) * T + t0 + t]);
+    }
+    __syncthreads();
+    float a0[16], a1[16];
+#pragma unroll
+    for (int h = 0; h < 16; h++) a0[h] = a1[h] = 0.f;
+    const uint16_t *yr = y + ((size_t)b * T + t0) * XT_D + d;
+    for (int t = 0; t < PX_PCH; t++) {
+        const uint32_t u = *(const uint32_t *)(yr + (size_t)t * XT_D);
+        const float v0 = h2f((uint16_t)(u & 0xffffu)), v1 = h2f((uint16_t)(u >> 16));
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 p = *(const float4 *)&sp[t][4 * q];
+            const float pp[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                a0[4 * q + k] = __builtin_fmaf(pp[k], v0, a0[4 * q + k]);
+                a1[4 * q + k] = __builtin_fmaf(pp[k], v1, a1[4 * q + k]);
+            }
+        }
+    }
+    float *po = part + (((size_t)b * gridDim.y + c) * 16) * XT_D + d;
+#pragma unroll
+    for (int h = 0; h < 16; h++) *(float2 *)(po + (size_t)h * XT_D) = make_float2(a0[h], a1[h]);
+}
+
+// k_px_hv (k_phv, 477-503): pooled[b][h] = the nch chunk partials summed in chunk order, then
+// o[b][64 h + n] = f16(Wv[64 h + n] . pooled[b][h]) (Wv fp16 [1024][1024]), written as fp32 holding the fp16 value
+// (the reference's fp16 o, ready for eva_k_quant_act). One block of 256 threads per (image, head): each wave takes 16
+// outputs, each lane 16 of the 1024 products in element order, met in the butterfly.
+__global__ void __launch_bounds__(256) k_px_hv(const float *__restrict__ part, int nch, const uint16_t *__restrict__ wv,
+                                               float *__restrict__ o)
+{
+    __shared__ __attribute__((aligned(16))) float pv[XT_D];
+    const int b = blockIdx.x >> 4, h = blockIdx.x & 15, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    {
+        const float *pp = part + ((size_t)b * nch * 16 + h) * XT_D + 4 * threadIdx.x;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int c = 0; c < nch; c++) {
+            const float4 v = *(const float4 *)(pp + (size_t)c * 16 * XT_D);
+            a.x += v.x;
+            a.y += v.y;
+            a.z += v.z;
+            a.w += v.w;
+        }
+        *(float4 *)(pv + 4 * threadIdx.x) = a;
+    }
+    __syncthreads();
+    float x[16];
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const float4 a = *(const float4 *)(pv + 512 * hh + 8 * lane), c = *(const float4 *)(pv + 512 * hh + 8 * lane + 4);
+        x[8 * hh + 0] = a.x; x[8 * hh + 1] = a.y; x[8 * hh + 2] = a.z; x[8 * hh + 3] = a.w;
+        x[8 * hh + 4] = c.x; x[8 * hh + 5] = c.y; x[8 * hh + 6] = c.z; x[8 * hh + 7] = c.w;
+    }
+    float mine = 0.f;
+    for (int k = 0; k < 16; k++) {
+        const int n = 64 * h + 16 * w + k;
+        float a = 0.f;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const uint4 u = *(const uint4 *)(wv + (size_t)n * XT_D + 512 * hh + 8 * lane);
+            const uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a = __builtin_fmaf(h2f((uint16_t)(ww[i] & 0xffffu)), x[8 * hh + 2 * i], a);
+                a = __builtin_fmaf(h2f((uint16_t)(ww[i] >> 16)), x[8 * hh + 2 * i + 1], a);
+            }
+        }
+        a = wave_sum(a);
+        mine = lane == k ? a : mine;
+    }
+    if (lane < 16) o[(size_t)b * XT_D + 64 * h + 16 * w + lane] = h2f(f2h(mine));
+}
+
+extern "C" int px_k_hsoft(const float *s, void *P, int nb, int T, void *stream)
+{
+    if (nb <= 0 || T <= 0) return xt_fail("px_k_hsoft", "bad shape (nb > 0, T > 0)");
+    hipLaunchKernelGGL(k_px_hsoft, dim3(nb * 16), dim3(256), 0, (hipStream_t)stream, s, (uint16_t *)P, T);
+    return xt_check("px_k_hsoft");
+}
+
+extern "C" int px_k_hpool(const void *P, const void *y, float *part, int nb, int T, void *stream)
+{
+    if (nb <= 0 || T <= 0 || T % PX_PCH) return xt_fail("px_k_hpool", "T must be a positive multiple of 144");
+    if (((uintptr_t)y & 3) || ((uintptr_t)part & 7)) return xt_fail("px_k_hpool", "y 4-byte, part 8-byte aligned");
+    hipLaunchKernelGGL(k_px_hpool, dim3(nb, T / PX_PCH, 2), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)P,
+                       (const uint16_t *)y, part, T);
+    return xt_check("px_k_hpool");
+}
+
+extern "C" int px_k_hv(const float *part, int nch, const void *wv, float *o, int nb, void *stream)
+{
+    if (nb <= 0 || nch <= 0) return xt_fail("px_k_hv", "bad shape (nb > 0, nch > 0)");
+    if (((uintptr_t)part | (uintptr_t)wv) & 15) return xt_fail("px_k_hv", "part and wv must be 16-byte aligned");
+    hipLaunchKernelGGL(k_px_hv, dim3(nb * 16), dim3(256), 0, (hipStream_t)stream, part, nch, (const uint16_t *)wv, o);
+    return xt_check("px_k_hv");
+}
+
 // GELU of n fp32 values by the fc1 epilogue's gelu_erf (test hook: its accuracy is not visible through the E4M3 output)
 __global__ void __launch_bounds__(256) k_px_gelu(const float *__restrict__ u, float *__restrict__ g, int n)
 {

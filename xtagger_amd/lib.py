@@ -26,6 +26,10 @@ _SIGS = {
     "px_k_fc1": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
     "px_k_fc2": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _p]),
     "px_probe_gelu": (_i, [_p, _p, _i, _p]),
+    "px_k_hln": (_i, [_p, _p, _p, _p, _i, _p, _p, _p, _i, _p]),
+    "px_k_hsoft": (_i, [_p, _p, _i, _i, _p]),
+    "px_k_hpool": (_i, [_p, _p, _p, _i, _i, _p]),
+    "px_k_hv": (_i, [_p, _i, _p, _p, _i, _p]),
     "eva_k_fc1": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _i, _p]),
     "eva_k_fc2": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
     "eva_k_head": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _p]),
