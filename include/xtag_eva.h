@@ -205,6 +205,11 @@ int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32
  * Rows are window-major tokens (px_kernels.cu:1-4): sequence s = rows L s .. L s + L - 1 with L = 576 (windowed
  * blocks, 9 windows per image) or 5184 (global blocks, one image); rows <= 2^19. LayerNorm is eva_k_ln, attention
  * eva_k_flash_seq (T = TP = L). */
+/* px_kernels.cu:133-138 k_ppe: x fp16 [rows][1024] = f16(in . pe^T), in fp16 [rows][592] patch operands in window-major
+ * order, pe fp16 [1024][592]; rows % 128 == 0 (an even batch, px.h:21) */
+int px_k_pe(const void *in, const void *pe, void *x, int rows, void *stream);
+/* px_kernels.cu:16-50 k_pembed: x = f16(LN_1e-5(x + pos[m % T]) g + b) in place, pos fp32 [T][1024] */
+int px_k_pembed(void *x, const float *pos, int T, const float *g, const float *b, int rows, void *stream);
 /* px_kernels.cu:54-131 k_pqkv: q, k bf16 [rows/L][16][L][64] = RoPE(h8 . Wqkv^T + b) with table row m % L of
  * cs [L][32][2] on every token, vt bf16 [rows/L][16][64][L] = (h8 . Wv^T + b)^T; w from eva_k_prep_w(perm 1), bias
  * fp32 [3072] in natural order; q rows of w and bias carry log2(e)/8. */

@@ -56,6 +56,8 @@ _SIGS = {
     "xo_px_res_epi": (None, [_p, _i, _p, _p]),
     "xo_px_fc1_epi": (None, [_p, _i, _p, _p, _p]),
     "xo_px_hln": (None, [_p, _i, _i, _p, _p, _p, _p, _p, _p]),
+    "xo_px_pe": (None, [_p, _p, _i, _p]),
+    "xo_px_pembed": (None, [_p, _i, _i, _p, _p, _p, _p]),
     "xo_px_hsoft": (None, [_p, _i, _i, _p]),
     "xo_px_hpool_hv": (None, [_p, _p, _i, _i, _p, _p]),
     "xo_embed": (None, [_p, _p, _p, _i, _p]),
@@ -294,6 +296,23 @@ def px_fc1_epi(acc, bias, rs=None):
     lib.xo_px_fc1_epi(_ptr(acc), acc.shape[0], _ptr(_c(bias, np.float32)),
                       None if rs is None else _ptr(_c(rs, np.float32)), _ptr(h))
     return h
+
+
+def px_pe(in16, pe16):
+    _done()
+    in16 = _c(in16, np.uint16)
+    x = np.empty((in16.shape[0], 1024), np.uint16)
+    lib.xo_px_pe(_ptr(in16), _ptr(_c(pe16, np.uint16)), in16.shape[0], _ptr(x))
+    return x
+
+
+def px_pembed(x16, T, pos, g, b):
+    _done()
+    x16 = _c(x16, np.uint16)
+    y = np.empty_like(x16)
+    lib.xo_px_pembed(_ptr(x16), x16.shape[0], T, _ptr(_c(pos, np.float32)), _ptr(_c(g, np.float32)),
+                     _ptr(_c(b, np.float32)), _ptr(y))
+    return y
 
 
 def px_hln(x16, T, g, b, hpos16, U):

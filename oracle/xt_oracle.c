@@ -649,6 +649,49 @@ void xo_px_fc1_epi(const float *acc, int M, const float *bias, const float *rs, 
     }
 }
 
+void xo_px_pe(const uint16_t *in, const uint16_t *pe, int M, uint16_t *x)
+{
+    int m;
+
+#pragma omp parallel for schedule(static)
+    for (m = 0; m < M; m++) {
+        int n, k;
+        for (n = 0; n < 1024; n++) {
+            double a = 0.0;
+            for (k = 0; k < 588; k++) a += (double)xo_f16_to_f32(in[(size_t)m * 592 + k]) * xo_f16_to_f32(pe[(size_t)n * 592 + k]);
+            x[(size_t)m * 1024 + n] = xo_f32_to_f16((float)a);
+        }
+    }
+}
+
+void xo_px_pembed(const uint16_t *x, int M, int T, const float *pos, const float *g, const float *b, uint16_t *y)
+{
+    int m;
+
+#pragma omp parallel for schedule(static)
+    for (m = 0; m < M; m++) {
+        float v[1024], ls[64], mean, var, rstd, d;
+        int l, j, e;
+
+        for (e = 0; e < 1024; e++) v[e] = xo_f16_to_f32(x[(size_t)m * 1024 + e]) + pos[(size_t)(m % T) * 1024 + e];
+        for (l = 0; l < 64; l++) {
+            ls[l] = 0.0f;
+            for (j = 0; j < 16; j++) ls[l] += v[ln_elem(l, j)];
+        }
+        mean = wave_sum64(ls) * (1.0f / 1024.0f);
+        for (l = 0; l < 64; l++) {
+            ls[l] = 0.0f;
+            for (j = 0; j < 16; j++) {
+                d = v[ln_elem(l, j)] - mean;
+                ls[l] = fmaf(d, d, ls[l]);
+            }
+        }
+        var = wave_sum64(ls) * (1.0f / 1024.0f);
+        rstd = 1.0f / sqrtf(var + 1e-5f);
+        for (e = 0; e < 1024; e++) y[(size_t)m * 1024 + e] = xo_f32_to_f16(fmaf((v[e] - mean) * rstd, g[e], b[e]));
+    }
+}
+
 void xo_px_hln(const uint16_t *x, int M, int T, const float *g, const float *b, const uint16_t *hpos, const float *U,
                uint16_t *y, double *s)
 {

@@ -96,6 +96,11 @@ void xo_px_res_epi(const float *acc, int M, const float *bias, uint16_t *x);
 /* k_pfc1 (px_kernels.cu:222-233): h [M][4736] = (u (0.5 (1 + erff(u 0.70710678)))) rs[n], u = acc + bias[n] (libm erff;
  * rs NULL = no multiply), fp32 */
 void xo_px_fc1_epi(const float *acc, int M, const float *bias, const float *rs, float *h);
+/* k_ppe (px_kernels.cu:133-138): x [M][1024] = f16(in [M][592] . pe [1024][592]^T) over the 588 real columns, float64 dot */
+void xo_px_pe(const uint16_t *in, const uint16_t *pe, int M, uint16_t *x);
+/* k_pembed (px_kernels.cu:16-50): y = f16(fma((v - mean) rstd, g, b)), v = x + pos[m % T] in fp32, LayerNorm eps 1e-5 in
+ * the device's summation order (as xo_ln_quant) */
+void xo_px_pembed(const uint16_t *x, int M, int T, const float *pos, const float *g, const float *b, uint16_t *y);
 /* attention-pool head (px_kernels.cu:344-503). k_phln + k_phscore: y = f16(fma((x - mean) rstd, g, b) + hpos[m % T])
  * with the LayerNorm (eps 1e-5, IEEE rstd) in the device's summation order (as xo_ln_quant), s [M][16] = U y in
  * float64 from the fp16 y */

@@ -334,3 +334,28 @@ def test_px_pool_head(dev, xt, orc):
                           xt.ptr(d_out), nb, nt, _st()), "eva_k_head")
     logit = orc.gemm_f64_rows(q_ref, qs_ref, qw, sw, nt, np.arange(nb))
     assert np.abs(d_out.cpu().numpy() - 1.0 / (1.0 + np.exp(-(logit + hb)))).max() < 1e-4
+
+
+def test_px_patch_embed(dev, xt, orc):
+    """k_ppe + k_pembed over 2 images (10368 window-major rows): the fp16 patch GEMM within one fp16 rounding of the
+    float64 product, then the position add + LayerNorm bit-exact on the kernel's own x."""
+    M, T = 2 * T_IMG, T_IMG
+    _say("px patch embed")
+    r = np.random.default_rng(161)
+    inp = np.zeros((M, 592), np.float16)
+    inp[:, :588] = r.uniform(-1, 1, (M, 588)).astype(np.float16)
+    pe = np.zeros((D, 592), np.float16)
+    pe[:, :588] = (r.standard_normal((D, 588)) * 0.05).astype(np.float16)
+    pos = (r.standard_normal((T, D)) * 0.3).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    b = (0.1 * r.standard_normal(D)).astype(np.float32)
+    d_x = torch.zeros((M, D), dtype=torch.int16, device=dev)
+    _ok(xt.lib.px_k_pe(xt.ptr(_d(inp, dev)), xt.ptr(_d(pe, dev)), xt.ptr(d_x), M, _st()), "px_k_pe")
+    x = d_x.cpu().numpy().view(np.uint16)
+    ref = orc.px_pe(inp.view(np.uint16), pe.view(np.uint16))
+    terms = np.abs(inp.astype(np.float64)) @ np.abs(pe.astype(np.float64)).T
+    err = np.abs(_f16_f32(x).astype(np.float64) - _f16_f32(ref))
+    assert np.all(err <= 2.0 ** -10 * np.abs(_f16_f32(ref)) + 1e-5 * terms)
+    _ok(xt.lib.px_k_pembed(xt.ptr(d_x), xt.ptr(_d(pos, dev)), T, xt.ptr(_d(g, dev)), xt.ptr(_d(b, dev)), M, _st()),
+        "px_k_pembed")
+    assert (d_x.cpu().numpy().view(np.uint16) == orc.px_pembed(x, T, pos, g, b)).all()

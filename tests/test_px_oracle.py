@@ -150,3 +150,31 @@ def test_px_hpool_hv_vs_matmul(orc):
     o2 = orc.px_hpool_hv((P.astype(np.float32) * 2).astype(np.float16).view(np.uint16), y.view(np.uint16), nb, T,
                          wv.view(np.uint16))
     assert np.allclose(o2, 2 * o, rtol=1e-12, atol=1e-12)                                   # linear in P
+
+
+def test_px_pe_and_pembed_vs_float64(orc):
+    """k_ppe + k_pembed (px_kernels.cu:16-50, 133-138): the patch GEMM against numpy's float64 matmul (one fp16
+    rounding), and LN_1e-5(x + pos[m % T]) g + b against the float64 formula (one fp16 rounding; a row whose x + pos
+    is constant gives b)."""
+    r = np.random.default_rng(13)
+    M, T = 64, 40
+    inp = np.zeros((M, 592), np.float16)
+    inp[:, :588] = _f16(r.uniform(-1, 1, (M, 588)))
+    pe = np.zeros((1024, 592), np.float16)
+    pe[:, :588] = _f16(r.standard_normal((1024, 588)) * 0.05)
+    x = orc.px_pe(inp.view(np.uint16), pe.view(np.uint16)).view(np.float16)
+    ref = inp.astype(np.float64) @ pe.astype(np.float64).T
+    assert np.all(np.abs(x.astype(np.float64) - ref) <= 2.0 ** -11 * np.abs(ref) + 2.0 ** -25)
+    pos = (r.standard_normal((T, 1024)) * 0.3).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(1024)).astype(np.float32)
+    b = (0.1 * r.standard_normal(1024)).astype(np.float32)
+    x2 = x.copy()
+    pos[3] = 0.0
+    x2[3] = np.float16(0.5)                                              # x + pos constant on row 3: variance 0
+    y = orc.px_pembed(x2.view(np.uint16), T, pos, g, b).view(np.float16).astype(np.float64)
+    assert (y[3] == b.astype(np.float16).astype(np.float64)).all()
+    v = x2.astype(np.float64) + pos[np.arange(M) % T].astype(np.float64)
+    mean = v.mean(1, keepdims=True)
+    yr = (v - mean) / np.sqrt(((v - mean) ** 2).mean(1, keepdims=True) + 1e-5) * g + b
+    rows = np.arange(M) != 3
+    assert np.all(np.abs(y[rows] - yr[rows]) <= 2.0 ** -10 * np.abs(yr[rows]) + 1e-5 * np.abs(yr[rows]).max())

@@ -329,6 +329,9 @@ __global__ void __launch_bounds__(HeadCfg::NT) k_head(const uint8_t *__restrict_
 // x[1025 b] = f16(pos[0]) (pos carries cls and the conv bias, export_eva.py:76-80). Block 128 patches x 128
 // columns, 4 waves of 64 x 64, K = 592 in steps of 64 halves (the last step holds 16; the rest is zeroed).
 // ---------------------------------------------------------------------------------------------------------------
+// PX: the PixAI patch GEMM (px_kernels.cu:133-138 k_ppe) instead: x[m] = f16(in[m] . pe^T) for window-major token rows
+// m (no cls, no position: k_px_pembed adds it before its LayerNorm), rows a multiple of 128.
+template <bool PX>
 __global__ void __launch_bounds__(256) k_pe(const uint16_t *__restrict__ in, const uint16_t *__restrict__ pe,
                                             const float *__restrict__ pos, uint16_t *__restrict__ x, int nb)
 {
@@ -371,6 +374,17 @@ __global__ void __launch_bounds__(256) k_pe(const uint16_t *__restrict__ in, con
         __syncthreads();
     }
     const int c16 = lane & 15;
+    if constexpr (PX) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                uint16_t *xr = x + (size_t)(m0 + wm0 + 16 * i + 4 * g + r) * XT_D;
+#pragma unroll
+                for (int j = 0; j < 4; j++) xr[n0 + wn0 + 16 * j + c16] = f2h(acc[i][j][r]);
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -506,7 +520,16 @@ extern "C" int eva_k_pe(const void *in, const void *pe, const float *pos, void *
 {
     if (nb <= 0) return xt_fail("eva_k_pe", "nb must be positive");
     if (!XT_ALIGNED(in) || !XT_ALIGNED(pe)) return xt_fail("eva_k_pe", "in and pe must be 16-byte aligned");
-    hipLaunchKernelGGL(k_pe, dim3(XT_D / 128, nb * XT_NP / 128), dim3(256), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(k_pe<false>, dim3(XT_D / 128, nb * XT_NP / 128), dim3(256), 0, (hipStream_t)stream,
                        (const uint16_t *)in, (const uint16_t *)pe, pos, (uint16_t *)x, nb);
     return xt_check("eva_k_pe");
+}
+
+extern "C" int px_k_pe(const void *in, const void *pe, void *x, int rows, void *stream)
+{
+    if (rows <= 0 || rows % 128) return xt_fail("px_k_pe", "rows must be a positive multiple of 128 (an even batch)");
+    if (!XT_ALIGNED(in) || !XT_ALIGNED(pe)) return xt_fail("px_k_pe", "in and pe must be 16-byte aligned");
+    hipLaunchKernelGGL(k_pe<true>, dim3(XT_D / 128, rows / 128), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)in, (const uint16_t *)pe, (const float *)nullptr, (uint16_t *)x, 0);
+    return xt_check("px_k_pe");
 }

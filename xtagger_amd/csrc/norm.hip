@@ -131,6 +131,33 @@ __global__ void __launch_bounds__(256) k_lnh(const float *__restrict__ p, const 
     quant_row16(v, q + (size_t)row * XT_D, s, lds, row, lane);
 }
 
+// k_px_pembed (px_kernels.cu:16-50 k_pembed): x = f16(LN_1e-5(x + pos[m % T]) g + b) in place, x fp16 [rows][1024]
+// window-major token rows, pos fp32 [T][1024]; the position is added in fp32 to the fp16 patch embedding.
+__global__ void __launch_bounds__(256) k_px_pembed(uint16_t *__restrict__ x, const float *__restrict__ pos, int T,
+                                                   const float *__restrict__ g, const float *__restrict__ b, int rows)
+{
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    float v[16];
+    uint16_t *xr = x + (size_t)row * XT_D;
+    load_row16_f16(xr, lane, v);
+    const float *pr = pos + (size_t)(row % T) * XT_D;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const float4 a = *(const float4 *)(pr + 512 * h + 8 * lane), c = *(const float4 *)(pr + 512 * h + 8 * lane + 4);
+        v[8 * h + 0] += a.x; v[8 * h + 1] += a.y; v[8 * h + 2] += a.z; v[8 * h + 3] += a.w;
+        v[8 * h + 4] += c.x; v[8 * h + 5] += c.y; v[8 * h + 6] += c.z; v[8 * h + 7] += c.w;
+    }
+    ln16(v, g, b, lane, 1e-5f);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = (uint32_t)f2h(v[8 * h + 2 * i]) | ((uint32_t)f2h(v[8 * h + 2 * i + 1]) << 16);
+        *(uint4 *)(xr + 512 * h + 8 * lane) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 // k_px_hln: the PixAI attention-pool head's keys / values and scores (px_kernels.cu:344-400 k_phln + k_phscore,
 // fused): y = f16(LN_1e-5(x) + hpos[m % T]) fp16 [rows][1024] and s [rows][16] = U y of the fp16 y (exp2 domain, the
 // constant query folded into U). U [16][1024] fp32 sits in shared memory; each wave takes 16 rows in turn, and each
@@ -225,4 +252,14 @@ extern "C" int px_k_hln(const void *x, const float *g, const float *b, const voi
     hipLaunchKernelGGL(k_px_hln, dim3((rows + per - 1) / per), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x,
                        g, b, (const uint16_t *)hpos, T, U, (uint16_t *)y, s, rows);
     return xt_check("px_k_hln");
+}
+
+extern "C" int px_k_pembed(void *x, const float *pos, int T, const float *g, const float *b, int rows, void *stream)
+{
+    if (rows <= 0 || T <= 0) return xt_fail("px_k_pembed", "bad shape (rows > 0, T > 0)");
+    if (((uintptr_t)x | (uintptr_t)pos | (uintptr_t)g | (uintptr_t)b) & 15)
+        return xt_fail("px_k_pembed", "x, pos, g, b must be 16-byte aligned");
+    hipLaunchKernelGGL(k_px_pembed, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, (uint16_t *)x, pos, T, g,
+                       b, rows);
+    return xt_check("px_k_pembed");
 }
