@@ -408,82 +408,38 @@ def bench_pixai_block(torch, L, nb=4, reps=10):
     return res
 
 
-def bench_pixai_forward(torch, L, nb=4, nt=13461, replays=5):
-    """The whole PixAI tagger forward (px.h:110-190) on the px_k_* kernels as one HIP graph at batch 4 (PX_NB):
-    patch GEMM + pre-LN, 32 ViTDet-L blocks (global attention in blocks 7, 15, 23, 31, windowed in the rest), the
-    attention-pool head and a 13461-row tag head; 32 distinct synthetic weight sets (438 MB of E4M3), inputs resident.
-    Returns (images/s, ms per batch)."""
-    dev = torch.device("cuda:0")
-    T5, PH = 5184, 4736
-    M = nb * T5
-    g = torch.Generator(device=dev).manual_seed(11)
-    t = lambda *s, dt=torch.uint8: torch.zeros(*s, dtype=dt, device=dev)
-    st = lambda: torch.cuda.current_stream().cuda_stream
-    P = L.ptr
-
-    def packw(n, k, perm=0):
-        w16 = (torch.randn(n, k, generator=g, device=dev) * 0.02).half()
-        scratch = torch.empty(n * k, dtype=torch.float32, device=dev)
-        q, s = t(n, k), t(n // 128, k // 128, dt=torch.float32)
-        L.check(L.lib.eva_k_prep_w(P(w16), k, n, k, n, k, perm, None, P(scratch), P(q), P(s), st()), "prep")
-        torch.cuda.synchronize()
-        return q, s
-
-    vec = lambda n, sc=0.1: torch.randn(n, generator=g, device=dev) * sc
-    blocks = []
-    for i in range(32):
-        blocks.append({"qkv": packw(3 * D, D, 1), "o": packw(D, D), "w1": packw(PH, D), "w2": packw(D, PH),
-                       "bqkv": vec(3 * D), "bo": vec(D), "b1": vec(PH), "b2": vec(D),
-                       "g1": 1 + vec(D), "e1": vec(D), "g2": 1 + vec(D), "e2": vec(D)})
-    cs = {576: torch.rand(576, 32, 2, generator=g, device=dev), 5184: torch.rand(5184, 32, 2, generator=g, device=dev)}
-    inp = t(M, 592, dt=torch.float16)
-    inp[:, :588] = torch.rand(M, 588, generator=g, device=dev).half() * 2 - 1
-    pe = t(D, 592, dt=torch.float16)
-    pe[:, :588] = (torch.randn(D, 588, generator=g, device=dev) * 0.05).half()
-    pos, pg, pb = torch.randn(T5, D, generator=g, device=dev) * 0.3, 1 + vec(D), vec(D)
-    hg, hbeta = 1 + vec(D), vec(D)
-    hpos = (torch.randn(T5, D, generator=g, device=dev) * 0.2).half()
-    U = torch.randn(16, D, generator=g, device=dev) * 0.05
-    wv = (torch.randn(D, D, generator=g, device=dev) * 0.03).half()
-    hw, hws = packw((nt + 127) // 128 * 128, D)
-    hb = vec(nt)
-    x, h8, hs = t(M, D, dt=torch.float16), t(M, D), t(8, M, dt=torch.float32)
-    q, k, vt = t(M * D, dt=torch.int16), t(M * D, dt=torch.int16), t(M * D, dt=torch.int16)
-    o8, os_ = t(M, D), t(8, M, dt=torch.float32)
-    m8, ms = t(M, PH), t(PH // 128, M, dt=torch.float32)
-    y, s = t(M, D, dt=torch.int16), t(M, 16, dt=torch.float32)
-    Pm, part = t(nb, 16, T5, dt=torch.int16), t(nb, T5 // 144, 16, D, dt=torch.float32)
-    o, oq, oqs, out = t(nb, D, dt=torch.float32), t(nb, D), t(8, nb, dt=torch.float32), t(nb, nt, dt=torch.float32)
-
-    def forward():
-        rc = [L.lib.px_k_pe(P(inp), P(pe), P(x), M, st()), L.lib.px_k_pembed(P(x), P(pos), T5, P(pg), P(pb), M, st())]
-        for i, B in enumerate(blocks):
-            Ls = 5184 if (i & 7) == 7 else 576
-            rc += [L.lib.eva_k_ln(P(x), P(B["g1"]), P(B["e1"]), P(h8), P(hs), M, M, st()),
-                   L.lib.px_k_qkv(P(h8), P(hs), M, P(B["qkv"][0]), P(B["qkv"][1]), P(B["bqkv"]), P(cs[Ls]), Ls, P(q),
-                                  P(k), P(vt), M, st()),
-                   L.lib.eva_k_flash_seq(P(q), P(k), P(vt), P(o8), P(os_), M, M // Ls, Ls, Ls, None, st()),
-                   L.lib.px_k_proj(P(o8), P(os_), M, P(B["o"][0]), P(B["o"][1]), P(B["bo"]), P(x), M, st()),
-                   L.lib.eva_k_ln(P(x), P(B["g2"]), P(B["e2"]), P(h8), P(hs), M, M, st()),
-                   L.lib.px_k_fc1(P(h8), P(hs), M, P(B["w1"][0]), P(B["w1"][1]), P(B["b1"]), None, P(m8), P(ms), M,
-                                  st()),
-                   L.lib.px_k_fc2(P(m8), P(ms), M, P(B["w2"][0]), P(B["w2"][1]), P(B["b2"]), P(x), M, st())]
-        rc += [L.lib.px_k_hln(P(x), P(hg), P(hbeta), P(hpos), T5, P(U), P(y), P(s), M, st()),
-               L.lib.px_k_hsoft(P(s), P(Pm), nb, T5, st()),
-               L.lib.px_k_hpool(P(Pm), P(y), P(part), nb, T5, st()),
-               L.lib.px_k_hv(P(part), T5 // 144, P(wv), P(o), nb, st()),
-               L.lib.eva_k_quant_act(P(o), 1, D, nb, D, P(oq), D, P(oqs), nb, st()),
-               L.lib.eva_k_head(P(oq), P(oqs), nb, P(hw), P(hws), P(hb), P(out), nb, nt, st())]
-        if any(rc):
-            raise RuntimeError("PixAI forward launch failed")
-
-    forward()
-    torch.cuda.synchronize()
-    if not torch.isfinite(out).all():
-        raise RuntimeError("PixAI forward produced non-finite scores")
-    gr = capture(torch, forward, 1)
-    time_graph(torch, gr, 2)
-    ms_b = time_graph(torch, gr, replays)
+def bench_pixai_forward(torch, L, nb=4, nt=13461, replays=10):
+    """The PixAI tagger engine (px_open_nb .. px_run, px.h:110-190) at batch 4 (PX_NB) on a synthetic pixai.bin v2:
+    one graph replay = patch embedding + pre-LN, 32 ViTDet-L blocks (global attention in blocks 7, 15, 23, 31), the
+    attention-pool head and a 13461-row tag head, 32 distinct random weight sets, inputs resident in the engine's
+    device buffer. Returns (images/s, ms per batch)."""
+    import tempfile
+    import numpy as np
+    from xtagger_amd import blob
+    from xtagger_amd.engine import PxEngine
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "pixai_synth_v2.bin")
+        blob.write_px_v2(path, blob.synth_px_model(seed=11, nt=nt))
+        eng = PxEngine(path, nb=nb)
+        eng.ready()
+    try:
+        r = np.random.default_rng(12)
+        inp = np.zeros((nb, 5184, 592), np.float16)
+        inp[..., :588] = r.uniform(-1, 1, (nb, 5184, 588)).astype(np.float16)
+        eng.submit(0, inp)
+        scores = eng.wait(0, nb)
+        if not np.isfinite(scores).all():
+            raise RuntimeError("PixAI forward produced non-finite scores")
+        for _ in range(2):
+            eng.run()
+        eng.sync()
+        t0 = time.perf_counter()
+        for _ in range(replays):
+            eng.run()
+        eng.sync()
+        ms_b = (time.perf_counter() - t0) * 1e3 / replays
+    finally:
+        eng.close()
     return nb / (ms_b * 1e-3), ms_b
 
 
@@ -678,7 +634,8 @@ def main():
     if not args.no_forward:
         ips, fms = bench_pixai_forward(torch, L)
         out["pixai_forward_b4"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
-                                   "input": "1008x1008 (5184 tokens)", "weights": "synthetic, 32 distinct blocks"}
+                                   "input": "1008x1008 (5184 tokens)", "path": "px_open_nb + px_run (engine graph)",
+                                   "weights": "synthetic pixai.bin v2, 32 distinct blocks"}
     ln_us, ln_gbs = bench_ln(torch, L)
     out["ln_m32800"] = {"us": round(ln_us, 2), "gbs": round(ln_gbs, 1), "frac_hbm_peak": round(ln_gbs / 8000.0, 3),
                         "bytes": 32 * T * D * 3 + 32 * T * 8 * 4}

@@ -201,6 +201,42 @@ size_t eva_img_prep_bytes(uint32_t S, uint32_t max_side);
 int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S, void *scratch,
                  size_t bytes, void *out, void *stream);
 
+/* ---- PixAI tagger engine (px.h:110-494): the ViTDet-L forward on the px_k_* kernels below ---- */
+#define PX_NB 4                               /* default model inputs per launch (px.h:21; even) */
+#define PX_NBUF 4                             /* host output buffers (px.h:28) */
+#define PX_T 5184                             /* tokens per 1008^2 input: 72 x 72 patches, window-major */
+#define PX_LW 576                             /* tokens per attention window */
+#define PX_HID 4736
+#define PX_NL 32
+#define PX_IN ((size_t)PX_T * EVA_K0P)        /* halves per model input */
+/* Caller-allocated like the reference's px struct; callers read nt and hout (px.h:68-88). */
+typedef struct px_impl px_impl;
+typedef struct {
+    uint32_t nt, ntp;                         /* tags of the file; rows of its head (nt rounded up to 8) */
+    uint32_t nb;                              /* model inputs per launch */
+    float *hout[PX_NBUF];                     /* sigmoid scores [nb][nt] of each batch */
+    px_impl *impl;
+} px;
+/* px.h:357. Reads the "PXAI" header and starts the bring-up on its own thread. The blob is version 2
+ * (export_pixai.py without a calibration file: fp16 block weights), packed to E4M3 with 128x128 scales on the GPU at
+ * bring-up. pool / poolb are accepted and unused (inputs are staged into engine-owned pinned memory). */
+int px_open(px *p, const char *weights, int device, void *pool, size_t poolb);
+/* px_open with the batch (even, 2..100: token rows stay within the kernels' 2^19) as a runtime parameter */
+int px_open_nb(px *p, const char *weights, int device, void *pool, size_t poolb, uint32_t nb);
+int px_ready(px *p);                                                /* px.h:388 */
+int px_poll(px *p);                                                 /* px.h:400 */
+/* px.h:406. n <= nb inputs, each an fp16 [5184][592] patch operand in window-major token order; buf < PX_NBUF. */
+int px_submit(px *p, uint32_t buf, uint16_t *const *in, uint32_t n);
+int px_query(px *p, uint32_t buf);                                  /* px.h:421 */
+const float *px_wait(px *p, uint32_t buf);                          /* px.h:426: scores [n][nt] */
+void px_close(px *p);                                               /* px.h:457 */
+/* Resident-input path, as eva_dev_input .. eva_sync (no reference counterpart; used by benchmarks and tests) */
+void *px_dev_input(px *p);
+int px_run(px *p);
+const float *px_dev_output(px *p);
+void *px_stream_handle(px *p);
+int px_sync(px *p);
+
 /* ---- PixAI tagger (ViTDet-L) block kernels on the same block-scaled main loop (px_kernels.cu) ----
  * Rows are window-major tokens (px_kernels.cu:1-4): sequence s = rows L s .. L s + L - 1 with L = 576 (windowed
  * blocks, 9 windows per image) or 5184 (global blocks, one image); rows <= 2^19. LayerNorm is eva_k_ln, attention

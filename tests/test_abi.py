@@ -4,6 +4,8 @@ import glob
 import os
 import re
 
+import numpy as np
+
 from xtagger_amd import LIB_PATH, REPO_DIR
 
 
@@ -60,6 +62,54 @@ def test_open_rejects_bad_header(tmp_path):
         Engine(str(p))
     with pytest.raises(RuntimeError):
         Engine(str(tmp_path / "missing.bin"))
+
+
+def test_px_open_rejects_bad_files(tmp_path):
+    """px.h:357-372: a file that is not a pixai.bin v2, or an odd batch, fails px_open with -1 (no device call)."""
+    import struct
+    import pytest
+    from xtagger_amd.engine import PxEngine
+    p = tmp_path / "bad.bin"
+    for hdr in (b"NOPE" + b"\0" * 12, struct.pack("<4sIII", b"PXAI", 3, 100, 0), struct.pack("<4sIII", b"PXAI", 2, 0, 0)):
+        p.write_bytes(hdr + b"\0" * 300)
+        with pytest.raises(RuntimeError):
+            PxEngine(str(p))
+    p.write_bytes(struct.pack("<4sIII", b"PXAI", 2, 10, 0) + b"\0" * 300)
+    with pytest.raises(RuntimeError):
+        PxEngine(str(p), nb=3)
+    with pytest.raises(RuntimeError):
+        PxEngine(str(tmp_path / "missing.bin"))
+
+
+def test_px_blob_layout_matches_engine_walk():
+    """The writer's byte count equals the walk of px.h:196-253 (every tensor on a 256-byte boundary) for nt = 13."""
+    from xtagger_amd import blob
+    sizes = [1024 * 592 * 2, 5184 * 1024 * 4, 4096, 4096, 576 * 64 * 4, 5184 * 64 * 4]
+    sizes += [4096, 4096, 3072 * 1024 * 2, 3072 * 4, 1024 * 1024 * 2, 4096, 4096, 4096, 4736 * 1024 * 2, 4736 * 4,
+              4736 * 4, 1024 * 4736 * 2, 4096] * 32
+    sizes += [4096, 4096, 16 * 4096, 5184 * 1024 * 2, 1024 * 1024 * 2, 16 * 1024 * 2, 16 * 4]
+    off = 0
+    for s in sizes:
+        off = (off + 255) // 256 * 256 + s
+    total = 0
+    for name, a, dt in blob.px_tensors(_fake_px_model(13)):
+        total = (total + 255) // 256 * 256 + np.asarray(a).size * np.dtype(dt).itemsize
+    assert total == off
+
+
+def _fake_px_model(nt):
+    """Zero tensors of the v2 shapes (cheap: broadcast views)."""
+    f16, f32 = np.float16, np.float32
+    z = lambda shape, dt: np.broadcast_to(np.zeros(1, dt), shape)
+    L = {"ln1w": z(1024, f32), "ln1b": z(1024, f32), "wqkv": z((3072, 1024), f16), "bqkv": z(3072, f32),
+         "wo": z((1024, 1024), f16), "bo": z(1024, f32), "ln2w": z(1024, f32), "ln2b": z(1024, f32),
+         "w1": z((4736, 1024), f16), "b1": z(4736, f32), "rs": z(4736, f32), "w2": z((1024, 4736), f16),
+         "b2": z(1024, f32)}
+    ntp = (nt + 7) & ~7
+    return {"nt": nt, "pe": z((1024, 592), f16), "pos": z((5184, 1024), f32), "lnpw": z(1024, f32),
+            "lnpb": z(1024, f32), "csw": z((576, 32, 2), f32), "csg": z((5184, 32, 2), f32), "layers": [L] * 32,
+            "hnw": z(1024, f32), "hnb": z(1024, f32), "U": z((16, 1024), f32), "hpos": z((5184, 1024), f16),
+            "wv": z((1024, 1024), f16), "hw": z((ntp, 1024), f16), "hb": z(ntp, f32)}
 
 
 def test_blob_roundtrip_small(tmp_path):

@@ -174,3 +174,95 @@ def synth_inputs(nb, seed=1):
     out = np.zeros((nb, NP, K0P), np.float16)
     out[:, :, :K0] = p.astype(np.float16)
     return out
+
+
+# ---- PixAI (ViTDet-L) pixai.bin version 2 (src/tools/export_pixai.py:110-152; read by src/engine/px.h:196-253 with
+# PX_VER 2): "PXAI", u32 2, u32 nt, u32 nbytes, 240 zero bytes, then every tensor on a 256-byte boundary:
+#   pe fp16 [1024][592], pos fp32 [5184][1024], pre-LN w, b fp32 [1024], rope fp32 [576][32][2] (windows) and
+#   [5184][32][2] (global), 32 x [ln1 w, b, Wqkv fp16 [3072][1024] (q rows carry log2(e) / 8), bqkv fp32 [3072] (q part
+#   likewise), Wo fp16 [1024][1024], bo, ln2 w, b, W1 fp16 [4736][1024], b1 fp32 [4736], rs fp32 [4736] (ones without
+#   calibration), W2 fp16 [1024][4736], b2], head LN w, b, U fp32 [16][1024], hpos fp16 [5184][1024], Wv fp16
+#   [1024][1024], head fp16 [ntp][1024], head bias fp32 [ntp] (ntp = nt rounded up to 8).
+PX_T, PX_LW, PX_HID, PX_NL = 5184, 576, 4736, 32
+
+
+def synth_px_layer(r, std=0.02):
+    f16, f32 = np.float16, np.float32
+
+    def n(shape, s):
+        return (r.standard_normal(shape, dtype=np.float32) * s).astype(f32)
+
+    L = {"ln1w": 1 + n(D, 0.1), "ln1b": n(D, 0.02), "ln2w": 1 + n(D, 0.1), "ln2b": n(D, 0.02)}
+    wqkv, bqkv = n((3 * D, D), std), n(3 * D, 0.05)
+    wqkv[:D] *= QSCALE
+    bqkv[:D] *= QSCALE
+    L["wqkv"], L["bqkv"] = wqkv.astype(f16), bqkv
+    L["wo"], L["bo"] = n((D, D), std).astype(f16), n(D, 0.05)
+    L["w1"], L["b1"] = n((PX_HID, D), std).astype(f16), n(PX_HID, 0.05)
+    L["rs"] = np.ones(PX_HID, f32)
+    L["w2"], L["b2"] = n((D, PX_HID), std).astype(f16), n(D, 0.05)
+    return L
+
+
+def synth_px_model(seed=0, nt=1000, head_std=0.05):
+    """Random-init PixAI tensors in the v2 export layout. Rope tables are (cos, sin) of random angles: the kernels
+    only need a valid table (the real one lives in the ONNX constants)."""
+    r = np.random.default_rng(seed)
+    f16, f32 = np.float16, np.float32
+
+    def n(shape, s):
+        return (r.standard_normal(shape, dtype=np.float32) * s).astype(f32)
+
+    def rope(rows):
+        a = r.random((rows, 32)) * 6.283185307179586
+        return np.stack([np.cos(a), np.sin(a)], -1).astype(f32)
+
+    m = {"nt": nt}
+    pe = np.zeros((D, K0P), f32)
+    pe[:, :K0] = n((D, K0), 0.02)
+    m["pe"], m["pos"] = pe.astype(f16), n((PX_T, D), 0.02)
+    m["lnpw"], m["lnpb"] = 1 + n(D, 0.1), n(D, 0.02)
+    m["csw"], m["csg"] = rope(PX_LW), rope(PX_T)
+    m["layers"] = [synth_px_layer(r) for _ in range(PX_NL)]
+    m["hnw"], m["hnb"] = 1 + n(D, 0.1), n(D, 0.02)
+    m["U"], m["hpos"] = n((16, D), 0.05), n((PX_T, D), 0.02).astype(f16)
+    m["wv"] = n((D, D), 0.03).astype(f16)
+    ntp = (nt + 7) & ~7
+    hw, hb = np.zeros((ntp, D), f32), np.zeros(ntp, f32)
+    hw[:nt], hb[:nt] = n((nt, D), head_std), n(nt, 0.1)
+    m["hw"], m["hb"] = hw.astype(f16), hb
+    return m
+
+
+def px_tensors(m):
+    """(name, array, dtype) in the blob's order."""
+    f16, f32 = np.float16, np.float32
+    out = [("pe", m["pe"], f16), ("pos", m["pos"], f32), ("lnpw", m["lnpw"], f32), ("lnpb", m["lnpb"], f32),
+           ("csw", m["csw"], f32), ("csg", m["csg"], f32)]
+    for i, L in enumerate(m["layers"]):
+        for k, dt in (("ln1w", f32), ("ln1b", f32), ("wqkv", f16), ("bqkv", f32), ("wo", f16), ("bo", f32),
+                      ("ln2w", f32), ("ln2b", f32), ("w1", f16), ("b1", f32), ("rs", f32), ("w2", f16), ("b2", f32)):
+            out.append((f"{k}{i}", L[k], dt))
+    out += [("hnw", m["hnw"], f32), ("hnb", m["hnb"], f32), ("U", m["U"], f32), ("hpos", m["hpos"], f16),
+            ("wv", m["wv"], f16), ("hw", m["hw"], f16), ("hb", m["hb"], f32)]
+    return out
+
+
+def write_px_v2(path, m):
+    """Write model tensors m (synth_px_model layout) as a pixai.bin v2 file, streamed tensor by tensor."""
+    tensors = px_tensors(m)
+    size = 0
+    for _, a, dt in tensors:
+        size += -size % 256
+        size += np.asarray(a).size * np.dtype(dt).itemsize
+    with open(path, "wb") as f:
+        f.write(struct.pack("<4sIII", b"PXAI", 2, m["nt"], size))
+        f.write(b"\0" * 240)
+        pos = 0
+        for _, a, dt in tensors:
+            pad = -pos % 256
+            f.write(b"\0" * pad)
+            data = np.ascontiguousarray(a, dtype=dt).tobytes()
+            f.write(data)
+            pos += pad + len(data)
+    return size

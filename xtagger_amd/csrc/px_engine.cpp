@@ -1,0 +1,389 @@
+// px_engine.cpp - the PixAI tagger (ViTDet-L, 1008^2 inputs) engine behind the reference's px.h host API
+// (src/engine/px.h:110-494), on HIP for one MI355X, with the same lifecycle as the wd engine: px_open returns at once;
+// the bring-up (device, weights, packing, buffers, graph capture) runs on its own thread and px_ready joins it. One
+// forward = one replay of a HIP graph captured once for nb inputs: patch embedding + pre-LN, 32 blocks (global
+// attention in blocks 7, 15, 23, 31, px.h:38), the attention-pool head and the tag head (px.h:110-190).
+#include <hip/hip_runtime.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "xt_abi.h"
+#include "xtag_eva.h"
+
+#define PX_CHUNK (32u << 20)  // weight streaming chunk
+#define PX_PCH 144            // attention-pool token chunk (px_kernels.cu:446)
+
+struct PxLayer {
+    const float *ln1w, *ln1b, *bqkv, *bo, *ln2w, *ln2b, *b1, *rs, *b2;  // in the blob
+    const uint16_t *wqkv16, *wo16, *w116, *w216;                        // fp16 block weights in the blob
+    uint8_t *wqkv, *wo, *w1, *w2;                                       // packed E4M3
+    float *sqkv, *so, *s1, *s2;
+};
+
+struct px_impl {
+    int devno, bstatus, up, booted;
+    pthread_t boot;
+    char *path;
+    size_t wbytes;
+    uint32_t nb, M;                                     // inputs per launch, token rows (nb * 5184)
+    hipStream_t st;
+    uint8_t *blob;
+    const uint16_t *pe, *hpos, *wv, *hw16;
+    const float *pos, *lnpw, *lnpb, *csw, *csg, *hnw, *hnb, *U, *hb;
+    PxLayer L[PX_NL];
+    uint8_t *hq;                                        // head E4M3 [ceil(nt/128)*128][1024]
+    float *hs;                                          // [ceil(nt/128)][8]
+    float *scratch;
+    // activations
+    uint16_t *in, *x, *q, *k, *vt, *y, *P;
+    uint8_t *h8, *o8, *m8, *oq;
+    float *sh, *so8, *sm, *s, *part, *o, *oqs, *out;
+    hipGraphExec_t graph;
+    hipEvent_t done[PX_NBUF];
+    uint16_t *stage;
+    std::vector<void *> allocs;
+};
+
+static int px_alloc(px_impl *E, void **p, size_t bytes, bool zero)
+{
+    if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) return xt_fail("hipMalloc", "out of device memory");
+    E->allocs.push_back(*p);
+    if (zero && hipMemset(*p, 0, bytes) != hipSuccess) return xt_fail("hipMemset", "failed");
+    return 0;
+}
+#define PX_ALLOC(E, p, bytes, zero)                                    \
+    do {                                                               \
+        void *tmp_;                                                    \
+        if (px_alloc((E), &tmp_, (bytes), (zero))) return -1;          \
+        (p) = (decltype(p))tmp_;                                       \
+    } while (0)
+#define PX_CK(call)                                                    \
+    do {                                                               \
+        if ((call)) return -1;                                         \
+    } while (0)
+
+// Blob layout of export_pixai.py version 2 (px.h:196-253 with PX_VER 2): every tensor on a 256-byte boundary.
+static int px_layout(px_impl *E, uint32_t ntp)
+{
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> uint8_t * {
+        off = (off + 255) & ~(size_t)255;
+        uint8_t *p = E->blob + off;
+        off += bytes;
+        return p;
+    };
+    E->pe = (const uint16_t *)take((size_t)EVA_D * EVA_K0P * 2);
+    E->pos = (const float *)take((size_t)PX_T * EVA_D * 4);
+    E->lnpw = (const float *)take(EVA_D * 4);
+    E->lnpb = (const float *)take(EVA_D * 4);
+    E->csw = (const float *)take((size_t)PX_LW * 32 * 2 * 4);
+    E->csg = (const float *)take((size_t)PX_T * 32 * 2 * 4);
+    for (int i = 0; i < PX_NL; i++) {
+        PxLayer &L = E->L[i];
+        L.ln1w = (const float *)take(EVA_D * 4);
+        L.ln1b = (const float *)take(EVA_D * 4);
+        L.wqkv16 = (const uint16_t *)take((size_t)3 * EVA_D * EVA_D * 2);
+        L.bqkv = (const float *)take(3 * EVA_D * 4);
+        L.wo16 = (const uint16_t *)take((size_t)EVA_D * EVA_D * 2);
+        L.bo = (const float *)take(EVA_D * 4);
+        L.ln2w = (const float *)take(EVA_D * 4);
+        L.ln2b = (const float *)take(EVA_D * 4);
+        L.w116 = (const uint16_t *)take((size_t)PX_HID * EVA_D * 2);
+        L.b1 = (const float *)take(PX_HID * 4);
+        L.rs = (const float *)take(PX_HID * 4);
+        L.w216 = (const uint16_t *)take((size_t)EVA_D * PX_HID * 2);
+        L.b2 = (const float *)take(EVA_D * 4);
+    }
+    E->hnw = (const float *)take(EVA_D * 4);
+    E->hnb = (const float *)take(EVA_D * 4);
+    E->U = (const float *)take((size_t)16 * EVA_D * 4);
+    E->hpos = (const uint16_t *)take((size_t)PX_T * EVA_D * 2);
+    E->wv = (const uint16_t *)take((size_t)EVA_D * EVA_D * 2);
+    E->hw16 = (const uint16_t *)take((size_t)ntp * EVA_D * 2);
+    E->hb = (const float *)take((size_t)ntp * 4);
+    if (off != E->wbytes) {
+        fprintf(stderr, "px: weight layout mismatch (%zu vs %zu bytes)\n", off, E->wbytes);
+        return -1;
+    }
+    return 0;
+}
+
+// file bytes [256, 256 + wbytes) -> device, through two pinned chunks (px.h:318-345)
+static int px_stream_weights(px_impl *E)
+{
+    FILE *f = fopen(E->path, "rb");
+    void *buf[2] = {NULL, NULL};
+    hipEvent_t ev[2] = {NULL, NULL};
+    size_t off = 0, n;
+    int i = 0, rc = -1;
+
+    if (!f) return xt_fail("weights", "cannot open");
+    if (fseek(f, 256, SEEK_SET)) goto out;
+    for (int j = 0; j < 2; j++)
+        if (hipHostMalloc(&buf[j], PX_CHUNK, hipHostMallocDefault) != hipSuccess || hipEventCreate(&ev[j]) != hipSuccess)
+            goto out;
+    for (off = 0; off < E->wbytes; off += n, i ^= 1) {
+        n = E->wbytes - off < PX_CHUNK ? E->wbytes - off : PX_CHUNK;
+        if (hipEventSynchronize(ev[i]) != hipSuccess || fread(buf[i], 1, n, f) != n) goto out;
+        if (hipMemcpyAsync(E->blob + off, buf[i], n, hipMemcpyHostToDevice, E->st) != hipSuccess) goto out;
+        if (hipEventRecord(ev[i], E->st) != hipSuccess) goto out;
+    }
+    if (hipStreamSynchronize(E->st) == hipSuccess) rc = 0;
+out:
+    (void)hipStreamSynchronize(E->st);
+    for (int j = 0; j < 2; j++) {
+        if (ev[j]) (void)hipEventDestroy(ev[j]);
+        if (buf[j]) (void)hipHostFree(buf[j]);
+    }
+    fclose(f);
+    if (rc) fprintf(stderr, "px: cannot stream weights from %s\n", E->path);
+    return rc;
+}
+
+// The whole forward for nb inputs on E->st (captured once into E->graph), px.h:110-190.
+static int px_forward(px *p)
+{
+    px_impl *E = p->impl;
+    void *st = (void *)E->st;
+    const int M = (int)E->M, nb = (int)E->nb;
+
+    PX_CK(px_k_pe(E->in, E->pe, E->x, M, st));
+    PX_CK(px_k_pembed(E->x, E->pos, PX_T, E->lnpw, E->lnpb, M, st));
+    for (int i = 0; i < PX_NL; i++) {
+        const PxLayer &L = E->L[i];
+        const bool glob = (i & 7) == 7;
+        const int Ls = glob ? PX_T : PX_LW;
+        PX_CK(eva_k_ln(E->x, L.ln1w, L.ln1b, E->h8, E->sh, M, M, st));
+        PX_CK(px_k_qkv(E->h8, E->sh, M, L.wqkv, L.sqkv, L.bqkv, glob ? E->csg : E->csw, Ls, E->q, E->k, E->vt, M, st));
+        PX_CK(eva_k_flash_seq(E->q, E->k, E->vt, E->o8, E->so8, M, M / Ls, Ls, Ls, NULL, st));
+        PX_CK(px_k_proj(E->o8, E->so8, M, L.wo, L.so, L.bo, E->x, M, st));
+        PX_CK(eva_k_ln(E->x, L.ln2w, L.ln2b, E->h8, E->sh, M, M, st));
+        PX_CK(px_k_fc1(E->h8, E->sh, M, L.w1, L.s1, L.b1, L.rs, E->m8, E->sm, M, st));
+        PX_CK(px_k_fc2(E->m8, E->sm, M, L.w2, L.s2, L.b2, E->x, M, st));
+    }
+    PX_CK(px_k_hln(E->x, E->hnw, E->hnb, E->hpos, PX_T, E->U, E->y, E->s, M, st));
+    PX_CK(px_k_hsoft(E->s, E->P, nb, PX_T, st));
+    PX_CK(px_k_hpool(E->P, E->y, E->part, nb, PX_T, st));
+    PX_CK(px_k_hv(E->part, PX_T / PX_PCH, E->wv, E->o, nb, st));
+    PX_CK(eva_k_quant_act(E->o, 1, EVA_D, nb, EVA_D, E->oq, EVA_D, E->oqs, nb, st));
+    PX_CK(eva_k_head(E->oq, E->oqs, nb, E->hq, E->hs, E->hb, E->out, nb, (int)p->nt, st));
+    return 0;
+}
+
+static int px_up(px *p)
+{
+    px_impl *E = p->impl;
+    const uint32_t nblk = (p->nt + 127) / 128;
+    void *st;
+
+    XT_HIP(hipSetDevice(E->devno));
+    XT_HIP(hipStreamCreateWithFlags(&E->st, hipStreamNonBlocking));
+    st = (void *)E->st;
+    PX_ALLOC(E, E->blob, E->wbytes, false);
+    if (px_stream_weights(E) || px_layout(E, p->ntp)) return -1;
+
+    // packed weights (bring-up packing on the GPU); q / k rows of Wqkv pair-split for the RoPE epilogue
+    const size_t scratch_f = (size_t)(nblk * 128 > PX_HID ? nblk * 128 : PX_HID) * EVA_D;
+    PX_ALLOC(E, E->scratch, scratch_f * 4, false);
+    for (int i = 0; i < PX_NL; i++) {
+        PxLayer &L = E->L[i];
+        PX_ALLOC(E, L.wqkv, (size_t)3 * EVA_D * EVA_D, false);
+        PX_ALLOC(E, L.sqkv, 24 * 8 * 4, false);
+        PX_ALLOC(E, L.wo, (size_t)EVA_D * EVA_D, false);
+        PX_ALLOC(E, L.so, 8 * 8 * 4, false);
+        PX_ALLOC(E, L.w1, (size_t)PX_HID * EVA_D, false);
+        PX_ALLOC(E, L.s1, 37 * 8 * 4, false);
+        PX_ALLOC(E, L.w2, (size_t)EVA_D * PX_HID, false);
+        PX_ALLOC(E, L.s2, 8 * 37 * 4, false);
+        PX_CK(eva_k_prep_w(L.wqkv16, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, NULL, E->scratch, L.wqkv, L.sqkv, st));
+        PX_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
+        PX_CK(eva_k_prep_w(L.w116, EVA_D, PX_HID, EVA_D, PX_HID, EVA_D, 0, NULL, E->scratch, L.w1, L.s1, st));
+        PX_CK(eva_k_prep_w(L.w216, PX_HID, EVA_D, PX_HID, EVA_D, PX_HID, 0, NULL, E->scratch, L.w2, L.s2, st));
+    }
+    // head: the file's fp16 rows packed per 128-row block (rows past nt zero)
+    PX_ALLOC(E, E->hq, (size_t)nblk * 128 * EVA_D, false);
+    PX_ALLOC(E, E->hs, (size_t)nblk * 8 * 4, false);
+    PX_CK(eva_k_prep_w(E->hw16, EVA_D, (int)p->nt, EVA_D, (int)(nblk * 128), EVA_D, 0, NULL, E->scratch, E->hq, E->hs,
+                       st));
+
+    // activations
+    const size_t M = E->M, nb = E->nb;
+    PX_ALLOC(E, E->in, nb * PX_IN * 2, true);
+    PX_ALLOC(E, E->x, M * EVA_D * 2, true);
+    PX_ALLOC(E, E->h8, M * EVA_D, true);
+    PX_ALLOC(E, E->sh, 8 * M * 4, true);
+    PX_ALLOC(E, E->q, M * EVA_D * 2, true);
+    PX_ALLOC(E, E->k, M * EVA_D * 2, true);
+    PX_ALLOC(E, E->vt, M * EVA_D * 2, true);
+    PX_ALLOC(E, E->o8, M * EVA_D, true);
+    PX_ALLOC(E, E->so8, 8 * M * 4, true);
+    PX_ALLOC(E, E->m8, M * PX_HID, true);
+    PX_ALLOC(E, E->sm, (PX_HID / 128) * M * 4, true);
+    PX_ALLOC(E, E->y, M * EVA_D * 2, true);
+    PX_ALLOC(E, E->s, M * 16 * 4, true);
+    PX_ALLOC(E, E->P, nb * 16 * PX_T * 2, true);
+    PX_ALLOC(E, E->part, nb * (PX_T / PX_PCH) * 16 * EVA_D * 4, true);
+    PX_ALLOC(E, E->o, nb * EVA_D * 4, true);
+    PX_ALLOC(E, E->oq, nb * EVA_D, true);
+    PX_ALLOC(E, E->oqs, 8 * nb * 4, true);
+    PX_ALLOC(E, E->out, nb * p->nt * 4, true);
+    XT_HIP(hipHostMalloc((void **)&E->stage, nb * PX_IN * 2, hipHostMallocDefault));
+    for (int s = 0; s < PX_NBUF; s++) {
+        XT_HIP(hipHostMalloc((void **)&p->hout[s], nb * p->nt * 4, hipHostMallocDefault));
+        XT_HIP(hipEventCreateWithFlags(&E->done[s], hipEventDisableTiming));
+    }
+    XT_HIP(hipStreamSynchronize(E->st));
+
+    hipGraph_t g;
+    XT_HIP(hipStreamBeginCapture(E->st, hipStreamCaptureModeThreadLocal));
+    if (px_forward(p)) {
+        (void)hipStreamEndCapture(E->st, &g);
+        return -1;
+    }
+    XT_HIP(hipStreamEndCapture(E->st, &g));
+    XT_HIP(hipGraphInstantiate(&E->graph, g, NULL, NULL, 0));
+    XT_HIP(hipGraphDestroy(g));
+    XT_HIP(hipGraphUpload(E->graph, E->st));
+    XT_HIP(hipStreamSynchronize(E->st));
+    return 0;
+}
+
+static void *px_boot(void *arg)
+{
+    px *p = (px *)arg;
+    p->impl->bstatus = px_up(p);
+    return NULL;
+}
+
+extern "C" int px_open_nb(px *p, const char *weights, int device, void *pool, size_t poolb, uint32_t nb)
+{
+    uint32_t hdr[4];
+    FILE *f;
+
+    (void)pool;
+    (void)poolb;
+    memset(p, 0, sizeof(*p));
+    if (nb < 2 || nb > 100 || (nb & 1)) return xt_fail("px_open", "batch must be even, 2..100");
+    f = fopen(weights, "rb");
+    if (!f || fread(hdr, 4, 4, f) != 4 || memcmp(hdr, "PXAI", 4) || hdr[1] != 2 || hdr[2] == 0) {
+        fprintf(stderr, "px: %s is not a pixai.bin v2 (run export_pixai.py without a calibration file)\n", weights);
+        if (f) fclose(f);
+        return -1;
+    }
+    fclose(f);
+    px_impl *E = new px_impl();
+    p->impl = E;
+    E->path = strdup(weights);
+    if (!E->path) return xt_fail("px_open", "out of memory");
+    E->devno = device;
+    E->wbytes = hdr[3];
+    E->nb = nb;
+    E->M = nb * PX_T;
+    p->nt = hdr[2];
+    p->ntp = (hdr[2] + 7) & ~7u;
+    p->nb = nb;
+    E->bstatus = -1;
+    if (pthread_create(&E->boot, NULL, px_boot, p)) return xt_fail("px_open", "cannot start the bring-up thread");
+    E->booted = 1;
+    return 0;
+}
+
+extern "C" int px_open(px *p, const char *weights, int device, void *pool, size_t poolb)
+{
+    return px_open_nb(p, weights, device, pool, poolb, PX_NB);
+}
+
+extern "C" int px_ready(px *p)
+{
+    px_impl *E = p->impl;
+    if (!E) return -1;
+    if (E->up) return 0;
+    if (E->booted) {
+        pthread_join(E->boot, NULL);
+        E->booted = 0;
+    }
+    if (E->bstatus) return -1;
+    XT_HIP(hipSetDevice(E->devno));
+    E->up = 1;
+    return 0;
+}
+
+extern "C" int px_poll(px *p)
+{
+    px_impl *E = p->impl;
+    if (!E) return 0;
+    if (E->up) return 1;
+    return E->booted ? pthread_tryjoin_np(E->boot, NULL) == 0 ? (E->booted = 0, 1) : 0 : 1;
+}
+
+extern "C" int px_submit(px *p, uint32_t buf, uint16_t *const *in, uint32_t n)
+{
+    if (px_ready(p)) return -1;
+    px_impl *E = p->impl;
+    if (buf >= PX_NBUF || n > E->nb) return xt_fail("px_submit", "buf >= PX_NBUF or n > nb");
+    XT_HIP(hipStreamSynchronize(E->st));
+    for (uint32_t i = 0; i < n; i++) memcpy(E->stage + (size_t)i * PX_IN, in[i], PX_IN * 2);
+    if (n) XT_HIP(hipMemcpyAsync(E->in, E->stage, (size_t)n * PX_IN * 2, hipMemcpyHostToDevice, E->st));
+    XT_HIP(hipGraphLaunch(E->graph, E->st));
+    if (n) XT_HIP(hipMemcpyAsync(p->hout[buf], E->out, (size_t)n * p->nt * 4, hipMemcpyDeviceToHost, E->st));
+    XT_HIP(hipEventRecord(E->done[buf], E->st));
+    return 0;
+}
+
+extern "C" int px_query(px *p, uint32_t buf)
+{
+    px_impl *E = p->impl;
+    if (!E || !E->up || buf >= PX_NBUF) return 1;
+    return hipEventQuery(E->done[buf]) != hipErrorNotReady;
+}
+
+extern "C" const float *px_wait(px *p, uint32_t buf)
+{
+    px_impl *E = p->impl;
+    if (!E || !E->up || buf >= PX_NBUF) return NULL;
+    return hipEventSynchronize(E->done[buf]) == hipSuccess ? p->hout[buf] : NULL;
+}
+
+extern "C" void px_close(px *p)
+{
+    px_impl *E = p->impl;
+    if (!E) return;
+    if (E->booted) {
+        pthread_join(E->boot, NULL);
+        E->booted = 0;
+    }
+    (void)hipSetDevice(E->devno);
+    if (E->st) (void)hipStreamSynchronize(E->st);
+    if (E->graph) (void)hipGraphExecDestroy(E->graph);
+    for (int s = 0; s < PX_NBUF; s++) {
+        if (E->done[s]) (void)hipEventDestroy(E->done[s]);
+        if (p->hout[s]) (void)hipHostFree(p->hout[s]);
+    }
+    if (E->stage) (void)hipHostFree(E->stage);
+    for (void *ptr : E->allocs) (void)hipFree(ptr);
+    if (E->st) (void)hipStreamDestroy(E->st);
+    free(E->path);
+    delete E;
+    memset(p, 0, sizeof(*p));
+}
+
+extern "C" void *px_dev_input(px *p) { return px_ready(p) ? NULL : (void *)p->impl->in; }
+extern "C" const float *px_dev_output(px *p) { return px_ready(p) ? NULL : p->impl->out; }
+extern "C" void *px_stream_handle(px *p) { return px_ready(p) ? NULL : (void *)p->impl->st; }
+extern "C" int px_run(px *p)
+{
+    if (px_ready(p)) return -1;
+    XT_HIP(hipGraphLaunch(p->impl->graph, p->impl->st));
+    return 0;
+}
+extern "C" int px_sync(px *p)
+{
+    if (px_ready(p)) return -1;
+    XT_HIP(hipStreamSynchronize(p->impl->st));
+    return 0;
+}

@@ -105,3 +105,83 @@ class Engine:
             self.close()
         except Exception:
             pass
+
+
+PX_NBUF = 4
+PX_IN = 5184 * 592
+
+
+class PxStruct(C.Structure):
+    """The caller-allocated `px` struct of include/xtag_eva.h."""
+    _fields_ = [("nt", C.c_uint32), ("ntp", C.c_uint32), ("nb", C.c_uint32), ("hout", C.c_void_p * PX_NBUF),
+                ("impl", C.c_void_p)]
+
+
+class PxEngine:
+    """px_open_nb .. px_close (the PixAI tagger engine, src/engine/px.h). Errors raise RuntimeError."""
+
+    def __init__(self, weights, device=0, nb=4):
+        self.p = PxStruct()
+        self.ref = C.byref(self.p)
+        if lib.px_open_nb(self.ref, str(weights).encode(), device, None, 0, nb) != 0:
+            raise RuntimeError("px_open failed")
+        self.open = True
+
+    @property
+    def nt(self):
+        return self.p.nt
+
+    @property
+    def nb(self):
+        return self.p.nb
+
+    def ready(self):
+        if lib.px_ready(self.ref) != 0:
+            raise RuntimeError("px bring-up failed")
+
+    def submit(self, buf, inputs):
+        """inputs: fp16 array [n][5184][592] window-major patch operands (n <= nb)."""
+        x = np.ascontiguousarray(inputs, dtype=np.float16)
+        n = x.shape[0]
+        ptrs = (C.c_void_p * max(n, 1))(*[x.ctypes.data + i * PX_IN * 2 for i in range(n)])
+        if lib.px_submit(self.ref, buf, ptrs, n) != 0:
+            raise RuntimeError("px_submit failed")
+        self._keep = x
+        return n
+
+    def wait(self, buf, n):
+        p = lib.px_wait(self.ref, buf)
+        if not p:
+            raise RuntimeError("px_wait failed")
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), (n * self.nt,)).reshape(n, self.nt).copy()
+
+    def query(self, buf):
+        return lib.px_query(self.ref, buf)
+
+    def dev_input(self):
+        return lib.px_dev_input(self.ref)
+
+    def dev_output(self):
+        return lib.px_dev_output(self.ref)
+
+    def stream(self):
+        return lib.px_stream_handle(self.ref)
+
+    def run(self):
+        if lib.px_run(self.ref) != 0:
+            raise RuntimeError("px_run failed")
+
+    def sync(self):
+        if lib.px_sync(self.ref) != 0:
+            raise RuntimeError("px_sync failed")
+
+    def close(self):
+        if self.open:
+            lib.px_close(self.ref)
+            self.open = False
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -58,6 +58,19 @@ _SIGS = {
     "eva_head_put": (_i, [_p, _u32, _p, _f]),
     "eva_head_get": (_i, [_p, _p, _p]),
     "eva_close": (None, [_p]),
+    "px_open": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t]),
+    "px_open_nb": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32]),
+    "px_ready": (_i, [_p]),
+    "px_poll": (_i, [_p]),
+    "px_submit": (_i, [_p, _u32, _p, _u32]),
+    "px_query": (_i, [_p, _u32]),
+    "px_wait": (_p, [_p, _u32]),
+    "px_close": (None, [_p]),
+    "px_dev_input": (_p, [_p]),
+    "px_run": (_i, [_p]),
+    "px_dev_output": (_p, [_p]),
+    "px_stream_handle": (_p, [_p]),
+    "px_sync": (_i, [_p]),
     "eva_dev_input": (_p, [_p]),
     "eva_run": (_i, [_p]),
     "eva_dev_output": (_p, [_p]),
