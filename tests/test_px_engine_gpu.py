@@ -84,6 +84,7 @@ def test_px_engine_matches_kernel_chain(dev, xt, tmp_path):
     nb = 2
     _say("px engine: synthetic pixai.bin v2")
     m = blob.synth_px_model(seed=5, nt=NT)
+    m["layers"][3]["rs"] = (np.random.default_rng(7).random(PH) + 0.5).astype(np.float32)   # one calibrated layer
     path = tmp_path / "pixai.bin"
     blob.write_px_v2(str(path), m)
     r = np.random.default_rng(6)

@@ -23,6 +23,7 @@ struct PxLayer {
     const uint16_t *wqkv16, *wo16, *w116, *w216;                        // fp16 block weights in the blob
     uint8_t *wqkv, *wo, *w1, *w2;                                       // packed E4M3
     float *sqkv, *so, *s1, *s2;
+    const float *rs_fc1;                                                // rs, or NULL where the file's rs are all 1
 };
 
 struct px_impl {
@@ -163,7 +164,7 @@ static int px_forward(px *p)
         PX_CK(eva_k_flash_seq(E->q, E->k, E->vt, E->o8, E->so8, M, M / Ls, Ls, Ls, NULL, st));
         PX_CK(px_k_proj(E->o8, E->so8, M, L.wo, L.so, L.bo, E->x, M, st));
         PX_CK(eva_k_ln(E->x, L.ln2w, L.ln2b, E->h8, E->sh, M, M, st));
-        PX_CK(px_k_fc1(E->h8, E->sh, M, L.w1, L.s1, L.b1, L.rs, E->m8, E->sm, M, st));
+        PX_CK(px_k_fc1(E->h8, E->sh, M, L.w1, L.s1, L.b1, L.rs_fc1, E->m8, E->sm, M, st));
         PX_CK(px_k_fc2(E->m8, E->sm, M, L.w2, L.s2, L.b2, E->x, M, st));
     }
     PX_CK(px_k_hln(E->x, E->hnw, E->hnb, E->hpos, PX_T, E->U, E->y, E->s, M, st));
@@ -186,6 +187,17 @@ static int px_up(px *p)
     st = (void *)E->st;
     PX_ALLOC(E, E->blob, E->wbytes, false);
     if (px_stream_weights(E) || px_layout(E, p->ntp)) return -1;
+
+    // per-unit fc1 multipliers: a file without calibration holds ones (export_pixai.py:83), and multiplying by 1 is
+    // exact, so fc1 then runs without the multiply
+    std::vector<float> rs(PX_HID);
+    for (int i = 0; i < PX_NL; i++) {
+        PxLayer &L = E->L[i];
+        XT_HIP(hipMemcpy(rs.data(), L.rs, PX_HID * 4, hipMemcpyDeviceToHost));
+        bool ones = true;
+        for (float v : rs) ones = ones && v == 1.0f;
+        L.rs_fc1 = ones ? NULL : L.rs;
+    }
 
     // packed weights (bring-up packing on the GPU); q / k rows of Wqkv pair-split for the RoPE epilogue
     const size_t scratch_f = (size_t)(nblk * 128 > PX_HID ? nblk * 128 : PX_HID) * EVA_D;
