@@ -187,7 +187,7 @@ def time_graph(torch, g, replays):
     return e0.elapsed_time(e1) / replays
 
 
-def bench_cfg1(torch, L, iters=50):
+def bench_qkv_m1025(torch, L, iters=50):
     """Single block-scaled GEMM at the qkv shape, M=1025, bf16 out (TFLOP/s)."""
     dev = torch.device("cuda:0")
     st = torch.cuda.current_stream().cuda_stream
@@ -219,7 +219,7 @@ def bench_vendor(torch, M=8 * T):
     one = torch.tensor(1.0, device=dev)
     res = {}
     for name, m, n, k in (("qkv", M, 3 * D, D), ("oproj", M, D, D), ("fc1", M, 2 * HIDP, D), ("fc2", M, D, HIDP),
-                          ("cfg1_qkv_m1025", T, 3 * D, D)):
+                          ("qkv_m1025", T, 3 * D, D)):
         a = torch.randn(m, k, generator=g, device=dev).to(torch.float8_e4m3fn)
         b = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.float8_e4m3fn)
         fn = lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
@@ -604,7 +604,7 @@ def main():
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP8, 4), "traffic": traffic_from_profiles(),
             "algorithmic_flops_per_launch": fl["fc1"]}
 
-    cfg1, cfg1_ms = bench_cfg1(torch, L)
+    qkv1, qkv1_ms = bench_qkv_m1025(torch, L)
     peaks = measured_peaks(torch, L)
     out = {"metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -614,10 +614,10 @@ def main():
                                   "+residual; M=8200 (batch 8); 1x128 act / 128x128 weight fp32 block scales",
                       "M": M, "gflop_per_step": round(step_flops / 1e9, 2)},
            "pct_fp8_peak": round(100 * tflops / PEAK_FP8, 2), "per_kernel": per,
-           "cfg1_qkv_gemm_m1025": {"tflops": round(cfg1, 1), "us": round(cfg1_ms * 1e3, 2)},
+           "qkv_gemm_m1025": {"tflops": round(qkv1, 1), "us": round(qkv1_ms * 1e3, 2)},
            "roofline": roof, "measured_peaks": peaks,
            "pct_measured_fp8_peak": round(100 * tflops / peaks["fp8_mfma_tflops"], 2)}
-    # 2:4-sparse weights (config 5): the same step on pruned weights, dense-equivalent FLOPs
+    # 2:4-sparse weights: the same step on pruned weights, dense-equivalent FLOPs
     st.make_sparse()
     gsp = capture(torch, st.step_sp, 1)
     time_graph(torch, gsp, args.warmup)
@@ -646,7 +646,7 @@ def main():
         ips, fms = bench_forward(torch, sparse=True)
         out["forward_b32_sparse24"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
                                        "tflops_dense_equivalent": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1)}
-        # config 4: 64 sequences of 1025 tokens (16 images x (1 full view + crops)) and a 13461-row head
+        # 64 sequences of 1025 tokens (16 images x (1 full view + crops)) and a 13461-row head
         ips, fms = bench_forward(torch, nb=64, extra=13461 - 10861)
         out["forward_ragged64_head13461"] = {"sequences_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
                                              "tflops": round((64 * 723.5e9 + 2 * 64 * 13461 * 1024)

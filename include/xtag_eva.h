@@ -152,7 +152,7 @@ int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_
 int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const float *beta, float *c, float *d,
                   void *stream);
 
-/* ---- 2:4 structured-sparse weights (BASELINE config 5; src/tools/prune24.py:43-56 prunes, mma.sp named at
+/* ---- 2:4 structured-sparse weights (src/tools/prune24.py:43-56 prunes, mma.sp named at
  * prune24.py:1 is never used there) ---- */
 /* In every group of 4 consecutive k of each row of the E4M3 weights w [N][K] (in place), zero the 2 smallest
  * |values| (prune24.py "mag" rule); ties drop the lower k first. K % 4 == 0. */

@@ -125,7 +125,7 @@ void xo_fold_w2(const uint16_t *w2, int ldw2, const float *gamma, const float *b
 /* c[n] = sum_k dec(q[n][k]) * s[n/128][k/128] over [1024][2816] (fp32, in k order) */
 void xo_fold_c(const uint8_t *q, const float *s, float *c);
 
-/* ---- 2:4 structured sparsity of the block weights ---- */
+/* ---- 2:4 structured sparsity of the block weights (the 2:4-sparse forward) ---- */
 /* 2:4 pruning along K of E4M3 weights (src/tools/prune24.py:43-56): in every group of 4 consecutive k of each row,
  * the 2 lowest scores are zeroed. Score |dec(q)| (the "mag" rule) or, with wanda != 0, |dec(q)| * max_n |dec(q[n][k])|
  * (prune24.py:50). Ties drop the lower k first (prune24.py's argsort order is unspecified for ties).

@@ -5,7 +5,7 @@
    GEMM-fed epilogues within one output rounding unit plus 2e-4 of the terms; attention within 4e-3; the head's
    sigmoid scores within 1e-4 (the contract asks 2e-3) with identical top-50 tag sets.
 2. The engine (eva_open .. eva_wait, one HIP graph replay) returns exactly the scores of that validated sequence.
-   With 2:4-sparse weights (BASELINE config 5, EVA_SPARSE24) the same holds against the oracle with the same pruned
+   With 2:4-sparse weights (EVA_SPARSE24) the same holds against the oracle with the same pruned
    weights (its "dense-decoded reference"), and the sparse engine's graph returns that validated sequence's bits.
 3. Free running, the GPU and the oracle drift apart through the per-layer E4M3 re-quantization exactly as the oracle
    drifts from itself when only its fp32 summation order changes (tests/golden/forward_self_divergence.json); the

@@ -1,4 +1,4 @@
-"""GPU parity of the 2:4-sparse weight path through the C-ABI.
+"""GPU parity of the 2:4-sparse weight path (EVA_SPARSE24) through the C-ABI.
 
 - eva_k_prune24 and eva_k_pack24 are bit-exact against the oracle's xo_prune24 / xo_pack24 (themselves pinned by
   tests/test_sparse_oracle.py against numpy restatements of src/tools/prune24.py and of the layout's definition).

@@ -1,4 +1,4 @@
-"""Pins the oracle's 2:4 pruning and compressed layout before they are trusted as checkers.
+"""Pins the oracle's 2:4 pruning and compressed layout (the 2:4-sparse forward) before they are trusted as checkers.
 
 xo_prune24 restates src/tools/prune24.py:43-56 (score, drop the 2 lowest of every 4 consecutive k). It is checked
 against an independent numpy restatement of that script (np.argsort over the same scores, here with a stable sort:

@@ -1,4 +1,4 @@
-// sparse.hip - 2:4 structured sparsity of the E4M3 block weights: magnitude pruning along K
+// sparse.hip - 2:4 structured sparsity of the E4M3 block weights (the 2:4-sparse workload): magnitude pruning along K
 // (the role of src/tools/prune24.py:43-56, "mag" rule) and packing into the compressed layout the sparse GEMM
 // (gemm_core.h, bs_mainloop_sp) reads. The 128 x 128 block scales of the dense weights are kept unchanged.
 #include "gemm_core.h"
