@@ -187,6 +187,46 @@ def time_graph(torch, g, replays):
     return e0.elapsed_time(e1) / replays
 
 
+def time_median(torch, g, per_replay, repeats=5):
+    """Median over `repeats` of one replay of g (a graph of `per_replay` back-to-back calls), each replay between HIP
+    events on the replay stream with torch.cuda.synchronize() on both sides; ms per call, and the per-repeat list."""
+    st = torch.cuda.current_stream()
+    times = []
+    for _ in range(repeats):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / per_replay)
+    return sorted(times)[len(times) // 2], times
+
+
+def time_calls(torch, fn, calls=50, repeats=5):
+    """Median ms per call of fn over graphs of `calls` back-to-back calls (one warm-up replay first)."""
+    g = capture(torch, fn, calls)
+    g.replay()
+    return time_median(torch, g, calls, repeats)[0]
+
+
+def time_engine(torch, eng, runs=3, repeats=5):
+    """Median ms per forward of an engine (Engine / PxEngine): `runs` back-to-back eva_run / px_run graph replays
+    between HIP events recorded on the engine's own stream, `repeats` times."""
+    st = torch.cuda.ExternalStream(eng.stream())
+    times = []
+    for _ in range(repeats):
+        eng.sync()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(runs):
+            eng.run()
+        e1.record(st)
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) / runs)
+    return sorted(times)[len(times) // 2]
+
+
 def bench_qkv_m1025(torch, L, iters=50):
     """Single block-scaled GEMM at the qkv shape, M=1025, bf16 out (TFLOP/s)."""
     dev = torch.device("cuda:0")
@@ -205,9 +245,7 @@ def bench_qkv_m1025(torch, L, iters=50):
         if L.lib.eva_k_gemm(L.ptr(qa), K, L.ptr(sa), M, L.ptr(qw), L.ptr(sw), M, N, K, L.ptr(c), N, 0,
                             torch.cuda.current_stream().cuda_stream) != 0:
             raise RuntimeError("eva_k_gemm")
-    g = capture(torch, f, iters)
-    time_graph(torch, g, 20)
-    ms = time_graph(torch, g, 20) / iters
+    ms = time_calls(torch, f, iters)
     return 2.0 * M * N * K / ms / 1e9, ms
 
 
@@ -223,9 +261,7 @@ def bench_vendor(torch, M=8 * T):
         a = torch.randn(m, k, generator=g, device=dev).to(torch.float8_e4m3fn)
         b = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.float8_e4m3fn)
         fn = lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
-        gr = capture(torch, fn, 20)
-        time_graph(torch, gr, 3)
-        res[name] = {"us": round(time_graph(torch, gr, 10) * 1e3 / 20, 2)}
+        res[name] = {"us": round(time_calls(torch, fn) * 1e3, 2)}
     step_us = sum(res[k]["us"] for k in ("qkv", "oproj", "fc1", "fc2"))
     step_flops = 2.0 * M * D * (3 * D + D + 2 * HID + HID)  # unpadded, as the metric
     res["step_tflops"] = round(step_flops / (step_us * 1e-6) / 1e12, 1)
@@ -244,9 +280,7 @@ def bench_ln(torch, L, M=32 * T):
     sc = torch.empty(8, M, dtype=torch.float32, device=dev)
     fn = lambda: L.check(L.lib.eva_k_ln(L.ptr(x), L.ptr(ga), L.ptr(be), L.ptr(q), L.ptr(sc), M, M,
                                         torch.cuda.current_stream().cuda_stream), "eva_k_ln")
-    gr = capture(torch, fn, 20)
-    time_graph(torch, gr, 3)
-    us = time_graph(torch, gr, 10) * 1e3 / 20
+    us = time_calls(torch, fn) * 1e3
     nbytes = M * D * 3 + M * 8 * 4
     return us, nbytes / (us * 1e-6) / 1e9
 
@@ -277,9 +311,7 @@ def bench_prep(torch, L, h=2048, w=3072, reps=20):
                                "eva_img_prep")
     res = {}
     for name, fn in (("pyramid_us", pyr), ("full_view_us", prep((0, 0, w, h))), ("crop900_us", prep((300, 200, 900, 900)))):
-        gr = capture(torch, fn, reps)
-        time_graph(torch, gr, 3)
-        res[name] = round(time_graph(torch, gr, 10) * 1e3 / reps, 2)
+        res[name] = round(time_calls(torch, fn, reps) * 1e3, 2)
     res["images_per_s"] = round(1e6 / (res["pyramid_us"] + res["full_view_us"]), 1)
     # CPU: the oracle's scalar restatement of the same full view (level 1 rect), one core
     from oracle import oracle as O
@@ -310,9 +342,7 @@ def bench_attention_seq(torch, L, reps=10):
         os_ = torch.empty(8, nseq * T, dtype=torch.float32, device=dev)
         fn = lambda: L.check(L.lib.eva_k_flash_seq(L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o8), L.ptr(os_), nseq * T, nseq,
                                                    T, T, None, torch.cuda.current_stream().cuda_stream), "flash_seq")
-        gr = capture(torch, fn, reps)
-        time_graph(torch, gr, 2)
-        us = time_graph(torch, gr, 5) * 1e3 / reps
+        us = time_calls(torch, fn, reps) * 1e3
         res[name] = {"us": round(us, 1), "tflops": round(4.0 * T * T * 64 * 16 * nseq / (us * 1e-6) / 1e12, 1)}
     return res
 
@@ -374,9 +404,7 @@ def bench_pixai_block(torch, L, nb=4, reps=10):
     res = {"M": M, "gflop_gemms": round(sum(fl.values()) / 1e9, 1)}
 
     def timed(fn, r=reps):
-        gr = capture(torch, fn, r)
-        time_graph(torch, gr, 2)
-        return time_graph(torch, gr, 5) * 1e3 / r                # us per call
+        return time_calls(torch, fn, r) * 1e3                     # us per call
 
     us = timed(run(qkv, proj, fc1, fc2))
     res["gemm_step"] = {"us": round(us, 1), "tflops": round(sum(fl.values()) / (us * 1e-6) / 1e12, 1)}
@@ -408,7 +436,7 @@ def bench_pixai_block(torch, L, nb=4, reps=10):
     return res
 
 
-def bench_pixai_forward(torch, L, nb=4, nt=13461, replays=10):
+def bench_pixai_forward(torch, L, nb=4, nt=13461):
     """The PixAI tagger engine (px_open_nb .. px_run, px.h:110-190) at batch 4 (PX_NB) on a synthetic pixai.bin v2:
     one graph replay = patch embedding + pre-LN, 32 ViTDet-L blocks (global attention in blocks 7, 15, 23, 31), the
     attention-pool head and a 13461-row tag head, 32 distinct random weight sets, inputs resident in the engine's
@@ -432,18 +460,13 @@ def bench_pixai_forward(torch, L, nb=4, nt=13461, replays=10):
             raise RuntimeError("PixAI forward produced non-finite scores")
         for _ in range(2):
             eng.run()
-        eng.sync()
-        t0 = time.perf_counter()
-        for _ in range(replays):
-            eng.run()
-        eng.sync()
-        ms_b = (time.perf_counter() - t0) * 1e3 / replays
+        ms_b = time_engine(torch, eng, runs=2)
     finally:
         eng.close()
     return nb / (ms_b * 1e-3), ms_b
 
 
-def bench_forward(torch, nb=32, iters=5, extra=0, sparse=False):
+def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False):
     """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
     resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores."""
     from xtagger_amd import blob
@@ -458,39 +481,74 @@ def bench_forward(torch, nb=32, iters=5, extra=0, sparse=False):
     e.wait(0, nb)
     for _ in range(2):
         e.run()
-    e.sync()
-    t0 = time.perf_counter()
-    for _ in range(iters):
-        e.run()
-    e.sync()
-    dt = (time.perf_counter() - t0) / iters
+    ms_b = time_engine(torch, e, runs=iters)
     e.close()
-    return nb / dt, dt * 1e3
+    return nb / (ms_b * 1e-3), ms_b
 
 
-def cpu_baseline(orc, M=8 * T, budget_s=12.0):
-    """The oracle's block-scaled GEMM (E4M3 LUT decode, fp32 128-element dot per block, fma(partial, sa*sw, acc),
-    bf16 out; AVX2 + FMA, OpenMP) on the four layer GEMMs at M rows, repeated until budget_s of timed CPU work."""
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(orc, runs=5):
+    """The CPU baseline GEMM (oracle/xt_cpugemm.c: E4M3 LUT decode, 128-element fp32 dot per K block,
+    fma(partial, sa*sw, acc) promotion, bf16 out) in its two builds, scalar (-O3 -ffp-contract=off) and AVX2
+    (-O3 -mavx2 -mfma -ffp-contract=off), OpenMP over 128-row blocks, on all usable host cores and on 1 thread.
+    Each leg is the median of `runs` timed calls after one warm-up (CLOCK_MONOTONIC via perf_counter). Workloads: the
+    four layer GEMMs at M=8200 (the headline step) and the qkv GEMM at M=1025; the slower legs run a bounded row
+    sample of the same GEMMs (the per-row work is identical, so the rate is that of the whole GEMM)."""
+    import ctypes as C
     import numpy as np
     r = np.random.default_rng(0)
-    aff = len(os.sched_getaffinity(0))
-    thr = min(aff, int(os.environ.get("OMP_NUM_THREADS", aff)))
-    ops = []
-    for N, K in ((3 * D, D), (D, D), (2 * HIDP, D), (D, HIDP)):
-        x = r.standard_normal((M, K)).astype(np.float32)
-        w = (r.standard_normal((N, K)) * 0.02).astype(np.float32)
-        n_alg = {3 * D: 3 * D, D: D, 2 * HIDP: 2 * HID}[N]
-        k_alg = HID if K == HIDP else K
-        ops.append((orc.quant_act(x), orc.quant_w(w), N, 2.0 * M * n_alg * k_alg))
-    total, secs, reps = 0.0, 0.0, 0
-    while secs < budget_s:
-        for (qa, sa), (qw, sw), N, fl in ops:
+    thr = len(os.sched_getaffinity(0))
+    libs = {k: C.CDLL(os.path.join(ROOT, "oracle", f"libcpugemm_{k}.so")) for k in ("scalar", "avx2")}
+    vp = lambda a: C.c_void_p(a.ctypes.data)
+
+    def ops_for(M, shapes):
+        ops = []
+        for N, K in shapes:
+            x = r.standard_normal((M, K)).astype(np.float32)
+            w = (r.standard_normal((N, K)) * 0.02).astype(np.float32)
+            n_alg = {3 * D: 3 * D, D: D, 2 * HIDP: 2 * HID}[N]
+            k_alg = HID if K == HIDP else K
+            qa, sa = orc.quant_act(x)
+            qw, sw = orc.quant_w(w)
+            ops.append((qa, sa, qw, sw, N, K, 2.0 * n_alg * k_alg, np.empty((M, N), np.uint16)))
+        return ops
+
+    def leg(lib, ops, rows, threads):
+        def once():
             t0 = time.perf_counter()
-            orc.gemm_f32(qa, sa, qw, sw, N, threads=thr, avx2=1, want_bf16=True)
-            secs += time.perf_counter() - t0
-            total += fl
-        reps += 1
-    return total / secs / 1e12, thr, secs, reps
+            for qa, sa, qw, sw, N, K, _, cb in ops:
+                lib.cg_gemm(vp(qa), K, vp(sa), sa.shape[1], vp(qw), vp(sw), N, K, 0, rows, vp(cb), N, threads)
+            return time.perf_counter() - t0
+        once()
+        ts = sorted(once() for _ in range(runs))
+        sec = ts[len(ts) // 2]
+        flops = rows * sum(o[6] for o in ops)
+        return {"tflops": round(flops / sec / 1e12, 4), "s_per_call": round(sec, 4), "rows": rows,
+                "threads": threads}
+
+    step = ops_for(8 * T, ((3 * D, D), (D, D), (2 * HIDP, D), (D, HIDP)))
+    qkv1 = ops_for(T, ((3 * D, D),))
+    t0 = time.perf_counter()
+    legs = {
+        "step_m8200_avx2_all": leg(libs["avx2"], step, 8 * T, thr),
+        "step_m8200_scalar_all": leg(libs["scalar"], step, 2048, thr),
+        "step_m8200_avx2_1thread": leg(libs["avx2"], step, 256, 1),
+        "step_m8200_scalar_1thread": leg(libs["scalar"], step, 256, 1),
+        "qkv_m1025_avx2_all": leg(libs["avx2"], qkv1, T, thr),
+        "qkv_m1025_scalar_all": leg(libs["scalar"], qkv1, T, thr),
+        "qkv_m1025_avx2_1thread": leg(libs["avx2"], qkv1, 256, 1),
+        "qkv_m1025_scalar_1thread": leg(libs["scalar"], qkv1, 256, 1),
+    }
+    return legs, thr, time.perf_counter() - t0
 
 
 def measured_peaks(torch, L):
@@ -579,24 +637,20 @@ def main():
     st = LayerStep(torch, L, M)
     fl = gemm_flops(M)
     step_flops = sum(fl.values())
-    # one step = the four kernels, replayed as one HIP graph (no host launch gaps between the kernels)
-    gstep = capture(torch, st.step, 1)
+    # warm-up: W steps launched eagerly; then exactly K steps as one HIP graph holding the K steps (no host launch
+    # gaps between kernels or steps), replayed between HIP events with torch.cuda.synchronize() on both sides, 5 times;
+    # ms_per_step is the median
     for _ in range(args.warmup):
-        gstep.replay()
+        st.step()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        gstep.replay()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    gK = capture(torch, st.step, args.steps)
+    ms, ms_runs = time_median(torch, gK, args.steps)
+    del gK
     tflops = step_flops / (ms * 1e-3) / 1e12
 
     per = {}
     for name in ("qkv", "oproj", "fc1", "fc2"):
-        reps = 20
-        g = st.kernel_graph(name, reps)
-        time_graph(torch, g, 5)
-        kms = time_graph(torch, g, 10) / reps
+        kms = time_calls(torch, getattr(st, name), 50)
         per[name] = {"us": round(kms * 1e3, 2), "tflops": round(fl[name] / (kms * 1e-3) / 1e12, 1)}
     fc1_ms = per["fc1"]["us"] * 1e-3
     achieved = fl["fc1"] / (fc1_ms * 1e-3) / 1e12
@@ -608,6 +662,7 @@ def main():
     peaks = measured_peaks(torch, L)
     out = {"metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+           "ms_per_step_repeats": [round(t, 4) for t in ms_runs],
            "vs_baseline": None, "dtype": "e4m3 (fp32 accumulate)", "data": "synthetic",
            "config": {"workload": "EVA02-L layer GEMMs with fused epilogues: qkv 1024->3072 +RoPE, proj 1024->1024 "
                                   "+residual, fc1 1024->2x2730 +SwiGLU +E4M3 repack, fc2 2730->1024 +folded LN "
@@ -619,9 +674,7 @@ def main():
            "pct_measured_fp8_peak": round(100 * tflops / peaks["fp8_mfma_tflops"], 2)}
     # 2:4-sparse weights: the same step on pruned weights, dense-equivalent FLOPs
     st.make_sparse()
-    gsp = capture(torch, st.step_sp, 1)
-    time_graph(torch, gsp, args.warmup)
-    sp_ms = time_graph(torch, gsp, args.steps)
+    sp_ms = time_calls(torch, st.step_sp, args.steps)
     out["sparse24_step"] = {"tflops_dense_equivalent": round(step_flops / (sp_ms * 1e-3) / 1e12, 1),
                             "ms_per_step": round(sp_ms, 4)}
     try:
@@ -653,11 +706,15 @@ def main():
                                                              / (fms * 1e-3) / 1e12, 1)}
     if not args.no_cpu:
         from oracle import oracle as O
-        cpu_tf, thr, secs, reps = cpu_baseline(O)
-        out["cpu_baseline"] = {"value": round(cpu_tf, 4), "unit": "TFLOP/s", "cores": thr, "kind": "port",
-                               "sample": f"the same four layer GEMMs at M=8200 (206.3 GFLOP per pass) x {reps} "
-                                         f"passes, {secs:.1f} s; block-scaled E4M3 semantics, bf16 out, AVX2+FMA C "
-                                         f"loop, OpenMP on {thr} threads; GEMM only (no fused epilogues)"}
+        legs, thr, secs = cpu_baseline(O)
+        out["cpu_baseline"] = {"value": legs["step_m8200_avx2_all"]["tflops"], "unit": "TFLOP/s", "cores": thr,
+                               "kind": "port", "cpu_model": cpu_model(),
+                               "sample": f"the four layer GEMMs at M=8200 (206.3 GFLOP), block-scaled E4M3 semantics, "
+                                         f"bf16 out, GEMM only (no fused epilogues): AVX2+FMA build (-O3 -mavx2 -mfma "
+                                         f"-ffp-contract=off), OpenMP on {thr} threads, median of 5 calls after one "
+                                         f"warm-up; legs: scalar build, 1 thread (256-row samples), and the qkv GEMM "
+                                         f"at M=1025; {secs:.1f} s of CPU work in all",
+                               "legs": legs}
     print(json.dumps(out), flush=True)
 
 
