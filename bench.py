@@ -421,7 +421,10 @@ def bench_pixai_block(torch, L, nb=4, reps=10):
     hpos = (torch.randn(T5, D, generator=g, device=dev) * 0.2).half()
     U = torch.randn(16, D, generator=g, device=dev) * 0.05
     wv = (torch.randn(D, D, generator=g, device=dev) * 0.03).half()
-    hw, hws = packw((nt + 127) // 128 * 128, D)
+    hw16 = (torch.randn(nt, D, generator=g, device=dev) * 0.02).half()
+    ldh = (nt + 63) // 64 * 64
+    hw, hws = t(nt, D), t(8, ldh, dt=torch.float32)
+    L.check(L.lib.eva_k_quant_act(L.ptr(hw16), 2, D, nt, D, L.ptr(hw), D, L.ptr(hws), ldh, st()), "head pack")
     hb = torch.zeros(nt, device=dev)
     y, s = t(M, D, dt=torch.int16), t(M, 16, dt=torch.float32)
     Pm, part = t(nb, 16, T5, dt=torch.int16), t(nb, T5 // 144, 16, D, dt=torch.float32)
@@ -431,7 +434,7 @@ def bench_pixai_block(torch, L, nb=4, reps=10):
                lambda: L.lib.px_k_hpool(P(Pm), P(y), P(part), nb, T5, st()),
                lambda: L.lib.px_k_hv(P(part), T5 // 144, P(wv), P(o), nb, st()),
                lambda: L.lib.eva_k_quant_act(P(o), 1, D, nb, D, P(oq), D, P(oqs), nb, st()),
-               lambda: L.lib.eva_k_head(P(oq), P(oqs), nb, P(hw), P(hws), P(hb), P(out), nb, nt, st()))
+               lambda: L.lib.eva_k_head(P(oq), P(oqs), nb, P(hw), P(hws), ldh, P(hb), P(out), nb, nt, st()))
     res["pool_head_us"] = round(timed(head), 1)
     return res
 

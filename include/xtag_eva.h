@@ -90,7 +90,7 @@ int eva_sync(eva *e);
 
 /* ---- kernel launchers (device pointers; stream = hipStream_t or NULL) ---- */
 
-/* Activation packing (kern_common.cuh:97-128 q2 / st4 / st8h): x [M][ldx], in_kind 0 = bf16, 1 = fp32,
+/* Activation packing (kern_common.cuh:97-128 q2 / st4 / st8h): x [M][ldx], in_kind 0 = bf16, 1 = fp32, 2 = fp16,
  * K % 128 == 0 -> q [M][ldq] E4M3, s [K/128][lds]. */
 int eva_k_quant_act(const void *x, int in_kind, int ldx, int M, int K, void *q, int ldq, float *s, int lds,
                     void *stream);
@@ -131,9 +131,11 @@ int eva_k_fc1(const void *h8, const float *hs, int lds, const void *w, const flo
 /* fc2 with the MLP LayerNorm folded + residual (eva_kernels.cu:286-334 k_fc2): x += rstd (m8 . W~^T - mean c) + d */
 int eva_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *stat,
               const float *cn, const float *dn, void *x, int rows, void *stream);
-/* Tag head (kern_common.cuh:679-727 k_headmv, here a block-scaled FP8 GEMM): out [nb][nt] = sigmoid(pq . Wh^T + hb) */
-int eva_k_head(const void *pq, const float *ps, int lds, const void *w, const float *ws, const float *hb, float *out,
-               int nb, int nt, void *stream);
+/* Tag head (kern_common.cuh:679-727 k_headmv, here an FP8 GEMM): out [nb][nt] = sigmoid(pq . Wh^T + hb). The head
+ * rows are packed like activations, each row with its own 1x128 scales (eva_k_quant_act of the fp16 rows: w [nt][1024]
+ * E4M3, ws [8][ldw] planes), so rewriting one row (eva_head_put) leaves every other row's codes unchanged. nb <= 128. */
+int eva_k_head(const void *pq, const float *ps, int lds, const void *w, const float *ws, int ldw, const float *hb,
+               float *out, int nb, int nt, void *stream);
 /* Patch embedding + position (eva_kernels.cu:126-130 k_pe, 21-33 k_embed): in fp16 [nb*1024][592], pe fp16
  * [1024][592], pos fp32 [1025][1024] -> x fp16 [nb*1025][1024] */
 int eva_k_pe(const void *in, const void *pe, const float *pos, void *x, int nb, void *stream);

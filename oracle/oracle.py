@@ -43,6 +43,7 @@ _SIGS = {
     "xo_quant_act": (None, [_p, _i, _i, _i, _p, _i, _p, _i]),
     "xo_quant_w": (None, [_p, _i, _i, _p, _p]),
     "xo_gemm_bs_f64_rows": (None, [_p, _i, _p, _i, _p, _p, _i, _i, _p, _i, _p]),
+    "xo_gemm_rr_f64_rows": (None, [_p, _i, _p, _i, _p, _p, _i, _i, _i, _p, _i, _p]),
     "xo_gemm_bs_f32": (None, [_p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _p, _p, _i, _i, _i]),
     "xo_max_threads": (_i, []),
     "xo_ln_quant": (None, [_p, _p, _p, _i, _p, _p, _i, _p]),
@@ -158,6 +159,25 @@ def gemm_f64_rows(qa, sa, qw, sw, N, rows):
     lib.xo_gemm_bs_f64_rows(_ptr(qa), K, _ptr(sa), sa.shape[1], _ptr(qw), _ptr(sw), N, K, _ptr(rows), rows.size,
                             _ptr(out))
     return out
+
+
+def gemm_rr_f64_rows(qa, sa, qw, sw, N, rows):
+    """fp64 rows of the head GEMM whose weight rows carry their own 1x128 scales: qw [N][K] E4M3, sw [K/128][ldw]."""
+    _done()
+    qa = _c(qa, np.uint8)
+    sa = _c(sa, np.float32)
+    qw = _c(qw, np.uint8)
+    sw = _c(sw, np.float32)
+    rows = _c(rows, np.int32)
+    out = np.empty((len(rows), N), np.float64)
+    lib.xo_gemm_rr_f64_rows(_ptr(qa), qa.shape[1], _ptr(sa), sa.shape[1], _ptr(qw), _ptr(sw), sw.shape[1], N,
+                            qa.shape[1], _ptr(rows), len(rows), _ptr(out))
+    return out
+
+
+def head_pack(hw16):
+    """The head's fp16 rows [nt][1024] -> (q [nt][1024] E4M3, s [8][nt]): every row packed with its own 1x128 scales."""
+    return quant_act(np.asarray(hw16).astype(np.float32))
 
 
 def gemm_f32(qa, sa, qw, sw, N, m0=0, m1=None, threads=0, avx2=1, want_bf16=False):

@@ -236,6 +236,31 @@ void xo_gemm_bs_f64_rows(const uint8_t *qa, int lda, const float *sa, int lds, c
     }
 }
 
+/* The tag head's GEMM (kern_common.cuh:679-727 k_headmv, as the build packs it): weight rows carry 1x128 scales of
+ * their own, planes sw [K/128][ldw], like activations: C[m][n] = sum_kb sa[kb][m] sw[kb][n] sum_{k in kb} qa qw, fp64. */
+void xo_gemm_rr_f64_rows(const uint8_t *qa, int lda, const float *sa, int lds, const uint8_t *qw, const float *sw,
+                         int ldw, int N, int K, const int *rows, int nrows, double *out)
+{
+    int r;
+
+    e4lut_init();
+#pragma omp parallel for schedule(static)
+    for (r = 0; r < nrows; r++) {
+        const int m = rows[r];
+        int n, kb, k;
+        for (n = 0; n < N; n++) {
+            double acc = 0.0;
+            for (kb = 0; kb < K / 128; kb++) {
+                double part = 0.0;
+                for (k = kb * 128; k < kb * 128 + 128; k++)
+                    part += (double)E4LUT[qa[(size_t)m * lda + k]] * (double)E4LUT[qw[(size_t)n * K + k]];
+                acc += part * (double)sa[(size_t)kb * lds + m] * (double)sw[(size_t)kb * ldw + n];
+            }
+            out[(size_t)r * N + n] = acc;
+        }
+    }
+}
+
 int xo_max_threads(void)
 {
 #ifdef _OPENMP
@@ -958,7 +983,7 @@ static float *f16_to_f32_pad(const uint16_t *w, int rows, int cols, int ld, int 
 int xo_forward(const xo_model *md, const uint16_t *in, int nb, int nl, float *out, uint16_t *pn, int threads)
 {
     const int avx = getenv("XO_SCALAR") ? 0 : 1;
-    const int M = nb * XO_T, nt = md->nt, NBh = (nt + 127) / 128;
+    const int M = nb * XO_T, nt = md->nt;
     uint16_t *x = (uint16_t *)malloc(sizeof(uint16_t) * M * XO_D);
     uint8_t *h8 = (uint8_t *)malloc((size_t)M * XO_HIDP);
     float *hs = (float *)malloc(sizeof(float) * 22 * M);
@@ -976,7 +1001,7 @@ int xo_forward(const xo_model *md, const uint16_t *in, int nb, int nl, float *ou
     float *pool = (float *)malloc(sizeof(float) * nb * XO_D);
     uint8_t *pq = (uint8_t *)malloc((size_t)nb * XO_D);
     float *ps = (float *)malloc(sizeof(float) * 8 * nb);
-    float *logit = (float *)malloc(sizeof(float) * nb * NBh * 128);
+    double *logit = (double *)malloc(sizeof(double) * nb * nt);
     float *wf;
     int i, r, n;
 
@@ -1019,17 +1044,21 @@ int xo_forward(const xo_model *md, const uint16_t *in, int nb, int nl, float *ou
     }
     xo_pool(x, nb, pool);
     xo_lnh(pool, md->fnw, md->fnb, nb, pn, pq, ps, nb);
-    {
-        uint8_t *hq = (uint8_t *)malloc((size_t)NBh * 128 * XO_D);
-        float *hsc = (float *)malloc(sizeof(float) * NBh * 8);
+    {   /* the head: every fp16 row packed with its own 1x128 scales, fp64 logits, fp32 sigmoid */
+        uint8_t *hq = (uint8_t *)malloc((size_t)nt * XO_D);
+        float *hsc = (float *)malloc(sizeof(float) * 8 * nt);
+        int *rows = (int *)malloc(sizeof(int) * nb);
         wf = f16_to_f32_pad(md->hw, nt, XO_D, XO_D, nt, XO_D);
-        xo_quant_w(wf, nt, XO_D, hq, hsc);
+        xo_quant_act(wf, nt, XO_D, XO_D, hq, XO_D, hsc, nt);
         free(wf);
-        xo_gemm_bs_f32(pq, XO_D, ps, nb, hq, hsc, nt, XO_D, 0, nb, logit, NULL, nt, threads, 1);
+        for (r = 0; r < nb; r++) rows[r] = r;
+        xo_gemm_rr_f64_rows(pq, XO_D, ps, nb, hq, hsc, nt, nt, XO_D, rows, nb, logit);
         for (r = 0; r < nb; r++)
-            for (n = 0; n < nt; n++) out[(size_t)r * nt + n] = 1.0f / (1.0f + expf(-(logit[(size_t)r * nt + n] + md->hb[n])));
+            for (n = 0; n < nt; n++)
+                out[(size_t)r * nt + n] = 1.0f / (1.0f + expf(-((float)logit[(size_t)r * nt + n] + md->hb[n])));
         free(hq);
         free(hsc);
+        free(rows);
     }
     free(x); free(h8); free(hs); free(acc); free(hf); free(stat); free(q); free(k); free(vt); free(o); free(of);
     free(wq); free(ws); free(cfold); free(dfold); free(pool); free(pq); free(ps); free(logit);

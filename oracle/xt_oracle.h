@@ -45,6 +45,9 @@ void xo_quant_w(const float *w, int N, int K, uint8_t *q, float *s);
 /* fp64 accumulate of the dequantized product, for the listed rows: out [nrows][N] */
 void xo_gemm_bs_f64_rows(const uint8_t *qa, int lda, const float *sa, int lds, const uint8_t *qw, const float *sw,
                          int N, int K, const int *rows, int nrows, double *out);
+/* head GEMM with per-row weight scales sw [K/128][ldw] (fp64) */
+void xo_gemm_rr_f64_rows(const uint8_t *qa, int lda, const float *sa, int lds, const uint8_t *qw, const float *sw,
+                         int ldw, int N, int K, const int *rows, int nrows, double *out);
 /* fp32 "repo convention": per K block an fp32 fma chain over 128 exact products, then
  * acc = fma(partial, sa * sw, acc). Rows [m0, m1). Output fp32 [M][ldc] and / or bf16 [M][ldc] (NULL to skip).
  * threads: OpenMP threads (<= 0: all). avx2: 1 = 8-lane AVX2 / FMA kernel, 0 = scalar loop. */

@@ -60,15 +60,13 @@ class StepForward:
             self.layers.append(d)
         nt = m["nt"]
         self.nt = nt
-        nblk = (nt + 127) // 128
-        hw16 = up(m["hw"])
-        self.hq = torch.zeros(nblk * 128, D, dtype=torch.uint8, device=dev)
-        self.hs = torch.zeros(nblk, 8, dtype=torch.float32, device=dev)
+        hw16 = up(m["hw"][:nt])
+        self.ldh = (nt + 63) // 64 * 64
+        self.hq = torch.zeros(nt, D, dtype=torch.uint8, device=dev)
+        self.hs = torch.zeros(8, self.ldh, dtype=torch.float32, device=dev)
         self.hb = up(m["hb"][:nt])
-        for b in range(nblk):
-            n = min(128, nt - 128 * b)
-            xt.check(L.eva_k_prep_w(P(hw16[128 * b:]), D, n, D, 128, D, 0, None, P(scratch), P(self.hq[128 * b:]),
-                                    P(self.hs[b:]), st), "head")
+        # the head rows each packed with their own 1x128 scales, as the engine's bring-up does
+        xt.check(L.eva_k_quant_act(P(hw16), 2, D, nt, D, P(self.hq), D, P(self.hs), self.ldh, st), "head")
         torch.cuda.synchronize()
         M, lds = self.M, self.lds
         self.x = torch.zeros(lds, D, dtype=torch.int16, device=dev)
@@ -158,8 +156,8 @@ class StepForward:
         xt.check(L.eva_k_pool(P(self.x), P(self.pool), nb, st), "pool")
         xt.check(L.eva_k_lnh(P(self.pool), P(self.fnw), P(self.fnb), P(self.pn), P(self.pq), P(self.ps), nb, nb, st),
                  "lnh")
-        xt.check(L.eva_k_head(P(self.pq), P(self.ps), nb, P(self.hq), P(self.hs), P(self.hb), P(self.out), nb,
-                              self.nt, st), "head")
+        xt.check(L.eva_k_head(P(self.pq), P(self.ps), nb, P(self.hq), P(self.hs), self.ldh, P(self.hb), P(self.out),
+                              nb, self.nt, st), "head")
         sync()
         if check:
             check("head", nl, {"x": h(self.x[:M]), "pool": h(self.pool), "pn": h(self.pn), "pq": h(self.pq),

@@ -124,3 +124,17 @@ def test_blob_roundtrip_small(tmp_path):
     assert np.array_equal(r["rope"], m["rope"])
     raw = open(tmp_path / "b.bin", "rb").read()
     assert raw[:4] == b"EVA2" and len(raw) == 256 + n
+
+
+def test_c_program_against_header(tmp_path):
+    """tests/abi_check.c, compiled by gcc against include/xtag_eva.h alone and linked to libxtag_eva.so: struct layout,
+    rejected files and arguments (-1 with the eva: message), a failed open that eva_close accepts."""
+    import subprocess
+    exe = str(tmp_path / "abi_check")
+    libdir = os.path.dirname(LIB_PATH)
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(REPO_DIR, "include"),
+                    os.path.join(REPO_DIR, "tests", "abi_check.c"), "-o", exe, "-L", libdir, "-l:libxtag_eva.so",
+                    "-Wl,-rpath," + libdir], check=True)
+    r = subprocess.run([exe, str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "abi ok" in r.stdout, r.stdout + r.stderr
+    assert "eva: " in r.stderr                                  # the reference's error convention

@@ -141,8 +141,8 @@ class OracleCheck:
             assert np.array_equal(g["pn"].view(np.uint16), pn) and np.array_equal(g["pq"], pq)
             assert np.array_equal(g["ps"], ps), "final LN packing differs"
             nt = m["nt"]
-            hq, hs = orc.quant_w(m["hw"][:nt].astype(np.float32))
-            logit = orc.gemm_f64_rows(pq, ps, hq, hs, nt, np.arange(nb))
+            hq, hs = orc.head_pack(m["hw"][:nt])
+            logit = orc.gemm_rr_f64_rows(pq, ps, hq, hs, nt, np.arange(nb))
             ref = 1.0 / (1.0 + np.exp(-(logit + m["hb"][:nt])))
             err = float(np.abs(g["out"] - ref).max())
             self.worst["head sigmoid |err|"] = err
@@ -249,24 +249,35 @@ def test_partial_batch_and_head_rows(dev, synth_blob):
     assert hpn is not None and hpn.shape == (3, 1024)
     w, b = e.head_get()
     assert np.array_equal(w, m["hw"][:m["nt"]]) and np.array_equal(b, m["hb"][:m["nt"]])
-    # a stolen row (eva_head_put, eva.h:645-650): the engine keeps the fp16 head as the master and repacks the
-    # row's 128-row block, which it shares with file rows 10752..10860; its score follows from the oracle packing of
-    # that master and the batch's fp16 head inputs (hpn)
+    # a stolen row (eva_head_put, eva.h:645-650) and an edited file row: the engine keeps the fp16 head as the master
+    # and repacks only the written row (every head row carries its own 1x128 scales); its score follows from the
+    # oracle packing of that row and the batch's fp16 head inputs (hpn), and no other row's score moves by a bit
     nt0 = m["nt"]
     e.head_put(nt0, m["hw"][7], float(m["hb"][7]))
     e.submit(2, inp)
     s2 = e.wait(2, 3)
     from oracle import oracle as O
-    master = np.zeros((nt0 + 3, 1024), np.float32)
-    master[:nt0] = m["hw"][:nt0].astype(np.float32)
-    master[nt0] = m["hw"][7].astype(np.float32)
-    hq, hs = O.quant_w(master)
     pq, ps = O.quant_act(e.hpn(2, 3).view(np.float16).astype(np.float32))
-    logit = O.gemm_f64_rows(pq, ps, hq, hs, nt0 + 3, np.arange(3))
-    ref = 1.0 / (1.0 + np.exp(-(logit[:, nt0] + m["hb"][7])))
+    hq, hs = O.head_pack(m["hw"][7:8])
+    ref = 1.0 / (1.0 + np.exp(-(O.gemm_rr_f64_rows(pq, ps, hq, hs, 1, np.arange(3))[:, 0] + m["hb"][7])))
     assert np.abs(s2[:, nt0] - ref).max() < 1e-4
-    blk = (nt0 // 128) * 128                                   # rows outside the repacked block are unchanged
-    assert np.array_equal(s2[:, :blk], s[:, :blk])
+    assert np.array_equal(s2[:, :nt0], s[:, :nt0]), "file-tag scores changed by an extra-row upload"
+    assert np.array_equal(s2[:, nt0 + 1:], s[:, nt0 + 1:])
+    # an edited file row next to others of the same 128-row range: only its own column changes
+    j = nt0 - 5
+    w_new = (m["hw"][j].astype(np.float32) * 40.0).astype(np.float16)   # a much larger row
+    e.head_put(j, w_new, 0.25)
+    e.submit(3, inp)
+    s3 = e.wait(3, 3)
+    others = np.ones(e.nt, bool)
+    others[j] = False
+    assert np.array_equal(s3[:, others], s2[:, others])
+    hq, hs = O.head_pack(w_new[None])
+    ref = 1.0 / (1.0 + np.exp(-(O.gemm_rr_f64_rows(pq, ps, hq, hs, 1, np.arange(3))[:, 0] + 0.25)))
+    assert np.abs(s3[:, j] - ref).max() < 1e-4
+    e.head_put(j, m["hw"][j], float(m["hb"][j]))                      # restore: the file row's scores come back
+    e.submit(4, inp)
+    assert np.array_equal(e.wait(4, 3), s2)
     # resident-input path: one graph replay on the inputs already in the device buffer gives the same scores
     e.run()
     e.sync()

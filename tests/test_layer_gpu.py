@@ -415,16 +415,25 @@ def test_fc2_folded_ln(dev, xt, orc):
     _check_close("x", _f16_f32(d_x.cpu().numpy().view(np.uint16)), _f16_f32(ref), scale, 2.0 ** -10)
 
 
-@pytest.mark.parametrize("nb,nt", [(32, 10861), (64, 13461), (1, 300)])
+@pytest.mark.parametrize("nb,nt", [(32, 10861), (64, 13461), (1, 300), (128, 1000), (37, 64)])
 def test_head_sigmoid(dev, xt, orc, nb, nt):
     _say(f"k_head nb={nb} nt={nt}")
     _, qa, sa = _packed_act(orc, nb, D, 81)
-    _, qw, sw = _packed_w(orc, nt, D, 82, std=0.05)
+    r = np.random.default_rng(82)
+    w16 = (r.standard_normal((nt, D)) * 0.05).astype(np.float16)
+    w16[::97] *= 30                                           # rows of very different size: each has its own scales
+    ldw = nt + 19
+    d_w16 = _d(w16, dev)
+    d_qw = torch.zeros((nt, D), dtype=torch.uint8, device=dev)
+    d_sw = torch.full((8, ldw), np.nan, dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_quant_act(xt.ptr(d_w16), 2, D, nt, D, xt.ptr(d_qw), D, xt.ptr(d_sw), ldw, _st()), "pack head")
+    qw, sw = orc.head_pack(w16)
+    assert (d_qw.cpu().numpy() == qw).all() and (d_sw.cpu().numpy()[:, :nt] == sw).all()   # fp16 packing bit-exact
     hb = (np.random.default_rng(83).standard_normal(nt) * 0.1).astype(np.float32)
     d_out = torch.zeros((nb, nt), dtype=torch.float32, device=dev)
-    _ok(xt.lib.eva_k_head(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa, dev)), nb, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)),
+    _ok(xt.lib.eva_k_head(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa, dev)), nb, xt.ptr(d_qw), xt.ptr(d_sw), ldw,
                           xt.ptr(_d(hb, dev)), xt.ptr(d_out), nb, nt, _st()), "eva_k_head")
-    logit = orc.gemm_f64_rows(qa, sa, qw, sw, nt, np.arange(nb))
+    logit = orc.gemm_rr_f64_rows(qa, sa, qw, sw, nt, np.arange(nb))
     ref = 1.0 / (1.0 + np.exp(-(logit + hb)))
     err = np.abs(d_out.cpu().numpy() - ref).max()
     _say(f"  sigmoid max |err| {err:.2e}")

@@ -217,6 +217,32 @@ def test_lnh_vs_float64(orc):
     assert (q == q2).all() and (s == s2).all()
 
 
+# ---------------------------------------------------------------- the head GEMM with per-row weight scales
+def test_head_gemm_rr_vs_numpy(orc):
+    r = np.random.default_rng(6)
+    nb, nt = 7, 333
+    x = (r.standard_normal((nb, 1024)) * 2).astype(np.float32)
+    w = (r.standard_normal((nt, 1024)) * 0.05).astype(np.float16)
+    w[::13] *= 50                                          # rows of very different size
+    qa, sa = orc.quant_act(x)
+    qw, sw = orc.head_pack(w)
+    lut = orc.E4M3_LUT.astype(np.float64)
+    A = lut[qa] * np.repeat(sa.T.astype(np.float64), 128, 1)
+    W = lut[qw] * np.repeat(sw.T.astype(np.float64), 128, 1)
+    ref = A @ W.T
+    got = orc.gemm_rr_f64_rows(qa, sa, qw, sw, nt, np.arange(nb))
+    assert np.abs(got - ref).max() <= 1e-12 * (np.abs(A) @ np.abs(W).T).max()
+    # each row's packing depends on that row alone: scaling one row leaves every other row's codes and scales
+    w2 = w.copy()
+    w2[5] *= 7
+    qw2, sw2 = orc.head_pack(w2)
+    keep = np.arange(nt) != 5
+    assert (qw2[keep] == qw[keep]).all() and (sw2[:, keep] == sw[:, keep]).all()
+    # and the packing is the 1x128 packing of the fp16 values, within E4M3 resolution of them
+    err = np.abs(W - w.astype(np.float64))
+    assert (err <= 2.0 ** -4 * np.repeat(sw.T.astype(np.float64), 128, 1) * 448).all()
+
+
 # ---------------------------------------------------------------- the forward, composed in float64
 def _f64_forward(orc, m, inp16, nl):
     """eva_forward's order (eva.h:227-310) from numpy float64 primitives. The storage formats the design fixes are
@@ -276,7 +302,7 @@ def _f64_forward(orc, m, inp16, nl):
     pool = x.reshape(nb, T, 1024)[:, 1:].mean(1)
     pn = f16(ln(pool, m["fnw"], m["fnb"]))
     nt = m["nt"]
-    logit = act(pn) @ wt(m["hw"][:nt].astype(np.float32))[:nt].T + m["hb"][:nt]
+    logit = act(pn) @ act(m["hw"][:nt]).T + m["hb"][:nt]     # head rows packed 1x128, each with its own scales
     return 1.0 / (1.0 + np.exp(-logit)), pn
 
 
@@ -314,9 +340,9 @@ def _sequenced_forward(orc, m, inp16, nl, sparse=False):
     p = orc.pool(x, nb)
     pn, pq, ps = orc.lnh(p, m["fnw"], m["fnb"])
     nt = m["nt"]
-    qh, sh = orc.quant_w(f32(m["hw"][:nt]))
-    logit = orc.gemm_f32(pq, ps, qh, sh, nt, threads=0, avx2=1)[:, :nt]
-    return (1.0 / (1.0 + np.exp(-(logit + m["hb"][:nt]).astype(np.float32)))).astype(np.float32), pn
+    qh, sh = orc.head_pack(m["hw"][:nt])
+    logit = orc.gemm_rr_f64_rows(pq, ps, qh, sh, nt, np.arange(nb)).astype(np.float32)
+    return (1.0 / (1.0 + np.exp(-(logit + m["hb"][:nt])))).astype(np.float32), pn
 
 
 @pytest.mark.parametrize("sparse", [False, True])

@@ -322,7 +322,7 @@ def test_px_pool_head(dev, xt, orc):
     assert np.all(err <= 2.0 ** -11 * np.abs(o_ref) + 2e-5 * bnd)
     # tag head on the packed o (the block-scaled FP8 head, as the wd model's)
     nt = 1000
-    qw, sw = _w(orc, nt, D, 152, std=0.05)
+    qw, sw = orc.head_pack((np.random.default_rng(152).standard_normal((nt, D)) * 0.05).astype(np.float16))
     hb = (r.standard_normal(nt) * 0.1).astype(np.float32)
     d_q = torch.zeros((nb, D), dtype=torch.uint8, device=dev)
     d_qs = torch.zeros((8, nb), dtype=torch.float32, device=dev)
@@ -330,9 +330,9 @@ def test_px_pool_head(dev, xt, orc):
     q_ref, qs_ref = orc.quant_act(o)
     assert (d_q.cpu().numpy() == q_ref).all() and (d_qs.cpu().numpy() == qs_ref).all()
     d_out = torch.zeros((nb, nt), dtype=torch.float32, device=dev)
-    _ok(xt.lib.eva_k_head(xt.ptr(d_q), xt.ptr(d_qs), nb, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)), xt.ptr(_d(hb, dev)),
-                          xt.ptr(d_out), nb, nt, _st()), "eva_k_head")
-    logit = orc.gemm_f64_rows(q_ref, qs_ref, qw, sw, nt, np.arange(nb))
+    _ok(xt.lib.eva_k_head(xt.ptr(d_q), xt.ptr(d_qs), nb, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)), nt,
+                          xt.ptr(_d(hb, dev)), xt.ptr(d_out), nb, nt, _st()), "eva_k_head")
+    logit = orc.gemm_rr_f64_rows(q_ref, qs_ref, qw, sw, nt, np.arange(nb))
     assert np.abs(d_out.cpu().numpy() - 1.0 / (1.0 + np.exp(-(logit + hb)))).max() < 1e-4
 
 

@@ -13,42 +13,12 @@
 #include "xt_abi.h"
 #include "xtag_eva.h"
 
-extern "C" {
-int eva_k_ln(const void *x, const float *g, const float *b, void *q, float *s, int rows, int lds, void *stream);
-int eva_k_qkv(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *cs, void *q, void *k,
-              void *vt, int rows, void *stream);
-int eva_k_flash(const void *q, const void *k, const void *vt, void *o8, float *os, int lds, int nb, float *o32,
-                void *stream);
-int eva_k_oproj(const void *a8, const float *as, int lds, const void *w, const float *ws, void *x, int rows, void *stream);
-int eva_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8, float *ms, float *stat,
-              int rows, void *stream);
-int eva_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *stat, const float *cn,
-              const float *dn, void *x, int rows, void *stream);
-int eva_k_head(const void *pq, const float *ps, int lds, const void *w, const float *ws, const float *hb, float *out,
-               int nb, int nt, void *stream);
-int eva_k_pe(const void *in, const void *pe, const float *pos, void *x, int nb, void *stream);
-int eva_k_pool(const void *x, float *p, int nb, void *stream);
-int eva_k_lnh(const float *p, const float *g, const float *b, void *pn, void *q, float *s, int rows, int lds,
-              void *stream);
-int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_out, int perm, const float *colscale,
-                 float *scratch, void *q, float *s, void *stream);
-int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const float *beta, float *c, float *d,
-                  void *stream);
-int eva_k_prune24(void *w, int N, int K, void *stream);
-int eva_k_pack24(const void *w, int N, int K, void *vals, void *idx, int *bad, void *stream);
-int eva_k_qkv_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx, const float *ws,
-                 const float *cs, void *q, void *k, void *vt, int rows, void *stream);
-int eva_k_oproj_sp(const void *a8, const float *as, int lds, const void *vals, const void *idx, const float *ws,
-                   void *x, int rows, void *stream);
-int eva_k_fc1_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx, const float *ws,
-                 void *m8, float *ms, float *stat, int rows, void *stream);
-int eva_k_fc2_sp(const void *m8, const float *ms, int lds, const void *vals, const void *idx, const float *ws,
-                 const float *stat, const float *cn, const float *dn, void *x, int rows, void *stream);
-}
 
 #define V2_HIDP 2736          // hidden padding of the reference's v2 blob (export_eva.py:19)
 #define EVA_CHUNK (32u << 20) // weight streaming chunk (eva.h:59)
 #define EVA_HB_OFF (-16.0f)   // bias of an extra head row nothing has written (eva.h:69)
+#define EV_HPUT_SLOTS 256     // eva_head_put rows staged at once before a call waits for the oldest copy
+#define EV_HPUT_SLOT 2304     // bytes per slot: 1024 fp16 weights, then the fp32 bias (256-byte multiple)
 
 struct Layer {
     const float *ln1w, *ln1b, *ln2w, *ln2b, *mlnw, *mlnb;  // in the blob
@@ -74,8 +44,12 @@ struct eva_impl {
     Layer L[EVA_NL];
     uint16_t *hmaster;                                     // head fp16 [nt][1024] (file rows, then extra rows)
     float *hb;                                             // [nt]
-    uint8_t *hq;                                           // head E4M3 [ceil(nt/128)*128][1024]
-    float *hs;                                             // [ceil(nt/128)][8]
+    uint8_t *hq;                                           // head E4M3 [nt][1024], each row with its own scales
+    float *hs;                                             // 1x128 scale planes [8][ldh]
+    uint32_t ldh;                                          // nt rounded up to 64
+    uint8_t *hput;                                         // pinned staging slots of eva_head_put (row + bias)
+    hipEvent_t hput_ev[EV_HPUT_SLOTS];                     // the last copy out of each slot
+    uint32_t hput_next;
     float *scratch;
     // activations
     uint16_t *in, *x, *q, *k, *vt, *pn;
@@ -199,23 +173,22 @@ static int ev_forward(eva *e)
     }
     EV_CK(eva_k_pool(E->x, E->pool, nb, st));
     EV_CK(eva_k_lnh(E->pool, E->fnw, E->fnb, E->pn, E->pq, E->ps, nb, nb, st));
-    EV_CK(eva_k_head(E->pq, E->ps, nb, E->hq, E->hs, E->hb, E->out, nb, (int)e->nt, st));
+    EV_CK(eva_k_head(E->pq, E->ps, nb, E->hq, E->hs, (int)E->ldh, E->hb, E->out, nb, (int)e->nt, st));
     return 0;
 }
 
-// pack one 128-row block of the head from the fp16 master
-static int ev_pack_head_block(eva *e, uint32_t blk)
+// pack head rows r0 .. r0 + n - 1 from the fp16 master, each row with its own 1x128 scales
+static int ev_pack_head_rows(eva *e, uint32_t r0, uint32_t n)
 {
     eva_impl *E = e->impl;
-    const uint32_t r0 = blk * 128, n = e->nt - r0 < 128 ? e->nt - r0 : 128;
-    return eva_k_prep_w(E->hmaster + (size_t)r0 * EVA_D, EVA_D, (int)n, EVA_D, 128, EVA_D, 0, NULL, E->scratch,
-                        E->hq + (size_t)r0 * EVA_D, E->hs + (size_t)blk * 8, (void *)E->st);
+    return eva_k_quant_act(E->hmaster + (size_t)r0 * EVA_D, 2, EVA_D, (int)n, EVA_D, E->hq + (size_t)r0 * EVA_D, EVA_D,
+                           E->hs + r0, (int)E->ldh, (void *)E->st);
 }
 
 static int ev_up(eva *e)
 {
     eva_impl *E = e->impl;
-    const uint32_t ntp = (e->nt0 + 7) & ~7u, nt = e->nt, nblk = (nt + 127) / 128;
+    const uint32_t ntp = (e->nt0 + 7) & ~7u, nt = e->nt;
     void *st;
 
     XT_HIP(hipSetDevice(E->devno));
@@ -257,18 +230,21 @@ static int ev_up(eva *e)
         }
         EV_CK(eva_k_fold_cd(L.w2, L.s2, L.w216, V2_HIDP, L.mlnb, L.cn, L.dn, st));
     }
-    // head: fp16 master (file rows, then zero extra rows with bias -16), packed per 128-row block
+    // head: fp16 master (file rows, then zero extra rows with bias -16), every row packed with its own scales
+    E->ldh = (nt + 63) & ~63u;
     EV_ALLOC(E, E->hmaster, (size_t)nt * EVA_D * 2, true);
     EV_ALLOC(E, E->hb, (size_t)nt * 4, false);
-    EV_ALLOC(E, E->hq, (size_t)nblk * 128 * EVA_D, false);
-    EV_ALLOC(E, E->hs, (size_t)nblk * 8 * 4, false);
+    EV_ALLOC(E, E->hq, (size_t)nt * EVA_D, false);
+    EV_ALLOC(E, E->hs, (size_t)8 * E->ldh * 4, true);
     XT_HIP(hipMemcpyAsync(E->hmaster, E->hw0, (size_t)e->nt0 * EVA_D * 2, hipMemcpyDeviceToDevice, E->st));
     XT_HIP(hipMemcpyAsync(E->hb, E->hb0, (size_t)e->nt0 * 4, hipMemcpyDeviceToDevice, E->st));
     if (nt > e->nt0) {
         std::vector<float> nb16(nt - e->nt0, EVA_HB_OFF);
         XT_HIP(hipMemcpy(E->hb + e->nt0, nb16.data(), nb16.size() * 4, hipMemcpyHostToDevice));
     }
-    for (uint32_t b = 0; b < nblk; b++) EV_CK(ev_pack_head_block(e, b));
+    EV_CK(ev_pack_head_rows(e, 0, nt));
+    XT_HIP(hipHostMalloc((void **)&E->hput, (size_t)EV_HPUT_SLOTS * EV_HPUT_SLOT, hipHostMallocDefault));
+    for (int s = 0; s < EV_HPUT_SLOTS; s++) XT_HIP(hipEventCreateWithFlags(&E->hput_ev[s], hipEventDisableTiming));
 
     // activations
     const size_t M = E->M, Mp = E->Mp, nb = E->nb;
@@ -424,10 +400,19 @@ extern "C" int eva_head_put(eva *e, uint32_t j, const uint16_t *w, float bias)
     if (eva_ready(e)) return -1;
     eva_impl *E = e->impl;
     if (j >= e->nt) return xt_fail("eva_head_put", "row past nt");
-    XT_HIP(hipMemcpyAsync(E->hmaster + (size_t)j * EVA_D, w, EVA_D * 2, hipMemcpyHostToDevice, E->st));
-    XT_HIP(hipMemcpyAsync(E->hb + j, &bias, 4, hipMemcpyHostToDevice, E->st));
-    XT_HIP(hipStreamSynchronize(E->st));  // bias and row are pageable: copied before the call returns
-    return ev_pack_head_block(e, j / 128);
+    // stream-ordered (eva.h:643-650): the row and bias go to a pinned slot before the call returns, so w may be reused
+    // at once; copies and the row's repack follow on the engine stream, and batches submitted later see the row. A
+    // call waits only when every slot still has a copy in flight.
+    const uint32_t slot = E->hput_next++ % EV_HPUT_SLOTS;
+    XT_HIP(hipEventSynchronize(E->hput_ev[slot]));
+    uint8_t *p = E->hput + (size_t)slot * EV_HPUT_SLOT;
+    memcpy(p, w, EVA_D * 2);
+    memcpy(p + EVA_D * 2, &bias, 4);
+    XT_HIP(hipMemcpyAsync(E->hmaster + (size_t)j * EVA_D, p, EVA_D * 2, hipMemcpyHostToDevice, E->st));
+    XT_HIP(hipMemcpyAsync(E->hb + j, p + EVA_D * 2, 4, hipMemcpyHostToDevice, E->st));
+    EV_CK(ev_pack_head_rows(e, j, 1));
+    XT_HIP(hipEventRecord(E->hput_ev[slot], E->st));
+    return 0;
 }
 
 extern "C" int eva_head_get(eva *e, uint16_t *w, float *bias)
@@ -457,6 +442,9 @@ extern "C" void eva_close(eva *e)
         if (e->hpn[s]) (void)hipHostFree(e->hpn[s]);
     }
     if (E->stage) (void)hipHostFree(E->stage);
+    if (E->hput) (void)hipHostFree(E->hput);
+    for (int s = 0; s < EV_HPUT_SLOTS; s++)
+        if (E->hput_ev[s]) (void)hipEventDestroy(E->hput_ev[s]);
     for (void *p : E->allocs) (void)hipFree(p);
     if (E->st) (void)hipStreamDestroy(E->st);
     free(E->path);

@@ -7,7 +7,6 @@
 // planes [K/128][lds]; residual x fp16 [rows][1024].
 #include "layer_core.h"
 
-typedef BsCfg<64, 128, 1, 2, 3> HeadCfg;    // head: few rows, 10861 columns
 
 // ---------------------------------------------------------------------------------------------------------------
 // k_qkv: h8 [rows][1024] x Wqkv [3072][1024] -> q, k bf16 [nb][16][1088][64] (RoPE on patch tokens), vt bf16
@@ -293,33 +292,56 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// k_head: out [nb][nt] = sigmoid(pq . Wh^T + hb) (kern_common.cuh:679-727 as a block-scaled FP8 GEMM)
+// k_head: out [nb][nt] = sigmoid(hb[n] + sum_kb ps[kb][m] hs[kb][n] sum_{k in kb} pq[m][k] hq[n][k])
+// (kern_common.cuh:679-727 k_headmv, here an FP8 GEMM). The head rows carry 1x128 scales of their own (planes
+// hs [8][ldh], as activations do), so every row is packed, and repacked by eva_head_put, independently of all others.
+// The head is a weight stream (nt x 1 KB) against at most 128 input rows: one block per 64 output columns and 64 rows,
+// 4 waves, wave w owning columns n0 + 16 w .. + 15 over the 4 row tiles of 16. Fragments come straight from L2 into
+// registers (a row of the weights is read once per row tile); descriptors that end at row nb of pq and row nt of hq
+// load zero past them.
 // ---------------------------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(HeadCfg::NT) k_head(const uint8_t *__restrict__ pq, const float *__restrict__ ps,
-                                                     int lds, const uint8_t *__restrict__ w,
-                                                     const float *__restrict__ ws, const float *__restrict__ hb,
-                                                     float *__restrict__ out, int nb, int nt)
+__global__ void __launch_bounds__(256) k_head(const uint8_t *__restrict__ pq, const float *__restrict__ ps, int lds,
+                                              const uint8_t *__restrict__ hq, const float *__restrict__ hs, int ldh,
+                                              const float *__restrict__ hb, float *__restrict__ out, int nb, int nt)
 {
-    using C = HeadCfg;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
-    v4f acc[C::TM][C::TN];
-    int m0, n0, wm0, wn0;
-    layer_tile<C>(nb, nt, m0, n0);
-    bs_mainloop<C>(pq, XT_D, ps, lds, w, ws, nb, (nt + 127) & ~127, XT_D, m0, n0, smem, acc);
-    bs_wave_origin<C>(wm0, wn0);
-    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const int n0 = blockIdx.x * 64 + 16 * w, m0 = blockIdx.y * 64;
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(pq, (uint32_t)nb * XT_D), rw = buf_rsrc(hq, (uint32_t)nt * XT_D);
+    const int nl = n0 + c16;                                  // weight row of this lane's B fragment, output column
+    const int ncl = nl < nt ? nl : nt - 1;                    // clamped for the scale and bias reads
+    v4f acc[4];
 #pragma unroll
-    for (int i = 0; i < C::TM; i++)
+    for (int i = 0; i < 4; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+    for (int kb = 0; kb < XT_D / 128; kb++) {
+        const uint32_t ko = (uint32_t)kb * 128u + 16u * g;
+        const v4u blo = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)((uint32_t)nl * XT_D + ko), 0, 0);
+        const v4u bhi = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)((uint32_t)nl * XT_D + ko + 64u), 0, 0);
+        const v8i b = {(int)blo[0], (int)blo[1], (int)blo[2], (int)blo[3], (int)bhi[0], (int)bhi[1], (int)bhi[2], (int)bhi[3]};
+        const float swv = hs[(size_t)kb * ldh + ncl];
 #pragma unroll
-        for (int j = 0; j < C::TN; j++) {
-            const int n = n0 + wn0 + 16 * j + c16;
-            if (n >= nt) continue;
-            const float bias = hb[n];
+        for (int i = 0; i < 4; i++) {
+            const uint32_t ar = (uint32_t)(m0 + 16 * i + c16) * XT_D;
+            const v4u alo = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(ar + ko), 0, 0);
+            const v4u ahi = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(ar + ko + 64u), 0, 0);
+            const v8i a = {(int)alo[0], (int)alo[1], (int)alo[2], (int)alo[3], (int)ahi[0], (int)ahi[1], (int)ahi[2], (int)ahi[3]};
+            const v4f p = mfma_e4m3_16x16x128(a, b);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm0 + 16 * i + 4 * g + r;
-                if (m < nb) out[(size_t)m * nt + n] = 1.0f / (1.0f + __expf(-(acc[i][j][r] + bias)));
+                const int m = m0 + 16 * i + 4 * g + r;
+                const float sa = m < nb ? ps[(size_t)kb * lds + m] : 0.f;
+                acc[i][r] = __builtin_fmaf(p[r], sa * swv, acc[i][r]);
             }
+        }
+    }
+    if (nl >= nt) return;
+    const float bias = hb[nl];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = m0 + 16 * i + 4 * g + r;
+            if (m < nb) out[(size_t)m * nt + nl] = 1.0f / (1.0f + __expf(-(acc[i][r] + bias)));
         }
 }
 
@@ -411,7 +433,8 @@ template <bool SP>
 static int qkv_launch(const char *what, const void *h8, const float *hs, int lds, const void *w, const void *wx,
                       const float *ws, const float *cs, void *q, void *k, void *vt, int rows, void *stream)
 {
-    if (rows <= 0 || lds < rows || rows % XT_T) return xt_fail(what, "rows must be nb * 1025, lds >= rows");
+    if (layer_rows_ok(what, rows, lds)) return -1;
+    if (rows % XT_T) return xt_fail(what, "rows must be nb * 1025");
     if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || (SP && !wx)) return xt_fail(what, "h8 and w must be 16-byte aligned");
     hipLaunchKernelGGL(k_qkv<SP>, dim3(layer_grid(rows, 3 * XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
                        (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w, (const uint32_t *)wx, ws,
@@ -423,7 +446,7 @@ template <bool SP>
 static int oproj_launch(const char *what, const void *a8, const float *as, int lds, const void *w, const void *wx,
                         const float *ws, void *x, int rows, void *stream)
 {
-    if (rows <= 0 || lds < rows) return xt_fail(what, "bad shape (rows > 0, lds >= rows)");
+    if (layer_rows_ok(what, rows, lds)) return -1;
     if (!XT_ALIGNED(a8) || !XT_ALIGNED(w) || (SP && !wx)) return xt_fail(what, "a8 and w must be 16-byte aligned");
     hipLaunchKernelGGL(k_oproj<SP>, dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
                        (hipStream_t)stream, (const uint8_t *)a8, as, lds, (const uint8_t *)w, (const uint32_t *)wx, ws,
@@ -435,7 +458,7 @@ template <bool SP>
 static int fc1_launch(const char *what, const void *h8, const float *hs, int lds, const void *w, const void *wx,
                       const float *ws, void *m8, float *ms, float *stat, int rows, void *stream)
 {
-    if (rows <= 0 || lds < rows) return xt_fail(what, "bad shape (rows > 0, lds >= rows)");
+    if (layer_rows_ok(what, rows, lds)) return -1;
     if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || !XT_ALIGNED(m8) || (SP && !wx))
         return xt_fail(what, "h8, w, m8 must be 16-byte aligned");
     hipLaunchKernelGGL(k_fc1<SP>, dim3(layer_grid(rows, 2 * XT_HIDP, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
@@ -449,7 +472,7 @@ static int fc2_launch(const char *what, const void *m8, const float *ms, int lds
                       const float *ws, const float *stat, const float *cn, const float *dn, void *x, int rows,
                       void *stream)
 {
-    if (rows <= 0 || lds < rows) return xt_fail(what, "bad shape (rows > 0, lds >= rows)");
+    if (layer_rows_ok(what, rows, lds)) return -1;
     if (!XT_ALIGNED(m8) || !XT_ALIGNED(w) || (SP && !wx)) return xt_fail(what, "m8 and w must be 16-byte aligned");
     hipLaunchKernelGGL(k_fc2<SP>, dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
                        (hipStream_t)stream, (const uint8_t *)m8, ms, lds, (const uint8_t *)w, (const uint32_t *)wx, ws,
@@ -506,13 +529,14 @@ extern "C" int eva_k_fc2_sp(const void *m8, const float *ms, int lds, const void
     return fc2_launch<true>("eva_k_fc2_sp", m8, ms, lds, vals, idx, ws, stat, cn, dn, x, rows, stream);
 }
 
-extern "C" int eva_k_head(const void *pq, const float *ps, int lds, const void *w, const float *ws, const float *hb,
-                          float *out, int nb, int nt, void *stream)
+extern "C" int eva_k_head(const void *pq, const float *ps, int lds, const void *w, const float *ws, int ldw,
+                          const float *hb, float *out, int nb, int nt, void *stream)
 {
-    if (nb <= 0 || nt <= 0 || lds < nb) return xt_fail("eva_k_head", "bad shape (nb > 0, nt > 0, lds >= nb)");
+    if (nb <= 0 || nt <= 0 || lds < nb || ldw < nt || nb > EVA_NBMAX || nt > (1 << 20))
+        return xt_fail("eva_k_head", "bad shape (0 < nb <= 128, 0 < nt <= 2^20, lds >= nb, ldw >= nt)");
     if (!XT_ALIGNED(pq) || !XT_ALIGNED(w)) return xt_fail("eva_k_head", "pq and w must be 16-byte aligned");
-    hipLaunchKernelGGL(k_head, dim3(layer_grid(nb, nt, HeadCfg::BM, HeadCfg::BN)), dim3(HeadCfg::NT), 0,
-                       (hipStream_t)stream, (const uint8_t *)pq, ps, lds, (const uint8_t *)w, ws, hb, out, nb, nt);
+    hipLaunchKernelGGL(k_head, dim3((nt + 63) / 64, (nb + 63) / 64), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t *)pq, ps, lds, (const uint8_t *)w, ws, ldw, hb, out, nb, nt);
     return xt_check("eva_k_head");
 }
 

@@ -107,3 +107,11 @@ static inline unsigned layer_grid(int rows, int N, int BM, int BN)
 }
 
 #define XT_ALIGNED(p) ((((uintptr_t)(p)) & 15) == 0)
+
+// Token rows a layer launcher accepts: every 32-bit buffer offset (rows x 4736 bytes of the widest E4M3 activation,
+// rows x 2048 of an fp16 residual or bf16 q / k, the XT_OOR = 2^31 sentinel of rows past the end) stays in range.
+static inline int layer_rows_ok(const char *what, int rows, int lds)
+{
+    if (rows <= 0 || lds < rows || rows > (1 << 19)) return xt_fail(what, "bad shape (0 < rows <= 2^19, lds >= rows)");
+    return 0;
+}

@@ -243,17 +243,11 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restri
 // ---------------------------------------------------------------------------------------------------------------
 // C-ABI launchers
 // ---------------------------------------------------------------------------------------------------------------
-static int px_rows_ok(const char *what, int rows, int lds)
-{
-    // every byte offset (rows x 4736 bytes of fc1's output and fc2's input, rows x 2048 of q / k) stays below 2^32
-    if (rows <= 0 || lds < rows || rows > (1 << 19)) return xt_fail(what, "bad shape (0 < rows <= 2^19, lds >= rows)");
-    return 0;
-}
 
 extern "C" int px_k_qkv(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *bias,
                         const float *cs, int L, void *q, void *k, void *vt, int rows, void *stream)
 {
-    if (px_rows_ok("px_k_qkv", rows, lds)) return -1;
+    if (layer_rows_ok("px_k_qkv", rows, lds)) return -1;
     if (L <= 0 || L % 64 || rows % L) return xt_fail("px_k_qkv", "L must be a positive multiple of 64 dividing rows");
     if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || ((uintptr_t)bias & 7) || ((uintptr_t)cs & 7))
         return xt_fail("px_k_qkv", "h8 and w must be 16-byte aligned, bias and cs 8-byte aligned");
@@ -267,7 +261,7 @@ template <int K>
 static int px_res_launch(const char *what, const void *a8, const float *as, int lds, const void *w, const float *ws,
                          const float *bias, void *x, int rows, void *stream)
 {
-    if (px_rows_ok(what, rows, lds)) return -1;
+    if (layer_rows_ok(what, rows, lds)) return -1;
     if (!XT_ALIGNED(a8) || !XT_ALIGNED(w)) return xt_fail(what, "a8 and w must be 16-byte aligned");
     hipLaunchKernelGGL((k_px_res<false, K>), dim3(layer_grid(rows, XT_D, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT),
                        0, (hipStream_t)stream, (const uint8_t *)a8, as, lds, (const uint8_t *)w,
@@ -290,7 +284,7 @@ extern "C" int px_k_fc2(const void *m8, const float *ms, int lds, const void *w,
 extern "C" int px_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, const float *bias,
                         const float *rs, void *m8, float *ms, int rows, void *stream)
 {
-    if (px_rows_ok("px_k_fc1", rows, lds)) return -1;
+    if (layer_rows_ok("px_k_fc1", rows, lds)) return -1;
     if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || ((uintptr_t)m8 & 7))
         return xt_fail("px_k_fc1", "h8 and w must be 16-byte aligned, m8 8-byte aligned");
     auto kern = rs ? k_px_fc1<false, true> : k_px_fc1<false, false>;  // the multiply only where rs is given

@@ -37,8 +37,9 @@ struct px_impl {
     const uint16_t *pe, *hpos, *wv, *hw16;
     const float *pos, *lnpw, *lnpb, *csw, *csg, *hnw, *hnb, *U, *hb;
     PxLayer L[PX_NL];
-    uint8_t *hq;                                        // head E4M3 [ceil(nt/128)*128][1024]
-    float *hs;                                          // [ceil(nt/128)][8]
+    uint8_t *hq;                                        // head E4M3 [nt][1024], each row with its own scales
+    float *hs;                                          // 1x128 scale planes [8][ldh]
+    uint32_t ldh;                                       // nt rounded up to 64
     float *scratch;
     // activations
     uint16_t *in, *x, *q, *k, *vt, *y, *P;
@@ -172,14 +173,13 @@ static int px_forward(px *p)
     PX_CK(px_k_hpool(E->P, E->y, E->part, nb, PX_T, st));
     PX_CK(px_k_hv(E->part, PX_T / PX_PCH, E->wv, E->o, nb, st));
     PX_CK(eva_k_quant_act(E->o, 1, EVA_D, nb, EVA_D, E->oq, EVA_D, E->oqs, nb, st));
-    PX_CK(eva_k_head(E->oq, E->oqs, nb, E->hq, E->hs, E->hb, E->out, nb, (int)p->nt, st));
+    PX_CK(eva_k_head(E->oq, E->oqs, nb, E->hq, E->hs, (int)E->ldh, E->hb, E->out, nb, (int)p->nt, st));
     return 0;
 }
 
 static int px_up(px *p)
 {
     px_impl *E = p->impl;
-    const uint32_t nblk = (p->nt + 127) / 128;
     void *st;
 
     XT_HIP(hipSetDevice(E->devno));
@@ -200,7 +200,7 @@ static int px_up(px *p)
     }
 
     // packed weights (bring-up packing on the GPU); q / k rows of Wqkv pair-split for the RoPE epilogue
-    const size_t scratch_f = (size_t)(nblk * 128 > PX_HID ? nblk * 128 : PX_HID) * EVA_D;
+    const size_t scratch_f = (size_t)PX_HID * EVA_D;
     PX_ALLOC(E, E->scratch, scratch_f * 4, false);
     for (int i = 0; i < PX_NL; i++) {
         PxLayer &L = E->L[i];
@@ -217,11 +217,11 @@ static int px_up(px *p)
         PX_CK(eva_k_prep_w(L.w116, EVA_D, PX_HID, EVA_D, PX_HID, EVA_D, 0, NULL, E->scratch, L.w1, L.s1, st));
         PX_CK(eva_k_prep_w(L.w216, PX_HID, EVA_D, PX_HID, EVA_D, PX_HID, 0, NULL, E->scratch, L.w2, L.s2, st));
     }
-    // head: the file's fp16 rows packed per 128-row block (rows past nt zero)
-    PX_ALLOC(E, E->hq, (size_t)nblk * 128 * EVA_D, false);
-    PX_ALLOC(E, E->hs, (size_t)nblk * 8 * 4, false);
-    PX_CK(eva_k_prep_w(E->hw16, EVA_D, (int)p->nt, EVA_D, (int)(nblk * 128), EVA_D, 0, NULL, E->scratch, E->hq, E->hs,
-                       st));
+    // head: the file's fp16 rows, each packed with its own 1x128 scales
+    E->ldh = (p->nt + 63) & ~63u;
+    PX_ALLOC(E, E->hq, (size_t)p->nt * EVA_D, false);
+    PX_ALLOC(E, E->hs, (size_t)8 * E->ldh * 4, true);
+    PX_CK(eva_k_quant_act(E->hw16, 2, EVA_D, (int)p->nt, EVA_D, E->hq, EVA_D, E->hs, (int)E->ldh, st));
 
     // activations
     const size_t M = E->M, nb = E->nb;

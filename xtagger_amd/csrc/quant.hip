@@ -4,7 +4,7 @@
 #include "gemm_core.h"
 #include "xt_abi.h"
 
-// ---- activations: x [M][ldx] (bf16 or fp32) -> q [M][ldq] E4M3, s [K/128][lds] ----
+// ---- activations: x [M][ldx] (bf16, fp32 or fp16) -> q [M][ldq] E4M3, s [K/128][lds] ----
 // One thread per 8 consecutive elements; the 16 threads of one 128-element block are 16 aligned lanes.
 template <typename TIn>
 __device__ __forceinline__ void load8(const TIn *p, float *v);
@@ -18,6 +18,13 @@ __device__ __forceinline__ void load8<uint16_t>(const uint16_t *p, float *v)
         v[2 * i] = __uint_as_float(w[i] << 16);
         v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
+}
+template <>
+__device__ __forceinline__ void load8<_Float16>(const _Float16 *p, float *v)
+{
+    const v8h h = *(const v8h *)p;
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (float)h[i];
 }
 template <>
 __device__ __forceinline__ void load8<float>(const float *p, float *v)
@@ -197,18 +204,21 @@ static int grid_for(long threads)
 extern "C" int eva_k_quant_act(const void *x, int in_kind, int ldx, int M, int K, void *q, int ldq, float *s, int lds,
                                void *stream)
 {
-    if (M < 0 || K % 128 || ldx < K || ldq < K || lds < M || (in_kind != 0 && in_kind != 1) || ldx % 8 || ldq % 8)
+    if (M < 0 || K % 128 || ldx < K || ldq < K || lds < M || in_kind < 0 || in_kind > 2 || ldx % 8 || ldq % 8)
         return xt_fail("eva_k_quant_act",
-                       "bad shape (K % 128, ldx >= K, ldq >= K, lds >= M, ldx and ldq multiples of 8, in_kind 0 or 1)");
+                       "bad shape (K % 128, ldx >= K, ldq >= K, lds >= M, ldx and ldq multiples of 8, in_kind 0..2)");
     if (((uintptr_t)x | (uintptr_t)q) & 15) return xt_fail("eva_k_quant_act", "x and q must be 16-byte aligned");
     if (!M) return 0;
     const long thr = (long)M * (K / 8);
     if (in_kind == 0)
         hipLaunchKernelGGL(k_quant_act<uint16_t>, dim3(grid_for(thr)), dim3(256), 0, (hipStream_t)stream,
                            (const uint16_t *)x, ldx, M, K, (uint8_t *)q, ldq, s, lds);
-    else
+    else if (in_kind == 1)
         hipLaunchKernelGGL(k_quant_act<float>, dim3(grid_for(thr)), dim3(256), 0, (hipStream_t)stream, (const float *)x,
                            ldx, M, K, (uint8_t *)q, ldq, s, lds);
+    else
+        hipLaunchKernelGGL(k_quant_act<_Float16>, dim3(grid_for(thr)), dim3(256), 0, (hipStream_t)stream,
+                           (const _Float16 *)x, ldx, M, K, (uint8_t *)q, ldq, s, lds);
     return xt_check("eva_k_quant_act");
 }
 
@@ -238,6 +248,12 @@ static int gemm_launch(const char *what, const void *qa, int lda, const float *s
         (out_kind != 0 && out_kind != 1))
         return xt_fail(what, "bad shape (K % 128, lda >= K and a multiple of 16, lds >= M, ldc >= N, out_kind 0 or 1)");
     if (((uintptr_t)qa | (uintptr_t)qw) & 15) return xt_fail(what, "qa and qw must be 16-byte aligned");
+    // buffer descriptors and row offsets are 32-bit: operands and output must stay below 2 GiB (the A-row sentinel
+    // XT_OOR = 2^31 must lie past every valid offset) and 4 GiB
+    const size_t Np = ((size_t)N + 255) / 256 * 256;
+    if ((size_t)M * lda >= (1u << 31) || Np * K >= (1u << 31) || (size_t)M * ldc * (out_kind ? 4 : 2) >= (1ull << 32) ||
+        (size_t)lds * (K / 128) * 4 >= (1u << 31))
+        return xt_fail(what, "operands too large for 32-bit offsets (M * lda, N * K < 2^31 bytes, C < 4 GiB)");
     if (SP && (N % 16 || !qx || ((uintptr_t)qx & 3))) return xt_fail(what, "sparse weights: N % 16 == 0, 4-byte aligned indices");
     if (!M) return 0;
     const uint8_t *A = (const uint8_t *)qa, *W = (const uint8_t *)qw;

@@ -1,8 +1,12 @@
 // xt_abi.h - error convention of the C-ABI: every entry point returns 0, or -1 after printing
-// "eva: <what>: <reason>" to stderr (the reference's EVA_CU convention, src/engine/eva.h:153-176).
+// "eva: <what>: <reason>" to stderr (the reference's EVA_CU convention, src/engine/eva.h:153-176). Every source that
+// defines an exported entry point includes this file, and with it the public declarations of include/xtag_eva.h, so
+// the compiler holds each definition to its declaration.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdio.h>
+
+#include "xtag_eva.h"
 
 static inline int xt_fail(const char *what, const char *why)
 {

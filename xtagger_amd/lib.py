@@ -34,7 +34,7 @@ _SIGS = {
     "px_k_hv": (_i, [_p, _i, _p, _p, _i, _p]),
     "eva_k_fc1": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _i, _p]),
     "eva_k_fc2": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
-    "eva_k_head": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _i, _p]),
+    "eva_k_head": (_i, [_p, _p, _i, _p, _p, _i, _p, _p, _i, _i, _p]),
     "eva_k_pe": (_i, [_p, _p, _p, _p, _i, _p]),
     "eva_k_pool": (_i, [_p, _p, _i, _p]),
     "eva_k_lnh": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _p]),
