@@ -6,7 +6,8 @@
    rows (every tile-boundary row class, the last rows, a random spread) are checked against the fp64 product of the
    same packed operands through the oracle's epilogues (src/engine/eva_kernels.cu:41-114, 134-162, 211-279, 286-334).
 2. The engine at batch 32 and at batch 64 with 2600 extra head rows (13461 in all): each image's scores equal that
-   image's batch-1 engine scores. Rows of a batch are computed independently, so batching may not move a score.
+   image's batch-1 engine scores bit for bit (the batch-1 forward is the one checked step by step against the oracle
+   in test_forward_gpu.py). Rows of a batch are computed independently, so batching may not move a score.
 """
 import numpy as np
 import pytest
@@ -256,6 +257,6 @@ def test_engine_batch32_and_batch64_head13461_match_batch1(dev, synth_blob):
         ref = single[:nb, :nt0 + ex]
         d = np.abs(s - ref)
         _say(f"  max |batch - single| {d.max():.3g}, bitwise equal rows {int((d.max(1) == 0).sum())}/{nb}")
-        assert d.max() <= 1e-4
-        for b in range(nb):
-            assert set(np.argsort(-s[b], kind="stable")[:50]) == set(np.argsort(-ref[b], kind="stable")[:50])
+        # every kernel computes a row from that row (or that image) alone, in an order that does not depend on where
+        # the row sits in its tile: the scores are bit-identical
+        assert np.array_equal(s, ref)

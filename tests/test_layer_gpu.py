@@ -435,9 +435,16 @@ def test_head_sigmoid(dev, xt, orc, nb, nt):
                           xt.ptr(_d(hb, dev)), xt.ptr(d_out), nb, nt, _st()), "eva_k_head")
     logit = orc.gemm_rr_f64_rows(qa, sa, qw, sw, nt, np.arange(nb))
     ref = 1.0 / (1.0 + np.exp(-(logit + hb)))
-    err = np.abs(d_out.cpu().numpy() - ref).max()
-    _say(f"  sigmoid max |err| {err:.2e}")
-    assert err < 1e-4
+    err = np.abs(d_out.cpu().numpy() - ref)
+    # the matrix core's fp32 sums sit within ~1e-5 of the terms of fp64; sigmoid' <= 1/4. The x30 rows have terms
+    # ~1500, the others ~50 (sigmoid within 1e-4 there, as the forward's head)
+    lut = orc.E4M3_LUT.astype(np.float64)
+    terms = (np.abs(lut[qa]) * np.repeat(sa.T, 128, 1)) @ (np.abs(lut[qw]) * np.repeat(sw.T, 128, 1)).T
+    big = np.zeros(nt, bool)
+    big[::97] = True
+    _say(f"  sigmoid max |err| {err[:, ~big].max():.2e} (ordinary rows), {err[:, big].max():.2e} (x30 rows)")
+    assert err[:, ~big].max() < 1e-4
+    assert (err <= 0.25 * 2e-5 * terms + 1e-6).all()
 
 
 def test_patch_embed(dev, xt, orc):
