@@ -202,6 +202,15 @@ size_t eva_img_prep_bytes(uint32_t S, uint32_t max_side);
  * picks, or normalised as is when the rect's long side on that level is S. The 4 pad halves of each patch row are 0. */
 int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S, void *scratch,
                  size_t bytes, void *out, void *stream);
+/* eva_img_prep that allocates nothing and takes no scratch argument. No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops). The vertical pass is staged in a
+ * library-owned device array of EVA_IMG_STATIC_BYTES on each GPU it runs on (held until the process ends; its address
+ * is looked up on the first call on each device): rects whose chosen level needs more than that (S x rect width on
+ * the level x 16 bytes, i.e. the long side on the level below 4 S - 1 at S = 448) fail with -1. All calls on one GPU
+ * share the array: calls that overlap in time on that GPU race, so issue them on one stream. */
+#define EVA_IMG_STATIC_BYTES ((size_t)448 * (4 * 448 - 1) * 16)
+int eva_img_prep_static(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S, void *out,
+                        void *stream);
 
 /* ---- PixAI tagger engine (px.h:110-494): the ViTDet-L forward on the px_k_* kernels below ---- */
 #define PX_NB 4                               /* default model inputs per launch (px.h:21; even) */

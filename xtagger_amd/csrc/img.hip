@@ -14,6 +14,8 @@
 // Each block builds the tap tables it needs (pi_axis) in shared memory: every tap weight in parallel, each output's sum
 // over its taps in the reference's order by one thread.
 // A rect whose long side is S skips the resample (pi_idrow): k_img_ident normalises and white-pads the band directly.
+#include <pthread.h>
+
 #include "xt_abi.h"
 #include "xtag_eva.h"
 
@@ -325,14 +327,15 @@ extern "C" size_t eva_img_prep_bytes(uint32_t S, uint32_t max_side)
     return img_scratch(S, max_side);
 }
 
-extern "C" int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S,
-                            void *scratch, size_t bytes, void *out, void *stream)
+// pi_prep with the vertical pass staged in `scratch` (bytes long); what names the entry point in errors
+static int img_prep(const char *what, const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S,
+                    void *scratch, size_t bytes, void *out, void *stream)
 {
     if (!S) S = EVA_S;
-    if (!p || !p->nlv || p->nlv > EVA_PYR_LV || !p->lv[0]) return xt_fail("eva_img_prep", "no pyramid");
+    if (!p || !p->nlv || p->nlv > EVA_PYR_LV || !p->lv[0]) return xt_fail(what, "no pyramid");
     if (S % 14 || S > 1008 || !out || ((uintptr_t)out & 15))
-        return xt_fail("eva_img_prep", "S must be a multiple of 14 up to 1008; out 16-byte aligned");
-    if (!cw || !ch || x0 >= p->lw[0] || y0 >= p->lh[0]) return xt_fail("eva_img_prep", "empty or outside rect");
+        return xt_fail(what, "S must be a multiple of 14 up to 1008; out 16-byte aligned");
+    if (!cw || !ch || x0 >= p->lw[0] || y0 >= p->lh[0]) return xt_fail(what, "empty or outside rect");
     // pi_level + pi_lsrc (procimg.h:691-716)
     uint32_t L = 0;
     const uint32_t side0 = cw > ch ? cw : ch;
@@ -353,15 +356,56 @@ extern "C" int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t
     hipStream_t st = (hipStream_t)stream;
     if (side == S) {
         hipLaunchKernelGGL(k_img_ident, bands, dim3(256), 0, st, src, stride, cw, ch, S, (uint16_t *)out);
-        return xt_check("eva_img_prep");
+        return xt_check(what);
     }
     const uint32_t mt = img_mt(side, S);
-    if (mt > IMG_MT_MAX) return xt_fail("eva_img_prep", "rect more than 5x the model side on its level");
+    if (mt > IMG_MT_MAX) return xt_fail(what, "rect more than 5x the model side on its level");
     if (!scratch || bytes < img_scratch(S, cw) || ((uintptr_t)scratch & 15))
-        return xt_fail("eva_img_prep", "scratch must be 16-byte aligned and hold eva_img_prep_bytes(S, side)");
+        return xt_fail(what, "scratch must be 16-byte aligned and hold S x (rect width on its level) x 16 bytes "
+                             "(eva_img_prep_bytes(S, side); EVA_IMG_STATIC_BYTES for eva_img_prep_static)");
     float4 *tmp = (float4 *)scratch;
     hipLaunchKernelGGL(k_img_vpass, dim3((cw + 255) / 256, S), dim3(256), 0, st, src, stride, cw, ch, S, side, mt, tmp);
     hipLaunchKernelGGL(k_img_hpass, bands, dim3(14 * 14 * IMG_BAND_P), 0, st, (const float4 *)tmp, cw, S, side, mt,
                        (uint16_t *)out);
-    return xt_check("eva_img_prep");
+    return xt_check(what);
+}
+
+extern "C" int eva_img_prep(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S,
+                            void *scratch, size_t bytes, void *out, void *stream)
+{
+    return img_prep("eva_img_prep", p, x0, y0, cw, ch, S, scratch, bytes, out, stream);
+}
+
+// ---- eva_img_prep without a scratch argument, for callers that cannot allocate. The vertical pass is staged in
+// img_static, a file-scope device array (one copy per GPU, held until the process ends). In host code the array's name
+// is only a stand-in: its device address on the current GPU comes from hipGetSymbolAddress, taken once per device on
+// that device's first call and kept in img_static_dev. Every element the horizontal pass reads was written by the
+// vertical pass of the same call, so nothing needs clearing between calls; calls that overlap on one GPU race.
+static __device__ __align__(256) uint8_t img_static[EVA_IMG_STATIC_BYTES];
+#define IMG_MAX_DEVICES 64
+static void *img_static_dev[IMG_MAX_DEVICES];
+static pthread_mutex_t img_static_mu = PTHREAD_MUTEX_INITIALIZER;
+
+static void *img_static_addr(int dev)
+{
+    void *ptr;
+    pthread_mutex_lock(&img_static_mu);
+    ptr = img_static_dev[dev];
+    if (!ptr) {
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(img_static)) != hipSuccess) ptr = NULL;
+        img_static_dev[dev] = ptr;
+    }
+    pthread_mutex_unlock(&img_static_mu);
+    return ptr;
+}
+
+extern "C" int eva_img_prep_static(const eva_pyr *p, uint32_t x0, uint32_t y0, uint32_t cw, uint32_t ch, uint32_t S,
+                                   void *out, void *stream)
+{
+    int dev;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= IMG_MAX_DEVICES)
+        return xt_fail("eva_img_prep_static", "no current device");
+    void *ptr = img_static_addr(dev);
+    if (!ptr) return xt_fail("eva_img_prep_static", "hipGetSymbolAddress of the static scratch failed");
+    return img_prep("eva_img_prep_static", p, x0, y0, cw, ch, S, ptr, EVA_IMG_STATIC_BYTES, out, stream);
 }

@@ -81,6 +81,7 @@ _SIGS = {
     "eva_img_pyramid": (_i, [_p, _p, C.c_size_t, _u32, _p]),
     "eva_img_prep_bytes": (C.c_size_t, [_u32, _u32]),
     "eva_img_prep": (_i, [_p, _u32, _u32, _u32, _u32, _u32, _p, C.c_size_t, _p, _p]),
+    "eva_img_prep_static": (_i, [_p, _u32, _u32, _u32, _u32, _u32, _p, _p]),
     "eva_probe_mfma_fp8": (_i, [_i, _i, _p, _p]),
     "eva_probe_copy": (_i, [_p, _p, C.c_size_t, _p]),
     "eva_probe_lds": (_i, [_i, _i, _p, _p]),
