@@ -310,6 +310,21 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
     }
 }
 
+// Kernel arguments first used after the main loop (epilogue outputs) are read by scalar loads the compiler may leave in
+// flight up to the loop. Scalar loads complete out of order, so with one pending at the loop header the compiler can
+// no longer count LDS reads exactly and waits for every fragment read of a step (lgkmcnt(0)) before its first MFMA.
+// Naming the arguments here, before the loop, makes the compiler load them and wait for the loads first.
+template <class T>
+__device__ __forceinline__ void arg_resident(T a)
+{
+    asm volatile("" ::"s"(a));
+}
+template <class... T>
+__device__ __forceinline__ void args_resident(T... a)
+{
+    (arg_resident(a), ...);
+}
+
 struct BsNoPre {
     __device__ __forceinline__ void operator()() const {}
 };

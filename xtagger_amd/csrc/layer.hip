@@ -28,6 +28,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 3 * XT_D, m0, n0);
+    args_resident(cs, q, k, vt, lds, rows);
     layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
@@ -116,6 +117,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, XT_D, m0, n0);
+    args_resident(x, lds, rows);
     layer_mainloop<C, SP>(a8, XT_D, as, lds, w, wx, ws, rows, XT_D, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows);
@@ -145,6 +147,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 2 * XT_HIDP, m0, n0);
+    args_resident(m8, ms, stat, lds, rows);
     layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
@@ -264,6 +267,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
             cd[threadIdx.x - C::BM] = make_float2(cn[n], dn[n]);
         }
     };
+    args_resident(x, stat, cn, dn, lds, rows);
     layer_mainloop<C, SP>(m8, XT_HIDP, ms, lds, w, wx, ws, rows, XT_D, XT_HIDP, m0, n0, smem, acc, rowstats);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;

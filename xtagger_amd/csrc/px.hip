@@ -60,6 +60,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_qkv(const uint8_t *__restri
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 3 * XT_D, m0, n0);
+    args_resident(bias, cs, q, k, vt, L, lds, rows);
     layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
@@ -154,6 +155,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_res(const uint8_t *__restri
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, XT_D, m0, n0);
+    args_resident(bias, x, lds, rows);
     layer_mainloop<C, SP>(a8, K, as, lds, w, wx, ws, rows, XT_D, K, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int c16 = threadIdx.x & 15;
@@ -184,6 +186,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restri
     v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, PX_HID, m0, n0);
+    args_resident(bias, rs, m8, ms, lds, rows);
     layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, PX_HID, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int blk = (n0 + wn0) >> 7;

@@ -130,6 +130,7 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
     tile_of_block((M + C::BM - 1) / C::BM, (N + C::BN - 1) / C::BN, tm, tn);
     const int m0 = tm * C::BM, n0 = tn * C::BN, lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int Npad = (N + 127) & ~127;
+    args_resident(Cp, ldc, N, M, lds);
     if constexpr (SP) bs_mainloop_sp<C>(A, lda, sa, lds, W, WX, sw, M, Npad, K, m0, n0, smem, acc);
     else bs_mainloop<C>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
     int wm0, wn0;
