@@ -56,9 +56,11 @@ typedef struct {
 
 /* eva.h:573. Reads the weight blob header and starts the device bring-up on its own thread. The blob is the
  * reference's "EVA2" version-2 file (fp16 block weights, export_eva.py without a calibration file); the bring-up
- * packs every block GEMM weight to E4M3 with 128x128 scales on the GPU, so no calibration pass is needed.
- * pool / poolb: the caller's input pool (page-locked at bring-up; may be NULL). extra: head rows past the file's
- * tags (tag stealing), written with eva_head_put. Batch EVA_NB. */
+ * packs every block GEMM weight to E4M3 with 128x128 scales on the GPU (each layer as soon as its bytes are on the
+ * device, while the host reads the next), so no calibration pass is needed. pool / poolb: accepted and unused (the
+ * reference page-locks the caller's pool in place, eva.h:522; this platform cannot register existing memory, so
+ * eva_submit stages inputs in engine-owned pinned memory instead). extra: head rows past the file's tags (tag
+ * stealing), written with eva_head_put. Batch EVA_NB. */
 int eva_open(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra);
 /* eva_open with the batch (model inputs per launch, 1..EVA_NBMAX) as a runtime parameter */
 int eva_open_nb(eva *e, const char *weights, int device, void *pool, size_t poolb, uint32_t extra, uint32_t nb);
@@ -71,11 +73,15 @@ int eva_open_ex(eva *e, const char *weights, int device, void *pool, size_t pool
 int eva_ready(eva *e);                                              /* eva.h:607 */
 int eva_poll(eva *e);                                               /* eva.h:620 */
 /* eva.h:627. n <= nb inputs, each an fp16 [1024][592] patch operand (BGR in [-1,1], element c*196 + ky*14 + kx,
- * columns 588..591 zero); buf < EVA_NBUF. Runs of inputs adjacent in memory go in one copy. */
+ * columns 588..591 zero); buf < EVA_NBUF. The inputs are copied into buf's own pinned staging slot (runs of inputs
+ * adjacent in memory in one host copy) before the call returns, so the caller may reuse them at once; the call waits
+ * only for buf's previous batch, never for batches on other bufs (up to EVA_NBUF in flight). */
 int eva_submit(eva *e, uint32_t buf, uint16_t *const *in, uint32_t n);
 int eva_query(eva *e, uint32_t buf);                                /* eva.h:662 */
 const float *eva_wait(eva *e, uint32_t buf);                        /* eva.h:667: scores [n][nt] */
-int eva_head_put(eva *e, uint32_t j, const uint16_t *w, float bias); /* eva.h:645: head row j, fp16 [1024] */
+/* eva.h:645: head row j, fp16 [1024], and its bias. Stream-ordered: batches submitted after the call see the row; w
+ * is copied before the call returns. Only row j is repacked (each head row has its own scales). */
+int eva_head_put(eva *e, uint32_t j, const uint16_t *w, float bias);
 int eva_head_get(eva *e, uint16_t *w, float *bias);                 /* eva.h:653: the file's nt0 rows */
 void eva_close(eva *e);                                             /* eva.h:704 */
 
@@ -230,7 +236,7 @@ typedef struct {
 } px;
 /* px.h:357. Reads the "PXAI" header and starts the bring-up on its own thread. The blob is version 2
  * (export_pixai.py without a calibration file: fp16 block weights), packed to E4M3 with 128x128 scales on the GPU at
- * bring-up. pool / poolb are accepted and unused (inputs are staged into engine-owned pinned memory). */
+ * bring-up. pool / poolb are accepted and unused (inputs are staged into a pinned slot per buf, as eva_submit). */
 int px_open(px *p, const char *weights, int device, void *pool, size_t poolb);
 /* px_open with the batch (even, 2..100: token rows stay within the kernels' 2^19) as a runtime parameter */
 int px_open_nb(px *p, const char *weights, int device, void *pool, size_t poolb, uint32_t nb);

@@ -304,3 +304,41 @@ def test_truncated_blob_fails_at_ready(dev, tmp_path, synth_blob):
     with pytest.raises(RuntimeError):
         e.ready()
     e.close()
+
+
+def test_submit_ring_nonblocking(dev, synth_blob):
+    """eva.h:627-680: up to EVA_NBUF batches are in flight at once. Eight eva_submit calls on bufs 0..7 with distinct
+    inputs return while the GPU is still busy with the earlier batches (each waits only for its own buf's previous
+    batch), and every buf's scores equal those of the same inputs submitted one at a time."""
+    import time
+    from xtagger_amd import blob
+    from xtagger_amd.engine import Engine
+    path, m = synth_blob
+    nb = 4
+    e = Engine(path, device=0, nb=nb)
+    e.ready()
+    inp = blob.synth_inputs(8 * nb, seed=77).reshape(8, nb, 1024, 592)
+    ref = []
+    for b in range(8):                                          # one at a time
+        e.submit(b, inp[b])
+        ref.append(e.wait(b, nb))
+    t_batch = []
+    for _ in range(2):                                          # the time of one forward, measured here
+        t0 = time.perf_counter()
+        e.submit(0, inp[0])
+        e.wait(0, nb)
+        t_batch.append(time.perf_counter() - t0)
+    t_one = min(t_batch)
+    t0 = time.perf_counter()
+    for b in range(8):
+        e.submit(b, inp[b])
+    t_submit = time.perf_counter() - t0
+    pending = [e.query(b) for b in range(8)]
+    got = [e.wait(b, nb) for b in range(8)]
+    e.close()
+    _say(f"  one forward {t_one * 1e3:.2f} ms, 8 submits returned in {t_submit * 1e3:.2f} ms, done right after: {pending}")
+    # a submit that waited for the stream would find every earlier batch done and take about 7 forwards in all
+    assert sum(pending[:7]) < 7, "every earlier batch was done when the eighth submit returned"
+    assert t_submit < 5 * t_one, "the submits waited for the GPU"
+    for b in range(8):
+        assert np.array_equal(got[b], ref[b]), f"buf {b}"

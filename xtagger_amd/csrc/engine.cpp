@@ -11,11 +11,11 @@
 #include <vector>
 
 #include "xt_abi.h"
+#include "xt_stream.h"
 #include "xtag_eva.h"
 
 
 #define V2_HIDP 2736          // hidden padding of the reference's v2 blob (export_eva.py:19)
-#define EVA_CHUNK (32u << 20) // weight streaming chunk (eva.h:59)
 #define EVA_HB_OFF (-16.0f)   // bias of an extra head row nothing has written (eva.h:69)
 #define EV_HPUT_SLOTS 256     // eva_head_put rows staged at once before a call waits for the oldest copy
 #define EV_HPUT_SLOT 2304     // bytes per slot: 1024 fp16 weights, then the fp32 bias (256-byte multiple)
@@ -27,6 +27,7 @@ struct Layer {
     float *sqkv, *so, *s12, *s2, *cn, *dn;
     uint8_t *vqkv, *vo, *v12, *v2;                         // EVA_SPARSE24: pack24 values of the pruned weights
     uint32_t *xqkv, *xo, *x12, *x2;                        // and their indices
+    size_t end;                                            // blob offset past the layer's last tensor
 };
 
 struct eva_impl {
@@ -57,7 +58,7 @@ struct eva_impl {
     float *sh, *sm, *stat, *pool, *ps, *out;
     hipGraphExec_t graph;
     hipEvent_t done[EVA_NBUF];
-    uint16_t *stage;                                       // pinned staging for inputs (nb inputs)
+    uint16_t *stage[EVA_NBUF];                             // pinned staging of each buf's inputs (at its first submit)
     std::vector<void *> allocs;
 };
 
@@ -104,6 +105,7 @@ static int ev_layout(eva_impl *E, uint32_t ntp)
         L.mlnw = (const float *)take(V2_HIDP * 4);
         L.mlnb = (const float *)take(V2_HIDP * 4);
         L.w216 = (const uint16_t *)take((size_t)EVA_D * V2_HIDP * 2);
+        L.end = off;
     }
     E->fnw = (const float *)take(EVA_D * 4);
     E->fnb = (const float *)take(EVA_D * 4);
@@ -114,38 +116,6 @@ static int ev_layout(eva_impl *E, uint32_t ntp)
         return -1;
     }
     return 0;
-}
-
-// file bytes [256, 256 + wbytes) -> device, through two pinned chunks (eva.h:343-376)
-static int ev_stream_weights(eva_impl *E)
-{
-    FILE *f = fopen(E->path, "rb");
-    void *buf[2] = {NULL, NULL};
-    hipEvent_t ev[2] = {NULL, NULL};
-    size_t off = 0, n;
-    int i = 0, rc = -1;
-
-    if (!f) return xt_fail("weights", "cannot open");
-    if (fseek(f, 256, SEEK_SET)) goto out;
-    for (int j = 0; j < 2; j++)
-        if (hipHostMalloc(&buf[j], EVA_CHUNK, hipHostMallocDefault) != hipSuccess || hipEventCreate(&ev[j]) != hipSuccess)
-            goto out;
-    for (off = 0; off < E->wbytes; off += n, i ^= 1) {
-        n = E->wbytes - off < EVA_CHUNK ? E->wbytes - off : EVA_CHUNK;
-        if (hipEventSynchronize(ev[i]) != hipSuccess || fread(buf[i], 1, n, f) != n) goto out;
-        if (hipMemcpyAsync(E->blob + off, buf[i], n, hipMemcpyHostToDevice, E->st) != hipSuccess) goto out;
-        if (hipEventRecord(ev[i], E->st) != hipSuccess) goto out;
-    }
-    if (hipStreamSynchronize(E->st) == hipSuccess) rc = 0;
-out:
-    (void)hipStreamSynchronize(E->st);
-    for (int j = 0; j < 2; j++) {
-        if (ev[j]) (void)hipEventDestroy(ev[j]);
-        if (buf[j]) (void)hipHostFree(buf[j]);
-    }
-    fclose(f);
-    if (rc) fprintf(stderr, "eva: cannot stream weights from %s\n", E->path);
-    return rc;
 }
 
 // The whole forward for nb inputs on E->st (captured once into E->graph), eva.h:227-310.
@@ -185,19 +155,42 @@ static int ev_pack_head_rows(eva *e, uint32_t r0, uint32_t n)
                            E->hs + r0, (int)E->ldh, (void *)E->st);
 }
 
+// bring-up packing of layer i from its fp16 tensors in the blob (export_eva.py:52-119 on the GPU), on E->st
+static int ev_pack_layer(eva_impl *E, int i)
+{
+    Layer &L = E->L[i];
+    void *st = (void *)E->st;
+    EV_CK(eva_k_prep_w(L.wqkv16, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, NULL, E->scratch, L.wqkv, L.sqkv, st));
+    EV_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
+    EV_CK(eva_k_prep_w(L.w1216, EVA_D, 2 * V2_HIDP, EVA_D, 2 * EVA_HIDP, EVA_D, 0, NULL, E->scratch, L.w12, L.s12, st));
+    EV_CK(eva_k_prep_w(L.w216, V2_HIDP, EVA_D, EVA_HID, EVA_D, EVA_HIDP, 0, L.mlnw, E->scratch, L.w2, L.s2, st));
+    if (E->flags & EVA_SPARSE24) {
+        // 2:4 magnitude pruning of the packed E4M3 weights (prune24.py "mag"); the fold term c below then sums the
+        // pruned W~, which keeps the folded LayerNorm exact for the weights the GEMM uses
+        struct { uint8_t *w; int n, k; uint8_t *v; uint32_t *x; } sw[4] = {
+            {L.wqkv, 3 * EVA_D, EVA_D, L.vqkv, L.xqkv}, {L.wo, EVA_D, EVA_D, L.vo, L.xo},
+            {L.w12, 2 * EVA_HIDP, EVA_D, L.v12, L.x12}, {L.w2, EVA_D, EVA_HIDP, L.v2, L.x2}};
+        for (auto &t : sw) {
+            EV_CK(eva_k_prune24(t.w, t.n, t.k, st));
+            EV_CK(eva_k_pack24(t.w, t.n, t.k, t.v, t.x, NULL, st));
+        }
+    }
+    EV_CK(eva_k_fold_cd(L.w2, L.s2, L.w216, V2_HIDP, L.mlnb, L.cn, L.dn, st));
+    return 0;
+}
+
 static int ev_up(eva *e)
 {
     eva_impl *E = e->impl;
     const uint32_t ntp = (e->nt0 + 7) & ~7u, nt = e->nt;
-    void *st;
 
     XT_HIP(hipSetDevice(E->devno));
     XT_HIP(hipStreamCreateWithFlags(&E->st, hipStreamNonBlocking));
-    st = (void *)E->st;
     EV_ALLOC(E, E->blob, E->wbytes, false);
-    if (ev_stream_weights(E) || ev_layout(E, ntp)) return -1;
+    if (ev_layout(E, ntp)) return -1;
 
-    // packed weights (bring-up packing on the GPU)
+    // packed weights: every layer is packed on the GPU (bring-up packing) as soon as its bytes are on the device, while
+    // the host still reads the layers after it (eva.h:343-376, 452 stream on a thread of their own)
     EV_ALLOC(E, E->scratch, (size_t)2 * EVA_HIDP * EVA_D * 4, false);
     for (int i = 0; i < EVA_NL; i++) {
         Layer &L = E->L[i];
@@ -211,24 +204,26 @@ static int ev_up(eva *e)
         EV_ALLOC(E, L.s2, 8 * 22 * 4, false);
         EV_ALLOC(E, L.cn, EVA_D * 4, false);
         EV_ALLOC(E, L.dn, EVA_D * 4, false);
-        EV_CK(eva_k_prep_w(L.wqkv16, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, NULL, E->scratch, L.wqkv, L.sqkv, st));
-        EV_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
-        EV_CK(eva_k_prep_w(L.w1216, EVA_D, 2 * V2_HIDP, EVA_D, 2 * EVA_HIDP, EVA_D, 0, NULL, E->scratch, L.w12, L.s12, st));
-        EV_CK(eva_k_prep_w(L.w216, V2_HIDP, EVA_D, EVA_HID, EVA_D, EVA_HIDP, 0, L.mlnw, E->scratch, L.w2, L.s2, st));
         if (E->flags & EVA_SPARSE24) {
-            // 2:4 magnitude pruning of the packed E4M3 weights (prune24.py "mag"); the fold term c below then sums
-            // the pruned W~, which keeps the folded LayerNorm exact for the weights the GEMM uses
-            struct { uint8_t *w; int n, k; uint8_t **v; uint32_t **x; } sw[4] = {
-                {L.wqkv, 3 * EVA_D, EVA_D, &L.vqkv, &L.xqkv}, {L.wo, EVA_D, EVA_D, &L.vo, &L.xo},
-                {L.w12, 2 * EVA_HIDP, EVA_D, &L.v12, &L.x12}, {L.w2, EVA_D, EVA_HIDP, &L.v2, &L.x2}};
-            for (auto &t : sw) {
-                EV_CK(eva_k_prune24(t.w, t.n, t.k, st));
-                EV_ALLOC(E, *t.v, (size_t)t.n * t.k / 2, false);
-                EV_ALLOC(E, *t.x, (size_t)t.n * t.k / 8, false);
-                EV_CK(eva_k_pack24(t.w, t.n, t.k, *t.v, *t.x, NULL, st));
-            }
+            EV_ALLOC(E, L.vqkv, (size_t)3 * EVA_D * EVA_D / 2, false);
+            EV_ALLOC(E, L.xqkv, (size_t)3 * EVA_D * EVA_D / 8, false);
+            EV_ALLOC(E, L.vo, (size_t)EVA_D * EVA_D / 2, false);
+            EV_ALLOC(E, L.xo, (size_t)EVA_D * EVA_D / 8, false);
+            EV_ALLOC(E, L.v12, (size_t)2 * EVA_HIDP * EVA_D / 2, false);
+            EV_ALLOC(E, L.x12, (size_t)2 * EVA_HIDP * EVA_D / 8, false);
+            EV_ALLOC(E, L.v2, (size_t)EVA_D * EVA_HIDP / 2, false);
+            EV_ALLOC(E, L.x2, (size_t)EVA_D * EVA_HIDP / 8, false);
         }
-        EV_CK(eva_k_fold_cd(L.w2, L.s2, L.w216, V2_HIDP, L.mlnb, L.cn, L.dn, st));
+    }
+    int packed = 0;
+    auto pack_ready = [&](size_t bytes) -> int {
+        for (; packed < EVA_NL && E->L[packed].end <= bytes; packed++)
+            if (ev_pack_layer(E, packed)) return -1;
+        return 0;
+    };
+    if (xt_stream_file(E->path, 256, E->blob, E->wbytes, E->st, pack_ready) || packed != EVA_NL) {
+        fprintf(stderr, "eva: cannot stream weights from %s\n", E->path);
+        return -1;
     }
     // head: fp16 master (file rows, then zero extra rows with bias -16), every row packed with its own scales
     E->ldh = (nt + 63) & ~63u;
@@ -265,7 +260,6 @@ static int ev_up(eva *e)
     EV_ALLOC(E, E->ps, 8 * nb * 4, true);
     EV_ALLOC(E, E->out, nb * nt * 4, true);
     (void)M;
-    XT_HIP(hipHostMalloc((void **)&E->stage, nb * EVA_IN * 2, hipHostMallocDefault));
     for (int s = 0; s < EVA_NBUF; s++) {
         XT_HIP(hipHostMalloc((void **)&e->hout[s], nb * nt * 4, hipHostMallocDefault));
         if (nt > e->nt0) XT_HIP(hipHostMalloc((void **)&e->hpn[s], nb * EVA_D * 2, hipHostMallocDefault));
@@ -370,10 +364,13 @@ extern "C" int eva_submit(eva *e, uint32_t buf, uint16_t *const *in, uint32_t n)
     if (eva_ready(e)) return -1;
     eva_impl *E = e->impl;
     if (buf >= EVA_NBUF || n > E->nb) return xt_fail("eva_submit", "buf >= EVA_NBUF or n > nb");
-    // inputs staged into engine-owned pinned memory (this platform does not page-lock caller memory in place)
-    XT_HIP(hipStreamSynchronize(E->st));
-    for (uint32_t i = 0; i < n; i++) memcpy(E->stage + (size_t)i * EVA_IN, in[i], EVA_IN * 2);
-    if (n) XT_HIP(hipMemcpyAsync(E->in, E->stage, (size_t)n * EVA_IN * 2, hipMemcpyHostToDevice, E->st));
+    // Every buf stages its inputs in a pinned slot of its own (this platform cannot page-lock the caller's memory in
+    // place, eva.h:522). Before refilling it, only the previous batch of the same buf must be done (its input copy
+    // has then left the slot): batches on the other bufs stay queued on the GPU (eva.h:627-641).
+    if (!E->stage[buf]) XT_HIP(hipHostMalloc((void **)&E->stage[buf], (size_t)E->nb * EVA_IN * 2, hipHostMallocDefault));
+    else XT_HIP(hipEventSynchronize(E->done[buf]));
+    xt_stage_inputs(E->stage[buf], in, n, EVA_IN);
+    if (n) XT_HIP(hipMemcpyAsync(E->in, E->stage[buf], (size_t)n * EVA_IN * 2, hipMemcpyHostToDevice, E->st));
     XT_HIP(hipGraphLaunch(E->graph, E->st));
     if (n) XT_HIP(hipMemcpyAsync(e->hout[buf], E->out, (size_t)n * e->nt * 4, hipMemcpyDeviceToHost, E->st));
     if (e->hpn[buf] && n) XT_HIP(hipMemcpyAsync(e->hpn[buf], E->pn, (size_t)n * EVA_D * 2, hipMemcpyDeviceToHost, E->st));
@@ -441,7 +438,8 @@ extern "C" void eva_close(eva *e)
         if (e->hout[s]) (void)hipHostFree(e->hout[s]);
         if (e->hpn[s]) (void)hipHostFree(e->hpn[s]);
     }
-    if (E->stage) (void)hipHostFree(E->stage);
+    for (int s = 0; s < EVA_NBUF; s++)
+        if (E->stage[s]) (void)hipHostFree(E->stage[s]);
     if (E->hput) (void)hipHostFree(E->hput);
     for (int s = 0; s < EV_HPUT_SLOTS; s++)
         if (E->hput_ev[s]) (void)hipEventDestroy(E->hput_ev[s]);

@@ -13,9 +13,9 @@
 #include <vector>
 
 #include "xt_abi.h"
+#include "xt_stream.h"
 #include "xtag_eva.h"
 
-#define PX_CHUNK (32u << 20)  // weight streaming chunk
 #define PX_PCH 144            // attention-pool token chunk (px_kernels.cu:446)
 
 struct PxLayer {
@@ -24,6 +24,7 @@ struct PxLayer {
     uint8_t *wqkv, *wo, *w1, *w2;                                       // packed E4M3
     float *sqkv, *so, *s1, *s2;
     const float *rs_fc1;                                                // rs, or NULL where the file's rs are all 1
+    size_t end;                                                         // blob offset past the layer's last tensor
 };
 
 struct px_impl {
@@ -47,7 +48,7 @@ struct px_impl {
     float *sh, *so8, *sm, *s, *part, *o, *oqs, *out;
     hipGraphExec_t graph;
     hipEvent_t done[PX_NBUF];
-    uint16_t *stage;
+    uint16_t *stage[PX_NBUF];                           // pinned staging of each buf's inputs (at its first submit)
     std::vector<void *> allocs;
 };
 
@@ -100,6 +101,7 @@ static int px_layout(px_impl *E, uint32_t ntp)
         L.rs = (const float *)take(PX_HID * 4);
         L.w216 = (const uint16_t *)take((size_t)EVA_D * PX_HID * 2);
         L.b2 = (const float *)take(EVA_D * 4);
+        L.end = off;
     }
     E->hnw = (const float *)take(EVA_D * 4);
     E->hnb = (const float *)take(EVA_D * 4);
@@ -113,38 +115,6 @@ static int px_layout(px_impl *E, uint32_t ntp)
         return -1;
     }
     return 0;
-}
-
-// file bytes [256, 256 + wbytes) -> device, through two pinned chunks (px.h:318-345)
-static int px_stream_weights(px_impl *E)
-{
-    FILE *f = fopen(E->path, "rb");
-    void *buf[2] = {NULL, NULL};
-    hipEvent_t ev[2] = {NULL, NULL};
-    size_t off = 0, n;
-    int i = 0, rc = -1;
-
-    if (!f) return xt_fail("weights", "cannot open");
-    if (fseek(f, 256, SEEK_SET)) goto out;
-    for (int j = 0; j < 2; j++)
-        if (hipHostMalloc(&buf[j], PX_CHUNK, hipHostMallocDefault) != hipSuccess || hipEventCreate(&ev[j]) != hipSuccess)
-            goto out;
-    for (off = 0; off < E->wbytes; off += n, i ^= 1) {
-        n = E->wbytes - off < PX_CHUNK ? E->wbytes - off : PX_CHUNK;
-        if (hipEventSynchronize(ev[i]) != hipSuccess || fread(buf[i], 1, n, f) != n) goto out;
-        if (hipMemcpyAsync(E->blob + off, buf[i], n, hipMemcpyHostToDevice, E->st) != hipSuccess) goto out;
-        if (hipEventRecord(ev[i], E->st) != hipSuccess) goto out;
-    }
-    if (hipStreamSynchronize(E->st) == hipSuccess) rc = 0;
-out:
-    (void)hipStreamSynchronize(E->st);
-    for (int j = 0; j < 2; j++) {
-        if (ev[j]) (void)hipEventDestroy(ev[j]);
-        if (buf[j]) (void)hipHostFree(buf[j]);
-    }
-    fclose(f);
-    if (rc) fprintf(stderr, "px: cannot stream weights from %s\n", E->path);
-    return rc;
 }
 
 // The whole forward for nb inputs on E->st (captured once into E->graph), px.h:110-190.
@@ -177,16 +147,52 @@ static int px_forward(px *p)
     return 0;
 }
 
+// bring-up packing of block i's GEMM weights from the blob's fp16 tensors, on E->st; q / k rows of Wqkv pair-split
+// for the RoPE epilogue
+static int px_pack_layer(px_impl *E, int i)
+{
+    PxLayer &L = E->L[i];
+    void *st = (void *)E->st;
+    PX_CK(eva_k_prep_w(L.wqkv16, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, NULL, E->scratch, L.wqkv, L.sqkv, st));
+    PX_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
+    PX_CK(eva_k_prep_w(L.w116, EVA_D, PX_HID, EVA_D, PX_HID, EVA_D, 0, NULL, E->scratch, L.w1, L.s1, st));
+    PX_CK(eva_k_prep_w(L.w216, PX_HID, EVA_D, PX_HID, EVA_D, PX_HID, 0, NULL, E->scratch, L.w2, L.s2, st));
+    return 0;
+}
+
 static int px_up(px *p)
 {
     px_impl *E = p->impl;
-    void *st;
 
     XT_HIP(hipSetDevice(E->devno));
     XT_HIP(hipStreamCreateWithFlags(&E->st, hipStreamNonBlocking));
-    st = (void *)E->st;
     PX_ALLOC(E, E->blob, E->wbytes, false);
-    if (px_stream_weights(E) || px_layout(E, p->ntp)) return -1;
+    if (px_layout(E, p->ntp)) return -1;
+
+    // packed weights: each block is packed on the GPU as soon as its bytes are on the device, while the host still
+    // reads the blocks after it
+    PX_ALLOC(E, E->scratch, (size_t)PX_HID * EVA_D * 4, false);
+    for (int i = 0; i < PX_NL; i++) {
+        PxLayer &L = E->L[i];
+        PX_ALLOC(E, L.wqkv, (size_t)3 * EVA_D * EVA_D, false);
+        PX_ALLOC(E, L.sqkv, 24 * 8 * 4, false);
+        PX_ALLOC(E, L.wo, (size_t)EVA_D * EVA_D, false);
+        PX_ALLOC(E, L.so, 8 * 8 * 4, false);
+        PX_ALLOC(E, L.w1, (size_t)PX_HID * EVA_D, false);
+        PX_ALLOC(E, L.s1, 37 * 8 * 4, false);
+        PX_ALLOC(E, L.w2, (size_t)EVA_D * PX_HID, false);
+        PX_ALLOC(E, L.s2, 8 * 37 * 4, false);
+    }
+    int packed = 0;
+    auto pack_ready = [&](size_t bytes) -> int {
+        for (; packed < PX_NL && E->L[packed].end <= bytes; packed++)
+            if (px_pack_layer(E, packed)) return -1;
+        return 0;
+    };
+    if (xt_stream_file(E->path, 256, E->blob, E->wbytes, E->st, pack_ready) || packed != PX_NL) {
+        fprintf(stderr, "px: cannot stream weights from %s\n", E->path);
+        return -1;
+    }
 
     // per-unit fc1 multipliers: a file without calibration holds ones (export_pixai.py:83), and multiplying by 1 is
     // exact, so fc1 then runs without the multiply
@@ -199,29 +205,11 @@ static int px_up(px *p)
         L.rs_fc1 = ones ? NULL : L.rs;
     }
 
-    // packed weights (bring-up packing on the GPU); q / k rows of Wqkv pair-split for the RoPE epilogue
-    const size_t scratch_f = (size_t)PX_HID * EVA_D;
-    PX_ALLOC(E, E->scratch, scratch_f * 4, false);
-    for (int i = 0; i < PX_NL; i++) {
-        PxLayer &L = E->L[i];
-        PX_ALLOC(E, L.wqkv, (size_t)3 * EVA_D * EVA_D, false);
-        PX_ALLOC(E, L.sqkv, 24 * 8 * 4, false);
-        PX_ALLOC(E, L.wo, (size_t)EVA_D * EVA_D, false);
-        PX_ALLOC(E, L.so, 8 * 8 * 4, false);
-        PX_ALLOC(E, L.w1, (size_t)PX_HID * EVA_D, false);
-        PX_ALLOC(E, L.s1, 37 * 8 * 4, false);
-        PX_ALLOC(E, L.w2, (size_t)EVA_D * PX_HID, false);
-        PX_ALLOC(E, L.s2, 8 * 37 * 4, false);
-        PX_CK(eva_k_prep_w(L.wqkv16, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, NULL, E->scratch, L.wqkv, L.sqkv, st));
-        PX_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
-        PX_CK(eva_k_prep_w(L.w116, EVA_D, PX_HID, EVA_D, PX_HID, EVA_D, 0, NULL, E->scratch, L.w1, L.s1, st));
-        PX_CK(eva_k_prep_w(L.w216, PX_HID, EVA_D, PX_HID, EVA_D, PX_HID, 0, NULL, E->scratch, L.w2, L.s2, st));
-    }
     // head: the file's fp16 rows, each packed with its own 1x128 scales
     E->ldh = (p->nt + 63) & ~63u;
     PX_ALLOC(E, E->hq, (size_t)p->nt * EVA_D, false);
     PX_ALLOC(E, E->hs, (size_t)8 * E->ldh * 4, true);
-    PX_CK(eva_k_quant_act(E->hw16, 2, EVA_D, (int)p->nt, EVA_D, E->hq, EVA_D, E->hs, (int)E->ldh, st));
+    PX_CK(eva_k_quant_act(E->hw16, 2, EVA_D, (int)p->nt, EVA_D, E->hq, EVA_D, E->hs, (int)E->ldh, (void *)E->st));
 
     // activations
     const size_t M = E->M, nb = E->nb;
@@ -244,7 +232,6 @@ static int px_up(px *p)
     PX_ALLOC(E, E->oq, nb * EVA_D, true);
     PX_ALLOC(E, E->oqs, 8 * nb * 4, true);
     PX_ALLOC(E, E->out, nb * p->nt * 4, true);
-    XT_HIP(hipHostMalloc((void **)&E->stage, nb * PX_IN * 2, hipHostMallocDefault));
     for (int s = 0; s < PX_NBUF; s++) {
         XT_HIP(hipHostMalloc((void **)&p->hout[s], nb * p->nt * 4, hipHostMallocDefault));
         XT_HIP(hipEventCreateWithFlags(&E->done[s], hipEventDisableTiming));
@@ -338,9 +325,11 @@ extern "C" int px_submit(px *p, uint32_t buf, uint16_t *const *in, uint32_t n)
     if (px_ready(p)) return -1;
     px_impl *E = p->impl;
     if (buf >= PX_NBUF || n > E->nb) return xt_fail("px_submit", "buf >= PX_NBUF or n > nb");
-    XT_HIP(hipStreamSynchronize(E->st));
-    for (uint32_t i = 0; i < n; i++) memcpy(E->stage + (size_t)i * PX_IN, in[i], PX_IN * 2);
-    if (n) XT_HIP(hipMemcpyAsync(E->in, E->stage, (size_t)n * PX_IN * 2, hipMemcpyHostToDevice, E->st));
+    // a pinned staging slot per buf: refilling it waits only for the previous batch of the same buf (px.h:406-419)
+    if (!E->stage[buf]) XT_HIP(hipHostMalloc((void **)&E->stage[buf], (size_t)E->nb * PX_IN * 2, hipHostMallocDefault));
+    else XT_HIP(hipEventSynchronize(E->done[buf]));
+    xt_stage_inputs(E->stage[buf], in, n, PX_IN);
+    if (n) XT_HIP(hipMemcpyAsync(E->in, E->stage[buf], (size_t)n * PX_IN * 2, hipMemcpyHostToDevice, E->st));
     XT_HIP(hipGraphLaunch(E->graph, E->st));
     if (n) XT_HIP(hipMemcpyAsync(p->hout[buf], E->out, (size_t)n * p->nt * 4, hipMemcpyDeviceToHost, E->st));
     XT_HIP(hipEventRecord(E->done[buf], E->st));
@@ -376,7 +365,8 @@ extern "C" void px_close(px *p)
         if (E->done[s]) (void)hipEventDestroy(E->done[s]);
         if (p->hout[s]) (void)hipHostFree(p->hout[s]);
     }
-    if (E->stage) (void)hipHostFree(E->stage);
+    for (int s = 0; s < PX_NBUF; s++)
+        if (E->stage[s]) (void)hipHostFree(E->stage[s]);
     for (void *ptr : E->allocs) (void)hipFree(ptr);
     if (E->st) (void)hipStreamDestroy(E->st);
     free(E->path);
