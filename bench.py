@@ -427,12 +427,12 @@ def bench_pixai_block(torch, L, nb=4, reps=10):
     L.check(L.lib.eva_k_quant_act(L.ptr(hw16), 2, D, nt, D, L.ptr(hw), D, L.ptr(hws), ldh, st()), "head pack")
     hb = torch.zeros(nt, device=dev)
     y, s = t(M, D, dt=torch.int16), t(M, 16, dt=torch.float32)
-    Pm, part = t(nb, 16, T5, dt=torch.int16), t(nb, T5 // 144, 16, D, dt=torch.float32)
+    stat, part = t(nb, T5 // 576, 16, 2, dt=torch.float32), t(nb, T5 // 288, 16, D, dt=torch.float32)
     o, oq, oqs, out = t(nb, D, dt=torch.float32), t(nb, D), t(8, nb, dt=torch.float32), t(nb, nt, dt=torch.float32)
     head = run(lambda: L.lib.px_k_hln(P(x), P(lng), P(lnb), P(hpos), T5, P(U), P(y), P(s), M, st()),
-               lambda: L.lib.px_k_hsoft(P(s), P(Pm), nb, T5, st()),
-               lambda: L.lib.px_k_hpool(P(Pm), P(y), P(part), nb, T5, st()),
-               lambda: L.lib.px_k_hv(P(part), T5 // 144, P(wv), P(o), nb, st()),
+               lambda: L.lib.px_k_hstat(P(s), P(stat), nb, T5, st()),
+               lambda: L.lib.px_k_hpool(P(s), P(stat), P(y), None, P(part), nb, T5, st()),
+               lambda: L.lib.px_k_hproj(P(part), T5 // 288, P(wv), P(o), nb, st()),
                lambda: L.lib.eva_k_quant_act(P(o), 1, D, nb, D, P(oq), D, P(oqs), nb, st()),
                lambda: L.lib.eva_k_head(P(oq), P(oqs), nb, P(hw), P(hws), ldh, P(hb), P(out), nb, nt, st()))
     res["pool_head_us"] = round(timed(head), 1)

@@ -283,13 +283,15 @@ int px_k_fc2(const void *m8, const float *ms, int lds, const void *w, const floa
  * s fp32 [rows][16] = U y (U fp32 [16][1024], exp2 domain). */
 int px_k_hln(const void *x, const float *g, const float *b, const void *hpos, int T, const float *U, void *y, float *s,
              int rows, void *stream);
-/* k_phsoft: P fp16 [nb][16][T] = softmax over the T tokens of each (image, head), exp2 domain */
-int px_k_hsoft(const float *s, void *P, int nb, int T, void *stream);
-/* k_phpool: part fp32 [nb][T/144][16][1024] = per 144-token chunk, sum_t P[b][h][t] y[b][t]; T % 144 == 0 */
-int px_k_hpool(const void *P, const void *y, float *part, int nb, int T, void *stream);
-/* k_phv: o [nb][1024] = f16(Wv[64 h + n] . pooled[b][h]) as fp32 values (pooled = the nch partials summed in order;
- * Wv fp16 [1024][1024]); the tag head follows as eva_k_quant_act(o, fp32) + eva_k_head. */
-int px_k_hv(const float *part, int nch, const void *wv, float *o, int nb, void *stream);
+/* k_phsoft + k_phpool + k_phv (px_kernels.cu:401-503) as three launches, T % 576 == 0 and T <= 9216:
+ * px_k_hstat: stat float2 [nb][T/576][16] = per 576-token window and head (max_t s, sum_t 2^(s - max));
+ * px_k_hpool: part fp32 [nb][T/288][16][1024] = per 288-token window, sum_t P[b][h][t] y[b][t], with P = f16 softmax
+ *   of s over all T tokens (exp2 domain) made from stat; P fp16 [nb][16][T] is also written when not NULL;
+ * px_k_hproj: o [nb][1024] = f16(Wv[64 h + n] . pooled[b][h]) as fp32 values (pooled = the nw = T/288 window partials
+ *   summed in window order; Wv fp16 [1024][1024]); the tag head follows as eva_k_quant_act(o, fp32) + eva_k_head. */
+int px_k_hstat(const float *s, float *stat, int nb, int T, void *stream);
+int px_k_hpool(const float *s, const float *stat, const void *y, void *P, float *part, int nb, int T, void *stream);
+int px_k_hproj(const float *part, int nw, const void *wv, float *o, int nb, void *stream);
 /* g[i] = u[i] Phi(u[i]) for n fp32 values by px_k_fc1's GELU (px_kernels.cu:228-229), for testing its accuracy */
 int px_probe_gelu(const float *u, float *g, int n, void *stream);
 

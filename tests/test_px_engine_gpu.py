@@ -66,15 +66,15 @@ def _chain(xt, m, d_in, nb, dev):
         ok(xt.lib.px_k_fc2(P(m8), P(ms), M, P(w2), P(s2), P(up(L["b2"])), P(x), M, st))
         torch.cuda.synchronize()
     y, s = z(M, D, dt=torch.int16), z(M, 16, dt=torch.float32)
-    Pm, part = z(nb, 16, T5, dt=torch.int16), z(nb, T5 // 144, 16, D, dt=torch.float32)
+    stat, part = z(nb, T5 // 576, 16, 2, dt=torch.float32), z(nb, T5 // 288, 16, D, dt=torch.float32)
     o, oq, oqs, out = z(nb, D, dt=torch.float32), z(nb, D), z(8, nb, dt=torch.float32), z(nb, NT, dt=torch.float32)
     ldh = (NT + 63) // 64 * 64
     hq, hsc = z(NT, D), z(8, ldh, dt=torch.float32)
     ok(xt.lib.eva_k_quant_act(P(up(m["hw"][:NT])), 2, D, NT, D, P(hq), D, P(hsc), ldh, st))
     ok(xt.lib.px_k_hln(P(x), P(up(m["hnw"])), P(up(m["hnb"])), P(up(m["hpos"])), T5, P(up(m["U"])), P(y), P(s), M, st))
-    ok(xt.lib.px_k_hsoft(P(s), P(Pm), nb, T5, st))
-    ok(xt.lib.px_k_hpool(P(Pm), P(y), P(part), nb, T5, st))
-    ok(xt.lib.px_k_hv(P(part), T5 // 144, P(up(m["wv"])), P(o), nb, st))
+    ok(xt.lib.px_k_hstat(P(s), P(stat), nb, T5, st))
+    ok(xt.lib.px_k_hpool(P(s), P(stat), P(y), None, P(part), nb, T5, st))
+    ok(xt.lib.px_k_hproj(P(part), T5 // 288, P(up(m["wv"])), P(o), nb, st))
     ok(xt.lib.eva_k_quant_act(P(o), 1, D, nb, D, P(oq), D, P(oqs), nb, st))
     ok(xt.lib.eva_k_head(P(oq), P(oqs), nb, P(hq), P(hsc), ldh, P(up(m["hb"])), P(out), nb, NT, st))
     torch.cuda.synchronize()

@@ -276,8 +276,8 @@ def test_px_block_chain_windowed(dev, xt, orc):
 
 def test_px_pool_head(dev, xt, orc):
     """The attention-pool head (px_kernels.cu:341-503) over 2 images of 5184 tokens, each kernel fed the previous
-    kernel's GPU output: LN + position (bit-exact) and scores, softmax over the tokens, chunked pooling and the
-    per-head value projection, then the tag head as eva_k_quant_act + eva_k_head."""
+    kernel's GPU output: LN + position (bit-exact) and scores, the per-window softmax statistics, P and the windowed
+    pooling on MFMA, the per-head value projection, then the tag head as eva_k_quant_act + eva_k_head."""
     nb, T = 2, T_IMG
     M = nb * T
     _say("px pool head nb=2")
@@ -299,19 +299,35 @@ def test_px_pool_head(dev, xt, orc):
     s = d_s.cpu().numpy()
     terms = np.abs(yf) @ np.abs(U.astype(np.float64)).T
     assert np.all(np.abs(s - s_ref) <= 2e-6 * terms)
-    # softmax over the tokens, from the kernel's own scores
+    # softmax over the tokens (window statistics, then P made inside the pooling kernel), from the kernel's own scores
+    nw = T // 576
+    d_stat = torch.zeros((nb, nw, 16, 2), dtype=torch.float32, device=dev)
     d_P = torch.zeros((nb, 16, T), dtype=torch.int16, device=dev)
-    _ok(xt.lib.px_k_hsoft(xt.ptr(d_s), xt.ptr(d_P), nb, T, _st()), "px_k_hsoft")
+    nq = T // 288
+    d_part = torch.zeros((nb, nq, 16, D), dtype=torch.float32, device=dev)
+    d_o = torch.zeros((nb, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.px_k_hstat(xt.ptr(d_s), xt.ptr(d_stat), nb, T, _st()), "px_k_hstat")
+    stat = d_stat.cpu().numpy().astype(np.float64)
+    sw = s.astype(np.float64).reshape(nb, nw, 576, 16)
+    m_ref = sw.max(axis=2)
+    assert (stat[..., 0] == m_ref).all()                                 # window maxima exact
+    l_ref = np.exp2(sw - m_ref[:, :, None, :]).sum(axis=2)
+    assert np.all(np.abs(stat[..., 1] - l_ref) <= 1e-5 * l_ref)
+    _ok(xt.lib.px_k_hpool(xt.ptr(d_s), xt.ptr(d_stat), xt.ptr(d_y), xt.ptr(d_P), xt.ptr(d_part), nb, T, _st()),
+        "px_k_hpool")
     P = d_P.cpu().numpy().view(np.uint16)
     Pf = P.view(np.float16).astype(np.float64)
     P_ref = orc.px_hsoft(s, nb, T)
     assert np.all(np.abs(Pf - P_ref) <= (2.0 ** -11 + 1e-5) * P_ref + 6e-8)
-    # pooling and the value projection, from the kernel's own P and y
-    nch = T // 144
-    d_part = torch.zeros((nb, nch, 16, D), dtype=torch.float32, device=dev)
-    d_o = torch.zeros((nb, D), dtype=torch.float32, device=dev)
-    _ok(xt.lib.px_k_hpool(xt.ptr(d_P), xt.ptr(d_y), xt.ptr(d_part), nb, T, _st()), "px_k_hpool")
-    _ok(xt.lib.px_k_hv(xt.ptr(d_part), nch, xt.ptr(_d(wv, dev)), xt.ptr(d_o), nb, _st()), "px_k_hv")
+    # the pooled partials of each window against float64 products of the kernel's own P and y
+    part = d_part.cpu().numpy().astype(np.float64)
+    yw = yf.reshape(nb, nq, 288, D)
+    Pw = Pf.reshape(nb, 16, nq, 288).transpose(0, 2, 1, 3)                 # [nb][nq][16][288]
+    part_ref = np.matmul(Pw, yw)
+    part_abs = np.matmul(Pw, np.abs(yw))
+    assert np.all(np.abs(part - part_ref) <= 8e-6 * part_abs + 1e-30)
+    # the value projection of the summed partials
+    _ok(xt.lib.px_k_hproj(xt.ptr(d_part), nq, xt.ptr(_d(wv, dev)), xt.ptr(d_o), nb, _st()), "px_k_hproj")
     o = d_o.cpu().numpy()
     assert (o.astype(np.float16).astype(np.float32) == o).all()         # fp16 values
     o_ref = orc.px_hpool_hv(P, y, nb, T, wv.view(np.uint16))

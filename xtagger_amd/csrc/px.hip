@@ -298,142 +298,241 @@ extern "C" int px_k_fc1(const void *h8, const float *hs, int lds, const void *w,
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Attention-pool head (px_kernels.cu:341-503): the scores s [nb T][16] of k_px_hln -> per (image, head) softmax over
-// the T tokens -> pooled = P y -> o = Wv pooled per head; the tag head is then eva_k_quant_act + eva_k_head.
+// Attention-pool head (px_kernels.cu:341-503, px.h:170-189): the scores s [nb T][16] of k_px_hln (exp2 domain) ->
+// per (image, head) softmax weights over the T tokens, rounded to fp16 as the reference's P -> pooled = P y per head
+// -> o = Wv pooled per head. Three launches, each over the whole batch:
+//   k_px_hstat  (image, 576-token window): each head's maximum over the window and sum of 2^(s - maximum)
+//   k_px_hpool  (image, 288-token window, 128 columns of y) per wave: P made in registers from s and the merged
+//               statistics; P y on v_mfma_f32_16x16x32_f16, the 16 heads being the MFMA's 16 rows, eight 16 x 16
+//               output tiles per wave -> an fp32 partial per window
+//   k_px_hproj  (head, 2 images): the window partials summed in window order, then the head's value projection,
+//               fp16 result
+// Every sum runs in an order fixed by the launch shape, so results repeat bit for bit. The tag head follows as
+// eva_k_quant_act + eva_k_head.
 // ---------------------------------------------------------------------------------------------------------------
-#define PX_PCH 144  // tokens per pooling chunk (px_kernels.cu:446 PCH)
+constexpr int PX_PW = 576;  // tokens per statistics window
 
-// k_px_hsoft (k_phsoft, 406-440): P [nb][16][T] fp16 = 2^(s - max) / sum, one block of 256 threads per (image, head);
-// the maximum and the sum run per thread in token order, then through the wave butterfly and the 4 waves in order.
-__global__ void __launch_bounds__(256) k_px_hsoft(const float *__restrict__ s, uint16_t *__restrict__ P, int T)
+// stat [nb][T / 576][16] float2 = (m, l): m = the window's maximum of s[.][h], l = sum_t 2^(s[t][h] - m). Thread
+// 4 r + q holds heads 4q .. 4q + 3 of tokens r, r + 64, .., r + 512 in registers (one read of the window); its nine
+// terms are added in token order, then across the 16 lanes of the same q by the xor butterfly, then waves 0 .. 3.
+__global__ void __launch_bounds__(256) k_px_hstat(const float *__restrict__ s, float2 *__restrict__ stat, int T)
 {
-    __shared__ float red[4];
-    const int b = blockIdx.x >> 4, h = blockIdx.x & 15, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const float *sb = s + (size_t)b * T * 16 + h;
-    float m = -3.0e38f;
-    for (int t = threadIdx.x; t < T; t += 256) m = __builtin_fmaxf(m, sb[(size_t)t * 16]);
-    m = wave_max(m);
-    if (lane == 0) red[w] = m;
+    __shared__ float rm[4][16], rl[4][16];
+    const int w = blockIdx.x, b = blockIdx.y, q = threadIdx.x & 3, r = threadIdx.x >> 2;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const float4 *sw = (const float4 *)(s + ((size_t)b * T + (size_t)w * PX_PW) * 16);
+    float v[PX_PW / 64][4];
+#pragma unroll
+    for (int i = 0; i < PX_PW / 64; i++) {
+        const float4 a = sw[(size_t)(r + 64 * i) * 4 + q];
+        v[i][0] = a.x, v[i][1] = a.y, v[i][2] = a.z, v[i][3] = a.w;
+    }
+    float m[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        m[e] = v[0][e];
+#pragma unroll
+        for (int i = 1; i < PX_PW / 64; i++) m[e] = __builtin_fmaxf(m[e], v[i][e]);
+#pragma unroll
+        for (int o = 4; o < 64; o <<= 1) m[e] = __builtin_fmaxf(m[e], __shfl_xor(m[e], o));
+    }
+    if (lane < 4)
+#pragma unroll
+        for (int e = 0; e < 4; e++) rm[wv][4 * q + e] = m[e];
     __syncthreads();
-    m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int h = 4 * q + e;
+        m[e] = __builtin_fmaxf(__builtin_fmaxf(rm[0][h], rm[1][h]), __builtin_fmaxf(rm[2][h], rm[3][h]));
+        l[e] = 0.f;
+#pragma unroll
+        for (int i = 0; i < PX_PW / 64; i++) l[e] += __builtin_amdgcn_exp2f(v[i][e] - m[e]);
+#pragma unroll
+        for (int o = 4; o < 64; o <<= 1) l[e] += __shfl_xor(l[e], o);
+    }
+    if (lane < 4)
+#pragma unroll
+        for (int e = 0; e < 4; e++) rl[wv][4 * q + e] = l[e];
     __syncthreads();
-    float l = 0.f;
-    for (int t = threadIdx.x; t < T; t += 256) l += __builtin_amdgcn_exp2f(sb[(size_t)t * 16] - m);
-    l = wave_sum(l);
-    if (lane == 0) red[w] = l;
-    __syncthreads();
-    const float inv = 1.0f / (((red[0] + red[1]) + red[2]) + red[3]);
-    for (int t = threadIdx.x; t < T; t += 256)
-        P[(size_t)blockIdx.x * T + t] = f2h(__builtin_amdgcn_exp2f(sb[(size_t)t * 16] - m) * inv);
+    if (threadIdx.x < 16) {
+        const int h = threadIdx.x;
+        stat[((size_t)b * gridDim.x + w) * 16 + h] =
+            make_float2(__builtin_fmaxf(__builtin_fmaxf(rm[0][h], rm[1][h]), __builtin_fmaxf(rm[2][h], rm[3][h])),
+                        (rl[0][h] + rl[1][h]) + (rl[2][h] + rl[3][h]));
+    }
 }
 
-// k_px_hpool (k_phpool, 447-473): part [nb][T/144][16][1024] fp32, the sum over one 144-token chunk of P[h][t] y[t][d],
-// tokens in order (fma chains); k_px_hv adds the chunks in order. Grid (nb, T/144, 2): 256 threads, two dims each,
-// all 16 heads at once, so y is read once; the chunk's P sits in shared memory as [token][head].
-__global__ void __launch_bounds__(256) k_px_hpool(const uint16_t *__restrict__ P, const uint16_t *__restrict__ y,
+// part [nb][T / 288][16][1024] fp32 = sum over pooling window w (288 tokens) of P[h][t] y[t][d], one wave per
+// (image, window, 128 columns), no shared memory. Head h's statistics merge in window order: M = max_i m_i,
+// L = sum_i l_i 2^(m_i - M) (every lane of head h, the 576-token windows read through a buffer resource that ends at
+// the image's last one). Lane (g, c), head h = c:
+//   A fragment of K step k = P[h][32 k + 8 g + e], e < 8: f16(2^(s - M) / L) of the lane's own eight scores;
+//   B fragments: the lane loads y[32 k + 8 g + e][col0 + 8 c .. + 7] (16 bytes, a 256-byte row segment per 16 lanes)
+//   for its eight tokens and transposes the 8 x 8 halves in registers (v_perm_b32), so tile q in 0 .. 7 holds columns
+//   col0 + 8 c + q and one y load feeds one MFMA; three K steps of scores and y are in flight ahead of the MFMAs.
+// P (optional, fp16 [nb][16][T]) is written by the waves of the first column group.
+constexpr int PX_QW = 288;     // tokens per pooling window
+constexpr int PX_PWMAX = 16;   // statistics windows per image (T <= 9216)
+__global__ void __launch_bounds__(256) k_px_hpool(const float *__restrict__ s, const float2 *__restrict__ stat,
+                                                  const uint16_t *__restrict__ y, uint16_t *__restrict__ P,
                                                   float *__restrict__ part, int T)
 {
-    __shared__ __attribute__((aligned(16))) float sp[PX_PCH][16];
-    const int b = blockIdx.x, c = blockIdx.y, t0 = c * PX_PCH, d = 512 * blockIdx.z + 2 * threadIdx.x;
-    for (int i = threadIdx.x; i < PX_PCH * 16; i += 256) {
-        const int h = i / PX_PCH, t = i - h * PX_PCH;
-        sp[t][h] = h2f(P[((size_t)b * 16 + h) * T + t0 + t]);
-    }
-    __syncthreads();
-    float a0[16], a1[16];
+    constexpr int KS = PX_QW / 32, DEPTH = 3;
+    const int w = blockIdx.y, b = blockIdx.z, nq = gridDim.y, nw = T / PX_PW, lane = threadIdx.x & 63;
+    const int g = lane >> 4, c = lane & 15, col0 = 512 * blockIdx.x + 128 * (threadIdx.x >> 6);
+    const size_t tok0 = (size_t)b * T + (size_t)w * PX_QW;
+    const __amdgpu_buffer_rsrc_t rst = buf_rsrc(stat + (size_t)b * nw * 16, (uint32_t)nw * 16 * 8);
+    v2f sv[PX_PWMAX];
 #pragma unroll
-    for (int h = 0; h < 16; h++) a0[h] = a1[h] = 0.f;
-    const uint16_t *yr = y + ((size_t)b * T + t0) * XT_D + d;
-    for (int t = 0; t < PX_PCH; t++) {
-        const uint32_t u = *(const uint32_t *)(yr + (size_t)t * XT_D);
-        const float v0 = h2f((uint16_t)(u & 0xffffu)), v1 = h2f((uint16_t)(u >> 16));
+    for (int i = 0; i < PX_PWMAX; i++)
+        sv[i] = __builtin_bit_cast(v2f, __builtin_amdgcn_raw_buffer_load_b64(rst, (16 * i + c) * 8, 0, 0));
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(s + tok0 * 16, PX_QW * 16 * 4);
+    const __amdgpu_buffer_rsrc_t ry = buf_rsrc(y + tok0 * XT_D, PX_QW * XT_D * 2);
+    const int soff = (8 * g * 16 + c) * 4, yoff = (8 * g * XT_D + col0 + 8 * c) * 2;
+    float sk[KS][8];
+    uint4 yk[KS][8];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 p = *(const float4 *)&sp[t][4 * q];
-            const float pp[4] = {p.x, p.y, p.z, p.w};
+    for (int k = 0; k < DEPTH; k++)
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                a0[4 * q + k] = __builtin_fmaf(pp[k], v0, a0[4 * q + k]);
-                a1[4 * q + k] = __builtin_fmaf(pp[k], v1, a1[4 * q + k]);
-            }
+        for (int e = 0; e < 8; e++) {
+            sk[k][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, soff, (32 * k + e) * 64, 0));
+            yk[k][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ry, yoff, (32 * k + e) * XT_D * 2, 0));
         }
-    }
-    float *po = part + (((size_t)b * gridDim.y + c) * 16) * XT_D + d;
+    float mx = sv[0][0], l = 0.f;
 #pragma unroll
-    for (int h = 0; h < 16; h++) *(float2 *)(po + (size_t)h * XT_D) = make_float2(a0[h], a1[h]);
-}
-
-// k_px_hv (k_phv, 477-503): pooled[b][h] = the nch chunk partials summed in chunk order, then
-// o[b][64 h + n] = f16(Wv[64 h + n] . pooled[b][h]) (Wv fp16 [1024][1024]), written as fp32 holding the fp16 value
-// (the reference's fp16 o, ready for eva_k_quant_act). One block of 256 threads per (image, head): each wave takes 16
-// outputs, each lane 16 of the 1024 products in element order, met in the butterfly.
-__global__ void __launch_bounds__(256) k_px_hv(const float *__restrict__ part, int nch, const uint16_t *__restrict__ wv,
-                                               float *__restrict__ o)
-{
-    __shared__ __attribute__((aligned(16))) float pv[XT_D];
-    const int b = blockIdx.x >> 4, h = blockIdx.x & 15, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    {
-        const float *pp = part + ((size_t)b * nch * 16 + h) * XT_D + 4 * threadIdx.x;
-        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int c = 0; c < nch; c++) {
-            const float4 v = *(const float4 *)(pp + (size_t)c * 16 * XT_D);
-            a.x += v.x;
-            a.y += v.y;
-            a.z += v.z;
-            a.w += v.w;
-        }
-        *(float4 *)(pv + 4 * threadIdx.x) = a;
-    }
-    __syncthreads();
-    float x[16];
+    for (int i = 1; i < PX_PWMAX; i++) mx = i < nw ? __builtin_fmaxf(mx, sv[i][0]) : mx;
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++) {
-        const float4 a = *(const float4 *)(pv + 512 * hh + 8 * lane), c = *(const float4 *)(pv + 512 * hh + 8 * lane + 4);
-        x[8 * hh + 0] = a.x; x[8 * hh + 1] = a.y; x[8 * hh + 2] = a.z; x[8 * hh + 3] = a.w;
-        x[8 * hh + 4] = c.x; x[8 * hh + 5] = c.y; x[8 * hh + 6] = c.z; x[8 * hh + 7] = c.w;
-    }
-    float mine = 0.f;
-    for (int k = 0; k < 16; k++) {
-        const int n = 64 * h + 16 * w + k;
-        float a = 0.f;
+    for (int i = 0; i < PX_PWMAX; i++) l = i < nw ? l + sv[i][1] * __builtin_amdgcn_exp2f(sv[i][0] - mx) : l;
+    const float inv = 1.0f / l;
+    v4f acc[8];
 #pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-            const uint4 u = *(const uint4 *)(wv + (size_t)n * XT_D + 512 * hh + 8 * lane);
-            const uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+    for (int q = 0; q < 8; q++) acc[q] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < KS; k++) {
+        uint32_t pa[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            pa[i] = (uint32_t)f2h(__builtin_amdgcn_exp2f(sk[k][2 * i] - mx) * inv) |
+                    ((uint32_t)f2h(__builtin_amdgcn_exp2f(sk[k][2 * i + 1] - mx) * inv) << 16);
+        const v8h a = __builtin_bit_cast(v8h, make_uint4(pa[0], pa[1], pa[2], pa[3]));
+        if (P && col0 == 0)
+            *(uint4 *)(P + ((size_t)b * 16 + c) * T + (size_t)w * PX_QW + 32 * k + 8 * g) = make_uint4(pa[0], pa[1], pa[2], pa[3]);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {  // columns 2m (low halves) and 2m + 1 (high halves) of the eight tokens
+            uint32_t lo[4], hi[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                a = __builtin_fmaf(h2f((uint16_t)(ww[i] & 0xffffu)), x[8 * hh + 2 * i], a);
-                a = __builtin_fmaf(h2f((uint16_t)(ww[i] >> 16)), x[8 * hh + 2 * i + 1], a);
+                const uint32_t r0 = ((const uint32_t *)&yk[k][2 * i])[m], r1 = ((const uint32_t *)&yk[k][2 * i + 1])[m];
+                lo[i] = __builtin_amdgcn_perm(r1, r0, 0x05040100u);
+                hi[i] = __builtin_amdgcn_perm(r1, r0, 0x07060302u);
+            }
+            acc[2 * m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(v8h, make_uint4(lo[0], lo[1], lo[2], lo[3])), acc[2 * m], 0, 0, 0);
+            acc[2 * m + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(v8h, make_uint4(hi[0], hi[1], hi[2], hi[3])), acc[2 * m + 1], 0, 0, 0);
+        }
+        if (k + DEPTH < KS)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                sk[k + DEPTH][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, soff, (32 * (k + DEPTH) + e) * 64, 0));
+                yk[k + DEPTH][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ry, yoff, (32 * (k + DEPTH) + e) * XT_D * 2, 0));
+            }
+    }
+    // acc[q][r] = head 4 g + r, column col0 + 8 c + q
+    float *po = part + (((size_t)b * nq + w) * 16 + 4 * g) * XT_D + col0 + 8 * c;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        *(float4 *)(po + (size_t)r * XT_D) = make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);
+        *(float4 *)(po + (size_t)r * XT_D + 4) = make_float4(acc[4][r], acc[5][r], acc[6][r], acc[7][r]);
+    }
+}
+
+// o [nb][1024] = f16(Wv[64 h + n] . pooled[b][h]) held as fp32 (ready for eva_k_quant_act), pooled[b][h] = the nw
+// window partials summed in window order. Block (head h, images 2 z, 2 z + 1), 256 threads. Thread (image t >> 7,
+// columns 8 (t & 127) ..) reads its partials four windows at a time through a buffer resource that ends at the image's
+// last window, so reads past it return zeros and every load of a round is in flight at once; the two pooled rows sit in
+// shared memory as [image][half][512 + 4]. Then thread (n, image, half) = (t >> 2, (t >> 1) & 1, t & 1) takes row
+// 64 h + n of Wv over its half of the columns as two interleaved fma chains, and one xor shuffle adds the halves.
+__global__ void __launch_bounds__(256) k_px_hproj(const float *__restrict__ part, int nw, const uint16_t *__restrict__ wv,
+                                                  float *__restrict__ o, int nb)
+{
+    constexpr int HS = XT_D / 2 + 4;
+    __shared__ __attribute__((aligned(16))) float pl[2 * 2 * HS];
+    const int h = blockIdx.x, b0 = 2 * blockIdx.y, t = threadIdx.x;
+    {
+        const int bi = __builtin_amdgcn_readfirstlane(t >> 7), d = 8 * (t & 127);  // bi is the same in a wave
+        const bool live = b0 + bi < nb;
+        const __amdgpu_buffer_rsrc_t rp = buf_rsrc(part + (size_t)(live ? b0 + bi : 0) * nw * 16 * XT_D,
+                                                   live ? (uint32_t)nw * 16 * XT_D * 4 : 0u);
+        float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
+        for (int i0 = 0; i0 < nw; i0 += 4) {
+            float4 v0[4], v1[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int off = (((i0 + k) * 16 + h) * XT_D + d) * 4;
+                v0[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, 0));
+                v1[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rp, off + 16, 0, 0));
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                a0.x += v0[k].x, a0.y += v0[k].y, a0.z += v0[k].z, a0.w += v0[k].w;
+                a1.x += v1[k].x, a1.y += v1[k].y, a1.z += v1[k].z, a1.w += v1[k].w;
             }
         }
-        a = wave_sum(a);
-        mine = lane == k ? a : mine;
+        float *dst = pl + (2 * bi + d / (XT_D / 2)) * HS + d % (XT_D / 2);
+        *(float4 *)dst = a0;
+        *(float4 *)(dst + 4) = a1;
     }
-    if (lane < 16) o[(size_t)b * XT_D + 64 * h + 16 * w + lane] = h2f(f2h(mine));
+    __syncthreads();
+    const int n = t >> 2, bi = (t >> 1) & 1, half = t & 1;
+    const uint16_t *wr = wv + (size_t)(64 * h + n) * XT_D + (XT_D / 2) * half;
+    const float *pr = pl + (2 * bi + half) * HS;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll 4
+    for (int k = 0; k < XT_D / 2; k += 16) {
+        const uint4 u0 = *(const uint4 *)(wr + k), u1 = *(const uint4 *)(wr + k + 8);
+        const uint32_t w0[4] = {u0.x, u0.y, u0.z, u0.w}, w1[4] = {u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float2 p0 = *(const float2 *)(pr + k + 2 * i), p1 = *(const float2 *)(pr + k + 8 + 2 * i);
+            a0 = __builtin_fmaf(h2f((uint16_t)(w0[i] & 0xffffu)), p0.x, a0);
+            a0 = __builtin_fmaf(h2f((uint16_t)(w0[i] >> 16)), p0.y, a0);
+            a1 = __builtin_fmaf(h2f((uint16_t)(w1[i] & 0xffffu)), p1.x, a1);
+            a1 = __builtin_fmaf(h2f((uint16_t)(w1[i] >> 16)), p1.y, a1);
+        }
+    }
+    float a = a0 + a1;
+    a += __shfl_xor(a, 1);
+    if (!half && b0 + bi < nb) o[(size_t)(b0 + bi) * XT_D + 64 * h + n] = h2f(f2h(a));
 }
 
-extern "C" int px_k_hsoft(const float *s, void *P, int nb, int T, void *stream)
+extern "C" int px_k_hstat(const float *s, float *stat, int nb, int T, void *stream)
 {
-    if (nb <= 0 || T <= 0) return xt_fail("px_k_hsoft", "bad shape (nb > 0, T > 0)");
-    hipLaunchKernelGGL(k_px_hsoft, dim3(nb * 16), dim3(256), 0, (hipStream_t)stream, s, (uint16_t *)P, T);
-    return xt_check("px_k_hsoft");
+    if (nb <= 0 || T <= 0 || T % PX_PW || T / PX_PW > 65535 || nb > 65535)
+        return xt_fail("px_k_hstat", "T must be a positive multiple of 576, nb in 1 .. 65535");
+    if (((uintptr_t)s & 15) || ((uintptr_t)stat & 7)) return xt_fail("px_k_hstat", "s 16-byte, stat 8-byte aligned");
+    hipLaunchKernelGGL(k_px_hstat, dim3(T / PX_PW, nb), dim3(256), 0, (hipStream_t)stream, s, (float2 *)stat, T);
+    return xt_check("px_k_hstat");
 }
 
-extern "C" int px_k_hpool(const void *P, const void *y, float *part, int nb, int T, void *stream)
+extern "C" int px_k_hpool(const float *s, const float *stat, const void *y, void *P, float *part, int nb, int T,
+                          void *stream)
 {
-    if (nb <= 0 || T <= 0 || T % PX_PCH) return xt_fail("px_k_hpool", "T must be a positive multiple of 144");
-    if (((uintptr_t)y & 3) || ((uintptr_t)part & 7)) return xt_fail("px_k_hpool", "y 4-byte, part 8-byte aligned");
-    hipLaunchKernelGGL(k_px_hpool, dim3(nb, T / PX_PCH, 2), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)P,
-                       (const uint16_t *)y, part, T);
+    if (nb <= 0 || T <= 0 || T % PX_PW || T / PX_PW > PX_PWMAX || nb > 65535)
+        return xt_fail("px_k_hpool", "T must be a positive multiple of 576 up to 9216, nb in 1 .. 65535");
+    if (((uintptr_t)s | (uintptr_t)P | (uintptr_t)y | (uintptr_t)part) & 15 || ((uintptr_t)stat & 7))
+        return xt_fail("px_k_hpool", "s, P, y and part must be 16-byte aligned, stat 8-byte");
+    hipLaunchKernelGGL(k_px_hpool, dim3(XT_D / 512, T / PX_QW, nb), dim3(256), 0, (hipStream_t)stream, s,
+                       (const float2 *)stat, (const uint16_t *)y, (uint16_t *)P, part, T);
     return xt_check("px_k_hpool");
 }
 
-extern "C" int px_k_hv(const float *part, int nch, const void *wv, float *o, int nb, void *stream)
+extern "C" int px_k_hproj(const float *part, int nw, const void *wv, float *o, int nb, void *stream)
 {
-    if (nb <= 0 || nch <= 0) return xt_fail("px_k_hv", "bad shape (nb > 0, nch > 0)");
-    if (((uintptr_t)part | (uintptr_t)wv) & 15) return xt_fail("px_k_hv", "part and wv must be 16-byte aligned");
-    hipLaunchKernelGGL(k_px_hv, dim3(nb * 16), dim3(256), 0, (hipStream_t)stream, part, nch, (const uint16_t *)wv, o);
-    return xt_check("px_k_hv");
+    if (nb <= 0 || nw <= 0 || nw > 2 * PX_PWMAX || nb > 2 * 65535)
+        return xt_fail("px_k_hproj", "bad shape (nb > 0, 0 < nw <= 32)");
+    if (((uintptr_t)part | (uintptr_t)wv) & 15) return xt_fail("px_k_hproj", "part and wv must be 16-byte aligned");
+    hipLaunchKernelGGL(k_px_hproj, dim3(16, (nb + 1) / 2), dim3(256), 0, (hipStream_t)stream, part, nw,
+                       (const uint16_t *)wv, o, nb);
+    return xt_check("px_k_hproj");
 }
 
 // GELU of n fp32 values by the fc1 epilogue's gelu_erf (test hook: its accuracy is not visible through the E4M3 output)

@@ -16,7 +16,8 @@
 #include "xt_stream.h"
 #include "xtag_eva.h"
 
-#define PX_PCH 144            // attention-pool token chunk (px_kernels.cu:446)
+#define PX_PW 576             // attention-pool statistics window of px_k_hstat
+#define PX_QW 288             // attention-pool pooling window of px_k_hpool / px_k_hproj
 
 struct PxLayer {
     const float *ln1w, *ln1b, *bqkv, *bo, *ln2w, *ln2b, *b1, *rs, *b2;  // in the blob
@@ -43,9 +44,9 @@ struct px_impl {
     uint32_t ldh;                                       // nt rounded up to 64
     float *scratch;
     // activations
-    uint16_t *in, *x, *q, *k, *vt, *y, *P;
+    uint16_t *in, *x, *q, *k, *vt, *y;
     uint8_t *h8, *o8, *m8, *oq;
-    float *sh, *so8, *sm, *s, *part, *o, *oqs, *out;
+    float *sh, *so8, *sm, *s, *stat, *part, *o, *oqs, *out;
     hipGraphExec_t graph;
     hipEvent_t done[PX_NBUF];
     uint16_t *stage[PX_NBUF];                           // pinned staging of each buf's inputs (at its first submit)
@@ -139,9 +140,9 @@ static int px_forward(px *p)
         PX_CK(px_k_fc2(E->m8, E->sm, M, L.w2, L.s2, L.b2, E->x, M, st));
     }
     PX_CK(px_k_hln(E->x, E->hnw, E->hnb, E->hpos, PX_T, E->U, E->y, E->s, M, st));
-    PX_CK(px_k_hsoft(E->s, E->P, nb, PX_T, st));
-    PX_CK(px_k_hpool(E->P, E->y, E->part, nb, PX_T, st));
-    PX_CK(px_k_hv(E->part, PX_T / PX_PCH, E->wv, E->o, nb, st));
+    PX_CK(px_k_hstat(E->s, E->stat, nb, PX_T, st));
+    PX_CK(px_k_hpool(E->s, E->stat, E->y, nullptr, E->part, nb, PX_T, st));
+    PX_CK(px_k_hproj(E->part, PX_T / PX_QW, E->wv, E->o, nb, st));
     PX_CK(eva_k_quant_act(E->o, 1, EVA_D, nb, EVA_D, E->oq, EVA_D, E->oqs, nb, st));
     PX_CK(eva_k_head(E->oq, E->oqs, nb, E->hq, E->hs, (int)E->ldh, E->hb, E->out, nb, (int)p->nt, st));
     return 0;
@@ -226,8 +227,8 @@ static int px_up(px *p)
     PX_ALLOC(E, E->sm, (PX_HID / 128) * M * 4, true);
     PX_ALLOC(E, E->y, M * EVA_D * 2, true);
     PX_ALLOC(E, E->s, M * 16 * 4, true);
-    PX_ALLOC(E, E->P, nb * 16 * PX_T * 2, true);
-    PX_ALLOC(E, E->part, nb * (PX_T / PX_PCH) * 16 * EVA_D * 4, true);
+    PX_ALLOC(E, E->stat, nb * (PX_T / PX_PW) * 16 * 2 * 4, true);
+    PX_ALLOC(E, E->part, nb * (PX_T / PX_QW) * 16 * EVA_D * 4, true);
     PX_ALLOC(E, E->o, nb * EVA_D * 4, true);
     PX_ALLOC(E, E->oq, nb * EVA_D, true);
     PX_ALLOC(E, E->oqs, 8 * nb * 4, true);

@@ -29,9 +29,9 @@ _SIGS = {
     "px_k_pe": (_i, [_p, _p, _p, _i, _p]),
     "px_k_pembed": (_i, [_p, _p, _i, _p, _p, _i, _p]),
     "px_k_hln": (_i, [_p, _p, _p, _p, _i, _p, _p, _p, _i, _p]),
-    "px_k_hsoft": (_i, [_p, _p, _i, _i, _p]),
-    "px_k_hpool": (_i, [_p, _p, _p, _i, _i, _p]),
-    "px_k_hv": (_i, [_p, _i, _p, _p, _i, _p]),
+    "px_k_hstat": (_i, [_p, _p, _i, _i, _p]),
+    "px_k_hpool": (_i, [_p, _p, _p, _p, _p, _i, _i, _p]),
+    "px_k_hproj": (_i, [_p, _i, _p, _p, _i, _p]),
     "eva_k_fc1": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _i, _p]),
     "eva_k_fc2": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
     "eva_k_head": (_i, [_p, _p, _i, _p, _p, _i, _p, _p, _i, _i, _p]),
