@@ -93,6 +93,14 @@ int eva_run(eva *e);
 const float *eva_dev_output(eva *e);
 void *eva_stream_handle(eva *e);
 int eva_sync(eva *e);
+/* eva.h:312-338 (eva_profile, built there with EVA_PROF): one direct (non-graph) forward with a GPU event after every
+ * op, summed per op kind over the layers and printed to stderr as "prof gpu <op> <ms> <share>"; ms (may be NULL)
+ * receives the EVA_PROF_OPS sums in the order eva_profile_opname(0 ..) names them: patch+embed, ln1, qkv, flash, oproj,
+ * ln2, fc1, fc2, pool+head (the reference's "stat clear" and "(mlp ln)" ops do not exist here: fc1 writes the LN
+ * statistics and fc2 folds the LN). Runs on the device input buffer as it stands. */
+#define EVA_PROF_OPS 9
+int eva_profile(eva *e, double *ms);
+const char *eva_profile_opname(int i);
 
 /* ---- kernel launchers (device pointers; stream = hipStream_t or NULL) ---- */
 

@@ -342,3 +342,38 @@ def test_submit_ring_nonblocking(dev, synth_blob):
     assert t_submit < 5 * t_one, "the submits waited for the GPU"
     for b in range(8):
         assert np.array_equal(got[b], ref[b]), f"buf {b}"
+
+
+def test_profile_per_op(dev, synth_blob):
+    """eva.h:312-338: eva_profile runs one direct forward with an event after every op and returns the GPU time per op
+    kind. Every kind takes time, the layer kinds dominate the total, the direct forward takes about as long as a graph
+    replay, and the profile leaves the scores of the next forward unchanged."""
+    import time
+    from xtagger_amd import blob
+    from xtagger_amd.engine import Engine
+    path, _ = synth_blob
+    nb = 4
+    e = Engine(path, device=0, nb=nb)
+    e.ready()
+    inp = blob.synth_inputs(nb, seed=3)
+    e.submit(0, inp)
+    ref = e.wait(0, nb)
+    prof = e.profile()
+    e.run()
+    e.sync()
+    reps = 5
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        e.run()
+    e.sync()
+    t_graph = (time.perf_counter() - t0) / reps * 1e3
+    e.submit(0, inp)
+    got = e.wait(0, nb)
+    e.close()
+    tot = sum(prof.values())
+    _say("  " + ", ".join(f"{k} {v:.3f}" for k, v in prof.items()) + f"; total {tot:.2f} ms, graph {t_graph:.2f} ms")
+    assert list(prof) == ["patch+embed", "ln1", "qkv", "flash", "oproj", "ln2", "fc1", "fc2", "pool+head"]
+    assert all(v > 0 for v in prof.values())
+    assert prof["qkv"] + prof["flash"] + prof["fc1"] + prof["fc2"] > 0.5 * tot
+    assert 0.5 * t_graph < tot < 2.0 * t_graph
+    assert np.array_equal(got, ref)

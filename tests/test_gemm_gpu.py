@@ -3,7 +3,8 @@
 Packing is bit-exact against the oracle; the GEMM is within 1e-3 (max-abs relative to max |ref|, and normwise) of
 the fp64 dequantized product, checked on the fp32-output build of the same kernel; the bf16 output is the RNE of
 the fp32 output. Shapes: the EVA02-L qkv shape at batch 1 (M=1025, K=1024, N=3072), the layer shapes at M=8200 on
-sampled rows, ragged M, and the reference's own kcheck.c method for k_oproj (LCG operands, 97 sampled rows).
+sampled rows, ragged M, and the reference's own kcheck.c method for its three GEMM kernels: k_pe, k_oproj and
+k_headmv (LCG operands drawn in kcheck's order, sampled rows against fp64 loops).
 """
 import numpy as np
 import pytest
@@ -172,3 +173,77 @@ def test_gemm_kcheck_oproj_method(dev, xt, orc):
     # kcheck's operands span products 2^-18 .. 56 inside one K block; the f8f6f4 matrix core sums them with less
     # than fp32 precision (observed ~6e-5 of max |ref|), so the bound is the GEMM contract, 1e-3
     assert err <= 1e-3 * np.abs(ref).max()
+
+
+def test_gemm_kcheck_pe_method(dev, xt, orc):
+    """kcheck.c:73-98 restated for the patch embedding: in fp16 [8192][592] = h(frand()) for k < 588 else 0,
+    pe fp16 [1024][592] = h(0.05 frand()), x row m + m / 1024 + 1 = in[m] . pe^T, fp64 loops on the 97 rows
+    m = 7919 i mod 8192. eva_k_pe adds the position table in the same pass, so it runs with a zero table."""
+    from tests.kcheck import sample_rows
+    nb, NP, K0P, T, D = 8, 1024, 592, 1025, 1024
+    g = orc.Lcg(12345)
+    inp = np.zeros((nb * NP, K0P), np.float16)
+    inp[:, :588] = g.frand(nb * NP * 588).reshape(nb * NP, 588).astype(np.float16)
+    pe = np.zeros((D, K0P), np.float16)
+    pe[:, :588] = (np.float32(0.05) * g.frand(D * 588).reshape(D, 588)).astype(np.float16)
+    pos = np.zeros((T, D), np.float32)
+    d_in, d_pe, d_pos = (torch.from_numpy(a).to(dev) for a in (inp, pe, pos))
+    d_x = torch.zeros((nb * T, D), dtype=torch.float16, device=dev)
+    _run(xt.lib.eva_k_pe(xt.ptr(d_in), xt.ptr(d_pe), xt.ptr(d_pos), xt.ptr(d_x), nb, _stream()), "eva_k_pe")
+    x = d_x.cpu().numpy()
+    rows = sample_rows(nb * NP)
+    a, w = inp[rows].astype(np.float64), pe.astype(np.float64)
+    ref = a @ w.T
+    terms = np.abs(a) @ np.abs(w).T
+    got = x[rows + rows // NP + 1].astype(np.float64)
+    err = np.abs(got - ref)
+    _say(f"kcheck k_pe max |err| {err.max():.5f} (max |ref| {np.abs(ref).max():.3f})")
+    # one fp16 rounding of the fp32 sum (half an ulp, 2^-25 in the subnormal range) plus the fp32 summation
+    assert (err <= 2.0 ** -11 * np.abs(ref) + 2.0 ** -25 + 1e-6 * terms).all()
+    assert (x[::T] == 0).all()                        # the cls rows are the (zero) position row
+
+
+def test_gemm_kcheck_headmv_method(dev, xt, orc):
+    """kcheck.c:128-153 restated for the tag head: after k_pe's and k_oproj's draws, hw fp16 [10868][1024] =
+    h(0.05 frand()), pn fp16 [8][1024] = h(frand()), hb = frand(); every 13th of the 8 x 10861 sigmoid outputs against
+    fp64 loops. The head here is block-scaled E4M3 (pn and every hw row packed 1x128 by eva_k_quant_act), so the
+    contract is against the fp64 product of the packed operands; the distance to kcheck's fp16 reference is the head's
+    quantization, reported and bounded separately."""
+    nb, nt, D, T = 8, 10861, 1024, 1025
+    g = orc.Lcg(12345)
+    g.frand(nb * 1024 * 588 + D * 588)                # k_pe's operands
+    g.e4m3(nb * T * D + D * D)                        # k_oproj's a and W (kcheck.c:104-107)
+    g.frand(nb * T * D)                               # k_oproj's x0 (kcheck.c:108)
+    hw = (np.float32(0.05) * g.frand((nt + 7) * D)).astype(np.float16).reshape(nt + 7, D)
+    pn = g.frand(nb * D).astype(np.float16).reshape(nb, D)
+    hb = g.frand(nt + 7)
+    ldw = nt + 7
+    d_hw, d_pn, d_hb = (torch.from_numpy(a).to(dev) for a in (hw, pn, hb))
+    d_qw = torch.zeros((nt + 7, D), dtype=torch.uint8, device=dev)
+    d_sw = torch.zeros((8, ldw), dtype=torch.float32, device=dev)
+    d_qa = torch.zeros((nb, D), dtype=torch.uint8, device=dev)
+    d_sa = torch.zeros((8, nb), dtype=torch.float32, device=dev)
+    d_out = torch.zeros((nb, nt), dtype=torch.float32, device=dev)
+    _run(xt.lib.eva_k_quant_act(xt.ptr(d_hw), 2, D, nt + 7, D, xt.ptr(d_qw), D, xt.ptr(d_sw), ldw, _stream()), "pack hw")
+    _run(xt.lib.eva_k_quant_act(xt.ptr(d_pn), 2, D, nb, D, xt.ptr(d_qa), D, xt.ptr(d_sa), nb, _stream()), "pack pn")
+    _run(xt.lib.eva_k_head(xt.ptr(d_qa), xt.ptr(d_sa), nb, xt.ptr(d_qw), xt.ptr(d_sw), ldw, xt.ptr(d_hb),
+                           xt.ptr(d_out), nb, nt, _stream()), "eva_k_head")
+    out = d_out.cpu().numpy().reshape(-1)
+    qa, sa, qw, sw = (t.cpu().numpy() for t in (d_qa, d_sa, d_qw, d_sw))
+    idx = np.arange(0, nb * nt, 13)
+    i, j = idx // nt, idx % nt
+    lut = orc.E4M3_LUT.astype(np.float64)
+    da = lut[qa] * np.repeat(sa.T, 128, 1)            # dequantized [nb][1024]
+    dw = lut[qw[j]] * np.repeat(sw.T[j], 128, 1)      # dequantized sampled rows
+    logit = np.einsum("sk,sk->s", da[i], dw) + hb[j]
+    ref_q = 1.0 / (1.0 + np.exp(-logit))
+    terms = np.einsum("sk,sk->s", np.abs(da[i]), np.abs(dw))
+    err_q = np.abs(out[idx] - ref_q)
+    logit16 = np.einsum("sk,sk->s", pn[i].astype(np.float64), hw[j].astype(np.float64)) + hb[j]
+    ref16 = 1.0 / (1.0 + np.exp(-logit16))
+    err16 = np.abs(out[idx] - ref16)
+    _say(f"kcheck k_headmv max |err| {err_q.max():.2e} vs the packed operands, {err16.max():.2e} vs fp16 operands "
+         f"(mean {err16.mean():.2e})")
+    assert (err_q <= 0.25 * 2e-5 * terms + 1e-6).all()
+    # E4M3 keeps 3 mantissa bits: over kcheck's uniform operands the logit moves by ~0.03 rms, the sigmoid by <= 1/4 of it
+    assert err16.max() < 0.05 and err16.mean() < 0.01

@@ -57,6 +57,10 @@ struct eva_impl {
     uint8_t *h8, *m8, *pq;
     float *sh, *sm, *stat, *pool, *ps, *out;
     hipGraphExec_t graph;
+    // eva_profile: an event after every op of one direct forward (eva.h:71-88, 312-338), 172 ops at 24 layers
+    hipEvent_t pev[256];
+    uint8_t pid[256];
+    int pk, pon;
     hipEvent_t done[EVA_NBUF];
     uint16_t *stage[EVA_NBUF];                             // pinned staging of each buf's inputs (at its first submit)
     std::vector<void *> allocs;
@@ -118,6 +122,23 @@ static int ev_layout(eva_impl *E, uint32_t ntp)
     return 0;
 }
 
+static const char *const ev_opname[EVA_PROF_OPS] = {"patch+embed", "ln1", "qkv", "flash", "oproj",
+                                                     "ln2", "fc1", "fc2", "pool+head"};
+
+// eva_profile's mark after an op of kind id (only while a profile runs, never inside the captured graph)
+static int ev_mark(eva_impl *E, int id)
+{
+    if (!E->pon) return 0;
+    if (E->pk >= 256) return xt_fail("eva_profile", "more than 255 ops");
+    E->pid[E->pk] = (uint8_t)id;
+    XT_HIP(hipEventRecord(E->pev[E->pk++], E->st));
+    return 0;
+}
+#define EV_OP(call, id)                                                \
+    do {                                                               \
+        if ((call) || ev_mark(E, (id))) return -1;                     \
+    } while (0)
+
 // The whole forward for nb inputs on E->st (captured once into E->graph), eva.h:227-310.
 static int ev_forward(eva *e)
 {
@@ -125,25 +146,25 @@ static int ev_forward(eva *e)
     void *st = (void *)E->st;
     const int M = (int)E->M, lds = (int)E->Mp, nb = (int)E->nb;
 
-    EV_CK(eva_k_pe(E->in, E->pe, E->pos, E->x, nb, st));
+    EV_OP(eva_k_pe(E->in, E->pe, E->pos, E->x, nb, st), 0);
     for (int i = 0; i < EVA_NL; i++) {
         const Layer &L = E->L[i];
         const bool sp = E->flags & EVA_SPARSE24;
-        EV_CK(eva_k_ln(E->x, L.ln1w, L.ln1b, E->h8, E->sh, M, lds, st));
-        if (sp) EV_CK(eva_k_qkv_sp(E->h8, E->sh, lds, L.vqkv, L.xqkv, L.sqkv, E->cs, E->q, E->k, E->vt, M, st));
-        else EV_CK(eva_k_qkv(E->h8, E->sh, lds, L.wqkv, L.sqkv, E->cs, E->q, E->k, E->vt, M, st));
-        EV_CK(eva_k_flash(E->q, E->k, E->vt, E->h8, E->sh, lds, nb, NULL, st));
-        if (sp) EV_CK(eva_k_oproj_sp(E->h8, E->sh, lds, L.vo, L.xo, L.so, E->x, M, st));
-        else EV_CK(eva_k_oproj(E->h8, E->sh, lds, L.wo, L.so, E->x, M, st));
-        EV_CK(eva_k_ln(E->x, L.ln2w, L.ln2b, E->h8, E->sh, M, lds, st));
-        if (sp) EV_CK(eva_k_fc1_sp(E->h8, E->sh, lds, L.v12, L.x12, L.s12, E->m8, E->sm, E->stat, M, st));
-        else EV_CK(eva_k_fc1(E->h8, E->sh, lds, L.w12, L.s12, E->m8, E->sm, E->stat, M, st));
-        if (sp) EV_CK(eva_k_fc2_sp(E->m8, E->sm, lds, L.v2, L.x2, L.s2, E->stat, L.cn, L.dn, E->x, M, st));
-        else EV_CK(eva_k_fc2(E->m8, E->sm, lds, L.w2, L.s2, E->stat, L.cn, L.dn, E->x, M, st));
+        EV_OP(eva_k_ln(E->x, L.ln1w, L.ln1b, E->h8, E->sh, M, lds, st), 1);
+        if (sp) EV_OP(eva_k_qkv_sp(E->h8, E->sh, lds, L.vqkv, L.xqkv, L.sqkv, E->cs, E->q, E->k, E->vt, M, st), 2);
+        else EV_OP(eva_k_qkv(E->h8, E->sh, lds, L.wqkv, L.sqkv, E->cs, E->q, E->k, E->vt, M, st), 2);
+        EV_OP(eva_k_flash(E->q, E->k, E->vt, E->h8, E->sh, lds, nb, NULL, st), 3);
+        if (sp) EV_OP(eva_k_oproj_sp(E->h8, E->sh, lds, L.vo, L.xo, L.so, E->x, M, st), 4);
+        else EV_OP(eva_k_oproj(E->h8, E->sh, lds, L.wo, L.so, E->x, M, st), 4);
+        EV_OP(eva_k_ln(E->x, L.ln2w, L.ln2b, E->h8, E->sh, M, lds, st), 5);
+        if (sp) EV_OP(eva_k_fc1_sp(E->h8, E->sh, lds, L.v12, L.x12, L.s12, E->m8, E->sm, E->stat, M, st), 6);
+        else EV_OP(eva_k_fc1(E->h8, E->sh, lds, L.w12, L.s12, E->m8, E->sm, E->stat, M, st), 6);
+        if (sp) EV_OP(eva_k_fc2_sp(E->m8, E->sm, lds, L.v2, L.x2, L.s2, E->stat, L.cn, L.dn, E->x, M, st), 7);
+        else EV_OP(eva_k_fc2(E->m8, E->sm, lds, L.w2, L.s2, E->stat, L.cn, L.dn, E->x, M, st), 7);
     }
     EV_CK(eva_k_pool(E->x, E->pool, nb, st));
     EV_CK(eva_k_lnh(E->pool, E->fnw, E->fnb, E->pn, E->pq, E->ps, nb, nb, st));
-    EV_CK(eva_k_head(E->pq, E->ps, nb, E->hq, E->hs, (int)E->ldh, E->hb, E->out, nb, (int)e->nt, st));
+    EV_OP(eva_k_head(E->pq, E->ps, nb, E->hq, E->hs, (int)E->ldh, E->hb, E->out, nb, (int)e->nt, st), 8);
     return 0;
 }
 
@@ -443,12 +464,50 @@ extern "C" void eva_close(eva *e)
     if (E->hput) (void)hipHostFree(E->hput);
     for (int s = 0; s < EV_HPUT_SLOTS; s++)
         if (E->hput_ev[s]) (void)hipEventDestroy(E->hput_ev[s]);
+    for (int i = 0; i < 256; i++)
+        if (E->pev[i]) (void)hipEventDestroy(E->pev[i]);
     for (void *p : E->allocs) (void)hipFree(p);
     if (E->st) (void)hipStreamDestroy(E->st);
     free(E->path);
     delete E;
     memset(e, 0, sizeof(*e));
 }
+
+// eva.h:312-338: two warm direct forwards, then one with an event after every op; per op kind the GPU time between
+// the previous op's event and its own, summed over the layers, printed to stderr and returned in ms[EVA_PROF_OPS]
+// (when not NULL). The forward reads the device input buffer as it stands (eva_dev_input / the last submit).
+extern "C" int eva_profile(eva *e, double *ms)
+{
+    if (eva_ready(e)) return -1;
+    eva_impl *E = e->impl;
+    double acc[EVA_PROF_OPS] = {0}, tot = 0;
+    XT_HIP(hipStreamSynchronize(E->st));
+    if (!E->pev[0])
+        for (int i = 0; i < 256; i++) XT_HIP(hipEventCreate(&E->pev[i]));
+    if (ev_forward(e) || ev_forward(e)) return -1;
+    E->pon = 1;
+    E->pk = 1;
+    E->pid[0] = 255;
+    const hipError_t r0 = hipEventRecord(E->pev[0], E->st);
+    const int rc = r0 != hipSuccess ? xt_fail("eva_profile", "hipEventRecord failed") : ev_forward(e);
+    E->pon = 0;
+    if (rc) return -1;
+    XT_HIP(hipStreamSynchronize(E->st));
+    for (int i = 1; i < E->pk; i++) {
+        float dt = 0.f;
+        XT_HIP(hipEventElapsedTime(&dt, E->pev[i - 1], E->pev[i]));
+        acc[E->pid[i]] += dt;
+        tot += dt;
+    }
+    for (int i = 0; i < EVA_PROF_OPS; i++) {
+        fprintf(stderr, "prof gpu %-12s %8.3f ms  %5.1f%%\n", ev_opname[i], acc[i], 100 * acc[i] / tot);
+        if (ms) ms[i] = acc[i];
+    }
+    fprintf(stderr, "prof gpu batch of %u     %8.3f ms (direct launches)\n", E->nb, tot);
+    return 0;
+}
+
+extern "C" const char *eva_profile_opname(int i) { return i >= 0 && i < EVA_PROF_OPS ? ev_opname[i] : NULL; }
 
 extern "C" void *eva_dev_input(eva *e) { return eva_ready(e) ? NULL : (void *)e->impl->in; }
 extern "C" const float *eva_dev_output(eva *e) { return eva_ready(e) ? NULL : e->impl->out; }

@@ -310,6 +310,54 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
     }
 }
 
+// The K step of a wave of a partial last row tile whose rows below M fill only its first TMV < 4 row tiles of 16:
+// those row tiles' MFMAs and promotions, with the operands, order of promotion and instructions bs_step_fixed uses
+// for them (so their accumulators are bit-identical), the others left at zero as the zero rows past M would leave
+// them. The stage's loads go out first, all at once.
+template <class C, int TMV>
+__device__ __forceinline__ void bs_step_rows(const uint8_t *st, int wm0, int wn0, v4f (&acc)[C::TM][C::TN],
+                                             const BsOperands<C> &op, uint32_t dstage, int dkb)
+{
+    static_assert(C::TM == 4 && C::TN == 8 && TMV >= 1 && TMV < 4, "partial row tiles of 64 x 128 wave tiles");
+    constexpr int LAG = 3, NM = 8 * TMV;
+    if (dkb >= 0) op.issue(dstage, dkb);
+    const int lane = threadIdx.x & 63, g = lane >> 4;
+    const uint8_t *ta = st, *tb = st + C::A_BYTES;
+    const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
+    v8i a[TMV], b[3];
+    b[0] = ld_frag(tb, wn0);
+    b[1] = ld_frag(tb, wn0 + 16);
+#pragma unroll
+    for (int i = 0; i < TMV; i++) a[i] = ld_frag(ta, wm0 + 16 * i);
+    const float swv = *(const float *)(st + C::A_BYTES + C::B_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
+    float sc[TMV][4];
+#pragma unroll
+    for (int i = 0; i < TMV; i++) {
+        const float4 s4 = *(const float4 *)(ts + wm0 + 16 * i + 4 * g);
+        sc[i][0] = s4.x * swv; sc[i][1] = s4.y * swv; sc[i][2] = s4.z * swv; sc[i][3] = s4.w * swv;
+    }
+    v4f pr[LAG + 1];
+#pragma unroll
+    for (int t = 0; t < NM + LAG; t++) {
+        if (t < NM) {
+            const int j = t / TMV, i = t % TMV;
+            mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
+            if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
+        }
+        if (t == LAG) asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // an XDL result is read 11+ slots later
+        if (t >= LAG) {
+            const int u = t - LAG, j = u / TMV, i = u % TMV;
+            const v4f p = pr[u % (LAG + 1)];
+            float x0 = acc[i][j][0], x1 = acc[i][j][1], x2 = acc[i][j][2], x3 = acc[i][j][3];
+            fmac_asm(x0, p[0], sc[i][0]);
+            fmac_asm(x1, p[1], sc[i][1]);
+            fmac_asm(x2, p[2], sc[i][2]);
+            fmac_asm(x3, p[3], sc[i][3]);
+            acc[i][j] = v4f{x0, x1, x2, x3};
+        }
+    }
+}
+
 // Kernel arguments first used after the main loop (epilogue outputs) are read by scalar loads the compiler may leave in
 // flight up to the loop. Scalar loads complete out of order, so with one pending at the loop header the compiler can
 // no longer count LDS reads exactly and waits for every fragment read of a step (lgkmcnt(0)) before its first MFMA.
@@ -329,12 +377,12 @@ struct BsNoPre {
     __device__ __forceinline__ void operator()() const {}
 };
 
-// Main loop. On return acc[i][j][r] holds output row m0 + wm0 + 16 i + 4 (lane >> 4) + r, column
+// Main loop (SKIP: waves whose rows are all past M skip their matrix work). On return acc[i][j][r] holds output row m0 + wm0 + 16 i + 4 (lane >> 4) + r, column
 // n0 + wn0 + 16 j + (lane & 15), where (wm0, wn0) = bs_wave_origin(). The block is synchronised, no load is in
 // flight and the whole shared memory is free for the epilogue. pre() runs once the first stages' loads are issued
 // (epilogue inputs can be fetched there, under the prologue's memory latency); it may write shared memory only past
 // C::LDS.
-template <class C, class Pre = BsNoPre>
+template <class C, class Pre = BsNoPre, bool SKIP = true>
 __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
                                             int lds, const uint8_t *__restrict__ W, const float *__restrict__ sw,
                                             int M, int Npad, int K, int m0, int n0, uint8_t *smem,
@@ -356,21 +404,39 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
     for (int s = 0; s < C::NS - 1; s++)
         if (s < KB) op.issue(base + s * C::STAGE, s);
     pre();
-    int cs = 0, is = C::NS - 1;  // stage computed now, stage issued now
-    for (int kb = 0; kb < KB; kb++) {
-        // stage kb must be resident; the min(NS - 2, KB - 1 - kb) stages issued after it may stay in flight
-        if (kb + C::NS - 2 < KB) wait_vmem_n<(C::NS - 2) * C::LPS>();
-        else wait_vmem();
-        lds_barrier();  // every wave's part of stage kb landed; every wave finished reading stage kb - 1
-        if constexpr (C::TM == 4 && C::TN == 8) {
-            bs_step_fixed<C>(smem + cs * C::STAGE, wm0, wn0, acc, op, base + is * C::STAGE,
-                             kb + C::NS - 1 < KB ? kb + C::NS - 1 : -1);
-        } else {
-            if (kb + C::NS - 1 < KB) op.issue(base + is * C::STAGE, kb + C::NS - 1);
-            bs_step<C>(smem + cs * C::STAGE, wm0, wn0, acc);
+    // rows of this wave below M (wave-uniform): in a partial last row tile a wave runs only the row tiles of 16 that
+    // hold such rows (a wave with none only issues its share of the loads); accumulators it skips stay zero, as the
+    // zero rows past M would leave them
+    const int live = SKIP ? M - __builtin_amdgcn_readfirstlane(m0 + wm0) : C::WM;
+    // the K loop around one kind of step (each kind runs its own copy of the loop, so their registers never meet)
+    auto kloop = [&](auto step) {
+        int cs = 0, is = C::NS - 1;  // stage computed now, stage issued now
+        for (int kb = 0; kb < KB; kb++) {
+            // stage kb must be resident; the min(NS - 2, KB - 1 - kb) stages issued after it may stay in flight
+            if (kb + C::NS - 2 < KB) wait_vmem_n<(C::NS - 2) * C::LPS>();
+            else wait_vmem();
+            lds_barrier();  // every wave's part of stage kb landed; every wave finished reading stage kb - 1
+            step(smem + cs * C::STAGE, base + is * C::STAGE, kb + C::NS - 1 < KB ? kb + C::NS - 1 : -1);
+            cs = cs == C::NS - 1 ? 0 : cs + 1;
+            is = is == C::NS - 1 ? 0 : is + 1;
         }
-        cs = cs == C::NS - 1 ? 0 : cs + 1;
-        is = is == C::NS - 1 ? 0 : is + 1;
+    };
+    if constexpr (C::TM == 4 && C::TN == 8) {
+        if (live > 32)
+            kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_fixed<C>(st, wm0, wn0, acc, op, dst, dkb); });
+        else if (live > 16)
+            kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_rows<C, 2>(st, wm0, wn0, acc, op, dst, dkb); });
+        else if (live > 0)
+            kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_rows<C, 1>(st, wm0, wn0, acc, op, dst, dkb); });
+        else
+            kloop([&](const uint8_t *, uint32_t dst, int dkb) {
+                if (dkb >= 0) op.issue(dst, dkb);
+            });
+    } else {
+        kloop([&](const uint8_t *st, uint32_t dst, int dkb) {
+            if (dkb >= 0) op.issue(dst, dkb);
+            bs_step<C>(st, wm0, wn0, acc);
+        });
     }
     lds_barrier();
 }
@@ -544,13 +610,15 @@ __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, in
     for (int s = 0; s < C::NS - 1; s++)
         if (s < KB) op.issue(base + s * C::STAGE_SP, s);
     pre();
+    // a wave whose rows are all past M skips its matrix work (accumulators stay zero)
+    const bool live = __builtin_amdgcn_readfirstlane(m0 + wm0) < M;
     int cs = 0, is = C::NS - 1;
     for (int kb = 0; kb < KB; kb++) {
         if (kb + C::NS - 2 < KB) wait_vmem_n<(C::NS - 2) * C::LPS_SP>();
         else wait_vmem();
         lds_barrier();
         if (kb + C::NS - 1 < KB) op.issue(base + is * C::STAGE_SP, kb + C::NS - 1);
-        bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT);
+        if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT);
         cs = cs == C::NS - 1 ? 0 : cs + 1;
         is = is == C::NS - 1 ? 0 : is + 1;
     }
@@ -560,15 +628,26 @@ __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, in
 }
 
 // XCD-aware tile order for a 1-D grid of T = tiles_m * tiles_n blocks. Blocks are dispatched to the 8 XCDs round
-// robin (block b -> XCD b % 8), so XCD x is given a contiguous run of a grouped raster (XT_GM row tiles walked
-// together across all column tiles): the blocks an XCD runs at once share a few A row tiles and W column tiles
-// in that XCD's L2.
-__device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int &tm, int &tn)
+// robin (block b -> XCD x = b % 8), so XCD x runs c_x = T / 8 + (x < T % 8) blocks. When the last row tile is partial
+// (rows past M), its tiles_n tiles cost far less than a full tile (the waves past M skip their matrix work), so the
+// Tf = T - tiles_n full tiles are dealt out evenly first, f_x = Tf / 8 + (x < Tf % 8) to XCD x, and the partial tiles
+// take the c_x - f_x >= 0 remaining slots, at the start of each XCD's sequence: a whole extra full tile never lands on
+// an XCD whose CUs already run as many as the others. Each XCD's full tiles are a contiguous run of a grouped raster
+// (XT_GM row tiles walked together across all column tiles): the blocks an XCD runs at once share a few A row tiles
+// and W column tiles in that XCD's L2.
+__device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, bool partial, int &tm, int &tn)
 {
-    const int T = tiles_m * tiles_n, b = blockIdx.x, x = b & 7, q = T >> 3, r = T & 7;
-    const int pos = x * q + (x < r ? x : r) + (b >> 3);
+    const int T = tiles_m * tiles_n, Tf = partial ? T - tiles_n : T, b = blockIdx.x, x = b & 7, k = b >> 3;
+    const int q = T >> 3, r = T & 7, qf = Tf >> 3, rf = Tf & 7;
+    const int npx = (q + (x < r)) - (qf + (x < rf));
+    if (k < npx) {
+        tm = tiles_m - 1;
+        tn = x * (q - qf) + (x < r ? x : r) - (x < rf ? x : rf) + k;
+        return;
+    }
+    const int pos = x * qf + (x < rf ? x : rf) + (k - npx), tmf = partial ? tiles_m - 1 : tiles_m;
     const int per_group = XT_GM * tiles_n, grp = pos / per_group, rem = pos - grp * per_group;
-    const int gm = tiles_m - grp * XT_GM < XT_GM ? tiles_m - grp * XT_GM : XT_GM;
+    const int gm = tmf - grp * XT_GM < XT_GM ? tmf - grp * XT_GM : XT_GM;
     tm = grp * XT_GM + rem % gm;
     tn = rem / gm;
 }

@@ -39,7 +39,7 @@ template <class C>
 __device__ __forceinline__ void layer_tile(int M, int N, int &m0, int &n0)
 {
     int tm, tn;
-    tile_of_block((M + C::BM - 1) / C::BM, (N + C::BN - 1) / C::BN, tm, tn);
+    tile_of_block((M + C::BM - 1) / C::BM, (N + C::BN - 1) / C::BN, M % C::BM != 0, tm, tn);
     m0 = tm * C::BM;
     n0 = tn * C::BN;
 }

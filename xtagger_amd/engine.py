@@ -95,6 +95,13 @@ class Engine:
         if lib.eva_sync(self.ref) != 0:
             raise RuntimeError("eva_sync failed")
 
+    def profile(self):
+        """eva_profile: GPU ms per op kind of one direct (non-graph) forward, summed over the layers."""
+        ms = (C.c_double * 9)()
+        if lib.eva_profile(self.ref, ms) != 0:
+            raise RuntimeError("eva_profile failed")
+        return {lib.eva_profile_opname(i).decode(): ms[i] for i in range(9)}
+
     def close(self):
         if self.open:
             lib.eva_close(self.ref)
