@@ -38,7 +38,9 @@ __device__ __forceinline__ v8bf pack_p(const v16f &s, int base)
 }
 
 // One block per (query block of 128, head pair, sequence): sequences of T tokens, q / k rows and v^T columns padded to
-// TP >= T rounded up to 64 (rows past T read as data must be finite; keys past T are masked).
+// TP >= T rounded up to 64 (rows past T read as data must be finite; keys past T are masked). When T = 64 n + 1
+// (n > 0: the wd model's 1025 tokens) the last key is not streamed as a 17th tile of one key: each lane adds it after
+// the n tiles from global memory (one score, one weight, 32 products).
 template <int DBG>
 __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
                                                const uint16_t *__restrict__ vt, uint8_t *__restrict__ o8,
@@ -51,25 +53,30 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     const int head = 2 * blockIdx.y + hsel;
     const int q0 = blockIdx.x * FA_QB + 32 * qt;
     const bool active = q0 < T;
-    const int nkt = (T + FA_KT - 1) / FA_KT;
+    const bool xkey = (T & (FA_KT - 1)) == 1 && T > FA_KT;   // the last key alone, after the tiles
+    const int nkt = xkey ? T / FA_KT : (T + FA_KT - 1) / FA_KT;
 
-    // operand loads: per stage 32 x 1 KB, 4 per wave (K: 8 contiguous KB per head; V^T: 64 rows of 128 B, stride Tp)
+    // operand loads: per stage 32 x 1 KB, 4 per wave: waves 0-1 K head 2p, 2-3 K head 2p+1, 4-5 V^T head 2p, 6-7 V^T
+    // head 2p+1 (K: 8 contiguous KB per head; V^T: 64 rows of 128 B, stride TP). The per-lane offsets are fixed; the
+    // key tile moves only the scalar offset (8 KB of K or 128 B of V^T per tile).
     const size_t hbase0 = ((size_t)b * XT_NH + 2 * blockIdx.y) * TP * XT_HD;  // elements, head 2p
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(k + hbase0, 2u * (uint32_t)TP * XT_HD * 2u);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vt + hbase0, 2u * (uint32_t)TP * XT_HD * 2u);
     const int wu = __builtin_amdgcn_readfirstlane(w);
-    const int r8 = lane >> 3, ch = (lane & 7) ^ r8;
+    const bool dk = wu < 4;
+    const int hh = (wu >> 1) & 1, r8 = lane >> 3, ch = (lane & 7) ^ r8;
+    const uint32_t kstep = dk ? FA_KT * 128u : FA_KT * 2u;
+    uint32_t voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int rowb = 8 * ((wu * 4 + i) & 7) + r8;
+        voff[i] = dk ? (uint32_t)((hh * TP + rowb) * 128 + ch * 16) : (uint32_t)((hh * XT_HD + rowb) * TP * 2 + ch * 16);
+    }
     auto issue = [&](uint8_t *st, int kt) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int seg = wu * 4 + i;                 // 0..31: [K h0 | K h1 | V h0 | V h1] x 8 segments
-            const int tsel = seg >> 3, hh = tsel & 1, rowb = 8 * (seg & 7) + r8;
-            uint32_t off;
-            if (tsel < 2) off = (uint32_t)(((hh * TP) + kt * FA_KT + rowb) * 128 + ch * 16);
-            else off = (uint32_t)(((hh * XT_HD + rowb) * TP + kt * FA_KT) * 2 + ch * 16);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(tsel < 2 ? rk : rv, (lds_void *)(st + 1024 * seg), 16, (int)off, 0,
-                                                     0, 0);
-        }
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(dk ? rk : rv, (lds_void *)(st + 1024 * (wu * 4 + i)), 16, voff[i],
+                                                     (uint32_t)kt * kstep, 0, 0);
     };
 
     // Q fragments (B operand of S^T): query q0 + l32, dims 16 step + 8 g .. + 8
@@ -82,85 +89,147 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     }
     const int jrow = 16 * ((l32 >> 3) >> 1) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);  // pi(l32)
 
+    // bit 16 u + e: the key of accumulator e of 32-key half u in the last tile lies below T
+    uint32_t kvalid = 0;
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int j = e >> 2, i = e & 3;
+            const int key = (nkt - 1) * FA_KT + 32 * u + 16 * (j >> 1) + 8 * g + 4 * (j & 1) + i;
+            kvalid |= (key < T ? 1u : 0u) << (16 * u + e);
+        }
+
     v16f o[2];
     o[0] = v16f{};
     o[1] = v16f{};
     float mrun = -INFINITY, lsum = 0.f;
 
-    issue(smem, 0);
-    for (int kt = 0; kt < nkt; kt++) {
-        uint8_t *st = smem + (kt & 1) * FA_STAGE;
+    // one key tile on a resident stage
+    auto tile = [&](const uint8_t *st, int kt) {
+        const uint8_t *tk = st + hsel * FA_TILE, *tv = st + (2 + hsel) * FA_TILE;
+        // the scores start from -mb (mb = the running max, 0 before the first tile): after the first tile they
+        // come out of the matrix core already relative to the running max, and the common no-rescale path
+        // feeds them to exp2 as they are
+        const float mb = kt == 0 ? 0.f : mrun;
+        v16f s[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) s[u][e] = -mb;
+#pragma unroll
+            for (int step = 0; step < 4; step++)
+                s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tk, 32 * u + jrow, 2 * step + g), qf[step], s[u],
+                                                              0, 0, 0);
+        }
+        if (!xkey && kt == nkt - 1 && (T & (FA_KT - 1))) {  // keys past T are padding
+            uint32_t vm = kvalid;
+            asm volatile("" : "+v"(vm));  // tested here, not as 32 lane masks held in scalar registers
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    if (!((vm >> (16 * u + e)) & 1u)) s[u][e] = -INFINITY;
+        }
+        float tmax = -INFINITY;  // relative to mb
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) tmax = __builtin_fmaxf(tmax, s[u][e]);
+        tmax = __builtin_fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mref = mrun - mb;  // the running max relative to mb: -inf on the first tile, 0 after it
+        if (__builtin_amdgcn_ballot_w64(tmax > mref + FA_RESCALE) != 0) {  // wave-uniform lazy rescale
+            const float mnew = __builtin_fmaxf(mref, tmax);
+            const float sc = __builtin_amdgcn_exp2f(mref - mnew);
+            lsum *= sc;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                o[0][e] *= sc;
+                o[1][e] *= sc;
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) s[u][e] -= mnew;
+            mrun = mb + mnew;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) s[u][e] = __builtin_amdgcn_exp2f(s[u][e]);
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int sp = 0; sp < 2; sp++) {
+                const v8bf pf = pack_p(s[u], 8 * sp);
+                // l sums the bf16 weights the PV product uses, two per v_dot2c_f32_bf16
+                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 0, 1), kOnes2, lsum, false);
+                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 2, 3), kOnes2, lsum, false);
+                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 4, 5), kOnes2, lsum, false);
+                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 6, 7), kOnes2, lsum, false);
+#pragma unroll
+                for (int dt = 0; dt < 2; dt++)
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tv, 32 * dt + l32, 4 * u + 2 * sp + g), pf,
+                                                                   o[dt], 0, 0, 0);
+            }
+    };
+
+    // two stages, the loop unrolled by two so each half's stage (and every LDS address in it) is fixed
+    uint8_t *const st0 = smem, *const st1 = smem + FA_STAGE;
+    if (nkt > 0) issue(st0, 0);
+    for (int kt = 0; kt < nkt; kt += 2) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (kt + 1 < nkt) issue(smem + ((kt + 1) & 1) * FA_STAGE, kt + 1);
-        if (active) {
-            const uint8_t *tk = st + hsel * FA_TILE, *tv = st + (2 + hsel) * FA_TILE;
-            // the scores start from -mb (mb = the running max, 0 before the first tile): after the first tile they
-            // come out of the matrix core already relative to the running max, and the common no-rescale path
-            // feeds them to exp2 as they are
-            const float mb = kt == 0 ? 0.f : mrun;
-            v16f s[2];
+        if (kt + 1 < nkt) issue(st1, kt + 1);
+        if (active) tile(st0, kt);
+        if (kt + 1 >= nkt) break;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (kt + 2 < nkt) issue(st0, kt + 2);
+        if (active) tile(st1, kt + 1);
+    }
+
+    if (xkey && active) {  // key T - 1: score from global memory, the same lazy rescale, one bf16 weight
+        const int kx = T - 1;
+        const size_t hrow = ((size_t)b * XT_NH + head) * TP * XT_HD;
+        const uint16_t *kr = k + hrow + (size_t)kx * XT_HD + 8 * g;
+        float sx = 0.f;
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-#pragma unroll
-                for (int e = 0; e < 16; e++) s[u][e] = -mb;
-#pragma unroll
-                for (int step = 0; step < 4; step++)
-                    s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tk, 32 * u + jrow, 2 * step + g), qf[step],
-                                                                  s[u], 0, 0, 0);
-            }
-            if (kt == nkt - 1 && (T & (FA_KT - 1))) {  // keys past T are padding
-#pragma unroll
-                for (int u = 0; u < 2; u++)
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const int j = e >> 2, i = e & 3;
-                        const int key = kt * FA_KT + 32 * u + 16 * (j >> 1) + 8 * g + 4 * (j & 1) + i;
-                        if (key >= T) s[u][e] = -INFINITY;
-                    }
-            }
-            float tmax = -INFINITY;  // relative to mb
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) tmax = __builtin_fmaxf(tmax, s[u][e]);
-            tmax = __builtin_fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-            const float mref = mrun - mb;  // the running max relative to mb: -inf on the first tile, 0 after it
-            if (__builtin_amdgcn_ballot_w64(tmax > mref + FA_RESCALE) != 0) {  // wave-uniform lazy rescale
-                const float mnew = __builtin_fmaxf(mref, tmax);
-                const float sc = __builtin_amdgcn_exp2f(mref - mnew);
-                lsum *= sc;
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    o[0][e] *= sc;
-                    o[1][e] *= sc;
-                }
-#pragma unroll
-                for (int u = 0; u < 2; u++)
-#pragma unroll
-                    for (int e = 0; e < 16; e++) s[u][e] -= mnew;
-                mrun = mb + mnew;
-            }
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) s[u][e] = __builtin_amdgcn_exp2f(s[u][e]);
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int sp = 0; sp < 2; sp++) {
-                    const v8bf pf = pack_p(s[u], 8 * sp);
-                    // l sums the bf16 weights the PV product uses, two per v_dot2c_f32_bf16
-                    lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 0, 1), kOnes2, lsum, false);
-                    lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 2, 3), kOnes2, lsum, false);
-                    lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 4, 5), kOnes2, lsum, false);
-                    lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 6, 7), kOnes2, lsum, false);
-#pragma unroll
-                    for (int dt = 0; dt < 2; dt++)
-                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tv, 32 * dt + l32, 4 * u + 2 * sp + g),
-                                                                       pf, o[dt], 0, 0, 0);
-                }
+        for (int s = 0; s < 4; s++) {
+            const v8bf kk = __builtin_bit_cast(v8bf, *(const uint4 *)(kr + 16 * s));
+            sx = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(qf[s], qf[s], 0, 1),
+                                                 __builtin_shufflevector(kk, kk, 0, 1), sx, false);
+            sx = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(qf[s], qf[s], 2, 3),
+                                                 __builtin_shufflevector(kk, kk, 2, 3), sx, false);
+            sx = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(qf[s], qf[s], 4, 5),
+                                                 __builtin_shufflevector(kk, kk, 4, 5), sx, false);
+            sx = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(qf[s], qf[s], 6, 7),
+                                                 __builtin_shufflevector(kk, kk, 6, 7), sx, false);
         }
+        sx += __shfl_xor(sx, 32, 64);
+        float rel = sx - mrun;  // mrun is finite: at least one tile ran
+        if (__builtin_amdgcn_ballot_w64(rel > FA_RESCALE) != 0) {
+            const float mnew = __builtin_fmaxf(0.f, rel), sc = __builtin_amdgcn_exp2f(-mnew);
+            lsum *= sc;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                o[0][e] *= sc;
+                o[1][e] *= sc;
+            }
+            rel -= mnew;
+            mrun += mnew;
+        }
+        const __bf16 pb = (__bf16)__builtin_amdgcn_exp2f(rel);
+        const float p = (float)pb;
+        lsum += g == 0 ? p : 0.f;  // one lane of each query pair counts it: the halves are summed below
+        const uint16_t *vr = vt + hrow + (size_t)kx;
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int d = 32 * dt + 8 * (e >> 2) + 4 * g + (e & 3);
+                o[dt][e] = __builtin_fmaf(p, __builtin_bit_cast(float, (uint32_t)vr[(size_t)d * TP] << 16), o[dt][e]);
+            }
     }
 
     // normalise, then E4M3 with one scale per (query, 128 columns = this head pair)
