@@ -813,15 +813,21 @@ void xo_embed(const uint16_t *in, const uint16_t *pe, const float *pos, int nb, 
     free(pef);
 }
 
+/* k_pool's order: per column, 32 groups of 32 tokens (1 + 32 g .. 32 g + 32) each summed in token order, the group
+ * sums added in group order, times 1/1024 (eva_kernels.cu:402-431 computes the same mean with its own grouping) */
 void xo_pool(const uint16_t *x, int nb, float *p)
 {
-    int b, n, t;
+    int b, n, g, t;
 
     for (b = 0; b < nb; b++)
         for (n = 0; n < XO_D; n++) {
-            float s = 0.0f;
-            for (t = 1; t < XO_T; t++) s += f16f(x[((size_t)b * XO_T + t) * XO_D + n]);
-            p[(size_t)b * XO_D + n] = s * (1.0f / 1024.0f);
+            float tot = 0.0f;
+            for (g = 0; g < 32; g++) {
+                float s = 0.0f;
+                for (t = 0; t < 32; t++) s += f16f(x[((size_t)b * XO_T + 1 + 32 * g + t) * XO_D + n]);
+                tot = g ? tot + s : s;
+            }
+            p[(size_t)b * XO_D + n] = tot * (1.0f / 1024.0f);
         }
 }
 

@@ -84,19 +84,37 @@ __global__ void __launch_bounds__(256) k_ln(const uint16_t *__restrict__ x, cons
     quant_row16(v, q + (size_t)row * XT_D, s, lds, row, lane);
 }
 
-// k_pool: mean over tokens 1..1024 of each image: x fp16 [nb * 1025][1024] -> p fp32 [nb][1024].
-// Grid (nb, 4), 128 threads, two columns per thread, tokens summed in order.
-__global__ void __launch_bounds__(128) k_pool(const uint16_t *__restrict__ x, float *__restrict__ p)
+// k_pool: mean over tokens 1..1024 of each image: x fp16 [nb * 1025][1024] -> p fp32 [nb][1024]. Grid (nb, 8) of
+// 512 threads, 128 columns per block: thread (g, c) = (t >> 4, t & 15) sums tokens 1 + 32 g .. 32 g + 32 of columns
+// 8 c .. 8 c + 7 in token order, one 16-byte load per token; a column's 32 group sums then meet in group order
+// through shared memory, and the total is scaled by 1/1024.
+__global__ void __launch_bounds__(512) k_pool(const uint16_t *__restrict__ x, float *__restrict__ p)
 {
-    const int c = blockIdx.y * 256 + 2 * threadIdx.x;
-    const uint16_t *xr = x + ((size_t)blockIdx.x * XT_T + 1) * XT_D + c;
-    float s0 = 0.f, s1 = 0.f;
-    for (int t = 0; t < XT_NP; t++) {
-        const uint32_t u = *(const uint32_t *)(xr + (size_t)t * XT_D);
-        s0 += h2f((uint16_t)(u & 0xffffu));
-        s1 += h2f((uint16_t)(u >> 16));
+    __shared__ __attribute__((aligned(16))) float red[32][128 + 4];
+    const int c = threadIdx.x & 15, g = threadIdx.x >> 4, col0 = blockIdx.y * 128;
+    const uint16_t *xr = x + ((size_t)blockIdx.x * XT_T + 1 + 32 * g) * XT_D + col0 + 8 * c;
+    float s[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) s[k] = 0.f;
+#pragma unroll 8
+    for (int t = 0; t < 32; t++) {
+        const uint4 u = *(const uint4 *)(xr + (size_t)t * XT_D);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            s[2 * k] += h2f((uint16_t)(w[k] & 0xffffu));
+            s[2 * k + 1] += h2f((uint16_t)(w[k] >> 16));
+        }
     }
-    *(float2 *)(p + (size_t)blockIdx.x * XT_D + c) = make_float2(s0 * (1.0f / XT_NP), s1 * (1.0f / XT_NP));
+    *(float4 *)&red[g][8 * c] = make_float4(s[0], s[1], s[2], s[3]);
+    *(float4 *)&red[g][8 * c + 4] = make_float4(s[4], s[5], s[6], s[7]);
+    __syncthreads();
+    if (threadIdx.x < 128) {
+        float a = red[0][threadIdx.x];
+#pragma unroll 8
+        for (int i = 1; i < 32; i++) a += red[i][threadIdx.x];
+        p[(size_t)blockIdx.x * XT_D + col0 + threadIdx.x] = a * (1.0f / XT_NP);
+    }
 }
 
 // k_lnh: final LayerNorm of the pooled rows (fc_norm) -> fp16 head input pn [nb][1024] (the reference's head
@@ -227,7 +245,7 @@ extern "C" int eva_k_ln(const void *x, const float *g, const float *b, void *q, 
 extern "C" int eva_k_pool(const void *x, float *p, int nb, void *stream)
 {
     if (nb <= 0) return xt_fail("eva_k_pool", "nb must be positive");
-    hipLaunchKernelGGL(k_pool, dim3(nb, 4), dim3(128), 0, (hipStream_t)stream, (const uint16_t *)x, p);
+    hipLaunchKernelGGL(k_pool, dim3(nb, XT_D / 128), dim3(512), 0, (hipStream_t)stream, (const uint16_t *)x, p);
     return xt_check("eva_k_pool");
 }
 

@@ -27,17 +27,21 @@ __global__ void __launch_bounds__(256) k_peak_mfma(int iters, float *__restrict_
     out[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
-// Stream copy: each thread moves 4 x 16 bytes per grid-stride step with all 4 loads issued before the stores.
-__global__ void __launch_bounds__(256) k_peak_copy(const uint4 *__restrict__ src, uint4 *__restrict__ dst, long n16)
+// Stream copy: each thread moves 4 x 16 bytes per grid-stride step with all 4 loads issued before the stores, loads
+// and stores nontemporal (streamed past the caches: 5.2 TB/s on MI355X against 4.5 TB/s for cached ones, and above
+// torch's device copy at 5.0 TB/s).
+typedef unsigned peak_v4u __attribute__((ext_vector_type(4)));
+__global__ void __launch_bounds__(256) k_peak_copy(const peak_v4u *__restrict__ src, peak_v4u *__restrict__ dst,
+                                                   long n16)
 {
     const long stride = (long)gridDim.x * 256;
     long i = (long)blockIdx.x * 256 + threadIdx.x;
     for (; i + 3 * stride < n16; i += 4 * stride) {
-        const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
-        dst[i] = a;
-        dst[i + stride] = b;
-        dst[i + 2 * stride] = c;
-        dst[i + 3 * stride] = d;
+        peak_v4u v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < 4; u++) __builtin_nontemporal_store(v[u], dst + i + u * stride);
     }
     for (; i < n16; i += stride) dst[i] = src[i];
 }
@@ -72,7 +76,7 @@ extern "C" int eva_probe_mfma_fp8(int blocks, int iters, float *out, void *strea
 extern "C" int eva_probe_copy(const void *src, void *dst, size_t bytes, void *stream)
 {
     if (bytes % 16 || (((uintptr_t)src | (uintptr_t)dst) & 15)) return xt_fail("eva_probe_copy", "16-byte multiples");
-    hipLaunchKernelGGL(k_peak_copy, dim3(8192), dim3(256), 0, (hipStream_t)stream, (const uint4 *)src, (uint4 *)dst,
+    hipLaunchKernelGGL(k_peak_copy, dim3(8192), dim3(256), 0, (hipStream_t)stream, (const peak_v4u *)src, (peak_v4u *)dst,
                        (long)(bytes / 16));
     return xt_check("eva_probe_copy");
 }
