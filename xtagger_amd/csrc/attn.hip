@@ -49,9 +49,14 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * FA_STAGE + 8 * 32 * 4];
     float *xamax = (float *)(smem + 2 * FA_STAGE);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, l32 = lane & 31;
-    const int hsel = w >> 2, qt = w & 3, b = blockIdx.z;
-    const int head = 2 * blockIdx.y + hsel;
-    const int q0 = blockIdx.x * FA_QB + 32 * qt;
+    // 1-D grid, XCD-aware: block i runs on XCD i % 8, and the query blocks of one (sequence, head pair) share its K
+    // and V^T, so they all take the same i % 8 (consecutive i / 8): their K / V^T tiles are fetched into one XCD's L2
+    // once instead of into every XCD's
+    const int nqb = (T + FA_QB - 1) / FA_QB, bi = blockIdx.x >> 3, grp = 8 * (bi / nqb) + (blockIdx.x & 7);
+    const int qb = bi - (bi / nqb) * nqb, hp = grp & (XT_NH / 2 - 1), b = grp / (XT_NH / 2);
+    const int hsel = w >> 2, qt = w & 3;
+    const int head = 2 * hp + hsel;
+    const int q0 = qb * FA_QB + 32 * qt;
     const bool active = q0 < T;
     const bool xkey = (T & (FA_KT - 1)) == 1 && T > FA_KT;   // the last key alone, after the tiles
     const int nkt = xkey ? T / FA_KT : (T + FA_KT - 1) / FA_KT;
@@ -59,7 +64,7 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     // operand loads: per stage 32 x 1 KB, 4 per wave: waves 0-1 K head 2p, 2-3 K head 2p+1, 4-5 V^T head 2p, 6-7 V^T
     // head 2p+1 (K: 8 contiguous KB per head; V^T: 64 rows of 128 B, stride TP). The per-lane offsets are fixed; the
     // key tile moves only the scalar offset (8 KB of K or 128 B of V^T per tile).
-    const size_t hbase0 = ((size_t)b * XT_NH + 2 * blockIdx.y) * TP * XT_HD;  // elements, head 2p
+    const size_t hbase0 = ((size_t)b * XT_NH + 2 * hp) * TP * XT_HD;  // elements, head 2p
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(k + hbase0, 2u * (uint32_t)TP * XT_HD * 2u);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vt + hbase0, 2u * (uint32_t)TP * XT_HD * 2u);
     const int wu = __builtin_amdgcn_readfirstlane(w);
@@ -114,14 +119,19 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
         const float mb = kt == 0 ? 0.f : mrun;
         v16f s[2];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
+        for (int u = 0; u < 2; u++)
 #pragma unroll
             for (int e = 0; e < 16; e++) s[u][e] = -mb;
+        // the two 32-key halves' chains interleaved, each K fragment read one matrix instruction ahead of its use
+        v8bf kf[2] = {frag_bf(tk, jrow, g), frag_bf(tk, 32 + jrow, g)};
 #pragma unroll
-            for (int step = 0; step < 4; step++)
-                s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tk, 32 * u + jrow, 2 * step + g), qf[step], s[u],
-                                                              0, 0, 0);
-        }
+        for (int step = 0; step < 4; step++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const v8bf f = kf[u];
+                if (step + 1 < 4) kf[u] = frag_bf(tk, 32 * u + jrow, 2 * (step + 1) + g);
+                s[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f, qf[step], s[u], 0, 0, 0);
+            }
         if (!xkey && kt == nkt - 1 && (T & (FA_KT - 1))) {  // keys past T are padding
             uint32_t vm = kvalid;
             asm volatile("" : "+v"(vm));  // tested here, not as 32 lane masks held in scalar registers
@@ -267,7 +277,7 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
                 *(float4 *)dd = make_float4(o[dt][4 * j], o[dt][4 * j + 1], o[dt][4 * j + 2], o[dt][4 * j + 3]);
             }
         }
-    if (hsel == 0 && g == 0) os[(size_t)blockIdx.y * lds + m] = sc;
+    if (hsel == 0 && g == 0) os[(size_t)hp * lds + m] = sc;
 }
 
 static int flash_launch(const char *what, const void *q, const void *k, const void *vt, void *o8, float *os, int lds,
@@ -277,7 +287,9 @@ static int flash_launch(const char *what, const void *q, const void *k, const vo
         return xt_fail(what, "bad shape (nseq, T > 0; TP >= T rounded up to 64; lds >= nseq * T)");
     if ((((uintptr_t)q) | ((uintptr_t)k) | ((uintptr_t)vt) | ((uintptr_t)o8)) & 15)
         return xt_fail(what, "q, k, vt, o8 must be 16-byte aligned");
-    const dim3 grid((T + FA_QB - 1) / FA_QB, XT_NH / 2, nseq);
+    static_assert(XT_NH / 2 == 8, "the XCD-aware block order groups 8 head pairs per sequence");
+    if ((size_t)(T + FA_QB - 1) / FA_QB * (XT_NH / 2) * nseq > 0x7fffffffu) return xt_fail(what, "grid too large");
+    const dim3 grid((T + FA_QB - 1) / FA_QB * (XT_NH / 2) * nseq);
     if (o32)
         hipLaunchKernelGGL(k_flash<1>, grid, dim3(512), 0, (hipStream_t)stream, (const uint16_t *)q, (const uint16_t *)k,
                            (const uint16_t *)vt, (uint8_t *)o8, os, lds, o32, T, TP);
