@@ -27,6 +27,11 @@ PEAK_FP8 = 5000.0   # TFLOP/s, MI355X dense FP8 (OCP E4M3) MFMA
 T, D, HID, HIDP = 1025, 1024, 2730, 2816
 
 
+def _note(msg):
+    """Progress on stderr (the result line on stdout stays the only stdout output)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def gemm_flops(M):
     return {"qkv": 2.0 * M * 3 * D * D, "oproj": 2.0 * M * D * D, "fc1": 2.0 * M * 2 * HID * D,
             "fc2": 2.0 * M * D * HID}
@@ -471,9 +476,10 @@ def bench_pixai_forward(torch, L, nb=4, nt=13461):
     return nb / (ms_b * 1e-3), ms_b
 
 
-def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False):
+def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False, profile=None):
     """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
-    resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores."""
+    resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores. profile (a
+    dict): filled with eva_profile's GPU ms per op kind of one direct forward."""
     from xtagger_amd import blob
     from xtagger_amd.engine import Engine
     path = os.path.join(os.environ.get("TMPDIR", "/tmp"), "xtag_bench_eva02_v2.bin")
@@ -487,6 +493,8 @@ def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False):
     for _ in range(2):
         e.run()
     ms_b = time_engine(torch, e, runs=iters)
+    if profile is not None:
+        profile.update({k: round(v, 3) for k, v in e.profile().items()})
     e.close()
     return nb / (ms_b * 1e-3), ms_b
 
@@ -676,8 +684,10 @@ def traffic_from_profiles():
 
 
 def profile_kernels(torch, L, M, launches=5, copy_bytes=1 << 30):
-    """Dispatches for hardware-counter passes: each layer kernel `launches` times at M rows, the four 2:4-sparse
-    layer kernels `launches` times each (on the pruned weights), then `launches` stream copies of copy_bytes (copy_bytes read + copy_bytes written per dispatch), the calibration of the byte counters."""
+    """Dispatches for hardware-counter passes: each layer kernel `launches` times at M rows, the attention `launches`
+    times on M / 1025 sequences, the four 2:4-sparse layer kernels `launches` times each (on the pruned weights), then
+    `launches` stream copies of copy_bytes (copy_bytes read + copy_bytes written per dispatch), the calibration of the
+    byte counters."""
     st = LayerStep(torch, L, M)
     for name in ("qkv", "oproj", "fc1", "fc2"):
         f = getattr(st, name)
@@ -685,6 +695,10 @@ def profile_kernels(torch, L, M, launches=5, copy_bytes=1 << 30):
             if f() != 0:
                 raise RuntimeError(name)
         torch.cuda.synchronize()
+    for _ in range(launches):                      # attention on the q / k / v^T the qkv launches wrote (nb = 8)
+        L.check(L.lib.eva_k_flash(L.ptr(st.q), L.ptr(st.k), L.ptr(st.vt), L.ptr(st.a8), L.ptr(st.as_), st.lds, st.nb,
+                                  None, st.st), "eva_k_flash")
+    torch.cuda.synchronize()
     st.make_sparse()
     for _ in range(launches):
         st.step_sp()
@@ -745,6 +759,7 @@ def main():
             "algorithmic_flops_per_launch": fl["fc1"]}
 
     qkv1, qkv1_ms = bench_qkv_m1025(torch, L)
+    _note("layer step, per-kernel and config-1 lines done")
     peaks = measured_peaks(torch, L)
     out = {"metric": METRIC, "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -767,9 +782,11 @@ def main():
         out["hipblaslt_fp8_per_tensor"] = bench_vendor(torch)
     except Exception as ex:  # the vendor path is only a reference point
         out["hipblaslt_fp8_per_tensor"] = {"error": str(ex)[:200]}
+    _note("peaks, sparse step and vendor reference done")
     out["prep_image_3072x2048"] = bench_prep(torch, L)
     out["attention_pixai_shapes"] = bench_attention_seq(torch, L)
     out["pixai_block_b4"] = bench_pixai_block(torch, L)
+    _note("producer, PixAI attention and block done")
     if not args.no_forward:
         ips, fms = bench_pixai_forward(torch, L)
         out["pixai_forward_b4"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
@@ -779,15 +796,19 @@ def main():
     out["ln_m32800"] = {"us": round(ln_us, 2), "gbs": round(ln_gbs, 1), "frac_hbm_peak": round(ln_gbs / 8000.0, 3),
                         "bytes": 32 * T * D * 3 + 32 * T * 8 * 4}
     if not args.no_forward:
-        ips, fms = bench_forward(torch)
+        prof = {}
+        ips, fms = bench_forward(torch, profile=prof)
         out["forward_b32"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
-                              "tflops": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1)}
+                              "tflops": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1),
+                              "eva_profile_ms": prof}
+        _note("forward b32 done")
         ips, fms = bench_forward(torch, sparse=True)
         out["forward_b32_sparse24"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
                                        "tflops_dense_equivalent": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1)}
         # 64 sequences of 1025 tokens (16 images x (1 full view + 0-4 crops), made by the GPU producer) and a
         # 13461-row head
         out["forward_ragged64_head13461"] = bench_forward_ragged(torch, L)
+        _note("sparse and ragged forwards done")
     if not args.no_cpu:
         from oracle import oracle as O
         legs, thr, secs = cpu_baseline(O)
