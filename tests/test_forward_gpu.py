@@ -9,7 +9,8 @@
    weights (its "dense-decoded reference"), and the sparse engine's graph returns that validated sequence's bits.
 3. Free running, the GPU and the oracle drift apart through the per-layer E4M3 re-quantization exactly as the oracle
    drifts from itself when only its fp32 summation order changes (tests/golden/forward_self_divergence.json); the
-   GPU's drift is held to 3x that envelope. The strict 2e-3 bound cannot hold free running for any implementation
+   GPU's drift is held to 2x that envelope, with a top-50 overlap within 6 tags of the oracle's overlap with itself.
+   The strict 2e-3 bound cannot hold free running for any implementation
    whose sums are ordered differently from the oracle's: the oracle against itself breaks it (0.053).
 """
 import json
@@ -227,8 +228,11 @@ def test_forward_free_running_envelope(dev, orc, synth_blob):
          f"order only): max {env['sigmoid_max_abs_diff']:.3e} mean {env['sigmoid_mean_abs_diff']:.3e} "
          f"top-50 overlap {env['top50_overlap']}")
     assert np.isfinite(got).all()
-    assert d.max() <= 3 * env["sigmoid_max_abs_diff"]
-    assert d.mean() <= 3 * env["sigmoid_mean_abs_diff"]
+    # the GPU's drift from the oracle is of the size of the oracle's drift from itself: within twice its envelope, and
+    # the top-50 tag sets overlap about as much (GPU runs have measured 1.6x the envelope and 43 common tags)
+    assert d.max() <= 2 * env["sigmoid_max_abs_diff"]
+    assert d.mean() <= 2 * env["sigmoid_mean_abs_diff"]
+    assert top >= env["top50_overlap"] - 6
 
 
 def test_partial_batch_and_head_rows(dev, synth_blob):
