@@ -139,7 +139,8 @@ int eva_k_flash_seq(const void *q, const void *k, const void *vt, void *o8, floa
 int eva_k_oproj(const void *a8, const float *as, int lds, const void *w, const float *ws, void *x, int rows,
                 void *stream);
 /* fc1 + SwiGLU + E4M3 repack + row partials (eva_kernels.cu:211-279 k_fc1): h8 [rows][1024] x W12 [5632][1024]
- * (16-unit g / x chunks) -> m8 [rows][2816] E4M3, ms [22][lds], stat [22][lds][2] = (sum h, sum h^2). */
+ * (16-unit g / x chunks) -> m8 [rows][2816] E4M3, ms [22][lds], stat [22][lds][2] = (sum h, sum h^2). The pad units
+ * 2730..2815 must have zero weights (they are read as zero from row 5472 on). */
 int eva_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8, float *ms,
               float *stat, int rows, void *stream);
 /* fc2 with the MLP LayerNorm folded + residual (eva_kernels.cu:286-334 k_fc2): x += rstd (m8 . W~^T - mean c) + d */

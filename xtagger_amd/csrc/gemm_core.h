@@ -386,7 +386,7 @@ template <class C, class Pre = BsNoPre, bool SKIP = true>
 __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
                                             int lds, const uint8_t *__restrict__ W, const float *__restrict__ sw,
                                             int M, int Npad, int K, int m0, int n0, uint8_t *smem,
-                                            v4f (&acc)[C::TM][C::TN], Pre pre = Pre())
+                                            v4f (&acc)[C::TM][C::TN], Pre pre = Pre(), int Nlive = -1)
 {
     BsOperands<C> op;
     const int KB = K >> 7;
@@ -407,7 +407,10 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
     // rows of this wave below M (wave-uniform): in a partial last row tile a wave runs only the row tiles of 16 that
     // hold such rows (a wave with none only issues its share of the loads); accumulators it skips stay zero, as the
     // zero rows past M would leave them
-    const int live = SKIP ? M - __builtin_amdgcn_readfirstlane(m0 + wm0) : C::WM;
+    // (a wave whose columns all lie at or past Nlive, the first column that is zero padding throughout, is dead too)
+    const int live = !SKIP ? C::WM
+                     : __builtin_amdgcn_readfirstlane(n0 + wn0) >= (Nlive < 0 ? Npad : Nlive) ? 0
+                                                                                               : M - __builtin_amdgcn_readfirstlane(m0 + wm0);
     // the K loop around one kind of step (each kind runs its own copy of the loop, so their registers never meet)
     auto kloop = [&](auto step) {
         int cs = 0, is = C::NS - 1;  // stage computed now, stage issued now
@@ -593,7 +596,8 @@ template <class C, class Pre = BsNoPre>
 __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
                                                int lds, const uint8_t *__restrict__ V, const uint32_t *__restrict__ X,
                                                const float *__restrict__ sw, int M, int Npad, int K, int m0, int n0,
-                                               uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre())
+                                               uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre(),
+                                               int Nlive = -1)
 {
     BsSpOperands<C> op;
     const int KB = K >> 7;
@@ -611,7 +615,8 @@ __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, in
         if (s < KB) op.issue(base + s * C::STAGE_SP, s);
     pre();
     // a wave whose rows are all past M skips its matrix work (accumulators stay zero)
-    const bool live = __builtin_amdgcn_readfirstlane(m0 + wm0) < M;
+    const bool live = __builtin_amdgcn_readfirstlane(m0 + wm0) < M &&
+                      __builtin_amdgcn_readfirstlane(n0 + wn0) < (Nlive < 0 ? Npad : Nlive);
     int cs = 0, is = C::NS - 1;
     for (int kb = 0; kb < KB; kb++) {
         if (kb + C::NS - 2 < KB) wait_vmem_n<(C::NS - 2) * C::LPS_SP>();

@@ -148,7 +148,9 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 2 * XT_HIDP, m0, n0);
     args_resident(m8, ms, stat, lds, rows);
-    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc);
+    // W12 rows past the last 16-unit chunk holding a real unit (2 x 2736) are zero padding
+    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc, BsNoPre(),
+                          2 * ((XT_HID + 15) / 16 * 16));
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int wn = wn0 / C::WN, ct = n0 >> 8;

@@ -25,14 +25,17 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b)
 }
 
 // The layer kernels take their weights dense (w, wx unused) or 2:4-sparse (SP: w = pack24 values, wx = indices).
+// Nlive (default Npad): columns from Nlive on hold zero weights throughout, so waves that own only such columns skip
+// their matrix work.
 template <class C, bool SP, class Pre = BsNoPre>
 __device__ __forceinline__ void layer_mainloop(const uint8_t *A, int lda, const float *sa, int lds, const uint8_t *w,
                                                const uint32_t *wx, const float *ws, int rows, int Npad, int K, int m0,
-                                               int n0, uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre())
+                                               int n0, uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre(),
+                                               int Nlive = -1)
 {
     static_assert(!SP || C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
-    if constexpr (SP) bs_mainloop_sp<C>(A, lda, sa, lds, w, wx, ws, rows, Npad, K, m0, n0, smem, acc, pre);
-    else bs_mainloop<C>(A, lda, sa, lds, w, ws, rows, Npad, K, m0, n0, smem, acc, pre);
+    if constexpr (SP) bs_mainloop_sp<C>(A, lda, sa, lds, w, wx, ws, rows, Npad, K, m0, n0, smem, acc, pre, Nlive);
+    else bs_mainloop<C>(A, lda, sa, lds, w, ws, rows, Npad, K, m0, n0, smem, acc, pre, Nlive);
 }
 
 template <class C>
