@@ -12,7 +12,9 @@
 // running max is refreshed only when some query of the wave grows past it by more than 8 (kern_common.cuh:480-493),
 // so p <= 2^8. l sums the bf16-rounded p that enter the PV product (the reference sums the fp32 p,
 // kern_common.cuh:505-506): the output's weights then sum to one exactly, and the row sum costs one v_dot2c per pair.
-// K and V^T tiles of 64 keys for both heads are double-buffered in LDS by buffer_load ... lds.
+// K and V^T tiles of 64 keys for both heads are double-buffered in LDS by buffer_load ... lds. The grid is 1-D and
+// XCD-aware (the query blocks of one sequence and head pair run on one XCD and share its L2 copy of K and V^T), and a
+// sequence of 64 n + 1 tokens takes its last key after the n tiles instead of as a tile of one key.
 #include "gemm_core.h"
 #include "xt_abi.h"
 
