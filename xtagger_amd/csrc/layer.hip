@@ -372,20 +372,30 @@ __global__ void __launch_bounds__(256) k_pe(const uint16_t *__restrict__ in, con
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < XT_K0P; k0 += 64) {
-        // stage: 128 rows x 8 chunks of 8 halves for A and B; chunks past column 592 are zero
+    // stage: 128 rows x 8 chunks of 8 halves for A and B; chunks past column 592 are zero. The next K step's chunks
+    // are loaded into registers while the current step's MFMAs run.
+    uint4 va[4], vb[4];
+    auto fetch = [&](int k0) {
 #pragma unroll
         for (int it = 0; it < 4; it++) {
             const int idx = t + 256 * it, row = idx >> 3, ch = idx & 7, col = k0 + 8 * ch;
-            uint4 va = make_uint4(0, 0, 0, 0), vb = make_uint4(0, 0, 0, 0);
+            va[it] = vb[it] = make_uint4(0, 0, 0, 0);
             if (col < XT_K0P) {
-                va = *(const uint4 *)(in + (size_t)(m0 + row) * XT_K0P + col);
-                vb = *(const uint4 *)(pe + (size_t)(n0 + row) * XT_K0P + col);
+                va[it] = *(const uint4 *)(in + (size_t)(m0 + row) * XT_K0P + col);
+                vb[it] = *(const uint4 *)(pe + (size_t)(n0 + row) * XT_K0P + col);
             }
-            *(uint4 *)(smem + swz(row, ch)) = va;
-            *(uint4 *)(smem + 128 * 128 + swz(row, ch)) = vb;
+        }
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < XT_K0P; k0 += 64) {
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const int idx = t + 256 * it, row = idx >> 3, ch = idx & 7;
+            *(uint4 *)(smem + swz(row, ch)) = va[it];
+            *(uint4 *)(smem + 128 * 128 + swz(row, ch)) = vb[it];
         }
         __syncthreads();
+        if (k0 + 64 < XT_K0P) fetch(k0 + 64);
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             v8h a[4], b[4];
