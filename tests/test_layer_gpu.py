@@ -240,12 +240,17 @@ def _attn_inputs(nb, seed):
     q[:, :, :T] = r.standard_normal((nb, 16, T, 64)) * 0.6
     k[:, :, :T] = r.standard_normal((nb, 16, T, 64)) * 0.6
     vt[:, :, :, :T] = r.standard_normal((nb, 16, 64, T))
-    q[0, 3, 5] *= 12.0                                        # a few peaked rows exercise the lazy rescale
-    k[0, 3, 700] = q[0, 3, 5]
+    q[0, 3, 5] *= 12.0                                        # peaked rows far above their first key tile
+    k[0, 3, 700] = q[0, 3, 5]                                 # raise the offset
     q[0, 7, 100] *= 12.0                                      # ... one whose maximum is the last key, which the
     k[0, 7, T - 1] = q[0, 7, 100]                             # kernel adds after the 16 tiles of 64 keys
     q[0, 9, T - 1] *= 12.0                                    # and the last query, alone in its query block
     k[0, 9, 3] = q[0, 9, T - 1]
+    b = nb - 1
+    q[b, 2, 50] *= 12.0                                       # a peak in an odd key tile (the loop's second stage)
+    k[b, 2, 750] = q[b, 2, 50]
+    q[b, 5, 10] *= 12.0                                       # a first key tile far below the row's other scores
+    k[b, 5, :64] = -2.0 * q[b, 5, 10]
     bf = lambda a: torch.from_numpy(a).to(torch.bfloat16)
     return bf(q), bf(k), bf(vt)
 

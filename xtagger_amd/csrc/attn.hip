@@ -8,10 +8,12 @@
 // fragment of lane l is read from key row pi(l & 31) with pi(8j + 4g + i) = 16(j >> 1) + 8g + 4(j & 1) + i, which
 // makes accumulators 8s .. 8s+7 exactly the keys 16s + 8g .. 16s + 8g + 7: P, converted to bf16 in place, is the
 // B operand of O^T += V^T P^T with V^T read as 16 contiguous bytes. No value moves between lanes.
-// Softmax runs in the exp2 domain (q carries log2(e)/8 from the weights) with the reference's lazy rescale: the
-// running max is refreshed only when some query of the wave grows past it by more than 8 (kern_common.cuh:480-493),
-// so p <= 2^8. l sums the bf16-rounded p that enter the PV product (the reference sums the fp32 p,
-// kern_common.cuh:505-506): the output's weights then sum to one exactly, and the row sum costs one v_dot2c per pair.
+// Softmax runs in the exp2 domain (q carries log2(e)/8 from the weights). The reference keeps a lazily refreshed
+// running max so that its E4M3 weights stay below 2^8 (kern_common.cuh:480-493); bf16 weights have fp32's exponent
+// range, so here each query's offset is its maximum over the first key tile and later tiles compute no maximum at all:
+// the offset is raised (that tile redone from LDS) only when a weight would pass 2^64, which the tile's weight sum
+// shows. l sums the bf16-rounded p that enter the PV product (the reference sums the fp32 p, kern_common.cuh:505-506):
+// the output's weights then sum to one exactly, and the row sum costs one v_dot2c per pair.
 // K and V^T tiles of 64 keys for both heads are double-buffered in LDS by buffer_load ... lds. The grid is 1-D and
 // XCD-aware (the query blocks of one sequence and head pair run on one XCD and share its L2 copy of K and V^T), and a
 // sequence of 64 n + 1 tokens takes its last key after the n tiles instead of as a tile of one key.
@@ -22,11 +24,17 @@
 #define FA_KT 64                     // keys per LDS tile
 #define FA_TILE (FA_KT * 128)        // bytes of one K or V^T tile of one head
 #define FA_STAGE (4 * FA_TILE)       // K head 0 | K head 1 | V^T head 0 | V^T head 1
-#define FA_RESCALE 8.0f
+#define FA_PLOG 64.0f                // weights stay below 2^FA_PLOG relative to the offset
+#define FA_PMAX 0x1p64f
+
+// K and V^T tiles: 128-byte rows whose 16-byte chunk c sits at c ^ ((row >> 1) & 7). A fragment read covers 16
+// consecutive rows per 16 lanes (one 256-byte LDS cycle): with row bits 1-3 in the swizzle and bit 0 choosing the
+// half of the 256 bytes, those rows fill all 16 slots (row & 7 alone would put rows r and r + 8 on the same banks)
+__device__ __forceinline__ uint32_t swz_kv(int row, int chunk) { return (uint32_t)(row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4)); }
 
 __device__ __forceinline__ v8bf frag_bf(const uint8_t *tile, int row, int chunk)
 {
-    return __builtin_bit_cast(v8bf, *(const uint4 *)(tile + swz(row, chunk)));
+    return __builtin_bit_cast(v8bf, *(const uint4 *)(tile + swz_kv(row, chunk)));
 }
 
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
@@ -71,12 +79,12 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vt + hbase0, 2u * (uint32_t)TP * XT_HD * 2u);
     const int wu = __builtin_amdgcn_readfirstlane(w);
     const bool dk = wu < 4;
-    const int hh = (wu >> 1) & 1, r8 = lane >> 3, ch = (lane & 7) ^ r8;
+    const int hh = (wu >> 1) & 1, r8 = lane >> 3;
     const uint32_t kstep = dk ? FA_KT * 128u : FA_KT * 2u;
     uint32_t voff[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int rowb = 8 * ((wu * 4 + i) & 7) + r8;
+    for (int i = 0; i < 4; i++) {  // lane: LDS row rowb, slot lane & 7, which holds chunk (lane & 7) ^ ((rowb >> 1) & 7)
+        const int rowb = 8 * ((wu * 4 + i) & 7) + r8, ch = (lane & 7) ^ ((rowb >> 1) & 7);
         voff[i] = dk ? (uint32_t)((hh * TP + rowb) * 128 + ch * 16) : (uint32_t)((hh * XT_HD + rowb) * TP * 2 + ch * 16);
     }
     auto issue = [&](uint8_t *st, int kt) {
@@ -112,18 +120,12 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     o[1] = v16f{};
     float mrun = -INFINITY, lsum = 0.f;
 
-    // one key tile on a resident stage
-    auto tile = [&](const uint8_t *st, int kt) {
-        const uint8_t *tk = st + hsel * FA_TILE, *tv = st + (2 + hsel) * FA_TILE;
-        // the scores start from -mb (mb = the running max, 0 before the first tile): after the first tile they
-        // come out of the matrix core already relative to the running max, and the common no-rescale path
-        // feeds them to exp2 as they are
-        const float mb = kt == 0 ? 0.f : mrun;
-        v16f s[2];
+    // scores of one 64-key tile relative to the offset off (the accumulators start from -off), padded keys -inf
+    auto scores = [&](const uint8_t *tk, int kt, float off, v16f (&s)[2]) {
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) s[u][e] = -mb;
+            for (int e = 0; e < 16; e++) s[u][e] = -off;
         // the two 32-key halves' chains interleaved, each K fragment read one matrix instruction ahead of its use
         v8bf kf[2] = {frag_bf(tk, jrow, g), frag_bf(tk, 32 + jrow, g)};
 #pragma unroll
@@ -143,28 +145,23 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
                 for (int e = 0; e < 16; e++)
                     if (!((vm >> (16 * u + e)) & 1u)) s[u][e] = -INFINITY;
         }
-        float tmax = -INFINITY;  // relative to mb
+    };
+    // the query's maximum over the tile (both lane halves)
+    auto tile_max = [&](const v16f (&s)[2]) {
+        float m0 = s[0][0], m1 = s[0][1], m2 = s[1][0], m3 = s[1][1];  // four chains, not one of 16
 #pragma unroll
-        for (int u = 0; u < 2; u++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) tmax = __builtin_fmaxf(tmax, s[u][e]);
-        tmax = __builtin_fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mref = mrun - mb;  // the running max relative to mb: -inf on the first tile, 0 after it
-        if (__builtin_amdgcn_ballot_w64(tmax > mref + FA_RESCALE) != 0) {  // wave-uniform lazy rescale
-            const float mnew = __builtin_fmaxf(mref, tmax);
-            const float sc = __builtin_amdgcn_exp2f(mref - mnew);
-            lsum *= sc;
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                o[0][e] *= sc;
-                o[1][e] *= sc;
-            }
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) s[u][e] -= mnew;
-            mrun = mb + mnew;
+        for (int e = 2; e < 16; e += 2) {
+            m0 = __builtin_fmaxf(m0, s[0][e]);
+            m1 = __builtin_fmaxf(m1, s[0][e + 1]);
+            m2 = __builtin_fmaxf(m2, s[1][e]);
+            m3 = __builtin_fmaxf(m3, s[1][e + 1]);
         }
+        const float t = __builtin_fmaxf(__builtin_fmaxf(m0, m1), __builtin_fmaxf(m2, m3));
+        return __builtin_fmaxf(t, __shfl_xor(t, 32, 64));
+    };
+    // p = exp2(s) as the bf16 B operands of the PV product, and the sum of those bf16 values (two per v_dot2c)
+    auto weights = [&](v16f (&s)[2], v8bf (&pf)[4]) {
+        float t[2] = {0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
@@ -173,17 +170,63 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
         for (int u = 0; u < 2; u++)
 #pragma unroll
             for (int sp = 0; sp < 2; sp++) {
-                const v8bf pf = pack_p(s[u], 8 * sp);
-                // l sums the bf16 weights the PV product uses, two per v_dot2c_f32_bf16
-                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 0, 1), kOnes2, lsum, false);
-                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 2, 3), kOnes2, lsum, false);
-                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 4, 5), kOnes2, lsum, false);
-                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 6, 7), kOnes2, lsum, false);
+                const v8bf f = pack_p(s[u], 8 * sp);
+                pf[2 * u + sp] = f;
+                t[u] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(f, f, 0, 1), kOnes2, t[u], false);
+                t[u] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(f, f, 2, 3), kOnes2, t[u], false);
+                t[u] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(f, f, 4, 5), kOnes2, t[u], false);
+                t[u] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(f, f, 6, 7), kOnes2, t[u], false);
+            }
+        return t[0] + t[1];
+    };
+
+    // one key tile on a resident stage. Each query's scores are taken relative to an offset mrun: the first tile
+    // sets it to the query's maximum over that tile, and it is raised only when a later tile's weights would pass
+    // 2^FA_PLOG (their bf16 sum, per lane, is the test), so no tile spends instructions on a running maximum
+    auto tile = [&](const uint8_t *st, int kt) {
+        const uint8_t *tk = st + hsel * FA_TILE, *tv = st + (2 + hsel) * FA_TILE;
+        v16f s[2];
+        v8bf pf[4];
+        float tl;
+        // at most two passes: the first tile's one pass sets the offset (key 0 is never padding, so its maximum is
+        // finite); a later tile takes a second pass, with the offset raised to its maximum, only if a weight passed
+        // the bound in the first
+        bool fix = kt == 0;
+        float off = kt == 0 ? 0.f : mrun;
+        for (;;) {
+            scores(tk, kt, off, s);
+            if (fix) {
+                const float tm = tile_max(s), mnew = kt == 0 ? tm : __builtin_fmaxf(tm, 0.f);
+                if (kt != 0) {
+                    const float sc = __builtin_amdgcn_exp2f(-mnew);
+                    lsum *= sc;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        o[0][e] *= sc;
+                        o[1][e] *= sc;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) s[u][e] -= mnew;
+                mrun = off + mnew;
+            }
+            tl = weights(s, pf);
+            if (fix || __builtin_amdgcn_ballot_w64(!(tl <= FA_PMAX)) == 0) break;  // wave-uniform
+            fix = true;
+            off = mrun;
+        }
+        lsum += tl;
+        // O^T += V^T P^T over the tile's four 16-key groups
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int sp = 0; sp < 2; sp++)
 #pragma unroll
                 for (int dt = 0; dt < 2; dt++)
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tv, 32 * dt + l32, 4 * u + 2 * sp + g), pf,
-                                                                   o[dt], 0, 0, 0);
-            }
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_bf(tv, 32 * dt + l32, 4 * u + 2 * sp + g),
+                                                                   pf[2 * u + sp], o[dt], 0, 0, 0);
     };
 
     // two stages, the loop unrolled by two so each half's stage (and every LDS address in it) is fixed
@@ -201,7 +244,7 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
         if (active) tile(st1, kt + 1);
     }
 
-    if (xkey && active) {  // key T - 1: score from global memory, the same lazy rescale, one bf16 weight
+    if (xkey && active) {  // key T - 1: score from global memory, the same offset test, one bf16 weight
         const int kx = T - 1;
         const size_t hrow = ((size_t)b * XT_NH + head) * TP * XT_HD;
         const uint16_t *kr = k + hrow + (size_t)kx * XT_HD + 8 * g;
@@ -220,7 +263,7 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
         }
         sx += __shfl_xor(sx, 32, 64);
         float rel = sx - mrun;  // mrun is finite: at least one tile ran
-        if (__builtin_amdgcn_ballot_w64(rel > FA_RESCALE) != 0) {
+        if (__builtin_amdgcn_ballot_w64(rel > FA_PLOG) != 0) {
             const float mnew = __builtin_fmaxf(0.f, rel), sc = __builtin_amdgcn_exp2f(-mnew);
             lsum *= sc;
 #pragma unroll
