@@ -1,5 +1,5 @@
 """Writes forward_self_divergence.json: how far the oracle's own full wd forward moves when only its fp32 GEMM
-summation order changes (scalar fma chain vs 8-lane AVX2), on the synthetic seed-0 model and one seed-1 image.
+summation order changes (scalar fma chain vs 8-lane AVX2), on the synthetic seed-0 model and two seed-1 images.
 The GPU forward is held to a multiple of this envelope (tests/test_forward_gpu.py). CPU only (~2 minutes).
 
     python tests/golden/make_forward_divergence.py
@@ -19,16 +19,16 @@ from xtagger_amd import blob  # noqa: E402
 
 def main():
     m = blob.synth_model(seed=0, nt=10861)
-    x = blob.synth_inputs(1, seed=1)
+    x = blob.synth_inputs(2, seed=1)
     os.environ.pop("XO_SCALAR", None)
     a, _ = O.forward(m, x, nl=24)
     os.environ["XO_SCALAR"] = "1"
     b, _ = O.forward(m, x, nl=24)
     d = np.abs(a - b)
-    top = len(set(np.argsort(-a[0])[:50]) & set(np.argsort(-b[0])[:50]))
-    out = {"model": "xtagger_amd.blob.synth_model(seed=0, nt=10861)", "input": "synth_inputs(1, seed=1)",
+    tops = [len(set(np.argsort(-a[i])[:50]) & set(np.argsort(-b[i])[:50])) for i in range(2)]
+    out = {"model": "xtagger_amd.blob.synth_model(seed=0, nt=10861)", "input": "synth_inputs(2, seed=1)",
            "layers": 24, "sigmoid_max_abs_diff": float(d.max()), "sigmoid_mean_abs_diff": float(d.mean()),
-           "top50_overlap": top}
+           "top50_overlap_per_image": tops, "top50_overlap": float(np.mean(tops))}
     with open(os.path.join(HERE, "forward_self_divergence.json"), "w") as f:
         json.dump(out, f, indent=1)
     print(out)

@@ -107,8 +107,28 @@ def test_f16_rne_vs_torch(orc):
 
 
 # ---------------------------------------------------------------- block packing
+def _pow2_scale(amax):
+    """The least power of two s with 448 s >= amax (exact: frexp of the float64 quotient), 1 below 2^-116."""
+    amax = np.asarray(amax, np.float64)
+    m, e = np.frexp(amax / 448.0)
+    s = np.ldexp(1.0, np.where(m == 0.5, e - 1, e))
+    return np.where(amax < 2.0 ** -116, 1.0, s).astype(np.float32)
+
+
+def test_block_scale_rule(orc):
+    """xo_block_scale: a power of two with amax / 448 <= s < amax / 224, on every binade edge and around 1.75."""
+    v = [2.0 ** -116, 2.0 ** -100, 1e-30, 0.5, 1.0, 1.75, np.nextafter(np.float32(1.75), np.float32(2)), 1.9999999,
+         447.0, 448.0, np.nextafter(np.float32(448), np.float32(1e9)), 449.0, 896.0, 3e38]
+    v = np.array(v, np.float32)
+    got = np.array([orc.lib.xo_block_scale(float(a)) for a in v], np.float32)
+    assert (got == _pow2_scale(v)).all()
+    assert (np.frexp(got)[0] == 0.5).all()
+    assert (448.0 * got.astype(np.float64) >= v).all() and (224.0 * got.astype(np.float64) < v).all()
+    assert orc.lib.xo_block_scale(0.0) == 1.0 and orc.lib.xo_block_scale(2.0 ** -117) == 1.0
+
+
 def _blocks_ok(x, q, s, orc):
-    """decode(q) * s reconstructs x to E4M3 precision; the block max lands on +-448."""
+    """decode(q) * s reconstructs x to E4M3 precision; the block max (in (224, 448] before rounding) decodes into [224, 448]."""
     M, K = x.shape
     dq = orc.e4m3_decode(q)[:, :K].reshape(M, K // 128, 128)
     sc = s[:, :M].T[:, :, None]
@@ -117,7 +137,8 @@ def _blocks_ok(x, q, s, orc):
     assert (err <= np.maximum(np.abs(xr) * 2.0 ** -4, sc * 2.0 ** -10) * 1.0001).all()
     amax = np.abs(xr).max(2)
     nz = amax >= 2.0 ** -116
-    assert (np.abs(dq).max(2)[nz] == 448.0).all()
+    bmax = np.abs(dq).max(2)[nz]
+    assert ((bmax >= 224.0) & (bmax <= 448.0)).all()
     assert (s[:, :M].T[~nz] == 1.0).all()
 
 
@@ -130,7 +151,7 @@ def test_quant_act_vs_independent(orc):
     q, s = orc.quant_act(x, lds=70)
     xb = x.reshape(67, 4, 128)
     amax = np.abs(xb).max(2)
-    sc = np.where(amax < np.float32(2.0 ** -116), np.float32(1), amax / np.float32(448)).astype(np.float32)
+    sc = _pow2_scale(amax)
     assert (s[:, :67].T == sc).all() and (s[:, 67:] == 0).all()
     inv = (np.float32(1) / sc).astype(np.float32)
     y = np.clip(xb * inv[:, :, None], -448, 448).astype(np.float32)
@@ -148,7 +169,7 @@ def test_quant_w_vs_independent(orc):
     for nb in range(3):
         for kb in range(2):
             blk = w[nb * 128:nb * 128 + 128, kb * 128:kb * 128 + 128]
-            sc = np.float32(np.abs(blk).max()) / np.float32(448)
+            sc = _pow2_scale(np.abs(blk).max())
             assert s[nb, kb] == sc
             y = np.clip(blk / sc, -448, 448).astype(np.float32)
             ref = torch.from_numpy(y).to(torch.float8_e4m3fn).view(torch.uint8).numpy()

@@ -41,17 +41,23 @@ __device__ __forceinline__ uint32_t e4_pack4(float a, float b, float c, float d)
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(e4_clamp(c), e4_clamp(d), w, true);
 }
 
-// e4_pack4 without the clamp, for values already scaled by 1 / block_scale(|max| of their block): |x| <= |max| / (|max|
-// / 448) <= 448 (1 + 2^-22), which rounds to 448 (the next code up, 480, is past the format and the midpoint is 464),
-// so the clamp cannot change a code.
+// e4_pack4 without the clamp, for values already scaled by 1 / block_scale(|max| of their block): the scale is a power
+// of two with 448 s >= |max|, so |x| / s <= 448 exactly and the clamp cannot change a code.
 __device__ __forceinline__ uint32_t e4_pack4_scaled(float a, float b, float c, float d)
 {
     int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
 }
 
-// Block scale from a block |max|: amax / 448 (IEEE division), 1 for a zero block (|max| < 2^-116).
-__device__ __forceinline__ float block_scale(float amax) { return amax < 0x1p-116f ? 1.0f : amax / XT_E4MAX; }
+// Block scale from a block |max|: the least power of two s with 448 s >= amax (so amax / 448 <= s < amax / 224), 1 for
+// a zero block (|max| < 2^-116). With amax = f 2^e (f in [1, 2)) that is 2^(e - 8), or 2^(e - 7) when f > 1.75. A
+// power of two makes x / s exact and lets the GEMMs apply the scale inside the matrix core as an E8M0 exponent.
+__device__ __forceinline__ float block_scale(float amax)
+{
+    if (amax < 0x1p-116f) return 1.0f;
+    const uint32_t u = __float_as_uint(amax);
+    return __uint_as_float(((u >> 23) - 8u + ((u & 0x7FFFFFu) > 0x600000u ? 1u : 0u)) << 23);
+}
 
 // ---- bf16 / fp16 (round to nearest even) ----
 __device__ __forceinline__ uint16_t f2bf(float x)
