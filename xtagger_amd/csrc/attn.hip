@@ -305,7 +305,7 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     __syncthreads();
     if (!active) return;
     amax = __builtin_fmaxf(amax, xamax[(w ^ 4) * 32 + l32]);
-    const float sc = block_scale(amax), inv = 1.0f / sc;
+    const float sc = block_scale(amax), inv = block_scale_inv(sc);
     const int query = q0 + l32;
     if (query >= T) return;
     const size_t m = (size_t)b * T + query;

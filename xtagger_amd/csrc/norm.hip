@@ -47,7 +47,7 @@ __device__ __forceinline__ void quant_row16(const float *v, uint8_t *__restrict_
 #pragma unroll
         for (int j = 0; j < 8; j++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[8 * h + j]));
         amax = group_max<16>(amax);
-        const float sc = block_scale(amax), inv = 1.0f / sc;
+        const float sc = block_scale(amax), inv = block_scale_inv(sc);
         const float *w = v + 8 * h;
         uint2 o;
         o.x = e4_pack4(w[0] * inv, w[1] * inv, w[2] * inv, w[3] * inv);

@@ -208,7 +208,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restri
             }
             amax = row16_max(amax);
             const float sc = block_scale(amax);
-            inv[i][r] = 1.0f / sc;
+            inv[i][r] = block_scale_inv(sc);
             const int m = m0 + wm0 + 16 * i + 4 * g + r;
             if (c16 == 0 && m < rows) ms[(size_t)blk * lds + m] = sc;
         }

@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(256) k_quant_act(const TIn *__restrict__ x, in
 #pragma unroll
         for (int i = 0; i < 8; i++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
         amax = group_max<16>(amax);
-        const float sc = block_scale(amax), inv = 1.0f / sc;
+        const float sc = block_scale(amax), inv = block_scale_inv(sc);
         uint2 o;
         o.x = e4_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
         o.y = e4_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);

@@ -58,6 +58,9 @@ __device__ __forceinline__ float block_scale(float amax)
     const uint32_t u = __float_as_uint(amax);
     return __uint_as_float(((u >> 23) - 8u + ((u & 0x7FFFFFu) > 0x600000u ? 1u : 0u)) << 23);
 }
+// 1 / s of a block scale, exactly: s = 2^e is a power of two in [2^-124, 2^121], so 1 / s = 2^-e has exponent field
+// 254 minus s's (one integer subtraction in place of an IEEE division)
+__device__ __forceinline__ float block_scale_inv(float s) { return __uint_as_float(0x7F000000u - __float_as_uint(s)); }
 
 // ---- bf16 / fp16 (round to nearest even) ----
 __device__ __forceinline__ uint16_t f2bf(float x)
