@@ -258,7 +258,8 @@ def test_engine_batch32_and_batch64_head13461_match_batch1(dev, synth_blob):
         e.close()
         ref = single[:nb, :nt0 + ex]
         d = np.abs(s - ref)
-        _say(f"  max |batch - single| {d.max():.3g}, bitwise equal rows {int((d.max(1) == 0).sum())}/{nb}")
+        _say(f"  max |batch - single| {d.max():.3g}, bitwise equal rows {int((d.max(1) == 0).sum())}/{nb}, "
+             f"differing images {np.flatnonzero(d.max(1) > 0).tolist()}")
         # every kernel computes a row from that row (or that image) alone, in an order that does not depend on where
         # the row sits in its tile: the scores are bit-identical
         assert np.array_equal(s, ref)

@@ -474,3 +474,100 @@ def test_patch_embed(dev, xt, orc):
     got = d_x.cpu().numpy().view(np.uint16)
     _check_close("x", _f16_f32(got), _f16_f32(ref), np.abs(_f16_f32(ref)).max(), 2.0 ** -10)
     assert (got[::T] == ref[::T]).all()                      # cls rows are pos[0] exactly
+
+
+@pytest.mark.parametrize("tail", [1, 8, 17, 32, 33, 64])
+def test_partial_row_tile_bit_identical(dev, xt, orc, tail):
+    """A last row tile with `tail` rows below M (its waves run only the 16-row tiles that hold such rows) gives its
+    rows bit for bit what a whole tile gives them: oproj and fc1 over M = 2048 + tail rows against the same rows of an
+    M = 2304 run (nine whole tiles)."""
+    MF, MT = 2304, 2048 + tail
+    _say(f"partial row tile of {tail} rows")
+    _, qa, sa = _packed_act(orc, MF, D, 71)
+    _, qw, sw = _packed_w(orc, D, D, 72)
+    x = (np.random.default_rng(73).standard_normal((MF, D)) * 2).astype(np.float16)
+    d_a, d_sa, d_w, d_sw = _d(qa, dev), _d(sa, dev), _d(qw, dev), _d(sw, dev)
+    outs = []
+    for rows in (MF, MT):
+        d_x = _d(x, dev)
+        _ok(xt.lib.eva_k_oproj(xt.ptr(d_a), xt.ptr(d_sa), MF, xt.ptr(d_w), xt.ptr(d_sw), xt.ptr(d_x), rows, _st()),
+            "eva_k_oproj")
+        outs.append(d_x.cpu().numpy())
+    assert np.array_equal(outs[0][:MT], outs[1][:MT])
+    assert np.array_equal(outs[1][MT:], x[MT:])               # rows past M untouched
+    r = np.random.default_rng(74)
+    w12 = (r.standard_normal((2 * HIDP, D)) * 0.02).astype(np.float32)
+    units = np.arange(HIDP)
+    pad = units[units >= 2730]
+    w12[32 * (pad // 16) + pad % 16] = 0
+    w12[32 * (pad // 16) + 16 + pad % 16] = 0
+    qw1, sw1 = orc.quant_w(w12)
+    d_w1, d_sw1 = _d(qw1, dev), _d(sw1, dev)
+    res = []
+    for rows in (MF, MT):
+        m8 = torch.zeros((MF, HIDP), dtype=torch.uint8, device=dev)
+        ms = torch.zeros((22, MF), dtype=torch.float32, device=dev)
+        st = torch.zeros((22, MF, 2), dtype=torch.float32, device=dev)
+        _ok(xt.lib.eva_k_fc1(xt.ptr(d_a), xt.ptr(d_sa), MF, xt.ptr(d_w1), xt.ptr(d_sw1), xt.ptr(m8), xt.ptr(ms),
+                             xt.ptr(st), rows, _st()), "eva_k_fc1")
+        res.append((m8.cpu().numpy(), ms.cpu().numpy(), st.cpu().numpy()))
+    (a8, as_, ast), (b8, bs, bst) = res
+    assert np.array_equal(a8[:MT], b8[:MT]) and np.array_equal(as_[:, :MT], bs[:, :MT])
+    assert np.array_equal(ast[:, :MT], bst[:, :MT])
+
+
+@pytest.mark.parametrize("tail", [8, 32])
+def test_partial_row_tile_bit_identical_fc2(dev, xt, orc, tail):
+    """fc2 (its row statistics and column terms staged while the first operands load) over M = 2048 + tail rows
+    against the same rows of a nine-tile run."""
+    MF, MT = 2304, 2048 + tail
+    r = np.random.default_rng(81)
+    h = (r.standard_normal((MF, HIDP)) * 0.3).astype(np.float32)
+    h[:, 2730:] = 0
+    qa, sa = orc.quant_act(h)
+    stat = np.stack([h.reshape(MF, 22, 128).sum(2).T, (h.astype(np.float64) ** 2).reshape(MF, 22, 128).sum(2).T], -1)
+    stat = stat.astype(np.float32)
+    _, qw, sw = _packed_w(orc, D, HIDP, 82)
+    c = (r.standard_normal(D) * 0.5).astype(np.float32)
+    d = (r.standard_normal(D) * 0.1).astype(np.float32)
+    x = (r.standard_normal((MF, D)) * 2).astype(np.float16)
+    args = [_d(t, dev) for t in (qa, sa, qw, sw, stat, c, d)]
+    outs = []
+    for rows in (MF, MT):
+        d_x = _d(x, dev)
+        _ok(xt.lib.eva_k_fc2(*(xt.ptr(t) for t in args[:2]), MF, *(xt.ptr(t) for t in args[2:]), xt.ptr(d_x), rows,
+                             _st()), "eva_k_fc2")
+        outs.append(d_x.cpu().numpy())
+    bad = np.flatnonzero((outs[0][:MT] != outs[1][:MT]).any(1))
+    assert bad.size == 0, f"rows differing: {bad.tolist()[:40]}"
+
+
+@pytest.mark.parametrize("nb", [2, 17, 32])
+def test_partial_row_tile_bit_identical_qkv(dev, xt, orc, nb):
+    """qkv over nb images (1025 nb rows: a last row tile of nb rows) against the same images inside an nb + 1 run,
+    where their rows sit in whole tiles."""
+    _say(f"k_qkv partial row tile, nb={nb}")
+    r = np.random.default_rng(91)
+    w16 = (r.standard_normal((3 * D, D)) * 0.02).astype(np.float16)
+    ang = r.random((1024, 32)) * 6.28
+    cs = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+    d_wq = torch.zeros((3 * D, D), dtype=torch.uint8, device=dev)
+    d_ws = torch.zeros((24, 8), dtype=torch.float32, device=dev)
+    scratch = torch.empty((3 * D, D), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_prep_w(xt.ptr(_d(w16, dev)), D, 3 * D, D, 3 * D, D, 1, None, xt.ptr(scratch), xt.ptr(d_wq),
+                            xt.ptr(d_ws), _st()), "prep")
+    MF = (nb + 1) * T
+    _, qa, sa = _packed_act(orc, MF, D, 92)
+    d_a, d_sa, d_cs = _d(qa, dev), _d(sa, dev), _d(cs, dev)
+    outs = []
+    for n in (nb + 1, nb):
+        kw = [torch.zeros((n, 16, TP, 64), dtype=torch.int16, device=dev) for _ in range(2)]
+        d_vt = torch.zeros((n, 16, 64, TP), dtype=torch.int16, device=dev)
+        _ok(xt.lib.eva_k_qkv(xt.ptr(d_a), xt.ptr(d_sa), MF, xt.ptr(d_wq), xt.ptr(d_ws), xt.ptr(d_cs), xt.ptr(kw[0]),
+                             xt.ptr(kw[1]), xt.ptr(d_vt), n * T, _st()), "eva_k_qkv")
+        outs.append([t.cpu().numpy()[:nb] for t in (kw[0], kw[1], d_vt)])
+    for name, a, b in zip(("q", "k", "vt"), *outs):
+        diff = a != b
+        toks = np.flatnonzero(diff.any(axis=(0, 1, 3) if name != "vt" else (0, 1, 2)))
+        imgs = np.flatnonzero(diff.reshape(nb, -1).any(1))
+        assert not diff.any(), f"{name}: images {imgs.tolist()}, tokens {toks.tolist()[:40]}"

@@ -383,17 +383,45 @@ __device__ __forceinline__ void mfma_mx_asm(v4f &acc, const v8i &a, const v8i &b
         asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
                      : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
 }
-template <int OPA>
-__device__ __forceinline__ void mfma_mx_row(v4f &acc, const v8i &a, const v8i &b, uint32_t sa, uint32_t sb)
-{
-    mfma_mx_asm<OPA>(acc, a, b, sa, sb);
-}
 __device__ __forceinline__ void mfma_mx(int i, v4f &acc, const v8i &a, const v8i &b, uint32_t sa, uint32_t sb)
 {
-    if (i == 0) mfma_mx_row<0>(acc, a, b, sa, sb);
-    else if (i == 1) mfma_mx_row<1>(acc, a, b, sa, sb);
-    else if (i == 2) mfma_mx_row<2>(acc, a, b, sa, sb);
-    else mfma_mx_row<3>(acc, a, b, sa, sb);
+    if (i == 0) mfma_mx_asm<0>(acc, a, b, sa, sb);
+    else if (i == 1) mfma_mx_asm<1>(acc, a, b, sa, sb);
+    else if (i == 2) mfma_mx_asm<2>(acc, a, b, sa, sb);
+    else mfma_mx_asm<3>(acc, a, b, sa, sb);
+}
+// The last MFMA of a K loop, with 32 wait states in the same asm statement. The compiler cannot see that these asm
+// MFMAs write the accumulators, so code it places after them (the epilogue, or a register copy it inserts where the
+// loop's paths join) may read an accumulator with VALU before the matrix core has written it; no separate statement
+// can guard that, as the copy may land between the two.
+template <int OPA>
+__device__ __forceinline__ void mfma_mx_asm_end(v4f &acc, const v8i &a, const v8i &b, uint32_t sa, uint32_t sb)
+{
+#define XT_MX_END "\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+    static_assert(OPA >= 0 && OPA < 4, "scale byte");
+    if constexpr (OPA == 0)
+        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0]" XT_MX_END
+                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
+    else if constexpr (OPA == 1)
+        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,0,0] op_sel_hi:[0,0,0]" XT_MX_END
+                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
+    else if constexpr (OPA == 2)
+        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[1,0,0]" XT_MX_END
+                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
+    else
+        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,0,0] op_sel_hi:[1,0,0]" XT_MX_END
+                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
+#undef XT_MX_END
+}
+// the step's last MFMA: with the wait states when no later K step follows (dkb < 0 at the last step of a 2-stage loop)
+__device__ __forceinline__ void mfma_mx_last(int i, bool end, v4f &acc, const v8i &a, const v8i &b, uint32_t sa,
+                                             uint32_t sb)
+{
+    if (!end) mfma_mx(i, acc, a, b, sa, sb);
+    else if (i == 0) mfma_mx_asm_end<0>(acc, a, b, sa, sb);
+    else if (i == 1) mfma_mx_asm_end<1>(acc, a, b, sa, sb);
+    else if (i == 2) mfma_mx_asm_end<2>(acc, a, b, sa, sb);
+    else mfma_mx_asm_end<3>(acc, a, b, sa, sb);
 }
 // E8M0 exponents of the activation scales of this lane's A rows wm0 + 16 i + (lane & 15), i < TMV, in byte i
 template <int TMV>
@@ -430,7 +458,8 @@ __device__ __forceinline__ void bs_step_mx(const uint8_t *st, int wm0, int wn0, 
 #pragma unroll
     for (int t = 0; t < 32; t++) {
         const int j = t >> 2, i = t & 3;
-        mfma_mx(i, acc[i][j], a[i], b[j % 3], sa, sb);
+        if (t < 31) mfma_mx(i, acc[i][j], a[i], b[j % 3], sa, sb);
+        else mfma_mx_last(i, dkb < 0, acc[i][j], a[i], b[j % 3], sa, sb);
         if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
         if (t >= 1 && t <= C::LPS && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
     }
@@ -457,7 +486,8 @@ __device__ __forceinline__ void bs_step_mx_rows(const uint8_t *st, int wm0, int 
 #pragma unroll
     for (int t = 0; t < 8 * TMV; t++) {
         const int j = t / TMV, i = t % TMV;
-        mfma_mx(i, acc[i][j], a[i], b[j % 3], sa, sb);
+        if (t < 8 * TMV - 1) mfma_mx(i, acc[i][j], a[i], b[j % 3], sa, sb);
+        else mfma_mx_last(i, dkb < 0, acc[i][j], a[i], b[j % 3], sa, sb);
         if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
     }
 }
@@ -539,9 +569,6 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
             kloop([&](const uint8_t *, uint32_t dst, int dkb) {
                 if (dkb >= 0) op.issue(dst, dkb);
             });
-        // the epilogue's VALU reads the accumulators the last MFMAs wrote from asm, which the compiler does not see:
-        // 18 wait states cover the XDL write-to-VALU-read distance
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory");
     } else if constexpr (C::TM == 4 && C::TN == 8) {
         if (live > 32)
             kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_fixed<C>(st, wm0, wn0, acc, op, dst, dkb); });
