@@ -253,6 +253,14 @@ def _attn_inputs(nb, seed):
     k[b, 2, 750] = q[b, 2, 50]
     q[b, 5, 10] *= 12.0                                       # a first key tile far below the row's other scores
     k[b, 5, :64] = -2.0 * q[b, 5, 10]
+    # the last query (its block's only one: the key tiles are split over four waves per head and merged)
+    q[b, 11, T - 1] *= 12.0                                   # its maximum in a tile of the third wave
+    k[b, 11, 900] = q[b, 11, T - 1]
+    q[b, 13, T - 1] *= 12.0                                   # its maximum at the last key, added after the tiles
+    k[b, 13, T - 1] = q[b, 13, T - 1]
+    q[b, 14, T - 1] *= 8.0                                    # every tile of the second wave far below the rest
+    for kt in (1, 5, 9, 13):
+        k[b, 14, 64 * kt:64 * kt + 64] = -2.0 * q[b, 14, T - 1]
     bf = lambda a: torch.from_numpy(a).to(torch.bfloat16)
     return bf(q), bf(k), bf(vt)
 
@@ -315,10 +323,11 @@ def test_flash_row_sums_and_permutation(dev, xt, orc):
     assert np.abs(a - b).max() <= 4e-3 * np.abs(a).max()
 
 
-@pytest.mark.parametrize("nseq,T,qstep", [(18, 576, 1), (1, 5184, 41), (3, 200, 1)])
+@pytest.mark.parametrize("nseq,T,qstep", [(18, 576, 1), (1, 5184, 41), (3, 200, 1), (2, 129, 1), (2, 385, 1)])
 def test_flash_seq_parity(dev, xt, orc, nseq, T, qstep):
     """Sequences of T tokens: the PixAI windows (9 per image x 2 images, L = 576) and its global attention (L = 5184,
-    every 41st query checked against fp64), plus a length that is not a multiple of 64 (masked keys)."""
+    every 41st query checked against fp64), a length that is not a multiple of 64 (masked keys), and lengths 128 n + 1
+    whose last query block holds one query, with key tiles that do not split evenly over four waves (2 and 6 tiles)."""
     TPad = (T + 63) // 64 * 64
     _say(f"k_flash_seq nseq={nseq} T={T}")
     r = np.random.default_rng(T)
