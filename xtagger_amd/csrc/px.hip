@@ -14,25 +14,26 @@
 typedef float v2f __attribute__((ext_vector_type(2)));
 
 // GELU with the exact normal CDF, u Phi(u) (px_kernels.cu:228-229 computes Phi as 0.5 (1 + erf(u / sqrt 2))), branch
-// free: with t = |u|, Phi(-t) = 2^Q(t), Q(t) = -t^2 / (2 ln 2) + R(t), and R a degree-7 polynomial in s = t / 3 - 1,
+// free: with t = |u|, Phi(-t) = 2^Q(t), Q(t) = -t^2 / (2 ln 2) + R(s), R a degree-7 polynomial in s = min(t / 6, 1),
 // the minimax fit (Remez exchange) to log2 Phi(-t) + t^2 / (2 ln 2) on [0, 6] (|R error| 4.7e-6); then
-// Phi(u) = 2^Q for u < 0 and 1 - 2^Q otherwise, with no cancellation on either side. In fp32 against float64:
-// Phi(-t) within 5e-6 relative on [0, 6] (R's error and the rounding of Q), so u Phi(u) within 3.4e-6 relative for
-// u >= 0. Past t = 6 R is held at R(6): Phi(-t) < 1e-9 there and comes out too large by at most a factor t / 6. One
-// v_exp_f32 and 12 fp32 operations per unit, where erff takes two divergent branches.
+// u Phi(u) = max(u, 0) - t Phi(-t) (u Phi(-t) for u < 0, u (1 - Phi(-t)) otherwise: Phi(u) + Phi(-u) = 1), one fma
+// with no cancellation on either side. In fp32 against float64: Phi(-t) within 5.2e-6 relative on [0, 6] (R's error
+// and the rounding of Q), so u Phi(u) within 3.4e-6 relative for u >= 0. Past t = 6 R is held at R(6): Phi(-t) < 1e-9
+// there and comes out too large by at most a factor t / 6. s is one multiply with the output clamp; the whole GELU is
+// one v_exp_f32 and 12 other instructions, where erff takes two divergent branches.
 __device__ __forceinline__ float gelu_erf(float u)
 {
-    const float t = __builtin_fabsf(u), s = __builtin_fmaf(__builtin_fminf(t, 6.0f), 0.333333343f, -1.0f);
-    float r = -4.012731370e-03f;
-    r = __builtin_fmaf(r, s, 1.681602933e-02f);
-    r = __builtin_fmaf(r, s, -4.095398635e-02f);
-    r = __builtin_fmaf(r, s, 9.168317169e-02f);
-    r = __builtin_fmaf(r, s, -2.038831115e-01f);
-    r = __builtin_fmaf(r, s, 4.581521153e-01f);
-    r = __builtin_fmaf(r, s, -1.225311637e+00f);
-    r = __builtin_fmaf(r, s, -3.040808201e+00f);
+    const float t = __builtin_fabsf(u), s = __builtin_fminf(__builtin_fmaxf(t * 0.166666672f, 0.0f), 1.0f);
+    float r = -5.136296153e-01f;
+    r = __builtin_fmaf(r, s, 2.873929501e+00f);
+    r = __builtin_fmaf(r, s, -7.235760689e+00f);
+    r = __builtin_fmaf(r, s, 1.102622604e+01f);
+    r = __builtin_fmaf(r, s, -1.165537453e+01f);
+    r = __builtin_fmaf(r, s, 9.463792801e+00f);
+    r = __builtin_fmaf(r, s, -6.907506466e+00f);
+    r = __builtin_fmaf(r, s, -9.999952912e-01f);
     const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(-0.72134752f, t * t, r));  // Phi(-t)
-    return u * (u < 0.0f ? e : 1.0f - e);
+    return __builtin_fmaf(-t, e, __builtin_fmaxf(u, 0.0f));
 }
 
 // ---------------------------------------------------------------------------------------------------------------
