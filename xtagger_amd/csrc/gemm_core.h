@@ -7,8 +7,11 @@
 // scales sw [Npad/128][K/128], rows padded with zeros to a multiple of 128). K % 128 == 0.
 //
 // CDNA4 mapping:
-//  - one K step = one 128-wide scale block = one v_mfma_f32_16x16x128_f8f6f4 per 16x16 output tile, so the block
-//    partial leaves the matrix core whole and is promoted with one fma per accumulator: acc = fma(p, sa*sw, acc);
+//  - one K step = one 128-wide scale block = one MFMA per 16x16 output tile. The layer GEMMs, whose scales are
+//    powers of two, use v_mfma_scale_f32_16x16x128_f8f6f4: the matrix core applies sa * sw as E8M0 exponents and
+//    accumulates in place (bs_step_mx). eva_k_gemm takes any fp32 scales: its block partial leaves the matrix core
+//    whole (v_mfma_f32_16x16x128_f8f6f4) and is promoted with one fma per accumulator, acc = fma(p, sa*sw, acc)
+//    (bs_step_fixed);
 //  - operands go HBM/L2 -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging), 1 KB = 8 rows x 128 bytes (whole
 //    cache lines) per wave instruction. The loads are issued from inline assembly: the compiler then does not track
 //    them, and its conservative "wait for every LDS DMA before any LDS read" rule (which would drain the whole
