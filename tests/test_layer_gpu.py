@@ -253,6 +253,7 @@ def _attn_inputs(nb, seed):
     k[b, 2, 750] = q[b, 2, 50]
     q[b, 5, 10] *= 12.0                                       # a first key tile far below the row's other scores
     k[b, 5, :64] = -2.0 * q[b, 5, 10]
+    k[b, 6, 500] = 20.0 * q[b, 6, 40]                         # an ordinary first tile, then one key 2^460 above it
     # the last query (its block's only one: the key tiles are split over four waves per head and merged)
     q[b, 11, T - 1] *= 12.0                                   # its maximum in a tile of the third wave
     k[b, 11, 900] = q[b, 11, T - 1]
