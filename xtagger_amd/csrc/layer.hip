@@ -209,13 +209,13 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
             q = __builtin_fmaf(v[c].z, v[c].z, q);
             q = __builtin_fmaf(v[c].w, v[c].w, q);
         }
-        amax = row8_max(amax);
+        amax = row8_absmax(amax);
         s = row8_sum(s);
         q = row8_sum(q);
-        const float sc = block_scale(amax), inv = block_scale_inv(sc);
+        const float sc = block_scale(amax);
         uint32_t w4[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) w4[c] = e4_pack4_scaled(v[c].x * inv, v[c].y * inv, v[c].z * inv, v[c].w * inv);
+        for (int c = 0; c < 4; c++) w4[c] = e4_pack4_s(v[c].x, v[c].y, v[c].z, v[c].w, sc);
         const v4u o = {w4[0], w4[1], w4[2], w4[3]};
         __builtin_amdgcn_raw_buffer_store_b128(o, rm, (int)((uint32_t)m * XT_HIDP + ct * 128 + u0), 0, 0);
         if ((idx & 7) == 0 && m < rows) {

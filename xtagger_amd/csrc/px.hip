@@ -207,7 +207,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restri
                 acc[i][j][r] = v;
                 amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
             }
-            amax = row16_max(amax);
+            amax = row16_absmax(amax);
             const float sc = block_scale(amax);
             inv[i][r] = block_scale_inv(sc);
             const int m = m0 + wm0 + 16 * i + 4 * g + r;

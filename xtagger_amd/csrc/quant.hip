@@ -48,10 +48,10 @@ __global__ void __launch_bounds__(256) k_quant_act(const TIn *__restrict__ x, in
 #pragma unroll
         for (int i = 0; i < 8; i++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
         amax = group_max<16>(amax);
-        const float sc = block_scale(amax), inv = block_scale_inv(sc);
+        const float sc = block_scale(amax);
         uint2 o;
-        o.x = e4_pack4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
-        o.y = e4_pack4(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+        o.x = e4_pack4_s(v[0], v[1], v[2], v[3], sc);
+        o.y = e4_pack4_s(v[4], v[5], v[6], v[7], sc);
         *(uint2 *)(q + (size_t)row * ldq + ch * 8) = o;
         if ((ch & 15) == 0) s[(size_t)(ch >> 4) * lds + row] = sc;
     }

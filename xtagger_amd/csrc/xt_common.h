@@ -49,6 +49,18 @@ __device__ __forceinline__ uint32_t e4_pack4_scaled(float a, float b, float c, f
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
 }
 
+// e4_pack4 of a / s, b / s, c / s, d / s for a block scale s (block_scale's rule: a power of two with 448 s >= the
+// block's |max|, so no code saturates). v_cvt_scalef32_pk_fp8_f32 divides by s inside the conversion: measured on
+// gfx950 bit-identical to multiplying by 1 / s first and converting, over every E4M3 rounding midpoint and scales
+// 2^-40 .. 2^29, so the packers save that multiply.
+__device__ __forceinline__ uint32_t e4_pack4_s(float a, float b, float c, float d, float s)
+{
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    v2s w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(v2s{0, 0}, a, b, s, false);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, c, d, s, true);
+    return __builtin_bit_cast(uint32_t, w);
+}
+
 // Block scale from a block |max|: the least power of two s with 448 s >= amax (so amax / 448 <= s < amax / 224), 1 for
 // a zero block (|max| < 2^-116). With amax = f 2^e (f in [1, 2)) that is 2^(e - 8), or 2^(e - 7) when f > 1.75. A
 // power of two makes x / s exact and lets the GEMMs apply the scale inside the matrix core as an E8M0 exponent.
@@ -130,20 +142,29 @@ __device__ __forceinline__ float row8_sum(float v)
     v += dpp_f<0x141>(v);
     return v;
 }
-__device__ __forceinline__ float row8_max(float v)
+// maxima of non-negative floats (block |max| values), which order as their bit patterns: an unsigned max folds into
+// the DPP move (v_max_u32_dpp), where a float max needs its own instruction after it
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v)
 {
-    v = __builtin_fmaxf(v, dpp_f<0xB1>(v));
-    v = __builtin_fmaxf(v, dpp_f<0x4E>(v));
-    v = __builtin_fmaxf(v, dpp_f<0x141>(v));
-    return v;
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
 }
-__device__ __forceinline__ float row16_max(float v)
+__device__ __forceinline__ float row8_absmax(float v)
 {
-    v = __builtin_fmaxf(v, dpp_f<0xB1>(v));
-    v = __builtin_fmaxf(v, dpp_f<0x4E>(v));
-    v = __builtin_fmaxf(v, dpp_f<0x141>(v));
-    v = __builtin_fmaxf(v, dpp_f<0x140>(v));
-    return v;
+    uint32_t u = __float_as_uint(v);
+    u = __builtin_elementwise_max(u, dpp_u<0xB1>(u));
+    u = __builtin_elementwise_max(u, dpp_u<0x4E>(u));
+    u = __builtin_elementwise_max(u, dpp_u<0x141>(u));
+    return __uint_as_float(u);
+}
+__device__ __forceinline__ float row16_absmax(float v)
+{
+    uint32_t u = __float_as_uint(v);
+    u = __builtin_elementwise_max(u, dpp_u<0xB1>(u));
+    u = __builtin_elementwise_max(u, dpp_u<0x4E>(u));
+    u = __builtin_elementwise_max(u, dpp_u<0x141>(u));
+    u = __builtin_elementwise_max(u, dpp_u<0x140>(u));
+    return __uint_as_float(u);
 }
 
 __device__ __forceinline__ v4f mfma_e4m3_16x16x128(v8i a, v8i b)
