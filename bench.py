@@ -476,10 +476,12 @@ def bench_pixai_forward(torch, L, nb=4, nt=13461):
     return nb / (ms_b * 1e-3), ms_b
 
 
-def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False, profile=None):
+def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False, profile=None, lanes=None):
     """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
     resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores. profile (a
-    dict): filled with eva_profile's GPU ms per op kind of one direct forward."""
+    dict): filled with eva_profile's GPU ms per op kind of one direct forward. lanes (a dict): filled with the
+    throughput of two batches in flight, bufs 0 and 1 replayed alternately on the engine's two lanes (median of 5
+    wall-clock runs of 8 batches between syncs of both lanes)."""
     from xtagger_amd import blob
     from xtagger_amd.engine import Engine
     path = os.path.join(os.environ.get("TMPDIR", "/tmp"), "xtag_bench_eva02_v2.bin")
@@ -495,6 +497,20 @@ def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False, profile=None):
     ms_b = time_engine(torch, e, runs=iters)
     if profile is not None:
         profile.update({k: round(v, 3) for k, v in e.profile().items()})
+    if lanes is not None:
+        e.submit(1, inp)
+        e.wait(1, nb)
+        ts = []
+        for _ in range(5):
+            e.sync()
+            t0 = time.perf_counter()
+            for i in range(8):
+                e.run_buf(i & 1)
+            e.sync()
+            ts.append((time.perf_counter() - t0) / 8)
+        ms_l = sorted(ts)[2] * 1e3
+        lanes.update({"images_per_s": round(nb / (ms_l * 1e-3), 1), "ms_per_batch": round(ms_l, 3),
+                      "batches_in_flight": 2})
     e.close()
     return nb / (ms_b * 1e-3), ms_b
 
@@ -796,11 +812,12 @@ def main():
     out["ln_m32800"] = {"us": round(ln_us, 2), "gbs": round(ln_gbs, 1), "frac_hbm_peak": round(ln_gbs / 8000.0, 3),
                         "bytes": 32 * T * D * 3 + 32 * T * 8 * 4}
     if not args.no_forward:
-        prof = {}
-        ips, fms = bench_forward(torch, profile=prof)
+        prof, two = {}, {}
+        ips, fms = bench_forward(torch, profile=prof, lanes=two)
         out["forward_b32"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
                               "tflops": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1),
                               "eva_profile_ms": prof}
+        out["forward_b32_two_in_flight"] = two
         _note("forward b32 done")
         ips, fms = bench_forward(torch, sparse=True)
         out["forward_b32_sparse24"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),

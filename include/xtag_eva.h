@@ -90,12 +90,16 @@ void eva_close(eva *e);                                             /* eva.h:704
 
 /* Resident-input path (no reference counterpart; used by benchmarks): the device input buffer
  * [nb][1024][592] fp16, one forward on the engine stream with no host copies, the device scores [nb][nt] fp32,
- * the engine stream, and a blocking wait on it. */
+ * the engine stream, and a blocking wait on both lanes. These address lane 0, which even bufs use: eva_submit runs
+ * even bufs on lane 0 and odd bufs on lane 1, each lane with its own activations, stream and graph, so two batches
+ * in flight overlap on the GPU. eva_run_buf replays buf's lane on the inputs standing in that lane's device buffer
+ * (the last batch submitted to it) and marks buf done like eva_submit, with no host copies. */
 void *eva_dev_input(eva *e);
 int eva_run(eva *e);
 const float *eva_dev_output(eva *e);
 void *eva_stream_handle(eva *e);
 int eva_sync(eva *e);
+int eva_run_buf(eva *e, uint32_t buf);
 /* eva.h:312-338 (eva_profile, built there with EVA_PROF): one direct (non-graph) forward with a GPU event after every
  * op, summed per op kind over the layers and printed to stderr as "prof gpu <op> <ms> <share>"; ms (may be NULL)
  * receives the EVA_PROF_OPS sums in the order eva_profile_opname(0 ..) names them: patch+embed, ln1, qkv, flash, oproj,

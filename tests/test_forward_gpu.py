@@ -354,6 +354,39 @@ def test_submit_ring_nonblocking(dev, synth_blob):
         assert np.array_equal(got[b], ref[b]), f"buf {b}"
 
 
+def test_two_lanes_replay(dev, synth_blob):
+    """Even and odd bufs run on the engine's two lanes (own activations, stream and graph). Distinct batches on bufs
+    0 and 1, then replays of both lanes in flight together (eva_run_buf): lane 0's device scores stay those of its
+    batch bit for bit, and a later submit to each lane still matches its batch."""
+    import ctypes
+    from xtagger_amd import blob
+    from xtagger_amd.engine import Engine
+    path, m = synth_blob
+    nb = 2
+    e = Engine(path, device=0, nb=nb)
+    e.ready()
+    inp = blob.synth_inputs(2 * nb, seed=91).reshape(2, nb, 1024, 592)
+    e.submit(0, inp[0])
+    e.submit(1, inp[1])
+    r0, r1 = e.wait(0, nb).copy(), e.wait(1, nb).copy()
+    assert not np.array_equal(r0, r1)
+    for _ in range(3):
+        e.run_buf(1)
+        e.run_buf(0)
+    e.sync()
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    out_t = torch.empty((nb, e.nt), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    assert hip.hipMemcpy(out_t.data_ptr(), e.dev_output(), out_t.numel() * 4, 3) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(out_t.cpu().numpy(), r0)
+    e.submit(3, inp[0])                                         # lane 1 on lane 0's batch, and the reverse
+    e.submit(2, inp[1])
+    assert np.array_equal(e.wait(3, nb), r0) and np.array_equal(e.wait(2, nb), r1)
+    e.close()
+
+
 def test_profile_per_op(dev, synth_blob):
     """eva.h:312-338: eva_profile runs one direct forward with an event after every op and returns the GPU time per op
     kind. Every kind takes time, the layer kinds dominate the total, the direct forward takes about as long as a graph

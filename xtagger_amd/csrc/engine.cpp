@@ -1,6 +1,9 @@
 // engine.cpp - the wd / EVA02-L engine behind the reference's C host API (src/engine/eva.h:573-745), on HIP for one
 // MI355X. eva_open returns at once; the bring-up (device, weights, packing, buffers, graph capture) runs on its own
 // thread and eva_ready joins it. One forward = one replay of a HIP graph captured once for nb inputs (eva.h:531-536).
+// The engine keeps two lanes, each with its own activations, stream and graph: batches submitted to even bufs run on
+// lane 0 (the engine stream), those on odd bufs on lane 1, so two batches in flight run concurrently and each fills
+// the CUs that the other's short last rounds of tiles leave idle.
 #include <hip/hip_runtime.h>
 #include <pthread.h>
 #include <stdint.h>
@@ -52,11 +55,20 @@ struct eva_impl {
     hipEvent_t hput_ev[EV_HPUT_SLOTS];                     // the last copy out of each slot
     uint32_t hput_next;
     float *scratch;
-    // activations
+    // activations of the lane ev_forward works on (lane 0 outside graph capture)
     uint16_t *in, *x, *q, *k, *vt, *pn;
     uint8_t *h8, *m8, *pq;
     float *sh, *sm, *stat, *pool, *ps, *out;
     hipGraphExec_t graph;
+    struct Acts {
+        uint16_t *in, *x, *q, *k, *vt, *pn;
+        uint8_t *h8, *m8, *pq;
+        float *sh, *sm, *stat, *pool, *ps, *out;
+    } act[2];
+    hipStream_t lst[2];                                    // lane streams (lst[0] = st)
+    hipGraphExec_t lgraph[2];                              // lane graphs (lgraph[0] = graph)
+    hipEvent_t lane_done;                                  // after the last batch submitted to lane 1
+    hipEvent_t head_ev;                                    // after the last eva_head_put's update (on st)
     // eva_profile: an event after every op of one direct forward (eva.h:71-88, 312-338), 172 ops at 24 layers
     hipEvent_t pev[256];
     uint8_t pid[256];
@@ -139,11 +151,11 @@ static int ev_mark(eva_impl *E, int id)
         if ((call) || ev_mark(E, (id))) return -1;                     \
     } while (0)
 
-// The whole forward for nb inputs on E->st (captured once into E->graph), eva.h:227-310.
-static int ev_forward(eva *e)
+// The whole forward for nb inputs on stream fst (captured once per lane into lgraph[lane]), eva.h:227-310.
+static int ev_forward(eva *e, hipStream_t fst)
 {
     eva_impl *E = e->impl;
-    void *st = (void *)E->st;
+    void *st = (void *)fst;
     const int M = (int)E->M, lds = (int)E->Mp, nb = (int)E->nb;
 
     EV_OP(eva_k_pe(E->in, E->pe, E->pos, E->x, nb, st), 0);
@@ -198,6 +210,15 @@ static int ev_pack_layer(eva_impl *E, int i)
     }
     EV_CK(eva_k_fold_cd(L.w2, L.s2, L.w216, V2_HIDP, L.mlnb, L.cn, L.dn, st));
     return 0;
+}
+
+// make lane l's activations the set ev_forward works on
+static void ev_use_lane(eva_impl *E, int l)
+{
+    const eva_impl::Acts &A = E->act[l];
+    E->in = A.in, E->x = A.x, E->q = A.q, E->k = A.k, E->vt = A.vt, E->pn = A.pn;
+    E->h8 = A.h8, E->m8 = A.m8, E->pq = A.pq;
+    E->sh = A.sh, E->sm = A.sm, E->stat = A.stat, E->pool = A.pool, E->ps = A.ps, E->out = A.out;
 }
 
 static int ev_up(eva *e)
@@ -262,25 +283,33 @@ static int ev_up(eva *e)
     XT_HIP(hipHostMalloc((void **)&E->hput, (size_t)EV_HPUT_SLOTS * EV_HPUT_SLOT, hipHostMallocDefault));
     for (int s = 0; s < EV_HPUT_SLOTS; s++) XT_HIP(hipEventCreateWithFlags(&E->hput_ev[s], hipEventDisableTiming));
 
-    // activations
-    const size_t M = E->M, Mp = E->Mp, nb = E->nb;
+    // activations, one set per lane
+    const size_t Mp = E->Mp, nb = E->nb;
     const size_t qkvb = nb * EVA_NH * 1088 * 64 * 2;
-    EV_ALLOC(E, E->in, nb * EVA_IN * 2, true);
-    EV_ALLOC(E, E->x, Mp * EVA_D * 2, true);
-    EV_ALLOC(E, E->h8, Mp * EVA_D, true);
-    EV_ALLOC(E, E->sh, 8 * Mp * 4, true);
-    EV_ALLOC(E, E->q, qkvb, true);                      // padded attention rows stay zero forever
-    EV_ALLOC(E, E->k, qkvb, true);
-    EV_ALLOC(E, E->vt, qkvb, true);
-    EV_ALLOC(E, E->m8, Mp * EVA_HIDP, true);
-    EV_ALLOC(E, E->sm, 22 * Mp * 4, true);
-    EV_ALLOC(E, E->stat, 22 * Mp * 8, true);
-    EV_ALLOC(E, E->pool, nb * EVA_D * 4, true);
-    EV_ALLOC(E, E->pn, nb * EVA_D * 2, true);
-    EV_ALLOC(E, E->pq, nb * EVA_D, true);
-    EV_ALLOC(E, E->ps, 8 * nb * 4, true);
-    EV_ALLOC(E, E->out, nb * nt * 4, true);
-    (void)M;
+    for (int l = 0; l < 2; l++) {
+        eva_impl::Acts &A = E->act[l];
+        EV_ALLOC(E, A.in, nb * EVA_IN * 2, true);
+        EV_ALLOC(E, A.x, Mp * EVA_D * 2, true);
+        EV_ALLOC(E, A.h8, Mp * EVA_D, true);
+        EV_ALLOC(E, A.sh, 8 * Mp * 4, true);
+        EV_ALLOC(E, A.q, qkvb, true);                   // padded attention rows stay zero forever
+        EV_ALLOC(E, A.k, qkvb, true);
+        EV_ALLOC(E, A.vt, qkvb, true);
+        EV_ALLOC(E, A.m8, Mp * EVA_HIDP, true);
+        EV_ALLOC(E, A.sm, 22 * Mp * 4, true);
+        EV_ALLOC(E, A.stat, 22 * Mp * 8, true);
+        EV_ALLOC(E, A.pool, nb * EVA_D * 4, true);
+        EV_ALLOC(E, A.pn, nb * EVA_D * 2, true);
+        EV_ALLOC(E, A.pq, nb * EVA_D, true);
+        EV_ALLOC(E, A.ps, 8 * nb * 4, true);
+        EV_ALLOC(E, A.out, nb * nt * 4, true);
+    }
+    XT_HIP(hipStreamCreateWithFlags(&E->lst[1], hipStreamNonBlocking));
+    E->lst[0] = E->st;
+    XT_HIP(hipEventCreateWithFlags(&E->lane_done, hipEventDisableTiming));
+    XT_HIP(hipEventCreateWithFlags(&E->head_ev, hipEventDisableTiming));
+    XT_HIP(hipEventRecord(E->lane_done, E->lst[1]));
+    XT_HIP(hipEventRecord(E->head_ev, E->st));
     for (int s = 0; s < EVA_NBUF; s++) {
         XT_HIP(hipHostMalloc((void **)&e->hout[s], nb * nt * 4, hipHostMallocDefault));
         if (nt > e->nt0) XT_HIP(hipHostMalloc((void **)&e->hpn[s], nb * EVA_D * 2, hipHostMallocDefault));
@@ -288,18 +317,22 @@ static int ev_up(eva *e)
     }
     XT_HIP(hipStreamSynchronize(E->st));
 
-    // graph capture of the forward
-    hipGraph_t g;
-    XT_HIP(hipStreamBeginCapture(E->st, hipStreamCaptureModeThreadLocal));
-    if (ev_forward(e)) {
-        (void)hipStreamEndCapture(E->st, &g);
-        return -1;
+    // graph capture of the forward, once per lane (lane 1 last, so lane 0's activations stay the current set)
+    for (int l = 1; l >= 0; l--) {
+        ev_use_lane(E, l);
+        hipGraph_t g;
+        XT_HIP(hipStreamBeginCapture(E->lst[l], hipStreamCaptureModeThreadLocal));
+        if (ev_forward(e, E->lst[l])) {
+            (void)hipStreamEndCapture(E->lst[l], &g);
+            return -1;
+        }
+        XT_HIP(hipStreamEndCapture(E->lst[l], &g));
+        XT_HIP(hipGraphInstantiate(&E->lgraph[l], g, NULL, NULL, 0));
+        XT_HIP(hipGraphDestroy(g));
+        XT_HIP(hipGraphUpload(E->lgraph[l], E->lst[l]));
+        XT_HIP(hipStreamSynchronize(E->lst[l]));
     }
-    XT_HIP(hipStreamEndCapture(E->st, &g));
-    XT_HIP(hipGraphInstantiate(&E->graph, g, NULL, NULL, 0));
-    XT_HIP(hipGraphDestroy(g));
-    XT_HIP(hipGraphUpload(E->graph, E->st));
-    XT_HIP(hipStreamSynchronize(E->st));
+    E->graph = E->lgraph[0];
     return 0;
 }
 
@@ -391,11 +424,18 @@ extern "C" int eva_submit(eva *e, uint32_t buf, uint16_t *const *in, uint32_t n)
     if (!E->stage[buf]) XT_HIP(hipHostMalloc((void **)&E->stage[buf], (size_t)E->nb * EVA_IN * 2, hipHostMallocDefault));
     else XT_HIP(hipEventSynchronize(E->done[buf]));
     xt_stage_inputs(E->stage[buf], in, n, EVA_IN);
-    if (n) XT_HIP(hipMemcpyAsync(E->in, E->stage[buf], (size_t)n * EVA_IN * 2, hipMemcpyHostToDevice, E->st));
-    XT_HIP(hipGraphLaunch(E->graph, E->st));
-    if (n) XT_HIP(hipMemcpyAsync(e->hout[buf], E->out, (size_t)n * e->nt * 4, hipMemcpyDeviceToHost, E->st));
-    if (e->hpn[buf] && n) XT_HIP(hipMemcpyAsync(e->hpn[buf], E->pn, (size_t)n * EVA_D * 2, hipMemcpyDeviceToHost, E->st));
-    XT_HIP(hipEventRecord(E->done[buf], E->st));
+    // even bufs run on lane 0 (the engine stream, where head updates are ordered too), odd bufs on lane 1, after
+    // every head update submitted before
+    const int l = buf & 1;
+    const hipStream_t s = E->lst[l];
+    const eva_impl::Acts &A = E->act[l];
+    if (l) XT_HIP(hipStreamWaitEvent(s, E->head_ev, 0));
+    if (n) XT_HIP(hipMemcpyAsync(A.in, E->stage[buf], (size_t)n * EVA_IN * 2, hipMemcpyHostToDevice, s));
+    XT_HIP(hipGraphLaunch(E->lgraph[l], s));
+    if (n) XT_HIP(hipMemcpyAsync(e->hout[buf], A.out, (size_t)n * e->nt * 4, hipMemcpyDeviceToHost, s));
+    if (e->hpn[buf] && n) XT_HIP(hipMemcpyAsync(e->hpn[buf], A.pn, (size_t)n * EVA_D * 2, hipMemcpyDeviceToHost, s));
+    XT_HIP(hipEventRecord(E->done[buf], s));
+    if (l) XT_HIP(hipEventRecord(E->lane_done, s));
     return 0;
 }
 
@@ -426,10 +466,14 @@ extern "C" int eva_head_put(eva *e, uint32_t j, const uint16_t *w, float bias)
     uint8_t *p = E->hput + (size_t)slot * EV_HPUT_SLOT;
     memcpy(p, w, EVA_D * 2);
     memcpy(p + EVA_D * 2, &bias, 4);
+    // the update waits for the batches already submitted to lane 1 (they read the head), and lane 1's later batches
+    // wait for it (head_ev); lane 0's batches are ordered with it on the engine stream
+    XT_HIP(hipStreamWaitEvent(E->st, E->lane_done, 0));
     XT_HIP(hipMemcpyAsync(E->hmaster + (size_t)j * EVA_D, p, EVA_D * 2, hipMemcpyHostToDevice, E->st));
     XT_HIP(hipMemcpyAsync(E->hb + j, p + EVA_D * 2, 4, hipMemcpyHostToDevice, E->st));
     EV_CK(ev_pack_head_rows(e, j, 1));
     XT_HIP(hipEventRecord(E->hput_ev[slot], E->st));
+    XT_HIP(hipEventRecord(E->head_ev, E->st));
     return 0;
 }
 
@@ -453,7 +497,12 @@ extern "C" void eva_close(eva *e)
     }
     (void)hipSetDevice(E->devno);
     if (E->st) (void)hipStreamSynchronize(E->st);
-    if (E->graph) (void)hipGraphExecDestroy(E->graph);
+    if (E->lst[1]) (void)hipStreamSynchronize(E->lst[1]);
+    for (int l = 0; l < 2; l++)
+        if (E->lgraph[l]) (void)hipGraphExecDestroy(E->lgraph[l]);
+    if (E->lst[1]) (void)hipStreamDestroy(E->lst[1]);
+    if (E->lane_done) (void)hipEventDestroy(E->lane_done);
+    if (E->head_ev) (void)hipEventDestroy(E->head_ev);
     for (int s = 0; s < EVA_NBUF; s++) {
         if (E->done[s]) (void)hipEventDestroy(E->done[s]);
         if (e->hout[s]) (void)hipHostFree(e->hout[s]);
@@ -484,12 +533,12 @@ extern "C" int eva_profile(eva *e, double *ms)
     XT_HIP(hipStreamSynchronize(E->st));
     if (!E->pev[0])
         for (int i = 0; i < 256; i++) XT_HIP(hipEventCreate(&E->pev[i]));
-    if (ev_forward(e) || ev_forward(e)) return -1;
+    if (ev_forward(e, E->st) || ev_forward(e, E->st)) return -1;
     E->pon = 1;
     E->pk = 1;
     E->pid[0] = 255;
     const hipError_t r0 = hipEventRecord(E->pev[0], E->st);
-    const int rc = r0 != hipSuccess ? xt_fail("eva_profile", "hipEventRecord failed") : ev_forward(e);
+    const int rc = r0 != hipSuccess ? xt_fail("eva_profile", "hipEventRecord failed") : ev_forward(e, E->st);
     E->pon = 0;
     if (rc) return -1;
     XT_HIP(hipStreamSynchronize(E->st));
@@ -522,5 +571,18 @@ extern "C" int eva_sync(eva *e)
 {
     if (eva_ready(e)) return -1;
     XT_HIP(hipStreamSynchronize(e->impl->st));
+    XT_HIP(hipStreamSynchronize(e->impl->lst[1]));
+    return 0;
+}
+extern "C" int eva_run_buf(eva *e, uint32_t buf)
+{
+    if (eva_ready(e)) return -1;
+    if (buf >= EVA_NBUF) return xt_fail("eva_run_buf", "buf >= EVA_NBUF");
+    eva_impl *E = e->impl;
+    const int l = buf & 1;
+    if (l) XT_HIP(hipStreamWaitEvent(E->lst[1], E->head_ev, 0));
+    XT_HIP(hipGraphLaunch(E->lgraph[l], E->lst[l]));
+    XT_HIP(hipEventRecord(E->done[buf], E->lst[l]));
+    if (l) XT_HIP(hipEventRecord(E->lane_done, E->lst[1]));
     return 0;
 }

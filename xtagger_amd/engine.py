@@ -91,6 +91,10 @@ class Engine:
         if lib.eva_run(self.ref) != 0:
             raise RuntimeError("eva_run failed")
 
+    def run_buf(self, buf):
+        if lib.eva_run_buf(self.ref, buf) != 0:
+            raise RuntimeError("eva_run_buf failed")
+
     def sync(self):
         if lib.eva_sync(self.ref) != 0:
             raise RuntimeError("eva_sync failed")
