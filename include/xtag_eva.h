@@ -263,12 +263,14 @@ int px_submit(px *p, uint32_t buf, uint16_t *const *in, uint32_t n);
 int px_query(px *p, uint32_t buf);                                  /* px.h:421 */
 const float *px_wait(px *p, uint32_t buf);                          /* px.h:426: scores [n][nt] */
 void px_close(px *p);                                               /* px.h:457 */
-/* Resident-input path, as eva_dev_input .. eva_sync (no reference counterpart; used by benchmarks and tests) */
+/* Resident-input path, as eva_dev_input .. eva_run_buf (no reference counterpart; used by benchmarks and tests): lane
+ * 0's buffers and stream; px_submit runs even bufs on lane 0 and odd bufs on lane 1; px_sync waits for both lanes. */
 void *px_dev_input(px *p);
 int px_run(px *p);
 const float *px_dev_output(px *p);
 void *px_stream_handle(px *p);
 int px_sync(px *p);
+int px_run_buf(px *p, uint32_t buf);
 
 /* ---- PixAI tagger (ViTDet-L) block kernels on the same block-scaled main loop (px_kernels.cu) ----
  * Rows are window-major tokens (px_kernels.cu:1-4): sequence s = rows L s .. L s + L - 1 with L = 576 (windowed

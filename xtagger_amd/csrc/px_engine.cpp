@@ -2,7 +2,9 @@
 // (src/engine/px.h:110-494), on HIP for one MI355X, with the same lifecycle as the wd engine: px_open returns at once;
 // the bring-up (device, weights, packing, buffers, graph capture) runs on its own thread and px_ready joins it. One
 // forward = one replay of a HIP graph captured once for nb inputs: patch embedding + pre-LN, 32 blocks (global
-// attention in blocks 7, 15, 23, 31, px.h:38), the attention-pool head and the tag head (px.h:110-190).
+// attention in blocks 7, 15, 23, 31, px.h:38), the attention-pool head and the tag head (px.h:110-190). As in the wd
+// engine, even bufs run on lane 0 and odd bufs on lane 1, each with its own activations, stream and graph, so two
+// batches in flight run at once.
 #include <hip/hip_runtime.h>
 #include <pthread.h>
 #include <stdint.h>
@@ -43,11 +45,19 @@ struct px_impl {
     float *hs;                                          // 1x128 scale planes [8][ldh]
     uint32_t ldh;                                       // nt rounded up to 64
     float *scratch;
-    // activations
+    // activations of the lane px_forward works on (lane 0 outside graph capture)
     uint16_t *in, *x, *q, *k, *vt, *y;
     uint8_t *h8, *o8, *m8, *oq;
     float *sh, *so8, *sm, *s, *stat, *part, *o, *oqs, *out;
     hipGraphExec_t graph;
+    // two lanes, each with its own activations, stream and graph: even bufs run on lane 0 (st), odd bufs on lane 1
+    struct Acts {
+        uint16_t *in, *x, *q, *k, *vt, *y;
+        uint8_t *h8, *o8, *m8, *oq;
+        float *sh, *so8, *sm, *s, *stat, *part, *o, *oqs, *out;
+    } act[2];
+    hipStream_t lst[2];
+    hipGraphExec_t lgraph[2];
     hipEvent_t done[PX_NBUF];
     uint16_t *stage[PX_NBUF];                           // pinned staging of each buf's inputs (at its first submit)
     std::vector<void *> allocs;
@@ -118,11 +128,21 @@ static int px_layout(px_impl *E, uint32_t ntp)
     return 0;
 }
 
-// The whole forward for nb inputs on E->st (captured once into E->graph), px.h:110-190.
-static int px_forward(px *p)
+// make lane l's activations the set px_forward works on
+static void px_use_lane(px_impl *E, int l)
+{
+    const px_impl::Acts &A = E->act[l];
+    E->in = A.in, E->x = A.x, E->q = A.q, E->k = A.k, E->vt = A.vt, E->y = A.y;
+    E->h8 = A.h8, E->o8 = A.o8, E->m8 = A.m8, E->oq = A.oq;
+    E->sh = A.sh, E->so8 = A.so8, E->sm = A.sm, E->s = A.s, E->stat = A.stat, E->part = A.part, E->o = A.o;
+    E->oqs = A.oqs, E->out = A.out;
+}
+
+// The whole forward for nb inputs on stream fst (captured once per lane into lgraph[lane]), px.h:110-190.
+static int px_forward(px *p, hipStream_t fst)
 {
     px_impl *E = p->impl;
-    void *st = (void *)E->st;
+    void *st = (void *)fst;
     const int M = (int)E->M, nb = (int)E->nb;
 
     PX_CK(px_k_pe(E->in, E->pe, E->x, M, st));
@@ -212,44 +232,54 @@ static int px_up(px *p)
     PX_ALLOC(E, E->hs, (size_t)8 * E->ldh * 4, true);
     PX_CK(eva_k_quant_act(E->hw16, 2, EVA_D, (int)p->nt, EVA_D, E->hq, EVA_D, E->hs, (int)E->ldh, (void *)E->st));
 
-    // activations
+    // activations, one set per lane
     const size_t M = E->M, nb = E->nb;
-    PX_ALLOC(E, E->in, nb * PX_IN * 2, true);
-    PX_ALLOC(E, E->x, M * EVA_D * 2, true);
-    PX_ALLOC(E, E->h8, M * EVA_D, true);
-    PX_ALLOC(E, E->sh, 8 * M * 4, true);
-    PX_ALLOC(E, E->q, M * EVA_D * 2, true);
-    PX_ALLOC(E, E->k, M * EVA_D * 2, true);
-    PX_ALLOC(E, E->vt, M * EVA_D * 2, true);
-    PX_ALLOC(E, E->o8, M * EVA_D, true);
-    PX_ALLOC(E, E->so8, 8 * M * 4, true);
-    PX_ALLOC(E, E->m8, M * PX_HID, true);
-    PX_ALLOC(E, E->sm, (PX_HID / 128) * M * 4, true);
-    PX_ALLOC(E, E->y, M * EVA_D * 2, true);
-    PX_ALLOC(E, E->s, M * 16 * 4, true);
-    PX_ALLOC(E, E->stat, nb * (PX_T / PX_PW) * 16 * 2 * 4, true);
-    PX_ALLOC(E, E->part, nb * (PX_T / PX_QW) * 16 * EVA_D * 4, true);
-    PX_ALLOC(E, E->o, nb * EVA_D * 4, true);
-    PX_ALLOC(E, E->oq, nb * EVA_D, true);
-    PX_ALLOC(E, E->oqs, 8 * nb * 4, true);
-    PX_ALLOC(E, E->out, nb * p->nt * 4, true);
+    for (int l = 0; l < 2; l++) {
+        px_impl::Acts &A = E->act[l];
+        PX_ALLOC(E, A.in, nb * PX_IN * 2, true);
+        PX_ALLOC(E, A.x, M * EVA_D * 2, true);
+        PX_ALLOC(E, A.h8, M * EVA_D, true);
+        PX_ALLOC(E, A.sh, 8 * M * 4, true);
+        PX_ALLOC(E, A.q, M * EVA_D * 2, true);
+        PX_ALLOC(E, A.k, M * EVA_D * 2, true);
+        PX_ALLOC(E, A.vt, M * EVA_D * 2, true);
+        PX_ALLOC(E, A.o8, M * EVA_D, true);
+        PX_ALLOC(E, A.so8, 8 * M * 4, true);
+        PX_ALLOC(E, A.m8, M * PX_HID, true);
+        PX_ALLOC(E, A.sm, (PX_HID / 128) * M * 4, true);
+        PX_ALLOC(E, A.y, M * EVA_D * 2, true);
+        PX_ALLOC(E, A.s, M * 16 * 4, true);
+        PX_ALLOC(E, A.stat, nb * (PX_T / PX_PW) * 16 * 2 * 4, true);
+        PX_ALLOC(E, A.part, nb * (PX_T / PX_QW) * 16 * EVA_D * 4, true);
+        PX_ALLOC(E, A.o, nb * EVA_D * 4, true);
+        PX_ALLOC(E, A.oq, nb * EVA_D, true);
+        PX_ALLOC(E, A.oqs, 8 * nb * 4, true);
+        PX_ALLOC(E, A.out, nb * p->nt * 4, true);
+    }
+    XT_HIP(hipStreamCreateWithFlags(&E->lst[1], hipStreamNonBlocking));
+    E->lst[0] = E->st;
     for (int s = 0; s < PX_NBUF; s++) {
         XT_HIP(hipHostMalloc((void **)&p->hout[s], nb * p->nt * 4, hipHostMallocDefault));
         XT_HIP(hipEventCreateWithFlags(&E->done[s], hipEventDisableTiming));
     }
     XT_HIP(hipStreamSynchronize(E->st));
 
-    hipGraph_t g;
-    XT_HIP(hipStreamBeginCapture(E->st, hipStreamCaptureModeThreadLocal));
-    if (px_forward(p)) {
-        (void)hipStreamEndCapture(E->st, &g);
-        return -1;
+    // one graph per lane (lane 1 first, so lane 0's activations stay the current set)
+    for (int l = 1; l >= 0; l--) {
+        px_use_lane(E, l);
+        hipGraph_t g;
+        XT_HIP(hipStreamBeginCapture(E->lst[l], hipStreamCaptureModeThreadLocal));
+        if (px_forward(p, E->lst[l])) {
+            (void)hipStreamEndCapture(E->lst[l], &g);
+            return -1;
+        }
+        XT_HIP(hipStreamEndCapture(E->lst[l], &g));
+        XT_HIP(hipGraphInstantiate(&E->lgraph[l], g, NULL, NULL, 0));
+        XT_HIP(hipGraphDestroy(g));
+        XT_HIP(hipGraphUpload(E->lgraph[l], E->lst[l]));
+        XT_HIP(hipStreamSynchronize(E->lst[l]));
     }
-    XT_HIP(hipStreamEndCapture(E->st, &g));
-    XT_HIP(hipGraphInstantiate(&E->graph, g, NULL, NULL, 0));
-    XT_HIP(hipGraphDestroy(g));
-    XT_HIP(hipGraphUpload(E->graph, E->st));
-    XT_HIP(hipStreamSynchronize(E->st));
+    E->graph = E->lgraph[0];
     return 0;
 }
 
@@ -330,10 +360,13 @@ extern "C" int px_submit(px *p, uint32_t buf, uint16_t *const *in, uint32_t n)
     if (!E->stage[buf]) XT_HIP(hipHostMalloc((void **)&E->stage[buf], (size_t)E->nb * PX_IN * 2, hipHostMallocDefault));
     else XT_HIP(hipEventSynchronize(E->done[buf]));
     xt_stage_inputs(E->stage[buf], in, n, PX_IN);
-    if (n) XT_HIP(hipMemcpyAsync(E->in, E->stage[buf], (size_t)n * PX_IN * 2, hipMemcpyHostToDevice, E->st));
-    XT_HIP(hipGraphLaunch(E->graph, E->st));
-    if (n) XT_HIP(hipMemcpyAsync(p->hout[buf], E->out, (size_t)n * p->nt * 4, hipMemcpyDeviceToHost, E->st));
-    XT_HIP(hipEventRecord(E->done[buf], E->st));
+    // even bufs on lane 0, odd bufs on lane 1: two batches in flight run at once
+    const int l = buf & 1;
+    const hipStream_t s = E->lst[l];
+    if (n) XT_HIP(hipMemcpyAsync(E->act[l].in, E->stage[buf], (size_t)n * PX_IN * 2, hipMemcpyHostToDevice, s));
+    XT_HIP(hipGraphLaunch(E->lgraph[l], s));
+    if (n) XT_HIP(hipMemcpyAsync(p->hout[buf], E->act[l].out, (size_t)n * p->nt * 4, hipMemcpyDeviceToHost, s));
+    XT_HIP(hipEventRecord(E->done[buf], s));
     return 0;
 }
 
@@ -361,7 +394,10 @@ extern "C" void px_close(px *p)
     }
     (void)hipSetDevice(E->devno);
     if (E->st) (void)hipStreamSynchronize(E->st);
-    if (E->graph) (void)hipGraphExecDestroy(E->graph);
+    if (E->lst[1]) (void)hipStreamSynchronize(E->lst[1]);
+    for (int l = 0; l < 2; l++)
+        if (E->lgraph[l]) (void)hipGraphExecDestroy(E->lgraph[l]);
+    if (E->lst[1]) (void)hipStreamDestroy(E->lst[1]);
     for (int s = 0; s < PX_NBUF; s++) {
         if (E->done[s]) (void)hipEventDestroy(E->done[s]);
         if (p->hout[s]) (void)hipHostFree(p->hout[s]);
@@ -388,5 +424,16 @@ extern "C" int px_sync(px *p)
 {
     if (px_ready(p)) return -1;
     XT_HIP(hipStreamSynchronize(p->impl->st));
+    XT_HIP(hipStreamSynchronize(p->impl->lst[1]));
+    return 0;
+}
+extern "C" int px_run_buf(px *p, uint32_t buf)
+{
+    if (px_ready(p)) return -1;
+    if (buf >= PX_NBUF) return xt_fail("px_run_buf", "buf >= PX_NBUF");
+    px_impl *E = p->impl;
+    const int l = buf & 1;
+    XT_HIP(hipGraphLaunch(E->lgraph[l], E->lst[l]));
+    XT_HIP(hipEventRecord(E->done[buf], E->lst[l]));
     return 0;
 }

@@ -182,6 +182,10 @@ class PxEngine:
         if lib.px_run(self.ref) != 0:
             raise RuntimeError("px_run failed")
 
+    def run_buf(self, buf):
+        if lib.px_run_buf(self.ref, buf) != 0:
+            raise RuntimeError("px_run_buf failed")
+
     def sync(self):
         if lib.px_sync(self.ref) != 0:
             raise RuntimeError("px_sync failed")

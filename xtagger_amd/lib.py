@@ -71,6 +71,7 @@ _SIGS = {
     "px_dev_output": (_p, [_p]),
     "px_stream_handle": (_p, [_p]),
     "px_sync": (_i, [_p]),
+    "px_run_buf": (_i, [_p, _u32]),
     "eva_dev_input": (_p, [_p]),
     "eva_run": (_i, [_p]),
     "eva_dev_output": (_p, [_p]),
