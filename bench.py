@@ -834,9 +834,11 @@ def main():
                               "eva_profile_ms": prof}
         out["forward_b32_two_in_flight"] = two
         _note("forward b32 done")
-        ips, fms = bench_forward(torch, sparse=True)
+        two_sp = {}
+        ips, fms = bench_forward(torch, sparse=True, lanes=two_sp)
         out["forward_b32_sparse24"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
-                                       "tflops_dense_equivalent": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1)}
+                                       "tflops_dense_equivalent": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1),
+                                       "two_in_flight": two_sp}
         # 64 sequences of 1025 tokens (16 images x (1 full view + 0-4 crops), made by the GPU producer) and a
         # 13461-row head
         out["forward_ragged64_head13461"] = bench_forward_ragged(torch, L)
