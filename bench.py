@@ -833,6 +833,11 @@ def main():
                               "tflops": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1),
                               "eva_profile_ms": prof}
         out["forward_b32_two_in_flight"] = two
+        # the reference engine's own batch (EVA_NB = 8), where the 1024-column GEMMs fill half of the CUs: one batch
+        # at a time, and two in flight on the engine's two lanes
+        two8 = {}
+        ips8, fms8 = bench_forward(torch, nb=8, lanes=two8)
+        out["forward_b8"] = {"images_per_s": round(ips8, 1), "ms_per_batch": round(fms8, 3), "two_in_flight": two8}
         _note("forward b32 done")
         two_sp = {}
         ips, fms = bench_forward(torch, sparse=True, lanes=two_sp)
