@@ -446,7 +446,7 @@ def bench_pixai_block(torch, L, nb=4, reps=10):
     return res
 
 
-def bench_pixai_forward(torch, L, nb=4, nt=13461, lanes=None):
+def bench_pixai_forward(torch, L, nb=4, nt=13461):
     """The PixAI tagger engine (px_open_nb .. px_run, px.h:110-190) at batch 4 (PX_NB) on a synthetic pixai.bin v2:
     one graph replay = patch embedding + pre-LN, 32 ViTDet-L blocks (global attention in blocks 7, 15, 23, 31), the
     attention-pool head and a 13461-row tag head, 32 distinct random weight sets, inputs resident in the engine's
@@ -471,31 +471,16 @@ def bench_pixai_forward(torch, L, nb=4, nt=13461, lanes=None):
         for _ in range(2):
             eng.run()
         ms_b = time_engine(torch, eng, runs=2)
-        if lanes is not None:                          # two batches in flight, one on each lane
-            eng.submit(1, inp)
-            eng.wait(1, nb)
-            ts = []
-            for _ in range(5):
-                eng.sync()
-                t0 = time.perf_counter()
-                for i in range(8):
-                    eng.run_buf(i & 1)
-                eng.sync()
-                ts.append((time.perf_counter() - t0) / 8)
-            ms_l = sorted(ts)[2] * 1e3
-            lanes.update({"images_per_s": round(nb / (ms_l * 1e-3), 1), "ms_per_batch": round(ms_l, 3),
-                          "batches_in_flight": 2})
     finally:
         eng.close()
     return nb / (ms_b * 1e-3), ms_b
 
 
-def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False, profile=None, lanes=None):
+def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False, profile=None):
     """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
-    resident. sparse: the layer GEMM weights 2:4-pruned at bring-up and run on the sparse matrix cores. profile (a
-    dict): filled with eva_profile's GPU ms per op kind of one direct forward. lanes (a dict): filled with the
-    throughput of two batches in flight, bufs 0 and 1 replayed alternately on the engine's two lanes (median of 5
-    wall-clock runs of 8 batches between syncs of both lanes)."""
+    resident (the engine runs each batch as two halves at once on its two lanes). sparse: the layer GEMM weights
+    2:4-pruned at bring-up and run on the sparse matrix cores. profile (a dict): filled with eva_profile's GPU ms per
+    op kind of one direct forward (the two halves one after the other)."""
     from xtagger_amd import blob
     from xtagger_amd.engine import Engine
     path = os.path.join(os.environ.get("TMPDIR", "/tmp"), "xtag_bench_eva02_v2.bin")
@@ -511,20 +496,6 @@ def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False, profile=None, la
     ms_b = time_engine(torch, e, runs=iters)
     if profile is not None:
         profile.update({k: round(v, 3) for k, v in e.profile().items()})
-    if lanes is not None:
-        e.submit(1, inp)
-        e.wait(1, nb)
-        ts = []
-        for _ in range(5):
-            e.sync()
-            t0 = time.perf_counter()
-            for i in range(8):
-                e.run_buf(i & 1)
-            e.sync()
-            ts.append((time.perf_counter() - t0) / 8)
-        ms_l = sorted(ts)[2] * 1e3
-        lanes.update({"images_per_s": round(nb / (ms_l * 1e-3), 1), "ms_per_batch": round(ms_l, 3),
-                      "batches_in_flight": 2})
     e.close()
     return nb / (ms_b * 1e-3), ms_b
 
@@ -818,32 +789,26 @@ def main():
     out["pixai_block_b4"] = bench_pixai_block(torch, L)
     _note("producer, PixAI attention and block done")
     if not args.no_forward:
-        two = {}
-        ips, fms = bench_pixai_forward(torch, L, lanes=two)
+        ips, fms = bench_pixai_forward(torch, L)
         out["pixai_forward_b4"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
                                    "input": "1008x1008 (5184 tokens)", "path": "px_open_nb + px_run (engine graph)",
-                                   "weights": "synthetic pixai.bin v2, 32 distinct blocks", "two_in_flight": two}
+                                   "weights": "synthetic pixai.bin v2, 32 distinct blocks"}
     ln_us, ln_gbs = bench_ln(torch, L)
     out["ln_m32800"] = {"us": round(ln_us, 2), "gbs": round(ln_gbs, 1), "frac_hbm_peak": round(ln_gbs / 8000.0, 3),
                         "bytes": 32 * T * D * 3 + 32 * T * 8 * 4}
     if not args.no_forward:
-        prof, two = {}, {}
-        ips, fms = bench_forward(torch, profile=prof, lanes=two)
+        prof = {}
+        ips, fms = bench_forward(torch, profile=prof)
         out["forward_b32"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
                               "tflops": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1),
                               "eva_profile_ms": prof}
-        out["forward_b32_two_in_flight"] = two
-        # the reference engine's own batch (EVA_NB = 8), where the 1024-column GEMMs fill half of the CUs: one batch
-        # at a time, and two in flight on the engine's two lanes
-        two8 = {}
-        ips8, fms8 = bench_forward(torch, nb=8, lanes=two8)
-        out["forward_b8"] = {"images_per_s": round(ips8, 1), "ms_per_batch": round(fms8, 3), "two_in_flight": two8}
+        # the reference engine's own batch (EVA_NB = 8)
+        ips8, fms8 = bench_forward(torch, nb=8)
+        out["forward_b8"] = {"images_per_s": round(ips8, 1), "ms_per_batch": round(fms8, 3)}
         _note("forward b32 done")
-        two_sp = {}
-        ips, fms = bench_forward(torch, sparse=True, lanes=two_sp)
+        ips, fms = bench_forward(torch, sparse=True)
         out["forward_b32_sparse24"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
-                                       "tflops_dense_equivalent": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1),
-                                       "two_in_flight": two_sp}
+                                       "tflops_dense_equivalent": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1)}
         # 64 sequences of 1025 tokens (16 images x (1 full view + 0-4 crops), made by the GPU producer) and a
         # 13461-row head
         out["forward_ragged64_head13461"] = bench_forward_ragged(torch, L)

@@ -89,22 +89,21 @@ int eva_head_get(eva *e, uint16_t *w, float *bias);                 /* eva.h:653
 void eva_close(eva *e);                                             /* eva.h:704 */
 
 /* Resident-input path (no reference counterpart; used by benchmarks): the device input buffer
- * [nb][1024][592] fp16, one forward on the engine stream with no host copies, the device scores [nb][nt] fp32,
- * the engine stream, and a blocking wait on both lanes. These address lane 0, which even bufs use: eva_submit runs
- * even bufs on lane 0 and odd bufs on lane 1, each lane with its own activations, stream and graph, so two batches
- * in flight overlap on the GPU. eva_run_buf replays buf's lane on the inputs standing in that lane's device buffer
- * (the last batch submitted to it) and marks buf done like eva_submit, with no host copies. */
+ * [nb][1024][592] fp16, one forward with no host copies, the device scores [nb][nt] fp32, the engine stream (a
+ * forward is complete on it: the stream waits for the second lane), and a blocking wait. Every forward, submitted or
+ * resident, runs as two halves at once: inputs 0 .. ceil(nb / 2) - 1 on the engine stream, the rest on a second lane
+ * with its own activations, stream and graph. */
 void *eva_dev_input(eva *e);
 int eva_run(eva *e);
 const float *eva_dev_output(eva *e);
 void *eva_stream_handle(eva *e);
 int eva_sync(eva *e);
-int eva_run_buf(eva *e, uint32_t buf);
 /* eva.h:312-338 (eva_profile, built there with EVA_PROF): one direct (non-graph) forward with a GPU event after every
  * op, summed per op kind over the layers and printed to stderr as "prof gpu <op> <ms> <share>"; ms (may be NULL)
  * receives the EVA_PROF_OPS sums in the order eva_profile_opname(0 ..) names them: patch+embed, ln1, qkv, flash, oproj,
  * ln2, fc1, fc2, pool+head (the reference's "stat clear" and "(mlp ln)" ops do not exist here: fc1 writes the LN
- * statistics and fc2 folds the LN). Runs on the device input buffer as it stands. */
+ * statistics and fc2 folds the LN). Runs on the device input buffer as it stands, the two halves of the batch one
+ * after the other (a graph replay runs them at once). */
 #define EVA_PROF_OPS 9
 int eva_profile(eva *e, double *ms);
 const char *eva_profile_opname(int i);
@@ -263,14 +262,13 @@ int px_submit(px *p, uint32_t buf, uint16_t *const *in, uint32_t n);
 int px_query(px *p, uint32_t buf);                                  /* px.h:421 */
 const float *px_wait(px *p, uint32_t buf);                          /* px.h:426: scores [n][nt] */
 void px_close(px *p);                                               /* px.h:457 */
-/* Resident-input path, as eva_dev_input .. eva_run_buf (no reference counterpart; used by benchmarks and tests): lane
- * 0's buffers and stream; px_submit runs even bufs on lane 0 and odd bufs on lane 1; px_sync waits for both lanes. */
+/* Resident-input path, as eva_dev_input .. eva_sync (no reference counterpart; used by benchmarks and tests). A
+ * forward runs as two halves at once, inputs 0 .. nb / 2 - 1 on the engine stream and the rest on a second lane. */
 void *px_dev_input(px *p);
 int px_run(px *p);
 const float *px_dev_output(px *p);
 void *px_stream_handle(px *p);
 int px_sync(px *p);
-int px_run_buf(px *p, uint32_t buf);
 
 /* ---- PixAI tagger (ViTDet-L) block kernels on the same block-scaled main loop (px_kernels.cu) ----
  * Rows are window-major tokens (px_kernels.cu:1-4): sequence s = rows L s .. L s + L - 1 with L = 576 (windowed

@@ -354,43 +354,51 @@ def test_submit_ring_nonblocking(dev, synth_blob):
         assert np.array_equal(got[b], ref[b]), f"buf {b}"
 
 
-def test_two_lanes_replay(dev, synth_blob):
-    """Even and odd bufs run on the engine's two lanes (own activations, stream and graph). Distinct batches on bufs
-    0 and 1, then replays of both lanes in flight together (eva_run_buf): lane 0's device scores stay those of its
-    batch bit for bit, and a later submit to each lane still matches its batch."""
+def test_batch_halves(dev, synth_blob):
+    """A batch runs as two halves at once (the first ceil(nb / 2) inputs on the engine stream, the rest on the second
+    lane). With nb = 3 (halves of 2 and 1): full, partial (n = 1: the second lane idle, n = 2: exactly the first half)
+    and resident batches give every image the scores an nb = 1 engine gives it, bit for bit."""
     import ctypes
     from xtagger_amd import blob
     from xtagger_amd.engine import Engine
     path, m = synth_blob
-    nb = 2
-    e = Engine(path, device=0, nb=nb)
+    inp = blob.synth_inputs(3, seed=93)
+    e1 = Engine(path, device=0, nb=1)
+    e1.ready()
+    ref = []
+    for i in range(3):
+        e1.submit(0, inp[i:i + 1])
+        ref.append(e1.wait(0, 1)[0].copy())
+    e1.close()
+    ref = np.stack(ref)
+    e = Engine(path, device=0, nb=3)
     e.ready()
-    inp = blob.synth_inputs(2 * nb, seed=91).reshape(2, nb, 1024, 592)
-    e.submit(0, inp[0])
-    e.submit(1, inp[1])
-    r0, r1 = e.wait(0, nb).copy(), e.wait(1, nb).copy()
-    assert not np.array_equal(r0, r1)
-    for _ in range(3):
-        e.run_buf(1)
-        e.run_buf(0)
-    e.sync()
+    e.submit(0, inp)
+    assert np.array_equal(e.wait(0, 3), ref)
+    e.submit(1, inp[2:3])
+    assert np.array_equal(e.wait(1, 1), ref[2:3])
+    e.submit(2, inp[1:3])
+    assert np.array_equal(e.wait(2, 2), ref[1:3])
     hip = ctypes.CDLL("libamdhip64.so")
     hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    out_t = torch.empty((nb, e.nt), dtype=torch.float32, device=dev)
+    d_in = torch.from_numpy(np.ascontiguousarray(inp)).to(dev)
     torch.cuda.synchronize()
+    assert hip.hipMemcpy(e.dev_input(), d_in.data_ptr(), d_in.numel() * 2, 3) == 0
+    torch.cuda.synchronize()
+    e.run()
+    e.sync()
+    out_t = torch.empty((3, e.nt), dtype=torch.float32, device=dev)
     assert hip.hipMemcpy(out_t.data_ptr(), e.dev_output(), out_t.numel() * 4, 3) == 0
     torch.cuda.synchronize()
-    assert np.array_equal(out_t.cpu().numpy(), r0)
-    e.submit(3, inp[0])                                         # lane 1 on lane 0's batch, and the reverse
-    e.submit(2, inp[1])
-    assert np.array_equal(e.wait(3, nb), r0) and np.array_equal(e.wait(2, nb), r1)
+    assert np.array_equal(out_t.cpu().numpy(), ref)
     e.close()
 
 
 def test_profile_per_op(dev, synth_blob):
     """eva.h:312-338: eva_profile runs one direct forward with an event after every op and returns the GPU time per op
-    kind. Every kind takes time, the layer kinds dominate the total, the direct forward takes about as long as a graph
-    replay, and the profile leaves the scores of the next forward unchanged."""
+    kind. Every kind takes time, the layer kinds dominate the total, the direct forward (the two halves of the batch one
+    after the other) takes about as long as a graph replay (the halves at once) up to the factor two of that
+    concurrency, and the profile leaves the scores of the next forward unchanged."""
     import time
     from xtagger_amd import blob
     from xtagger_amd.engine import Engine
@@ -418,5 +426,5 @@ def test_profile_per_op(dev, synth_blob):
     assert list(prof) == ["patch+embed", "ln1", "qkv", "flash", "oproj", "ln2", "fc1", "fc2", "pool+head"]
     assert all(v > 0 for v in prof.values())
     assert prof["qkv"] + prof["flash"] + prof["fc1"] + prof["fc2"] > 0.5 * tot
-    assert 0.5 * t_graph < tot < 2.0 * t_graph
+    assert 0.5 * t_graph < tot < 4.0 * t_graph
     assert np.array_equal(got, ref)

@@ -116,15 +116,5 @@ def test_px_engine_matches_kernel_chain(dev, xt, tmp_path):
         got = np.empty((nb, NT), np.float32)
         assert hip.hipMemcpy(C.c_void_p(got.ctypes.data), C.c_void_p(eng.dev_output()), C.c_size_t(got.nbytes), 2) == 0
         assert (got == ref).all(), f"resident path differs: max |d| {np.abs(got - ref).max():.3g}"
-        # both lanes at once: bufs 0 (lane 0) and 1 (lane 1) submitted back to back, then replayed together
-        eng.submit(0, inp)
-        eng.submit(2, inp[1:])
-        assert (eng.wait(0, nb) == ref).all() and (eng.wait(2, 1) == ref[1:]).all()
-        for _ in range(2):
-            eng.run_buf(1)
-            eng.run_buf(0)
-        eng.sync()
-        assert hip.hipMemcpy(C.c_void_p(got.ctypes.data), C.c_void_p(eng.dev_output()), C.c_size_t(got.nbytes), 2) == 0
-        assert (got[:1] == ref[1:]).all(), "lane 0 after concurrent replays"
     finally:
         eng.close()

@@ -1,9 +1,9 @@
 // engine.cpp - the wd / EVA02-L engine behind the reference's C host API (src/engine/eva.h:573-745), on HIP for one
 // MI355X. eva_open returns at once; the bring-up (device, weights, packing, buffers, graph capture) runs on its own
 // thread and eva_ready joins it. One forward = one replay of a HIP graph captured once for nb inputs (eva.h:531-536).
-// The engine keeps two lanes, each with its own activations, stream and graph: batches submitted to even bufs run on
-// lane 0 (the engine stream), those on odd bufs on lane 1, so two batches in flight run concurrently and each fills
-// the CUs that the other's short last rounds of tiles leave idle.
+// A batch of nb inputs runs as two halves at once, on two lanes with their own activations, stream and graph (images
+// 0 .. ceil(nb / 2) - 1 on lane 0, the engine stream, the rest on lane 1): each half fills the CUs that the other's
+// short last rounds of tiles leave idle. Input and score buffers are shared, each lane using its slice.
 #include <hip/hip_runtime.h>
 #include <pthread.h>
 #include <stdint.h>
@@ -39,7 +39,9 @@ struct eva_impl {
     pthread_t boot;
     char *path;                                            // own copy of the weights path
     size_t wbytes;
-    uint32_t nb, M, Mp;                                    // inputs per launch, token rows, rows padded to 256
+    uint32_t nb;                                           // inputs per launch
+    uint32_t nl, lnb[2], loff[2];                          // lanes (1 when nb = 1); each lane's inputs and first one
+    uint32_t cnb, cM, cMp;                                 // the lane ev_forward works on: inputs, rows, padded rows
     hipStream_t st;
     uint8_t *blob;                                         // the file's tensors, resident
     const uint16_t *pe;
@@ -65,13 +67,15 @@ struct eva_impl {
         uint8_t *h8, *m8, *pq;
         float *sh, *sm, *stat, *pool, *ps, *out;
     } act[2];
+    uint16_t *in_all, *pn_all;                             // inputs [nb][1024][592], head inputs [nb][1024]
+    float *out_all;                                        // scores [nb][nt]
     hipStream_t lst[2];                                    // lane streams (lst[0] = st)
     hipGraphExec_t lgraph[2];                              // lane graphs (lgraph[0] = graph)
-    hipEvent_t lane_done;                                  // after the last batch submitted to lane 1
+    hipEvent_t lane_ev;                                    // after lane 1's half of the last batch
     hipEvent_t head_ev;                                    // after the last eva_head_put's update (on st)
     // eva_profile: an event after every op of one direct forward (eva.h:71-88, 312-338), 172 ops at 24 layers
-    hipEvent_t pev[256];
-    uint8_t pid[256];
+    hipEvent_t pev[512];
+    uint8_t pid[512];
     int pk, pon;
     hipEvent_t done[EVA_NBUF];
     uint16_t *stage[EVA_NBUF];                             // pinned staging of each buf's inputs (at its first submit)
@@ -141,7 +145,7 @@ static const char *const ev_opname[EVA_PROF_OPS] = {"patch+embed", "ln1", "qkv",
 static int ev_mark(eva_impl *E, int id)
 {
     if (!E->pon) return 0;
-    if (E->pk >= 256) return xt_fail("eva_profile", "more than 255 ops");
+    if (E->pk >= (int)(sizeof(E->pev) / sizeof(E->pev[0]))) return xt_fail("eva_profile", "too many ops");
     E->pid[E->pk] = (uint8_t)id;
     XT_HIP(hipEventRecord(E->pev[E->pk++], E->st));
     return 0;
@@ -156,7 +160,7 @@ static int ev_forward(eva *e, hipStream_t fst)
 {
     eva_impl *E = e->impl;
     void *st = (void *)fst;
-    const int M = (int)E->M, lds = (int)E->Mp, nb = (int)E->nb;
+    const int M = (int)E->cM, lds = (int)E->cMp, nb = (int)E->cnb;
 
     EV_OP(eva_k_pe(E->in, E->pe, E->pos, E->x, nb, st), 0);
     for (int i = 0; i < EVA_NL; i++) {
@@ -216,6 +220,9 @@ static int ev_pack_layer(eva_impl *E, int i)
 static void ev_use_lane(eva_impl *E, int l)
 {
     const eva_impl::Acts &A = E->act[l];
+    E->cnb = E->lnb[l];
+    E->cM = E->cnb * EVA_T;
+    E->cMp = (E->cM + 255) & ~255u;
     E->in = A.in, E->x = A.x, E->q = A.q, E->k = A.k, E->vt = A.vt, E->pn = A.pn;
     E->h8 = A.h8, E->m8 = A.m8, E->pq = A.pq;
     E->sh = A.sh, E->sm = A.sm, E->stat = A.stat, E->pool = A.pool, E->ps = A.ps, E->out = A.out;
@@ -283,12 +290,17 @@ static int ev_up(eva *e)
     XT_HIP(hipHostMalloc((void **)&E->hput, (size_t)EV_HPUT_SLOTS * EV_HPUT_SLOT, hipHostMallocDefault));
     for (int s = 0; s < EV_HPUT_SLOTS; s++) XT_HIP(hipEventCreateWithFlags(&E->hput_ev[s], hipEventDisableTiming));
 
-    // activations, one set per lane
-    const size_t Mp = E->Mp, nb = E->nb;
-    const size_t qkvb = nb * EVA_NH * 1088 * 64 * 2;
-    for (int l = 0; l < 2; l++) {
+    // inputs, head inputs and scores of the whole batch; activations per lane, for its half
+    EV_ALLOC(E, E->in_all, (size_t)E->nb * EVA_IN * 2, true);
+    EV_ALLOC(E, E->pn_all, (size_t)E->nb * EVA_D * 2, true);
+    EV_ALLOC(E, E->out_all, (size_t)E->nb * nt * 4, true);
+    for (uint32_t l = 0; l < E->nl; l++) {
         eva_impl::Acts &A = E->act[l];
-        EV_ALLOC(E, A.in, nb * EVA_IN * 2, true);
+        const size_t nb = E->lnb[l], Mp = (nb * EVA_T + 255) & ~(size_t)255;
+        const size_t qkvb = nb * EVA_NH * 1088 * 64 * 2;
+        A.in = E->in_all + (size_t)E->loff[l] * EVA_IN;
+        A.pn = E->pn_all + (size_t)E->loff[l] * EVA_D;
+        A.out = E->out_all + (size_t)E->loff[l] * nt;
         EV_ALLOC(E, A.x, Mp * EVA_D * 2, true);
         EV_ALLOC(E, A.h8, Mp * EVA_D, true);
         EV_ALLOC(E, A.sh, 8 * Mp * 4, true);
@@ -299,26 +311,26 @@ static int ev_up(eva *e)
         EV_ALLOC(E, A.sm, 22 * Mp * 4, true);
         EV_ALLOC(E, A.stat, 22 * Mp * 8, true);
         EV_ALLOC(E, A.pool, nb * EVA_D * 4, true);
-        EV_ALLOC(E, A.pn, nb * EVA_D * 2, true);
         EV_ALLOC(E, A.pq, nb * EVA_D, true);
         EV_ALLOC(E, A.ps, 8 * nb * 4, true);
-        EV_ALLOC(E, A.out, nb * nt * 4, true);
     }
-    XT_HIP(hipStreamCreateWithFlags(&E->lst[1], hipStreamNonBlocking));
     E->lst[0] = E->st;
-    XT_HIP(hipEventCreateWithFlags(&E->lane_done, hipEventDisableTiming));
     XT_HIP(hipEventCreateWithFlags(&E->head_ev, hipEventDisableTiming));
-    XT_HIP(hipEventRecord(E->lane_done, E->lst[1]));
     XT_HIP(hipEventRecord(E->head_ev, E->st));
+    if (E->nl > 1) {
+        XT_HIP(hipStreamCreateWithFlags(&E->lst[1], hipStreamNonBlocking));
+        XT_HIP(hipEventCreateWithFlags(&E->lane_ev, hipEventDisableTiming));
+        XT_HIP(hipEventRecord(E->lane_ev, E->lst[1]));
+    }
     for (int s = 0; s < EVA_NBUF; s++) {
-        XT_HIP(hipHostMalloc((void **)&e->hout[s], nb * nt * 4, hipHostMallocDefault));
-        if (nt > e->nt0) XT_HIP(hipHostMalloc((void **)&e->hpn[s], nb * EVA_D * 2, hipHostMallocDefault));
+        XT_HIP(hipHostMalloc((void **)&e->hout[s], (size_t)E->nb * nt * 4, hipHostMallocDefault));
+        if (nt > e->nt0) XT_HIP(hipHostMalloc((void **)&e->hpn[s], (size_t)E->nb * EVA_D * 2, hipHostMallocDefault));
         XT_HIP(hipEventCreateWithFlags(&E->done[s], hipEventDisableTiming));
     }
     XT_HIP(hipStreamSynchronize(E->st));
 
     // graph capture of the forward, once per lane (lane 1 last, so lane 0's activations stay the current set)
-    for (int l = 1; l >= 0; l--) {
+    for (int l = (int)E->nl - 1; l >= 0; l--) {
         ev_use_lane(E, l);
         hipGraph_t g;
         XT_HIP(hipStreamBeginCapture(E->lst[l], hipStreamCaptureModeThreadLocal));
@@ -368,8 +380,11 @@ extern "C" int eva_open_ex(eva *e, const char *weights, int device, void *pool, 
     E->flags = flags;
     E->wbytes = hdr[3];
     E->nb = nb;
-    E->M = nb * EVA_T;
-    E->Mp = (E->M + 255) & ~255u;
+    E->nl = nb > 1 ? 2 : 1;
+    E->lnb[0] = (nb + 1) / 2;
+    E->lnb[1] = nb / 2;
+    E->loff[0] = 0;
+    E->loff[1] = E->lnb[0];
     e->nt0 = hdr[2];
     e->nt = hdr[2] + extra;
     e->ntp = (hdr[2] + 7) & ~7u;
@@ -424,18 +439,29 @@ extern "C" int eva_submit(eva *e, uint32_t buf, uint16_t *const *in, uint32_t n)
     if (!E->stage[buf]) XT_HIP(hipHostMalloc((void **)&E->stage[buf], (size_t)E->nb * EVA_IN * 2, hipHostMallocDefault));
     else XT_HIP(hipEventSynchronize(E->done[buf]));
     xt_stage_inputs(E->stage[buf], in, n, EVA_IN);
-    // even bufs run on lane 0 (the engine stream, where head updates are ordered too), odd bufs on lane 1, after
-    // every head update submitted before
-    const int l = buf & 1;
-    const hipStream_t s = E->lst[l];
-    const eva_impl::Acts &A = E->act[l];
-    if (l) XT_HIP(hipStreamWaitEvent(s, E->head_ev, 0));
-    if (n) XT_HIP(hipMemcpyAsync(A.in, E->stage[buf], (size_t)n * EVA_IN * 2, hipMemcpyHostToDevice, s));
-    XT_HIP(hipGraphLaunch(E->lgraph[l], s));
-    if (n) XT_HIP(hipMemcpyAsync(e->hout[buf], A.out, (size_t)n * e->nt * 4, hipMemcpyDeviceToHost, s));
-    if (e->hpn[buf] && n) XT_HIP(hipMemcpyAsync(e->hpn[buf], A.pn, (size_t)n * EVA_D * 2, hipMemcpyDeviceToHost, s));
-    XT_HIP(hipEventRecord(E->done[buf], s));
-    if (l) XT_HIP(hipEventRecord(E->lane_done, s));
+    // the first ceil(nb / 2) inputs on lane 0 (the engine stream, where head updates are ordered too), the rest on
+    // lane 1 after every head update submitted before; the batch is done when lane 0 has also waited for lane 1
+    const uint32_t n0 = n < E->lnb[0] ? n : E->lnb[0], n1 = n - n0;
+    if (n0) XT_HIP(hipMemcpyAsync(E->in_all, E->stage[buf], (size_t)n0 * EVA_IN * 2, hipMemcpyHostToDevice, E->st));
+    XT_HIP(hipGraphLaunch(E->lgraph[0], E->st));
+    if (n0) XT_HIP(hipMemcpyAsync(e->hout[buf], E->out_all, (size_t)n0 * e->nt * 4, hipMemcpyDeviceToHost, E->st));
+    if (e->hpn[buf] && n0) XT_HIP(hipMemcpyAsync(e->hpn[buf], E->pn_all, (size_t)n0 * EVA_D * 2, hipMemcpyDeviceToHost, E->st));
+    if (n1) {
+        const hipStream_t s = E->lst[1];
+        const size_t o = E->loff[1];
+        XT_HIP(hipStreamWaitEvent(s, E->head_ev, 0));
+        XT_HIP(hipMemcpyAsync(E->in_all + o * EVA_IN, E->stage[buf] + (size_t)n0 * EVA_IN, (size_t)n1 * EVA_IN * 2,
+                              hipMemcpyHostToDevice, s));
+        XT_HIP(hipGraphLaunch(E->lgraph[1], s));
+        XT_HIP(hipMemcpyAsync(e->hout[buf] + (size_t)n0 * e->nt, E->out_all + o * e->nt, (size_t)n1 * e->nt * 4,
+                              hipMemcpyDeviceToHost, s));
+        if (e->hpn[buf])
+            XT_HIP(hipMemcpyAsync(e->hpn[buf] + (size_t)n0 * EVA_D, E->pn_all + o * EVA_D, (size_t)n1 * EVA_D * 2,
+                                  hipMemcpyDeviceToHost, s));
+        XT_HIP(hipEventRecord(E->lane_ev, s));
+        XT_HIP(hipStreamWaitEvent(E->st, E->lane_ev, 0));
+    }
+    XT_HIP(hipEventRecord(E->done[buf], E->st));
     return 0;
 }
 
@@ -466,9 +492,8 @@ extern "C" int eva_head_put(eva *e, uint32_t j, const uint16_t *w, float bias)
     uint8_t *p = E->hput + (size_t)slot * EV_HPUT_SLOT;
     memcpy(p, w, EVA_D * 2);
     memcpy(p + EVA_D * 2, &bias, 4);
-    // the update waits for the batches already submitted to lane 1 (they read the head), and lane 1's later batches
-    // wait for it (head_ev); lane 0's batches are ordered with it on the engine stream
-    XT_HIP(hipStreamWaitEvent(E->st, E->lane_done, 0));
+    // the engine stream has waited for lane 1's half of every batch submitted before, so the update follows them all;
+    // lane 1's later halves wait for it (head_ev)
     XT_HIP(hipMemcpyAsync(E->hmaster + (size_t)j * EVA_D, p, EVA_D * 2, hipMemcpyHostToDevice, E->st));
     XT_HIP(hipMemcpyAsync(E->hb + j, p + EVA_D * 2, 4, hipMemcpyHostToDevice, E->st));
     EV_CK(ev_pack_head_rows(e, j, 1));
@@ -501,7 +526,7 @@ extern "C" void eva_close(eva *e)
     for (int l = 0; l < 2; l++)
         if (E->lgraph[l]) (void)hipGraphExecDestroy(E->lgraph[l]);
     if (E->lst[1]) (void)hipStreamDestroy(E->lst[1]);
-    if (E->lane_done) (void)hipEventDestroy(E->lane_done);
+    if (E->lane_ev) (void)hipEventDestroy(E->lane_ev);
     if (E->head_ev) (void)hipEventDestroy(E->head_ev);
     for (int s = 0; s < EVA_NBUF; s++) {
         if (E->done[s]) (void)hipEventDestroy(E->done[s]);
@@ -513,7 +538,7 @@ extern "C" void eva_close(eva *e)
     if (E->hput) (void)hipHostFree(E->hput);
     for (int s = 0; s < EV_HPUT_SLOTS; s++)
         if (E->hput_ev[s]) (void)hipEventDestroy(E->hput_ev[s]);
-    for (int i = 0; i < 256; i++)
+    for (int i = 0; i < 512; i++)
         if (E->pev[i]) (void)hipEventDestroy(E->pev[i]);
     for (void *p : E->allocs) (void)hipFree(p);
     if (E->st) (void)hipStreamDestroy(E->st);
@@ -532,13 +557,23 @@ extern "C" int eva_profile(eva *e, double *ms)
     double acc[EVA_PROF_OPS] = {0}, tot = 0;
     XT_HIP(hipStreamSynchronize(E->st));
     if (!E->pev[0])
-        for (int i = 0; i < 256; i++) XT_HIP(hipEventCreate(&E->pev[i]));
-    if (ev_forward(e, E->st) || ev_forward(e, E->st)) return -1;
+        for (int i = 0; i < 512; i++) XT_HIP(hipEventCreate(&E->pev[i]));
+    // the two halves of the batch one after the other on the engine stream, each forward twice to warm up
+    auto halves = [&]() -> int {
+        int rc = 0;
+        for (uint32_t l = 0; l < E->nl && !rc; l++) {
+            ev_use_lane(E, (int)l);
+            rc = ev_forward(e, E->st);
+        }
+        ev_use_lane(E, 0);
+        return rc;
+    };
+    if (halves() || halves()) return -1;
     E->pon = 1;
     E->pk = 1;
     E->pid[0] = 255;
     const hipError_t r0 = hipEventRecord(E->pev[0], E->st);
-    const int rc = r0 != hipSuccess ? xt_fail("eva_profile", "hipEventRecord failed") : ev_forward(e, E->st);
+    const int rc = r0 != hipSuccess ? xt_fail("eva_profile", "hipEventRecord failed") : halves();
     E->pon = 0;
     if (rc) return -1;
     XT_HIP(hipStreamSynchronize(E->st));
@@ -558,31 +593,26 @@ extern "C" int eva_profile(eva *e, double *ms)
 
 extern "C" const char *eva_profile_opname(int i) { return i >= 0 && i < EVA_PROF_OPS ? ev_opname[i] : NULL; }
 
-extern "C" void *eva_dev_input(eva *e) { return eva_ready(e) ? NULL : (void *)e->impl->in; }
-extern "C" const float *eva_dev_output(eva *e) { return eva_ready(e) ? NULL : e->impl->out; }
+extern "C" void *eva_dev_input(eva *e) { return eva_ready(e) ? NULL : (void *)e->impl->in_all; }
+extern "C" const float *eva_dev_output(eva *e) { return eva_ready(e) ? NULL : e->impl->out_all; }
 extern "C" void *eva_stream_handle(eva *e) { return eva_ready(e) ? NULL : (void *)e->impl->st; }
 extern "C" int eva_run(eva *e)
 {
     if (eva_ready(e)) return -1;
-    XT_HIP(hipGraphLaunch(e->impl->graph, e->impl->st));
+    eva_impl *E = e->impl;
+    XT_HIP(hipGraphLaunch(E->lgraph[0], E->st));
+    if (E->nl > 1) {
+        XT_HIP(hipStreamWaitEvent(E->lst[1], E->head_ev, 0));
+        XT_HIP(hipGraphLaunch(E->lgraph[1], E->lst[1]));
+        XT_HIP(hipEventRecord(E->lane_ev, E->lst[1]));
+        XT_HIP(hipStreamWaitEvent(E->st, E->lane_ev, 0));
+    }
     return 0;
 }
 extern "C" int eva_sync(eva *e)
 {
     if (eva_ready(e)) return -1;
     XT_HIP(hipStreamSynchronize(e->impl->st));
-    XT_HIP(hipStreamSynchronize(e->impl->lst[1]));
-    return 0;
-}
-extern "C" int eva_run_buf(eva *e, uint32_t buf)
-{
-    if (eva_ready(e)) return -1;
-    if (buf >= EVA_NBUF) return xt_fail("eva_run_buf", "buf >= EVA_NBUF");
-    eva_impl *E = e->impl;
-    const int l = buf & 1;
-    if (l) XT_HIP(hipStreamWaitEvent(E->lst[1], E->head_ev, 0));
-    XT_HIP(hipGraphLaunch(E->lgraph[l], E->lst[l]));
-    XT_HIP(hipEventRecord(E->done[buf], E->lst[l]));
-    if (l) XT_HIP(hipEventRecord(E->lane_done, E->lst[1]));
+    if (e->impl->nl > 1) XT_HIP(hipStreamSynchronize(e->impl->lst[1]));
     return 0;
 }

@@ -3,8 +3,8 @@
 // the bring-up (device, weights, packing, buffers, graph capture) runs on its own thread and px_ready joins it. One
 // forward = one replay of a HIP graph captured once for nb inputs: patch embedding + pre-LN, 32 blocks (global
 // attention in blocks 7, 15, 23, 31, px.h:38), the attention-pool head and the tag head (px.h:110-190). As in the wd
-// engine, even bufs run on lane 0 and odd bufs on lane 1, each with its own activations, stream and graph, so two
-// batches in flight run at once.
+// engine, a batch runs as two halves at once (inputs 0 .. nb / 2 - 1 on the engine stream, the rest on a second lane
+// with its own activations, stream and graph), each filling the CUs the other's short last rounds of tiles leave idle.
 #include <hip/hip_runtime.h>
 #include <pthread.h>
 #include <stdint.h>
@@ -35,7 +35,9 @@ struct px_impl {
     pthread_t boot;
     char *path;
     size_t wbytes;
-    uint32_t nb, M;                                     // inputs per launch, token rows (nb * 5184)
+    uint32_t nb;                                        // inputs per launch (even)
+    uint32_t nl, lnb[2], loff[2];                       // lanes in use; inputs per lane (even); first input of a lane
+    uint32_t cnb, cM;                                   // inputs and token rows of the lane px_forward works on
     hipStream_t st;
     uint8_t *blob;
     const uint16_t *pe, *hpos, *wv, *hw16;
@@ -50,14 +52,18 @@ struct px_impl {
     uint8_t *h8, *o8, *m8, *oq;
     float *sh, *so8, *sm, *s, *stat, *part, *o, *oqs, *out;
     hipGraphExec_t graph;
-    // two lanes, each with its own activations, stream and graph: even bufs run on lane 0 (st), odd bufs on lane 1
+    // two lanes, each with its own activations, stream and graph: a batch's first lnb[0] inputs run on lane 0 (st),
+    // the rest on lane 1 at the same time
     struct Acts {
         uint16_t *in, *x, *q, *k, *vt, *y;
         uint8_t *h8, *o8, *m8, *oq;
         float *sh, *so8, *sm, *s, *stat, *part, *o, *oqs, *out;
     } act[2];
+    uint16_t *in_all;                                   // inputs [nb][5184][592]
+    float *out_all;                                     // scores [nb][nt]
     hipStream_t lst[2];
     hipGraphExec_t lgraph[2];
+    hipEvent_t lane_ev;                                 // after lane 1's half of the last batch
     hipEvent_t done[PX_NBUF];
     uint16_t *stage[PX_NBUF];                           // pinned staging of each buf's inputs (at its first submit)
     std::vector<void *> allocs;
@@ -132,6 +138,8 @@ static int px_layout(px_impl *E, uint32_t ntp)
 static void px_use_lane(px_impl *E, int l)
 {
     const px_impl::Acts &A = E->act[l];
+    E->cnb = E->lnb[l];
+    E->cM = E->lnb[l] * PX_T;
     E->in = A.in, E->x = A.x, E->q = A.q, E->k = A.k, E->vt = A.vt, E->y = A.y;
     E->h8 = A.h8, E->o8 = A.o8, E->m8 = A.m8, E->oq = A.oq;
     E->sh = A.sh, E->so8 = A.so8, E->sm = A.sm, E->s = A.s, E->stat = A.stat, E->part = A.part, E->o = A.o;
@@ -143,7 +151,7 @@ static int px_forward(px *p, hipStream_t fst)
 {
     px_impl *E = p->impl;
     void *st = (void *)fst;
-    const int M = (int)E->M, nb = (int)E->nb;
+    const int M = (int)E->cM, nb = (int)E->cnb;
 
     PX_CK(px_k_pe(E->in, E->pe, E->x, M, st));
     PX_CK(px_k_pembed(E->x, E->pos, PX_T, E->lnpw, E->lnpb, M, st));
@@ -232,11 +240,14 @@ static int px_up(px *p)
     PX_ALLOC(E, E->hs, (size_t)8 * E->ldh * 4, true);
     PX_CK(eva_k_quant_act(E->hw16, 2, EVA_D, (int)p->nt, EVA_D, E->hq, EVA_D, E->hs, (int)E->ldh, (void *)E->st));
 
-    // activations, one set per lane
-    const size_t M = E->M, nb = E->nb;
-    for (int l = 0; l < 2; l++) {
+    // inputs and scores of the whole batch; activations per lane, for its half
+    PX_ALLOC(E, E->in_all, (size_t)E->nb * PX_IN * 2, true);
+    PX_ALLOC(E, E->out_all, (size_t)E->nb * p->nt * 4, true);
+    for (uint32_t l = 0; l < E->nl; l++) {
         px_impl::Acts &A = E->act[l];
-        PX_ALLOC(E, A.in, nb * PX_IN * 2, true);
+        const size_t nb = E->lnb[l], M = nb * PX_T;
+        A.in = E->in_all + (size_t)E->loff[l] * PX_IN;
+        A.out = E->out_all + (size_t)E->loff[l] * p->nt;
         PX_ALLOC(E, A.x, M * EVA_D * 2, true);
         PX_ALLOC(E, A.h8, M * EVA_D, true);
         PX_ALLOC(E, A.sh, 8 * M * 4, true);
@@ -254,18 +265,18 @@ static int px_up(px *p)
         PX_ALLOC(E, A.o, nb * EVA_D * 4, true);
         PX_ALLOC(E, A.oq, nb * EVA_D, true);
         PX_ALLOC(E, A.oqs, 8 * nb * 4, true);
-        PX_ALLOC(E, A.out, nb * p->nt * 4, true);
     }
-    XT_HIP(hipStreamCreateWithFlags(&E->lst[1], hipStreamNonBlocking));
+    if (E->nl > 1) XT_HIP(hipStreamCreateWithFlags(&E->lst[1], hipStreamNonBlocking));
     E->lst[0] = E->st;
+    XT_HIP(hipEventCreateWithFlags(&E->lane_ev, hipEventDisableTiming));
     for (int s = 0; s < PX_NBUF; s++) {
-        XT_HIP(hipHostMalloc((void **)&p->hout[s], nb * p->nt * 4, hipHostMallocDefault));
+        XT_HIP(hipHostMalloc((void **)&p->hout[s], (size_t)E->nb * p->nt * 4, hipHostMallocDefault));
         XT_HIP(hipEventCreateWithFlags(&E->done[s], hipEventDisableTiming));
     }
     XT_HIP(hipStreamSynchronize(E->st));
 
     // one graph per lane (lane 1 first, so lane 0's activations stay the current set)
-    for (int l = 1; l >= 0; l--) {
+    for (int l = (int)E->nl - 1; l >= 0; l--) {
         px_use_lane(E, l);
         hipGraph_t g;
         XT_HIP(hipStreamBeginCapture(E->lst[l], hipStreamCaptureModeThreadLocal));
@@ -313,7 +324,12 @@ extern "C" int px_open_nb(px *p, const char *weights, int device, void *pool, si
     E->devno = device;
     E->wbytes = hdr[3];
     E->nb = nb;
-    E->M = nb * PX_T;
+    // halves of even size (an odd half would leave a partial pair of images): nb = 2 runs on one lane, 6 as 4 + 2
+    E->lnb[0] = ((uint32_t)nb / 2 + 1) & ~1u;
+    E->lnb[1] = (uint32_t)nb - E->lnb[0];
+    E->nl = E->lnb[1] ? 2 : 1;
+    E->loff[0] = 0;
+    E->loff[1] = E->lnb[0];
     p->nt = hdr[2];
     p->ntp = (hdr[2] + 7) & ~7u;
     p->nb = nb;
@@ -360,13 +376,23 @@ extern "C" int px_submit(px *p, uint32_t buf, uint16_t *const *in, uint32_t n)
     if (!E->stage[buf]) XT_HIP(hipHostMalloc((void **)&E->stage[buf], (size_t)E->nb * PX_IN * 2, hipHostMallocDefault));
     else XT_HIP(hipEventSynchronize(E->done[buf]));
     xt_stage_inputs(E->stage[buf], in, n, PX_IN);
-    // even bufs on lane 0, odd bufs on lane 1: two batches in flight run at once
-    const int l = buf & 1;
-    const hipStream_t s = E->lst[l];
-    if (n) XT_HIP(hipMemcpyAsync(E->act[l].in, E->stage[buf], (size_t)n * PX_IN * 2, hipMemcpyHostToDevice, s));
-    XT_HIP(hipGraphLaunch(E->lgraph[l], s));
-    if (n) XT_HIP(hipMemcpyAsync(p->hout[buf], E->act[l].out, (size_t)n * p->nt * 4, hipMemcpyDeviceToHost, s));
-    XT_HIP(hipEventRecord(E->done[buf], s));
+    // the first lnb[0] inputs on the engine stream, the rest on lane 1; the batch is done when the engine stream has
+    // also waited for lane 1
+    const uint32_t n0 = n < E->lnb[0] ? n : E->lnb[0], n1 = n - n0;
+    if (n0) XT_HIP(hipMemcpyAsync(E->in_all, E->stage[buf], (size_t)n0 * PX_IN * 2, hipMemcpyHostToDevice, E->st));
+    XT_HIP(hipGraphLaunch(E->lgraph[0], E->st));
+    if (n0) XT_HIP(hipMemcpyAsync(p->hout[buf], E->out_all, (size_t)n0 * p->nt * 4, hipMemcpyDeviceToHost, E->st));
+    if (n1) {
+        const hipStream_t s = E->lst[1];
+        XT_HIP(hipMemcpyAsync(E->in_all + (size_t)E->loff[1] * PX_IN, E->stage[buf] + (size_t)n0 * PX_IN,
+                              (size_t)n1 * PX_IN * 2, hipMemcpyHostToDevice, s));
+        XT_HIP(hipGraphLaunch(E->lgraph[1], s));
+        XT_HIP(hipMemcpyAsync(p->hout[buf] + (size_t)n0 * p->nt, E->out_all + (size_t)E->loff[1] * p->nt,
+                              (size_t)n1 * p->nt * 4, hipMemcpyDeviceToHost, s));
+        XT_HIP(hipEventRecord(E->lane_ev, s));
+        XT_HIP(hipStreamWaitEvent(E->st, E->lane_ev, 0));
+    }
+    XT_HIP(hipEventRecord(E->done[buf], E->st));
     return 0;
 }
 
@@ -398,6 +424,7 @@ extern "C" void px_close(px *p)
     for (int l = 0; l < 2; l++)
         if (E->lgraph[l]) (void)hipGraphExecDestroy(E->lgraph[l]);
     if (E->lst[1]) (void)hipStreamDestroy(E->lst[1]);
+    if (E->lane_ev) (void)hipEventDestroy(E->lane_ev);
     for (int s = 0; s < PX_NBUF; s++) {
         if (E->done[s]) (void)hipEventDestroy(E->done[s]);
         if (p->hout[s]) (void)hipHostFree(p->hout[s]);
@@ -411,29 +438,25 @@ extern "C" void px_close(px *p)
     memset(p, 0, sizeof(*p));
 }
 
-extern "C" void *px_dev_input(px *p) { return px_ready(p) ? NULL : (void *)p->impl->in; }
-extern "C" const float *px_dev_output(px *p) { return px_ready(p) ? NULL : p->impl->out; }
+extern "C" void *px_dev_input(px *p) { return px_ready(p) ? NULL : (void *)p->impl->in_all; }
+extern "C" const float *px_dev_output(px *p) { return px_ready(p) ? NULL : p->impl->out_all; }
 extern "C" void *px_stream_handle(px *p) { return px_ready(p) ? NULL : (void *)p->impl->st; }
 extern "C" int px_run(px *p)
 {
     if (px_ready(p)) return -1;
-    XT_HIP(hipGraphLaunch(p->impl->graph, p->impl->st));
+    px_impl *E = p->impl;
+    XT_HIP(hipGraphLaunch(E->lgraph[0], E->st));
+    if (E->nl > 1) {
+        XT_HIP(hipGraphLaunch(E->lgraph[1], E->lst[1]));
+        XT_HIP(hipEventRecord(E->lane_ev, E->lst[1]));
+        XT_HIP(hipStreamWaitEvent(E->st, E->lane_ev, 0));
+    }
     return 0;
 }
 extern "C" int px_sync(px *p)
 {
     if (px_ready(p)) return -1;
     XT_HIP(hipStreamSynchronize(p->impl->st));
-    XT_HIP(hipStreamSynchronize(p->impl->lst[1]));
-    return 0;
-}
-extern "C" int px_run_buf(px *p, uint32_t buf)
-{
-    if (px_ready(p)) return -1;
-    if (buf >= PX_NBUF) return xt_fail("px_run_buf", "buf >= PX_NBUF");
-    px_impl *E = p->impl;
-    const int l = buf & 1;
-    XT_HIP(hipGraphLaunch(E->lgraph[l], E->lst[l]));
-    XT_HIP(hipEventRecord(E->done[buf], E->lst[l]));
+    if (p->impl->lst[1]) XT_HIP(hipStreamSynchronize(p->impl->lst[1]));
     return 0;
 }

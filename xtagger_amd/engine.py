@@ -91,10 +91,6 @@ class Engine:
         if lib.eva_run(self.ref) != 0:
             raise RuntimeError("eva_run failed")
 
-    def run_buf(self, buf):
-        if lib.eva_run_buf(self.ref, buf) != 0:
-            raise RuntimeError("eva_run_buf failed")
-
     def sync(self):
         if lib.eva_sync(self.ref) != 0:
             raise RuntimeError("eva_sync failed")
@@ -181,10 +177,6 @@ class PxEngine:
     def run(self):
         if lib.px_run(self.ref) != 0:
             raise RuntimeError("px_run failed")
-
-    def run_buf(self, buf):
-        if lib.px_run_buf(self.ref, buf) != 0:
-            raise RuntimeError("px_run_buf failed")
 
     def sync(self):
         if lib.px_sync(self.ref) != 0:

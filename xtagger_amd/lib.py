@@ -71,13 +71,11 @@ _SIGS = {
     "px_dev_output": (_p, [_p]),
     "px_stream_handle": (_p, [_p]),
     "px_sync": (_i, [_p]),
-    "px_run_buf": (_i, [_p, _u32]),
     "eva_dev_input": (_p, [_p]),
     "eva_run": (_i, [_p]),
     "eva_dev_output": (_p, [_p]),
     "eva_stream_handle": (_p, [_p]),
     "eva_sync": (_i, [_p]),
-    "eva_run_buf": (_i, [_p, _u32]),
     "eva_profile": (_i, [_p, _p]),
     "eva_profile_opname": (C.c_char_p, [_i]),
     "eva_img_over_white": (_i, [_p, C.c_size_t, _u32, _u32, _p]),
