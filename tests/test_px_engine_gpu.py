@@ -118,3 +118,51 @@ def test_px_engine_matches_kernel_chain(dev, xt, tmp_path):
         assert (got == ref).all(), f"resident path differs: max |d| {np.abs(got - ref).max():.3g}"
     finally:
         eng.close()
+
+
+def test_px_batch_halves(dev, tmp_path):
+    """A batch runs as two halves of even size at once (px_open_nb with nb = 6: 4 inputs on the engine stream, 2 on the
+    second lane). Full, partial (n = 3: the second lane idle, n = 5: one input on it) and resident batches give every
+    image the scores a one-lane nb = 2 engine gives it, bit for bit."""
+    m = blob.synth_px_model(seed=8, nt=NT)
+    path = tmp_path / "pixai.bin"
+    blob.write_px_v2(str(path), m)
+    r = np.random.default_rng(12)
+    inp = np.zeros((6, T5, 592), np.float16)
+    inp[..., :588] = r.uniform(-1, 1, (6, T5, 588)).astype(np.float16)
+    _say("px halves: nb = 2 reference engine")
+    e2 = PxEngine(path, nb=2)
+    try:
+        e2.ready()
+        ref = []
+        for i in range(0, 6, 2):
+            e2.submit(0, inp[i:i + 2])
+            ref.append(e2.wait(0, 2).copy())
+    finally:
+        e2.close()
+    ref = np.concatenate(ref)
+    assert np.isfinite(ref).all() and ref.std() > 1e-3
+    _say("px halves: nb = 6 engine (4 + 2)")
+    e = PxEngine(path, nb=6)
+    try:
+        e.ready()
+        e.submit(0, inp)
+        assert np.array_equal(e.wait(0, 6), ref)
+        e.submit(1, inp[3:6])
+        assert np.array_equal(e.wait(1, 3), ref[3:6])
+        e.submit(2, inp[1:6])
+        assert np.array_equal(e.wait(2, 5), ref[1:6])
+        hip = C.CDLL("libamdhip64.so")
+        d_in = torch.from_numpy(inp).to(dev)
+        torch.cuda.synchronize()
+        assert hip.hipMemcpy(C.c_void_p(e.dev_input()), C.c_void_p(d_in.data_ptr()), C.c_size_t(inp.nbytes), 3) == 0
+        assert hip.hipDeviceSynchronize() == 0
+        e.run()
+        e.sync()
+        out_t = torch.empty((6, e.nt), dtype=torch.float32, device=dev)
+        assert hip.hipMemcpy(C.c_void_p(out_t.data_ptr()), C.c_void_p(e.dev_output()), C.c_size_t(out_t.numel() * 4),
+                             3) == 0
+        assert hip.hipDeviceSynchronize() == 0
+        assert np.array_equal(out_t.cpu().numpy(), ref)
+    finally:
+        e.close()
