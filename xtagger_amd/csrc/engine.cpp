@@ -73,7 +73,8 @@ struct eva_impl {
     hipGraphExec_t lgraph[2];                              // lane graphs (lgraph[0] = graph)
     hipEvent_t lane_ev;                                    // after lane 1's half of the last batch
     hipEvent_t head_ev;                                    // after the last eva_head_put's update (on st)
-    // eva_profile: an event after every op of one direct forward (eva.h:71-88, 312-338), 172 ops at 24 layers
+    // eva_profile: an event after every op of one direct forward (eva.h:71-88, 312-338), 172 ops per half at 24
+    // layers
     hipEvent_t pev[512];
     uint8_t pid[512];
     int pk, pon;
@@ -329,7 +330,7 @@ static int ev_up(eva *e)
     }
     XT_HIP(hipStreamSynchronize(E->st));
 
-    // graph capture of the forward, once per lane (lane 1 last, so lane 0's activations stay the current set)
+    // graph capture of the forward, once per lane (lane 1 first, so lane 0's activations stay the current set)
     for (int l = (int)E->nl - 1; l >= 0; l--) {
         ev_use_lane(E, l);
         hipGraph_t g;
