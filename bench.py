@@ -768,7 +768,8 @@ def main():
            "vs_baseline": None, "dtype": "e4m3 (fp32 accumulate)", "data": "synthetic",
            "config": {"workload": "EVA02-L layer GEMMs with fused epilogues: qkv 1024->3072 +RoPE, proj 1024->1024 "
                                   "+residual, fc1 1024->2x2730 +SwiGLU +E4M3 repack, fc2 2730->1024 +folded LN "
-                                  "+residual; M=8200 (batch 8); 1x128 act / 128x128 weight fp32 block scales",
+                                  "+residual; M=8200 (batch 8); 1x128 act / 128x128 weight fp32 block scales "
+                                  "s = amax/448, promoted per 128-wide K block in fp32",
                       "M": M, "gflop_per_step": round(step_flops / 1e9, 2)},
            "pct_fp8_peak": round(100 * tflops / PEAK_FP8, 2), "per_kernel": per,
            "qkv_gemm_m1025": {"tflops": round(qkv1, 1), "us": round(qkv1_ms * 1e3, 2)},

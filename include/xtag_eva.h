@@ -12,13 +12,13 @@
  * (eva.h:153-176). eva_wait returns NULL on failure.
  *
  * Numerics (all kernels): E4M3 = OCP FP8 E4M3 "fn", encode round-to-nearest-even saturating to +-448.
- * Block scale s = the least power of two with 448 s >= amax, s = 1 for a block with |max| < 2^-116. Activations
- * q = sat_rne(x * (1/s)) per 1x128 block along K; weights q = sat_rne(w / s) per 128x128 block. Activation scales are
+ * Block scale s = amax / 448 (one IEEE division, correctly rounded), s = 1 for a block with |max| < 2^-116: the
+ * reference's per-tensor rule (export_eva.py:64-66) applied per block. Activations q = sat_rne(x * (1/s)) per 1x128
+ * block along K, 1/s rounded once (eva.h:408); weights q = sat_rne(w / s) per 128x128 block. Activation scales are
  * stored as planes s[K/128][lds] (lds >= rows); weight scales as s[ceil(N/128)][K/128]; weight rows are padded with
- * zeros to a multiple of 128. The layer GEMM roles (eva_k_qkv, _oproj, _fc1, _fc2 and px_k_qkv, _proj, _fc1, _fc2)
- * apply the scales inside the matrix core as E8M0 exponents, so their scale inputs must be powers of two (as every
- * packer here writes them; other values act as their power-of-two part). eva_k_gemm and the _sp roles take any fp32
- * scales.
+ * zeros to a multiple of 128. Every GEMM role promotes each 128-wide K block's partial sum into an fp32 accumulator,
+ * acc = fma(partial, sa * sw, acc), so any finite fp32 scales are honoured (with all scales equal this is the
+ * reference's alpha * acc, eva.h:415-418).
  */
 #ifndef XTAG_EVA_H
 #define XTAG_EVA_H

@@ -151,15 +151,9 @@ float xo_f16_to_f32(uint16_t h)
 
 float xo_block_scale(float amax)
 {
-    /* the least power of two s with 448 s >= amax: amax = f 2^e (f in [1, 2)) gives 2^(e - 8), or 2^(e - 7) when
-     * f > 1.75. A block whose |max| is below 2^-116 is a zero block (scale 1). */
-    uint32_t u;
-    float s;
-    if (amax < 0x1p-116f) return 1.0f;
-    memcpy(&u, &amax, 4);
-    u = ((u >> 23) - 8u + ((u & 0x7FFFFFu) > 0x600000u ? 1u : 0u)) << 23;
-    memcpy(&s, &u, 4);
-    return s;
+    /* export_eva.py:64-66's sc = amax / 448 per block (one IEEE division); a block whose |max| is below 2^-116
+     * (where 448 / amax would leave the normal range) is a zero block, scale 1 */
+    return amax < 0x1p-116f ? 1.0f : amax / 448.0f;
 }
 
 /* ---------------------------------------------------------------------------------------------------------------

@@ -7,7 +7,7 @@
  *   E4M3      OCP FP8 E4M3 ("fn": no inf, 0x7F/0xFF NaN), encode RNE with saturation to +-448
  *             (src/engine/kern_common.cuh:97-100 __NV_SATFINITE; src/tools/export_eva.py:64-66 clip + RNE cast),
  *             decode as src/tools/kcheck.c:25-33.
- *   scales    s = the least power of two with 448 s >= amax; s = 1 when amax < 2^-116 (zero block).
+ *   scales    s = amax / 448 (IEEE, correctly rounded); s = 1 when amax < 2^-116 (zero block).
  *             activations: q = sat_rne(x * (1 / s)), 1/s rounded once per 1x128 block (eva.h:408 + kern_common.cuh:106)
  *             weights:     q = sat_rne(w / s) per 128x128 block (export_eva.py:65)
  *   GEMM      C[m][n] = sum_kb sa[kb][m] * sw[n/128][kb] * sum_{k in kb} qa[m][k] * qw[n][k]
@@ -33,7 +33,7 @@ uint16_t xo_f32_to_bf16(float x);                /* RNE */
 float xo_bf16_to_f32(uint16_t h);
 uint16_t xo_f32_to_f16(float x);                 /* RNE, overflow -> inf */
 float xo_f16_to_f32(uint16_t h);
-float xo_block_scale(float amax);                /* least power of two >= amax / 448, 1 for a zero block */
+float xo_block_scale(float amax);                /* amax / 448, or 1 for a zero block */
 
 /* ---- packing ---- */
 /* x fp32 [M][ldx], K % 128 == 0 -> q [M][ldq] bytes, s [K/128][lds] */

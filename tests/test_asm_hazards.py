@@ -1,8 +1,9 @@
 """The layer GEMMs issue their MFMAs from inline asm (to hold a fixed issue order), which the compiler's hazard
-recognizer does not see. Code the compiler places after them (the epilogue, or a register copy where paths join) must
-not read an accumulator with VALU before the matrix core has written it. This test compiles the kernels that use the
-asm MFMAs to gfx950 assembly and checks that no VALU instruction reads a VGPR written by a v_mfma within 19 wait
-states (the distance a 16-pass XDL result needs; the 16x16x128 FP8 MFMA is 8 passes and needs 11). CPU only."""
+recognizer does not see. The VALU promotion of a block partial, and code the compiler places after the K loop, must not
+read an MFMA's result before the matrix core has written it. This test compiles the kernels that use the asm MFMAs to
+gfx950 assembly and checks that no VALU instruction reads a VGPR written by a v_mfma within the number of wait states
+hipcc itself inserts between the same MFMA and a VALU read of its result (the s_nop it emits in a one-MFMA probe
+kernel, plus one). CPU only."""
 import os
 import re
 import shutil
@@ -23,7 +24,7 @@ def _regs(spec):
     return {int(m.group(1))} if m else set()
 
 
-def _early_reads(lines, need=19):
+def _early_reads(lines, need):
     """(line, instruction) of VALU reads of an MFMA's destination VGPRs fewer than `need` wait states after it."""
     out = []
     for i, line in enumerate(lines):
@@ -50,14 +51,46 @@ def _early_reads(lines, need=19):
     return out
 
 
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Xclang", "-target-feature",
+         "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S"]
+
+PROBE = r"""
+#include <hip/hip_runtime.h>
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+__global__ void probe(const v8i *a, const v8i *b, float *o, float s)
+{
+    v4f z = {0.f, 0.f, 0.f, 0.f};
+    v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[threadIdx.x], b[threadIdx.x], z, 0, 0, 0, 0, 0, 0);
+    o[threadIdx.x] = __builtin_fmaf(p[0], s, p[1]);
+}
+"""
+
+
+def _compiler_wait_states(tmp_path):
+    src = tmp_path / "probe.hip"
+    src.write_text(PROBE)
+    asm = tmp_path / "probe.s"
+    r = subprocess.run([HIPCC] + FLAGS + [str(src), "-o", str(asm)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [x.strip() for x in asm.read_text().splitlines()]
+    i = next(k for k, x in enumerate(lines) if x.startswith("v_mfma_f32_16x16x128_f8f6f4"))
+    nop = lines[i + 1]
+    assert nop.startswith("s_nop"), f"expected the compiler's s_nop after the probe MFMA, got {nop!r}"
+    return int(nop.split()[1]) + 1
+
+
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not available")
-@pytest.mark.parametrize("src", ["layer.hip", "px.hip"])
+@pytest.mark.parametrize("src", ["layer.hip", "px.hip", "quant.hip"])
 def test_no_early_accumulator_reads(tmp_path, src):
+    need = _compiler_wait_states(tmp_path)
+    assert need >= 11
     asm = tmp_path / (src + ".s")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Xclang",
-           "-target-feature", "-Xclang", "-packed-fp32-ops", "-I" + os.path.join(os.path.dirname(CSRC), "..", "include"),
-           "-I" + CSRC, "--cuda-device-only", "-S", os.path.join(CSRC, src), "-o", str(asm)]
+    cmd = [HIPCC] + FLAGS + ["-I" + os.path.join(os.path.dirname(CSRC), "..", "include"), "-I" + CSRC,
+                             os.path.join(CSRC, src), "-o", str(asm)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stderr[-2000:]
-    bad = _early_reads(asm.read_text().splitlines())
-    assert not bad, f"VALU reads of MFMA results too early in {src}: {bad[:5]}"
+    lines = asm.read_text().splitlines()
+    assert sum(1 for x in lines if x.strip().startswith("v_mfma")) > 0
+    bad = _early_reads(lines, need)
+    assert not bad, f"VALU reads of MFMA results too early in {src} (need {need} wait states): {bad[:5]}"

@@ -1,10 +1,10 @@
-"""Why the build drops the reference's SmoothQuant (export_eva.py:52-58, 100-110), and what its power-of-two block
-scales cost. With 1x128 activation and 128x128 weight block scales, channel outliers in the activations cost less
-accuracy than the reference's production scheme (SmoothQuant with alpha 0.5, then one E4M3 scale per tensor, the
-activation scale from the calibrated maximum times HEADROOM 1.25), and smoothing on top of block scales changes nothing
-measurable. The build's block scale is the least power of two s with 448 s >= |max| (so the matrix core applies it
-as an E8M0 exponent); against the exact |max| / 448 it loses only where a block's maximum carries much of the energy
-(the exact scale puts that maximum on 448 without rounding), and it stays at or below the reference's error. The real
+"""Why the build drops the reference's SmoothQuant (export_eva.py:52-58, 100-110). With 1x128 activation and 128x128
+weight block scales s = |max| / 448 (the reference's own scale rule, export_eva.py:64-66, applied per block), channel
+outliers in the activations cost less accuracy than the reference's production scheme (SmoothQuant with alpha 0.5,
+then one E4M3 scale per tensor, the activation scale from the calibrated maximum times HEADROOM 1.25), and smoothing on
+top of block scales changes nothing measurable. The test also prices the power-of-two alternative (the least power of
+two s with 448 s >= |max|, which a matrix core could apply as an E8M0 exponent): it is never more accurate and up to
+1.4x worse where a few outliers carry the energy, which is why the build keeps exact |max| / 448 scales. The real
 activation statistics are not available (the calibration file of the reference does not parse), so the test uses
 synthetic activations with outlier channels of the kind SmoothQuant targets. E4M3 rounding is torch's
 float8_e4m3fn cast after a +-448 clamp."""
@@ -23,7 +23,7 @@ def _per_tensor(x, amax):
 
 
 def _scale(amax, pow2):
-    """|max| / 448, or the least power of two at or above it (the build's rule: exact frexp in float64)"""
+    """|max| / 448 (the build's rule), or the least power of two at or above it (exact frexp in float64)"""
     s = np.asarray(amax, np.float64) / 448.0
     if pow2:
         m, e = np.frexp(s)
@@ -32,14 +32,14 @@ def _scale(amax, pow2):
     return s
 
 
-def _act_blocks(x, pow2=True):
+def _act_blocks(x, pow2=False):
     M, K = x.shape
     xb = x.reshape(M, K // 128, 128)
     s = _scale(np.abs(xb).max(-1, keepdims=True), pow2)
     return (_q8(xb / s) * s).reshape(M, K).astype(np.float64)
 
 
-def _w_blocks(w, pow2=True):
+def _w_blocks(w, pow2=False):
     N, K = w.shape
     wb = w.reshape(N // 128, 128, K // 128, 128)
     s = _scale(np.abs(wb).max((1, 3), keepdims=True), pow2)
@@ -71,9 +71,9 @@ def test_block_scales_vs_smoothquant(n_out, mag):
     e_ref = err(_per_tensor(xs, 1.25 * np.abs(xs).max()) @ _per_tensor(ws, np.abs(ws).max()).T)
     e_blk = err(_act_blocks(x) @ _w_blocks(w).T)
     e_blk_sq = err(_act_blocks(xs) @ _w_blocks(ws).T)
-    e_exact = err(_act_blocks(x, False) @ _w_blocks(w, False).T)
-    print(f"outliers {n_out} x{mag}: SmoothQuant + per-tensor {e_ref:.4f}, power-of-two blocks {e_blk:.4f}, "
-          f"+ SmoothQuant {e_blk_sq:.4f}, exact |max| / 448 blocks {e_exact:.4f}")
+    e_pow2 = err(_act_blocks(x, True) @ _w_blocks(w, True).T)
+    print(f"outliers {n_out} x{mag}: SmoothQuant + per-tensor {e_ref:.4f}, |max| / 448 blocks {e_blk:.4f}, "
+          f"+ SmoothQuant {e_blk_sq:.4f}, power-of-two blocks {e_pow2:.4f}")
     assert e_blk <= 1.02 * e_ref
     assert abs(e_blk_sq - e_blk) <= 0.05 * e_blk
-    assert e_exact <= e_blk <= 1.5 * e_exact
+    assert e_blk <= e_pow2 <= 1.5 * e_blk

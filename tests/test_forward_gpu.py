@@ -21,8 +21,6 @@ import numpy as np
 import pytest
 import torch
 
-from tests.scales import block_amax, blocks_agree, codes_differing
-
 pytestmark = pytest.mark.gpu
 
 T, D, HIDP = 1025, 1024, 2816
@@ -119,14 +117,13 @@ class OracleCheck:
             acc = orc.gemm_f32(g["h8"], g["sh"], *W["w12"], 2 * HIDP)
             hf, stat = orc.fc1_epi(acc)
             q, s = orc.quant_act(hf)
-            # the block scale follows one GEMM-fed maximum over 128 units: where that maximum sits on a power-of-two
-            # boundary, the matrix core's sum can put the kernel's scale one binade from the oracle's
-            eq = blocks_agree(g["sm"], s, block_amax(hf, 22), rel=1e-3)
-            self.worst["fc1 block scales a binade apart"] = max(self.worst["fc1 block scales a binade apart"],
-                                                                int((~eq).sum()))
-            frac = codes_differing(g["m8"], q, eq)
+            frac = float(np.mean(g["m8"] != q))
             self.worst["fc1 codes differing (frac)"] = max(self.worst["fc1 codes differing (frac)"], frac)
             assert frac < 2e-3, f"fc1 layer {i}: {frac:.2e} of codes differ"
+            # the block scale is one GEMM-fed maximum over 128 units: the matrix core's sum moves it by ~1e-5
+            sdev = float(np.abs(g["sm"] / s - 1).max())
+            self.worst["fc1 block scale rel"] = max(self.worst["fc1 block scale rel"], sdev)
+            assert sdev < 1e-3
             dq = orc.e4m3_decode(g["m8"]) * np.repeat(g["sm"].T, 128, 1)
             self.close("fc1+swiglu (dequantized)", dq, hf, np.abs(hf).max(), 2.0 ** -3)
             self.close("fc1 row sums", g["stat"][..., 0], stat[..., 0], np.abs(stat[..., 1]).max() ** 0.5, 0.0)
@@ -354,16 +351,17 @@ def test_submit_ring_nonblocking(dev, synth_blob):
         assert np.array_equal(got[b], ref[b]), f"buf {b}"
 
 
-def test_batch_halves(dev, synth_blob):
+@pytest.mark.parametrize("sparse", [False, True])
+def test_batch_halves(dev, synth_blob, sparse):
     """A batch runs as two halves at once (the first ceil(nb / 2) inputs on the engine stream, the rest on the second
     lane). With nb = 3 (halves of 2 and 1): full, partial (n = 1: the second lane idle, n = 2: exactly the first half)
-    and resident batches give every image the scores an nb = 1 engine gives it, bit for bit."""
+    and resident batches give every image the scores an nb = 1 engine gives it, bit for bit; dense and 2:4-sparse."""
     import ctypes
     from xtagger_amd import blob
     from xtagger_amd.engine import Engine
     path, m = synth_blob
     inp = blob.synth_inputs(3, seed=93)
-    e1 = Engine(path, device=0, nb=1)
+    e1 = Engine(path, device=0, nb=1, sparse=sparse)
     e1.ready()
     ref = []
     for i in range(3):
@@ -371,7 +369,7 @@ def test_batch_halves(dev, synth_blob):
         ref.append(e1.wait(0, 1)[0].copy())
     e1.close()
     ref = np.stack(ref)
-    e = Engine(path, device=0, nb=3)
+    e = Engine(path, device=0, nb=3, sparse=sparse)
     e.ready()
     e.submit(0, inp)
     assert np.array_equal(e.wait(0, 3), ref)

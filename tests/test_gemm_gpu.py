@@ -155,7 +155,7 @@ def test_gemm_layer_shapes_m8200(dev, xt, orc, N, K):
 
 
 def test_gemm_kcheck_oproj_method(dev, xt, orc):
-    """kcheck.c:100-127 restated for the k_oproj operands: LCG E4M3 bytes (no NaN, exponent <= 9), alpha 0.001
+    """kcheck.c:100-127's operands on the standalone GEMM (eva_k_gemm, fp32 out): LCG E4M3 bytes (no NaN, exponent <= 9), alpha 0.001
     (all activation scales 0.001, all weight scales 1), fp64 loops on the 97 rows m = 7919 i mod 8200."""
     from tests.kcheck import sample_rows
     rows_n, D = 8 * 1025, 1024
@@ -173,6 +173,43 @@ def test_gemm_kcheck_oproj_method(dev, xt, orc):
     # kcheck's operands span products 2^-18 .. 56 inside one K block; the f8f6f4 matrix core sums them with less
     # than fp32 precision (observed ~6e-5 of max |ref|), so the bound is the GEMM contract, 1e-3
     assert err <= 1e-3 * np.abs(ref).max()
+
+
+def test_oproj_kcheck_method(dev, xt, orc):
+    """kcheck.c:100-127 run on the k_oproj kernel itself (eva_k_oproj): x [8200][1024] fp16 = h(frand()) from the LCG
+    stream after k_pe's operands and the E4M3 operand bytes, x += alpha a W^T with alpha = 0.001 given as the block
+    scales (every activation scale 0.001, every weight scale 1: not a power of two, so a kernel that applied only a
+    scale's exponent would compute with 2^-10 and miss by 2.3%); fp64 loops on the 97 rows m = 7919 i mod 8200 against
+    ref = float(alpha s + x0)."""
+    from tests.kcheck import sample_rows
+    rows_n, D = 8 * 1025, 1024
+    g = orc.Lcg(12345)
+    g.frand(8 * 1024 * 588 + 1024 * 588)              # k_pe's operands come first (kcheck.c:80-83, 588 draws a row)
+    a = g.e4m3(rows_n * D).reshape(rows_n, D)
+    w = g.e4m3(D * D).reshape(D, D)
+    x0 = g.frand(rows_n * D).astype(np.float16).reshape(rows_n, D)
+    alpha = np.float32(0.001)
+    sa = np.full((D // 128, rows_n), alpha, np.float32)
+    sw = np.ones((D // 128, D // 128), np.float32)
+    d_a, d_sa, d_w, d_sw = (torch.from_numpy(np.ascontiguousarray(t)).to(dev) for t in (a, sa, w, sw))
+    d_x = torch.from_numpy(x0).to(dev)
+    _run(xt.lib.eva_k_oproj(xt.ptr(d_a), xt.ptr(d_sa), rows_n, xt.ptr(d_w), xt.ptr(d_sw), xt.ptr(d_x), rows_n,
+                            _stream()), "eva_k_oproj")
+    x = d_x.cpu().numpy()
+    rows = sample_rows(rows_n)
+    lut = orc.E4M3_LUT.astype(np.float64)
+    da, dw = lut[a[rows]], lut[w]
+    s = da @ dw.T
+    ref = (float(alpha) * s + x0[rows].astype(np.float64)).astype(np.float32).astype(np.float64)
+    terms = float(alpha) * (np.abs(da) @ np.abs(dw).T)
+    got = x[rows].astype(np.float64)
+    err = np.abs(got - ref)
+    _say(f"kcheck k_oproj max |err| {err.max():.5f} (max |ref| {np.abs(ref).max():.3f})")
+    # one fp16 rounding of the fp32 result (half an ulp) plus the matrix core's summation within 2e-4 of the terms
+    assert (err <= 2.0 ** -11 * np.abs(ref) + 2.0 ** -25 + 2e-4 * terms).all()
+    # the bound tells alpha from its power-of-two part: a kernel that computed with 2^-10 would fail it
+    wrong = (2.0 ** -10 * s + x0[rows].astype(np.float64)).astype(np.float32).astype(np.float64)
+    assert (np.abs(wrong - ref) > 2.0 ** -11 * np.abs(ref) + 2.0 ** -25 + 2e-4 * terms).any()
 
 
 def test_gemm_kcheck_pe_method(dev, xt, orc):

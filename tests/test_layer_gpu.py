@@ -11,8 +11,6 @@ import numpy as np
 import pytest
 import torch
 
-from tests.scales import block_amax, blocks_agree, codes_differing
-
 pytestmark = pytest.mark.gpu
 
 T, D, TP, HIDP = 1025, 1024, 1088, 2816
@@ -397,11 +395,11 @@ def test_fc1_swiglu_pack(dev, xt, orc):
     h, stat = orc.fc1_epi(_acc_ref(orc, qa, sa, qw, sw, 2 * HIDP))
     q, s = orc.quant_act(h)
     ms = d_ms.cpu().numpy()[:, :M]
-    eq = blocks_agree(ms, s, block_amax(h, 22))
+    assert np.abs(ms / s - 1).max() < 1e-4
     m8 = d_m8.cpu().numpy()
-    frac = codes_differing(m8, q, eq)
-    _say(f"  E4M3 codes differing: {frac:.2e}, block scales a binade apart: {int((~eq).sum())}")
-    assert frac < 2e-3
+    same = m8 == q
+    _say(f"  E4M3 codes differing: {np.mean(~same):.2e}")
+    assert np.mean(~same) < 2e-3
     dq = orc.e4m3_decode(m8) * np.repeat(ms.T, 128, 1)
     assert np.abs(dq - h).max() <= 2.0 ** -3 * np.abs(h).max() + 1e-6
     st = d_st.cpu().numpy()[:, :M]

@@ -107,28 +107,30 @@ def test_f16_rne_vs_torch(orc):
 
 
 # ---------------------------------------------------------------- block packing
-def _pow2_scale(amax):
-    """The least power of two s with 448 s >= amax (exact: frexp of the float64 quotient), 1 below 2^-116."""
-    amax = np.asarray(amax, np.float64)
-    m, e = np.frexp(amax / 448.0)
-    s = np.ldexp(1.0, np.where(m == 0.5, e - 1, e))
-    return np.where(amax < 2.0 ** -116, 1.0, s).astype(np.float32)
+def _contract_scale(amax):
+    """export_eva.py:64-66's sc = amax / 448 in float64, rounded once to fp32 (a float64 quotient of two fp32 values
+    rounds to the correctly rounded fp32 quotient: 53 >= 2 * 24 + 2), 1 below 2^-116."""
+    amax = np.asarray(amax, np.float32).astype(np.float64)
+    return np.where(amax < 2.0 ** -116, 1.0, amax / 448.0).astype(np.float32)
 
 
 def test_block_scale_rule(orc):
-    """xo_block_scale: a power of two with amax / 448 <= s < amax / 224, on every binade edge and around 1.75."""
-    v = [2.0 ** -116, 2.0 ** -100, 1e-30, 0.5, 1.0, 1.75, np.nextafter(np.float32(1.75), np.float32(2)), 1.9999999,
-         447.0, 448.0, np.nextafter(np.float32(448), np.float32(1e9)), 449.0, 896.0, 3e38]
-    v = np.array(v, np.float32)
+    """xo_block_scale = amax / 448 correctly rounded, on binade edges, near the zero-block threshold and on 20000 random
+    maxima (where amax * float32(1 / 448), a plausible slip, differs from the quotient in a large share of cases)."""
+    edge = [2.0 ** -116, np.nextafter(np.float32(2.0 ** -116), np.float32(0)), 2.0 ** -100, 1e-30, 0.5, 1.0, 1.75,
+            1.9999999, 447.0, 448.0, np.nextafter(np.float32(448), np.float32(1e9)), 449.0, 896.0, 3e38]
+    r = np.random.default_rng(11)
+    rnd = (r.random(20000) * 2.0 ** r.integers(-60, 60, 20000)).astype(np.float32)
+    v = np.concatenate([np.array(edge, np.float32), rnd])
     got = np.array([orc.lib.xo_block_scale(float(a)) for a in v], np.float32)
-    assert (got == _pow2_scale(v)).all()
-    assert (np.frexp(got)[0] == 0.5).all()
-    assert (448.0 * got.astype(np.float64) >= v).all() and (224.0 * got.astype(np.float64) < v).all()
+    assert (got == _contract_scale(v)).all()
+    slip = (v * np.float32(1.0 / 448.0)).astype(np.float32)
+    assert np.mean(slip != got) > 0.1, "the random maxima must tell a quotient from a product with 1/448"
     assert orc.lib.xo_block_scale(0.0) == 1.0 and orc.lib.xo_block_scale(2.0 ** -117) == 1.0
 
 
 def _blocks_ok(x, q, s, orc):
-    """decode(q) * s reconstructs x to E4M3 precision; the block max (in (224, 448] before rounding) decodes into [224, 448]."""
+    """decode(q) * s reconstructs x to E4M3 precision; every non-zero block's maximum decodes to exactly 448."""
     M, K = x.shape
     dq = orc.e4m3_decode(q)[:, :K].reshape(M, K // 128, 128)
     sc = s[:, :M].T[:, :, None]
@@ -137,8 +139,7 @@ def _blocks_ok(x, q, s, orc):
     assert (err <= np.maximum(np.abs(xr) * 2.0 ** -4, sc * 2.0 ** -10) * 1.0001).all()
     amax = np.abs(xr).max(2)
     nz = amax >= 2.0 ** -116
-    bmax = np.abs(dq).max(2)[nz]
-    assert ((bmax >= 224.0) & (bmax <= 448.0)).all()
+    assert (np.abs(dq).max(2)[nz] == 448.0).all()
     assert (s[:, :M].T[~nz] == 1.0).all()
 
 
@@ -151,7 +152,7 @@ def test_quant_act_vs_independent(orc):
     q, s = orc.quant_act(x, lds=70)
     xb = x.reshape(67, 4, 128)
     amax = np.abs(xb).max(2)
-    sc = _pow2_scale(amax)
+    sc = _contract_scale(amax)
     assert (s[:, :67].T == sc).all() and (s[:, 67:] == 0).all()
     inv = (np.float32(1) / sc).astype(np.float32)
     y = np.clip(xb * inv[:, :, None], -448, 448).astype(np.float32)
@@ -169,7 +170,7 @@ def test_quant_w_vs_independent(orc):
     for nb in range(3):
         for kb in range(2):
             blk = w[nb * 128:nb * 128 + 128, kb * 128:kb * 128 + 128]
-            sc = _pow2_scale(np.abs(blk).max())
+            sc = _contract_scale(np.abs(blk).max())
             assert s[nb, kb] == sc
             y = np.clip(blk / sc, -448, 448).astype(np.float32)
             ref = torch.from_numpy(y).to(torch.float8_e4m3fn).view(torch.uint8).numpy()

@@ -10,8 +10,6 @@ import numpy as np
 import pytest
 import torch
 
-from tests.scales import block_amax, blocks_agree, codes_differing
-
 pytestmark = pytest.mark.gpu
 
 D, HID, T_IMG = 1024, 4736, 5184
@@ -186,9 +184,9 @@ def test_px_fc1_gelu_pack(dev, xt, orc, with_rs):
     ms = d_ms.cpu().numpy()
     assert (ms[:, M:] == 0).all()                             # nothing written past `rows`
     ms = ms[:, :M]
-    eq = blocks_agree(ms, s, block_amax(h, HID // 128))
+    assert np.abs(ms / s - 1).max() < 1e-4
     m8 = d_m8.cpu().numpy()
-    diff = codes_differing(m8, q, eq)
+    diff = np.mean(m8 != q)
     _say(f"  E4M3 codes differing: {diff:.2e}")
     assert diff < 2e-3
     dq = orc.e4m3_decode(m8) * np.repeat(ms.T, 128, 1)
@@ -267,8 +265,7 @@ def test_px_block_chain(dev, xt, orc, L, qstep):
     hh = orc.px_fc1_epi(_acc(orc, h8, hs, qw1, sw1, HID), bf1)
     qh, sh = orc.quant_act(hh)
     m8, ms = d_m8.cpu().numpy(), d_ms.cpu().numpy()
-    eq = blocks_agree(ms[:, :M], sh, block_amax(hh, HID // 128))
-    assert codes_differing(m8, qh, eq) < 2e-3
+    assert np.mean(m8 != qh) < 2e-3 and np.abs(ms[:, :M] / sh - 1).max() < 1e-4
     # fc2 over the kernel's own packed hidden activations
     x2 = x1g.copy()
     _ok(xt.lib.px_k_fc2(xt.ptr(d_m8), xt.ptr(d_ms), lds, xt.ptr(_d(qw2, dev)), xt.ptr(_d(sw2, dev)),

@@ -12,8 +12,6 @@ import numpy as np
 import pytest
 import torch
 
-from tests.scales import block_amax, blocks_agree, codes_differing
-
 pytestmark = pytest.mark.gpu
 
 T, D, HID, HIDP = 1025, 1024, 2730, 2816
@@ -240,8 +238,8 @@ def test_fc1_sp(dev, xt, orc, layer):
         _ok(rc, "fc1")
         outs.append((m8.cpu().numpy(), ms.cpu().numpy()[:, :M], st.cpu().numpy()[:, :M]))
     (a8, as_, ast), (b8, bs, bst) = outs
-    eq = blocks_agree(bs, as_, got_codes=b8, ref_codes=a8, decode=orc.e4m3_decode)
-    diff = codes_differing(b8, a8, eq)
-    _say(f"  fc1: E4M3 codes differing {diff:.2e}, block scales a binade apart: {int((~eq).sum())}")
+    diff = np.mean(a8 != b8)
+    _say(f"  fc1: E4M3 codes differing {diff:.2e}, scales rel {np.abs(bs / as_ - 1).max():.2e}")
     assert diff < 2e-3
+    assert np.abs(bs / as_ - 1).max() < 1e-4
     assert np.abs(bst - ast).max() <= 1e-4 * np.abs(ast).max()

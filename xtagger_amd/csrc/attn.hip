@@ -305,7 +305,7 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
     __syncthreads();
     if (!active) return;
     amax = __builtin_fmaxf(amax, xamax[(w ^ 4) * 32 + l32]);
-    const float sc = block_scale(amax);
+    const float sc = block_scale(amax), inv = block_scale_inv(sc);
     const int query = q0 + l32;
     if (query >= T) return;
     const size_t m = (size_t)b * T + query;
@@ -315,7 +315,8 @@ __global__ void __launch_bounds__(512) k_flash(const uint16_t *__restrict__ q, c
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int d = 32 * dt + 8 * j + 4 * g;
-            *(uint32_t *)(dst + d) = e4_pack4_s(o[dt][4 * j], o[dt][4 * j + 1], o[dt][4 * j + 2], o[dt][4 * j + 3], sc);
+            *(uint32_t *)(dst + d) = e4_pack4_scaled(o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv,
+                                                     o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv);
             if (DBG) {
                 float *dd = o32 + m * XT_D + head * XT_HD + d;
                 *(float4 *)dd = make_float4(o[dt][4 * j], o[dt][4 * j + 1], o[dt][4 * j + 2], o[dt][4 * j + 3]);

@@ -7,11 +7,10 @@
 // scales sw [Npad/128][K/128], rows padded with zeros to a multiple of 128). K % 128 == 0.
 //
 // CDNA4 mapping:
-//  - one K step = one 128-wide scale block = one MFMA per 16x16 output tile. The layer GEMMs, whose scales are
-//    powers of two, use v_mfma_scale_f32_16x16x128_f8f6f4: the matrix core applies sa * sw as E8M0 exponents and
-//    accumulates in place (bs_step_mx). eva_k_gemm takes any fp32 scales: its block partial leaves the matrix core
-//    whole (v_mfma_f32_16x16x128_f8f6f4) and is promoted with one fma per accumulator, acc = fma(p, sa*sw, acc)
-//    (bs_step_fixed);
+//  - one K step = one 128-wide scale block = one MFMA per 16x16 output tile: the block partial leaves the matrix core
+//    whole (v_mfma_f32_16x16x128_f8f6f4, fp32 result) and is promoted with one fma per accumulator,
+//    acc = fma(p, sa * sw, acc), so any fp32 scales are honoured (the reference's alpha * acc, eva.h:415-418, with the
+//    scale product taken per row and per K block);
 //  - operands go HBM/L2 -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging), 1 KB = 8 rows x 128 bytes (whole
 //    cache lines) per wave instruction. The loads are issued from inline assembly: the compiler then does not track
 //    them, and its conservative "wait for every LDS DMA before any LDS read" rule (which would drain the whole
@@ -250,7 +249,8 @@ __device__ __forceinline__ void bs_step(const uint8_t *st, int wm0, int wn0, v4f
 //  - A 0 and B 0 are read first, then the scales, then A 1-3 and B 1: the first MFMA waits for four reads only;
 //  - B fragment j + 2 is read right after MFMA (j, 0), into the slot B fragment j - 1 has left (3-slot ring);
 //  - the promotion of MFMA t - 3 follows MFMA t. In steady state 15 instructions separate an MFMA from the first
-//    VALU read of its result (an 8-pass XDL result needs 11); the first promotion of a step is preceded by s_nop 7;
+//    VALU read of its result, and 12 after the step's last MFMA (gfx950 asks 12 wait states of this MFMA's result
+//    before a VALU read: hipcc puts s_nop 11 there); the first promotion of a step is preceded by s_nop 7;
 //  - the LPS loads of K step dkb (dkb < 0: none) go out one per MFMA from MFMA 1 on, not in a burst that would stall
 //    this wave's issue behind the vector-memory queue.
 __device__ __forceinline__ void mfma_asm(v4f &p, const v8i &a, const v8i &b)
@@ -361,140 +361,6 @@ __device__ __forceinline__ void bs_step_rows(const uint8_t *st, int wm0, int wn0
     }
 }
 
-// ---- K steps with the block scales applied inside the matrix core ----
-// When every scale is a power of two (block_scale's rule, which all the packers of this library follow), the product of
-// a row's activation scale and the column block's weight scale is 2^(ea - 127) 2^(eb - 127) with ea, eb the scales'
-// fp32 exponent fields, which v_mfma_scale_f32_16x16x128_f8f6f4 takes as E8M0 operands: lane l supplies the exponent
-// of A row l & 15 and of B column l & 15 (measured on gfx950: with exponents that vary by row and column the product
-// matches the fp64 one; they apply to the lane's whole 128-wide K step here because our scales do). The block partial
-// then never leaves the matrix core: no promotion, acc += 2^(ea + eb - 254) (a . b) per 16 x 16 tile per step.
-// Byte OPA of sa holds ea (the four A row tiles of a wave tile use bytes 0..3 of one word), byte 0 of sb holds eb.
-template <int OPA>
-__device__ __forceinline__ void mfma_mx_asm(v4f &acc, const v8i &a, const v8i &b, uint32_t sa, uint32_t sb)
-{
-    static_assert(OPA >= 0 && OPA < 4, "scale byte");
-    if constexpr (OPA == 0)
-        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0]"
-                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
-    else if constexpr (OPA == 1)
-        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,0,0] op_sel_hi:[0,0,0]"
-                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
-    else if constexpr (OPA == 2)
-        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[1,0,0]"
-                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
-    else
-        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
-}
-__device__ __forceinline__ void mfma_mx(int i, v4f &acc, const v8i &a, const v8i &b, uint32_t sa, uint32_t sb)
-{
-    if (i == 0) mfma_mx_asm<0>(acc, a, b, sa, sb);
-    else if (i == 1) mfma_mx_asm<1>(acc, a, b, sa, sb);
-    else if (i == 2) mfma_mx_asm<2>(acc, a, b, sa, sb);
-    else mfma_mx_asm<3>(acc, a, b, sa, sb);
-}
-// The last MFMA of a K loop, with 32 wait states in the same asm statement. The compiler cannot see that these asm
-// MFMAs write the accumulators, so code it places after them (the epilogue, or a register copy it inserts where the
-// loop's paths join) may read an accumulator with VALU before the matrix core has written it; no separate statement
-// can guard that, as the copy may land between the two.
-template <int OPA>
-__device__ __forceinline__ void mfma_mx_asm_end(v4f &acc, const v8i &a, const v8i &b, uint32_t sa, uint32_t sb)
-{
-#define XT_MX_END "\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-    static_assert(OPA >= 0 && OPA < 4, "scale byte");
-    if constexpr (OPA == 0)
-        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0]" XT_MX_END
-                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
-    else if constexpr (OPA == 1)
-        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,0,0] op_sel_hi:[0,0,0]" XT_MX_END
-                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
-    else if constexpr (OPA == 2)
-        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[1,0,0]" XT_MX_END
-                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
-    else
-        asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel:[1,0,0] op_sel_hi:[1,0,0]" XT_MX_END
-                     : "+v"(acc) : "v"(a), "v"(b), "v"(sa), "v"(sb) : "memory");
-#undef XT_MX_END
-}
-// the step's last MFMA: with the wait states when no later K step follows (dkb < 0 at the last step of a 2-stage loop)
-__device__ __forceinline__ void mfma_mx_last(int i, bool end, v4f &acc, const v8i &a, const v8i &b, uint32_t sa,
-                                             uint32_t sb)
-{
-    if (!end) mfma_mx(i, acc, a, b, sa, sb);
-    else if (i == 0) mfma_mx_asm_end<0>(acc, a, b, sa, sb);
-    else if (i == 1) mfma_mx_asm_end<1>(acc, a, b, sa, sb);
-    else if (i == 2) mfma_mx_asm_end<2>(acc, a, b, sa, sb);
-    else mfma_mx_asm_end<3>(acc, a, b, sa, sb);
-}
-// E8M0 exponents of the activation scales of this lane's A rows wm0 + 16 i + (lane & 15), i < TMV, in byte i
-template <int TMV>
-__device__ __forceinline__ uint32_t mx_row_scales(const float *ts, int wm0, int r16)
-{
-    uint32_t w = 0;
-#pragma unroll
-    for (int i = 0; i < TMV; i++) w |= (__float_as_uint(ts[wm0 + 16 * i + r16]) >> 23) << (8 * i);
-    return w;
-}
-
-// The K step of bs_step_fixed with the scales in the matrix core: the same fragment reads, ring and load issue, the 32
-// MFMAs accumulate in place, and no VALU work is left in the step but the scale word
-template <class C>
-__device__ __forceinline__ void bs_step_mx(const uint8_t *st, int wm0, int wn0, v4f (&acc)[C::TM][C::TN],
-                                           const BsOperands<C> &op, uint32_t dstage, int dkb)
-{
-    static_assert(C::TM == 4 && C::TN == 8 && C::LPS < 32, "schedule written for 64 x 128 wave tiles");
-    const int r16 = threadIdx.x & 15;
-    const uint8_t *ta = st, *tb = st + C::A_BYTES;
-    const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
-    v8i a[4], b[3];
-    b[0] = ld_frag(tb, wn0);
-    a[0] = ld_frag(ta, wm0);
-    asm volatile("" ::: "memory");  // the first MFMA waits for these reads and the scales only
-    const uint32_t sb = __float_as_uint(*(const float *)(st + C::A_BYTES + C::B_BYTES + C::S_BYTES + 4 * (wn0 >> 7))) >> 23;
-    const uint32_t sa = mx_row_scales<4>(ts, wm0, r16);
-    asm volatile("" ::: "memory");
-    a[1] = ld_frag(ta, wm0 + 16);
-    a[2] = ld_frag(ta, wm0 + 32);
-    a[3] = ld_frag(ta, wm0 + 48);
-    b[1] = ld_frag(tb, wn0 + 16);
-    asm volatile("" ::: "memory");
-#pragma unroll
-    for (int t = 0; t < 32; t++) {
-        const int j = t >> 2, i = t & 3;
-        if (t < 31) mfma_mx(i, acc[i][j], a[i], b[j % 3], sa, sb);
-        else mfma_mx_last(i, dkb < 0, acc[i][j], a[i], b[j % 3], sa, sb);
-        if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
-        if (t >= 1 && t <= C::LPS && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
-    }
-}
-
-// bs_step_mx for a wave of a partial last row tile whose rows below M fill only its first TMV < 4 row tiles: those row
-// tiles' MFMAs, with the operands and scale words bs_step_mx uses for them (so their accumulators are bit-identical)
-template <class C, int TMV>
-__device__ __forceinline__ void bs_step_mx_rows(const uint8_t *st, int wm0, int wn0, v4f (&acc)[C::TM][C::TN],
-                                                const BsOperands<C> &op, uint32_t dstage, int dkb)
-{
-    static_assert(C::TM == 4 && C::TN == 8 && TMV >= 1 && TMV < 4, "partial row tiles of 64 x 128 wave tiles");
-    if (dkb >= 0) op.issue(dstage, dkb);
-    const int r16 = threadIdx.x & 15;
-    const uint8_t *ta = st, *tb = st + C::A_BYTES;
-    const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
-    v8i a[TMV], b[3];
-    b[0] = ld_frag(tb, wn0);
-    b[1] = ld_frag(tb, wn0 + 16);
-#pragma unroll
-    for (int i = 0; i < TMV; i++) a[i] = ld_frag(ta, wm0 + 16 * i);
-    const uint32_t sb = __float_as_uint(*(const float *)(st + C::A_BYTES + C::B_BYTES + C::S_BYTES + 4 * (wn0 >> 7))) >> 23;
-    const uint32_t sa = mx_row_scales<TMV>(ts, wm0, r16);
-#pragma unroll
-    for (int t = 0; t < 8 * TMV; t++) {
-        const int j = t / TMV, i = t % TMV;
-        if (t < 8 * TMV - 1) mfma_mx(i, acc[i][j], a[i], b[j % 3], sa, sb);
-        else mfma_mx_last(i, dkb < 0, acc[i][j], a[i], b[j % 3], sa, sb);
-        if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
-    }
-}
-
 // Kernel arguments first used after the main loop (epilogue outputs) are read by scalar loads the compiler may leave in
 // flight up to the loop. Scalar loads complete out of order, so with one pending at the loop header the compiler can
 // no longer count LDS reads exactly and waits for every fragment read of a step (lgkmcnt(0)) before its first MFMA.
@@ -519,7 +385,7 @@ struct BsNoPre {
 // flight and the whole shared memory is free for the epilogue. pre() runs once the first stages' loads are issued
 // (epilogue inputs can be fetched there, under the prologue's memory latency); it may write shared memory only past
 // C::LDS.
-template <class C, class Pre = BsNoPre, bool SKIP = true, bool MX = true>
+template <class C, class Pre = BsNoPre, bool SKIP = true>
 __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
                                             int lds, const uint8_t *__restrict__ W, const float *__restrict__ sw,
                                             int M, int Npad, int K, int m0, int n0, uint8_t *smem,
@@ -561,18 +427,7 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
             is = is == C::NS - 1 ? 0 : is + 1;
         }
     };
-    if constexpr (C::TM == 4 && C::TN == 8 && MX) {
-        if (live > 32)
-            kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_mx<C>(st, wm0, wn0, acc, op, dst, dkb); });
-        else if (live > 16)
-            kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_mx_rows<C, 2>(st, wm0, wn0, acc, op, dst, dkb); });
-        else if (live > 0)
-            kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_mx_rows<C, 1>(st, wm0, wn0, acc, op, dst, dkb); });
-        else
-            kloop([&](const uint8_t *, uint32_t dst, int dkb) {
-                if (dkb >= 0) op.issue(dst, dkb);
-            });
-    } else if constexpr (C::TM == 4 && C::TN == 8) {
+    if constexpr (C::TM == 4 && C::TN == 8) {
         if (live > 32)
             kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_fixed<C>(st, wm0, wn0, acc, op, dst, dkb); });
         else if (live > 16)

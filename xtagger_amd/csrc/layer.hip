@@ -185,7 +185,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     __syncthreads();
     // 8 consecutive threads per row, 16 consecutive units each: the row's |max| and sums over its 128 units meet in
     // a DPP tree over the 8 lanes; each thread packs its 16 units to E4M3 (one 16-byte store) and the first thread
-    // of the row writes the block scale (a power of two) and the partial sums. Item it of a thread reads row
+    // of the row writes the block scale and the partial sums. Item it of a thread reads row
     // (tid >> 3) + 64 it, whose row & 7 does not depend on it: the four chunk addresses are bases plus 8192 it words.
     const __amdgpu_buffer_rsrc_t rm = buf_rsrc(m8, (uint32_t)rows * XT_HIDP);
     const int k8 = threadIdx.x & 7, r0 = threadIdx.x >> 3;
@@ -212,10 +212,10 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
         amax = row8_absmax(amax);
         s = row8_sum(s);
         q = row8_sum(q);
-        const float sc = block_scale(amax);
+        const float sc = block_scale(amax), inv = block_scale_inv(sc);
         uint32_t w4[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) w4[c] = e4_pack4_s(v[c].x, v[c].y, v[c].z, v[c].w, sc);
+        for (int c = 0; c < 4; c++) w4[c] = e4_pack4_scaled(v[c].x * inv, v[c].y * inv, v[c].z * inv, v[c].w * inv);
         const v4u o = {w4[0], w4[1], w4[2], w4[3]};
         __builtin_amdgcn_raw_buffer_store_b128(o, rm, (int)((uint32_t)m * XT_HIDP + ct * 128 + u0), 0, 0);
         if ((idx & 7) == 0 && m < rows) {

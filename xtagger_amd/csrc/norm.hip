@@ -47,11 +47,11 @@ __device__ __forceinline__ void quant_row16(const float *v, uint8_t *__restrict_
 #pragma unroll
         for (int j = 0; j < 8; j++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[8 * h + j]));
         amax = group_max<16>(amax);
-        const float sc = block_scale(amax);
+        const float sc = block_scale(amax), inv = block_scale_inv(sc);
         const float *w = v + 8 * h;
         uint2 o;
-        o.x = e4_pack4_s(w[0], w[1], w[2], w[3], sc);
-        o.y = e4_pack4_s(w[4], w[5], w[6], w[7], sc);
+        o.x = e4_pack4_scaled(w[0] * inv, w[1] * inv, w[2] * inv, w[3] * inv);
+        o.y = e4_pack4_scaled(w[4] * inv, w[5] * inv, w[6] * inv, w[7] * inv);
         *(uint2 *)(q + 512 * h + 8 * lane) = o;
         if ((lane & 15) == 0) s[(size_t)(4 * h + (lane >> 4)) * lds + row] = sc;
     }

@@ -48,10 +48,10 @@ __global__ void __launch_bounds__(256) k_quant_act(const TIn *__restrict__ x, in
 #pragma unroll
         for (int i = 0; i < 8; i++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
         amax = group_max<16>(amax);
-        const float sc = block_scale(amax);
+        const float sc = block_scale(amax), inv = block_scale_inv(sc);
         uint2 o;
-        o.x = e4_pack4_s(v[0], v[1], v[2], v[3], sc);
-        o.y = e4_pack4_s(v[4], v[5], v[6], v[7], sc);
+        o.x = e4_pack4_scaled(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+        o.y = e4_pack4_scaled(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
         *(uint2 *)(q + (size_t)row * ldq + ch * 8) = o;
         if ((ch & 15) == 0) s[(size_t)(ch >> 4) * lds + row] = sc;
     }
@@ -132,7 +132,7 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
     const int Npad = (N + 127) & ~127;
     args_resident(Cp, ldc, N, M, lds);
     if constexpr (SP) bs_mainloop_sp<C>(A, lda, sa, lds, W, WX, sw, M, Npad, K, m0, n0, smem, acc);
-    else bs_mainloop<C, BsNoPre, false, false>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
+    else bs_mainloop<C, BsNoPre, false>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
     int wm0, wn0;
     bs_wave_origin<C>(wm0, wn0);
     if (OUT == 1) {

@@ -41,38 +41,22 @@ __device__ __forceinline__ uint32_t e4_pack4(float a, float b, float c, float d)
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(e4_clamp(c), e4_clamp(d), w, true);
 }
 
-// e4_pack4 without the clamp, for values already scaled by 1 / block_scale(|max| of their block): the scale is a power
-// of two with 448 s >= |max|, so |x| / s <= 448 exactly and the clamp cannot change a code.
+// e4_pack4 without the clamp, for values x * (1 / s) of a block scaled by the inverse of its block scale
+// s = block_scale(|max|): |x| <= |max|, s = |max| / 448 (1 + d1) and 1 / s rounded once (1 + d2), so
+// |x * (1 / s)| <= 448 (1 + 2^-22) after the product's own rounding, which rounds to 448 (the next code up, 480, is
+// past the format and the midpoint is 464): the clamp cannot change a code.
 __device__ __forceinline__ uint32_t e4_pack4_scaled(float a, float b, float c, float d)
 {
     int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
 }
 
-// e4_pack4 of a / s, b / s, c / s, d / s for a block scale s (block_scale's rule: a power of two with 448 s >= the
-// block's |max|, so no code saturates). v_cvt_scalef32_pk_fp8_f32 divides by s inside the conversion: measured on
-// gfx950 bit-identical to multiplying by 1 / s first and converting, over every E4M3 rounding midpoint and scales
-// 2^-40 .. 2^29, so the packers save that multiply.
-__device__ __forceinline__ uint32_t e4_pack4_s(float a, float b, float c, float d, float s)
-{
-    typedef short v2s __attribute__((ext_vector_type(2)));
-    v2s w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(v2s{0, 0}, a, b, s, false);
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, c, d, s, true);
-    return __builtin_bit_cast(uint32_t, w);
-}
-
-// Block scale from a block |max|: the least power of two s with 448 s >= amax (so amax / 448 <= s < amax / 224), 1 for
-// a zero block (|max| < 2^-116). With amax = f 2^e (f in [1, 2)) that is 2^(e - 8), or 2^(e - 7) when f > 1.75. A
-// power of two makes x / s exact and lets the GEMMs apply the scale inside the matrix core as an E8M0 exponent.
-__device__ __forceinline__ float block_scale(float amax)
-{
-    if (amax < 0x1p-116f) return 1.0f;
-    const uint32_t u = __float_as_uint(amax);
-    return __uint_as_float(((u >> 23) - 8u + ((u & 0x7FFFFFu) > 0x600000u ? 1u : 0u)) << 23);
-}
-// 1 / s of a block scale, exactly: s = 2^e is a power of two in [2^-124, 2^121], so 1 / s = 2^-e has exponent field
-// 254 minus s's (one integer subtraction in place of an IEEE division)
-__device__ __forceinline__ float block_scale_inv(float s) { return __uint_as_float(0x7F000000u - __float_as_uint(s)); }
+// Block scale from a block |max|: amax / 448, one IEEE division (correctly rounded: HIP device code keeps fp32
+// division exact unless fast math is asked for), 1 for a zero block (|max| < 2^-116, where 448 / amax would leave the
+// normal range). The reference's per-tensor rule sc = amax / 448 (export_eva.py:64-66) applied per block.
+__device__ __forceinline__ float block_scale(float amax) { return amax < 0x1p-116f ? 1.0f : amax / XT_E4MAX; }
+// 1 / s, rounded once per block (the reference's qs = 1 / scl, eva.h:408): activations are packed as x * (1 / s)
+__device__ __forceinline__ float block_scale_inv(float s) { return 1.0f / s; }
 
 // ---- bf16 / fp16 (round to nearest even) ----
 __device__ __forceinline__ uint16_t f2bf(float x)
