@@ -94,3 +94,36 @@ def test_no_early_accumulator_reads(tmp_path, src):
     assert sum(1 for x in lines if x.strip().startswith("v_mfma")) > 0
     bad = _early_reads(lines, need)
     assert not bad, f"VALU reads of MFMA results too early in {src} (need {need} wait states): {bad[:5]}"
+
+
+def _resources(tmp_path, src):
+    """{kernel: (VGPRs, VGPR spills, scratch bytes per lane)} from hipcc's resource-usage remarks."""
+    r = subprocess.run([HIPCC] + FLAGS[:-1] + ["-c", "-I" + os.path.join(os.path.dirname(CSRC), "..", "include"),
+                                                "-I" + CSRC, os.path.join(CSRC, src), "-o", str(tmp_path / "k.o"),
+                                                "-Rpass-analysis=kernel-resource-usage"],
+                       capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    out, cur = {}, None
+    for line in r.stderr.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            cur = m.group(1)
+            out[cur] = [None, None, None]
+        for i, key in enumerate((r"VGPRs: (\d+)", r"VGPRs Spill: (\d+)", r"ScratchSize \[bytes/lane\]: (\d+)")):
+            m = re.search(key, line)
+            if m and cur:
+                out[cur][i] = int(m.group(1))
+    return out
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not available")
+@pytest.mark.parametrize("src", ["layer.hip", "px.hip", "quant.hip", "attn.hip", "norm.hip"])
+def test_no_scratch(tmp_path, src):
+    """No kernel spills registers or keeps an array in scratch memory: a dynamically indexed accumulator array, or
+    two main loops whose registers the allocator cannot keep apart, silently moves the accumulators to memory and
+    slows the kernel several times over."""
+    res = _resources(tmp_path, src)
+    assert res
+    bad = {k: v for k, v in res.items() if v[1] or v[2]}
+    assert not bad, f"kernels with spills or scratch in {src}: {bad}"
+

@@ -119,6 +119,44 @@ def test_gemm_sp_contract(dev, xt, orc, M, N, K):
     assert vs_dense <= 1e-4
 
 
+def test_gemm_sp_extreme_scales(dev, xt, orc):
+    """Block scales over a wide range on the sparse loop, whose per-K-block promotion must honour any fp32 scale: rows
+    with a block 2^-60 smaller than the rest (at K block 5, and at block 0), a row 2^70 larger throughout, a row with one
+    block 2^70 larger, and waves of ordinary rows next to them: every row within 1e-3 of its own fp64 maximum, and
+    within 1e-4 of the dense kernel on the same pruned weights. (A variant that carried the accumulators in units of
+    each block's scale product overflows on such rows unless it checks them first.)"""
+    M, N, K = 320, 512, 1024
+    r = np.random.default_rng(77)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    x[70, 640:768] *= np.float32(2.0 ** -60)      # wave of rows 64..127: scale product below 2^-40 at K block 5
+    x[75, 0:128] *= np.float32(2.0 ** -60)        # the same wave, at block 0 as well
+    x[200, :] *= np.float32(2.0 ** 70)            # wave of rows 192..255: products above 2^40 from the start
+    x[260, 384:512] *= np.float32(2.0 ** 70)      # wave of rows 256..319: one huge block at K block 3
+    qa, sa = orc.quant_act(x)
+    qw, sw = orc.quant_w((r.standard_normal((N, K)) * 0.02).astype(np.float32))
+    qp = orc.prune24(qw)
+    vals, idx, bad = _pack_dev(xt, dev, qp)
+    assert bad == 0
+    d_qa, d_sa, d_sw = _d(qa, dev), _d(sa, dev), _d(sw, dev)
+    c_sp = torch.empty((M, N), dtype=torch.float32, device=dev)
+    c_dn = torch.empty((M, N), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_gemm_sp(xt.ptr(d_qa), K, xt.ptr(d_sa), M, xt.ptr(vals), xt.ptr(idx), xt.ptr(d_sw), M, N, K,
+                             xt.ptr(c_sp), N, 1, _st()), "eva_k_gemm_sp")
+    _ok(xt.lib.eva_k_gemm(xt.ptr(d_qa), K, xt.ptr(d_sa), M, xt.ptr(_d(qp, dev)), xt.ptr(d_sw), M, N, K, xt.ptr(c_dn), N,
+                          1, _st()), "eva_k_gemm")
+    sp, dn = c_sp.cpu().numpy().astype(np.float64), c_dn.cpu().numpy().astype(np.float64)
+    rows = np.arange(M, dtype=np.int32)
+    ref = orc.gemm_f64_rows(qa, sa, qp, sw, N, rows)
+    assert np.isfinite(sp).all()
+    rmax = np.abs(ref).max(1, keepdims=True)
+    err = (np.abs(sp - ref) / rmax).max(1)
+    vs_dense = (np.abs(sp - dn) / np.abs(dn).max(1, keepdims=True)).max(1)
+    _say(f"  worst row vs fp64 {err.max():.2e} (rows 70, 75, 200, 260: {err[[70, 75, 200, 260]]}), "
+         f"vs dense {vs_dense.max():.2e}")
+    assert err.max() <= 1e-3
+    assert vs_dense.max() <= 1e-4
+
+
 # ---------------------------------------------------------------- layer kernels: sparse vs dense on pruned weights
 class _Layer:
     def __init__(self, torch_, xt, orc, dev, M, seed=5):
