@@ -48,11 +48,12 @@ class _Blob:
         self.buf += np.ascontiguousarray(a, dtype=dt).tobytes()
 
 
-def synth_model(seed=0, nt=10861, nl=NL, head_std=0.02, layer_scale=1.0):
-    """Random-init EVA02-L tensors in the v2 export layout (fp16 / fp32 numpy arrays). layer_scale multiplies the two
-    residual-branch outputs of every block (Wo and W2), as a trained network's layer scale keeps its blocks near the
-    identity: at 1.0 (all weights N(0, 0.02)) the 24 blocks amplify a change in any rounding into sigmoid drifts of
-    ~0.06, at 0.1 the forward is well conditioned."""
+def synth_model(seed=0, nt=10861, nl=NL, head_std=0.02, layer_scale=1.0, qk_scale=1.0, lead_tags=0, lead=1.0):
+    """Random-init EVA02-L tensors in the v2 export layout (fp16 / fp32 numpy arrays).
+    layer_scale multiplies the two residual-branch outputs of every block (Wo and W2), as a trained network's layer
+    scale keeps its blocks near the identity; qk_scale multiplies the q and k rows of Wqkv (sharper attention);
+    lead_tags tags (chosen by the seed) get `lead` added to their bias, so that the top-50 has a margin at rank 50/51
+    as a tagger's confident tags do."""
     r = np.random.default_rng(seed)
     f16, f32 = np.float16, np.float32
 
@@ -70,6 +71,7 @@ def synth_model(seed=0, nt=10861, nl=NL, head_std=0.02, layer_scale=1.0):
         L = {}
         L["ln1w"], L["ln1b"] = 1 + n(D, 0.1), n(D, 0.02)
         wqkv = n((3 * D, D), 0.02)
+        wqkv[:2 * D] *= np.float32(qk_scale)
         wqkv[:D] *= QSCALE
         L["wqkv"] = wqkv.astype(f16)
         L["wo"] = (n((D, D), 0.02) * np.float32(layer_scale)).astype(f16)
@@ -92,6 +94,8 @@ def synth_model(seed=0, nt=10861, nl=NL, head_std=0.02, layer_scale=1.0):
     hw[:nt] = n((nt, D), head_std)
     hb = np.zeros(ntp, f32)
     hb[:nt] = n(nt, 0.1)
+    if lead_tags:
+        hb[r.choice(nt, lead_tags, replace=False)] += np.float32(lead)
     m["hw"], m["hb"] = hw.astype(f16), hb
     return m
 
@@ -165,6 +169,27 @@ def read_v2(path):
     if off[0] != nbytes:
         raise ValueError(f"{path}: layout mismatch ({off[0]} vs {nbytes} bytes)")
     return m
+
+
+def synth_smooth_inputs(nb, seed=1):
+    """nb patch operands like synth_inputs, from smooth 448^2 images: per channel a base level in [0, 1) plus a
+    vertical and a horizontal sinusoid (amplitude < 0.3, under 3 periods), plus N(0, 0.05) pixel noise, clipped to
+    [0, 1]. Neighbouring patches see similar content, so the pooled features carry the image rather than the noise."""
+    r = np.random.default_rng(seed)
+    yy, xx = np.meshgrid(np.linspace(0, 1, 448), np.linspace(0, 1, 448), indexing="ij")
+    img = np.empty((nb, 448, 448, 3), np.float32)
+    for b in range(nb):
+        for c in range(3):
+            base = r.random()
+            a1, a2 = r.random(2) * 0.3
+            f1, f2 = r.random(2) * 3
+            img[b, :, :, c] = base + a1 * np.sin(2 * np.pi * f1 * yy) + a2 * np.cos(2 * np.pi * f2 * xx)
+    img = np.clip(img + 0.05 * r.standard_normal(img.shape).astype(np.float32), 0, 1)
+    bgr = img[..., ::-1] * 2.0 - 1.0
+    p = bgr.reshape(nb, 32, 14, 32, 14, 3).transpose(0, 1, 3, 5, 2, 4).reshape(nb, NP, K0)
+    out = np.zeros((nb, NP, K0P), np.float16)
+    out[:, :, :K0] = p.astype(np.float16)
+    return out
 
 
 def synth_inputs(nb, seed=1):
