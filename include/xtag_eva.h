@@ -149,6 +149,10 @@ int eva_k_oproj(const void *a8, const float *as, int lds, const void *w, const f
  * 2730..2815 must have zero weights (they are read as zero from row 5472 on). */
 int eva_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8, float *ms,
               float *stat, int rows, void *stream);
+/* eva_k_fc1 with the reference's per-unit quantization multiplier rs [2816] (eva_kernels.cu:211-279 takes rs: the v3
+ * blob's 1 / (adq s~), export_eva.py:144): m8 packs h * rs[unit] with 1x128 scales, stat still sums h itself. */
+int eva_k_fc1_rs(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8, float *ms,
+                 float *stat, const float *rs, int rows, void *stream);
 /* fc2 with the MLP LayerNorm folded + residual (eva_kernels.cu:286-334 k_fc2): x += rstd (m8 . W~^T - mean c) + d */
 int eva_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *stat,
               const float *cn, const float *dn, void *x, int rows, void *stream);
@@ -174,6 +178,14 @@ int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_
  * [1024][2816], d[n] = sum_{k<2730} w2[n][k] beta[k] */
 int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const float *beta, float *c, float *d,
                   void *stream);
+/* v3 blob weights (export_eva.py:64-66, 133-147: E4M3 with one fp32 scale per tensor) to the kernels' layout: E4M3
+ * rows w8 [n_in][ldw] -> q [n_out][k_out] (rows >= n_in and columns >= k_in zero; perm 1 pair-splits the q and k heads
+ * as eva_k_prep_w), every 128 x 128 block scale s [n_out/128][k_out/128] = scale. */
+int eva_k_prep_w8(const void *w8, int ldw, int n_in, int k_in, int n_out, int k_out, int perm, float scale, void *q,
+                  float *s, void *stream);
+/* c[n] = sum_k dec(q[n][k]) s[n/128][k/128] rs[k] over W~ [1024][2816] with its v3 per-unit multipliers rs (the v3
+ * blob's c, export_eva.py:145, recomputed for 2:4-pruned W~) */
+int eva_k_fold_c_rs(const void *q, const float *s, const float *rs, float *c, void *stream);
 
 /* ---- 2:4 structured-sparse weights (src/tools/prune24.py:43-56 prunes, mma.sp named at
  * prune24.py:1 is never used there) ---- */
@@ -196,6 +208,8 @@ int eva_k_oproj_sp(const void *a8, const float *as, int lds, const void *vals, c
                    void *x, int rows, void *stream);
 int eva_k_fc1_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx, const float *ws,
                  void *m8, float *ms, float *stat, int rows, void *stream);
+int eva_k_fc1_rs_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx, const float *ws,
+                    void *m8, float *ms, float *stat, const float *rs, int rows, void *stream);
 int eva_k_fc2_sp(const void *m8, const float *ms, int lds, const void *vals, const void *idx, const float *ws,
                  const float *stat, const float *cn, const float *dn, void *x, int rows, void *stream);
 

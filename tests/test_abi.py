@@ -49,7 +49,8 @@ def test_px_bad_shapes_rejected_without_gpu():
 
 
 def test_open_rejects_bad_header(tmp_path):
-    """eva.h:580-586: a file that is not an EVA2 v2 blob fails eva_open with -1 (no device call)."""
+    """eva.h:580-586: a file that is not an EVA2 v2 or v3 blob, or a v3 blob whose scale table is cut short, fails
+    eva_open with -1 (no device call)."""
     from xtagger_amd.engine import Engine
     p = tmp_path / "bad.bin"
     p.write_bytes(b"NOPE" + b"\0" * 300)
@@ -138,3 +139,60 @@ def test_c_program_against_header(tmp_path):
     r = subprocess.run([exe, str(tmp_path)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and "abi ok" in r.stdout, r.stdout + r.stderr
     assert "eva: " in r.stderr                                  # the reference's error convention
+
+
+def _eva_walk(ver, ntp):
+    """Byte offsets of the wd blob's tensors as the reference's reader takes them (eva.h:380-428 eva_layout: EVA_TAKE
+    rounds every offset up to 256; v3 leads with the [24][12] fp32 table and stores E4M3 weights with rs | W~2 | c | d
+    in place of the MLP LN's gamma | beta | W2), restated from that walk, independently of the writer."""
+    D, T, NP, K0P, HIDP, NL = 1024, 1025, 1024, 592, 2736, 24
+    wb = 1 if ver == 3 else 2
+    sizes = ([("table", NL * 12 * 4)] if ver == 3 else []) + [("pe", D * K0P * 2), ("pos", T * D * 4),
+                                                           ("rope", NP * 32 * 2 * 4)]
+    for i in range(NL):
+        sizes += [(f"ln1w{i}", D * 4), (f"ln1b{i}", D * 4), (f"wqkv{i}", 3 * D * D * wb), (f"wo{i}", D * D * wb),
+                  (f"ln2w{i}", D * 4), (f"ln2b{i}", D * 4), (f"w12{i}", 2 * HIDP * D * wb)]
+        if ver == 3:
+            sizes += [(f"rs{i}", HIDP * 4), (f"w2{i}", D * HIDP), (f"cn{i}", D * 4), (f"dn{i}", D * 4)]
+        else:
+            sizes += [(f"mlnw{i}", HIDP * 4), (f"mlnb{i}", HIDP * 4), (f"w2{i}", D * HIDP * 2)]
+    sizes += [("fnw", D * 4), ("fnb", D * 4), ("hw", ntp * D * 2), ("hb", ntp * 4)]
+    off, out = 0, {}
+    for name, n in sizes:
+        off = (off + 255) & ~255
+        out[name] = off
+        off += n
+    return out, off
+
+
+def test_wd_blob_layouts_match_the_reference_walk(tmp_path):
+    """blob.write_v2 and blob.write_v3 put every tensor where eva.h's eva_layout takes it, and the header's byte count
+    is the walk's end (the engine checks the same count, eva.h:424-427)."""
+    import struct
+    from xtagger_amd import blob
+    m = blob.synth_model(seed=3, nt=13)
+    p2 = str(tmp_path / "v2.bin")
+    nbytes = blob.write_v2(p2, m)
+    want, end = _eva_walk(2, 16)
+    assert nbytes == end
+    with open(p2, "rb") as f:
+        assert struct.unpack("<4sIII", f.read(16)) == (b"EVA2", 2, 13, end)
+    b3 = blob.write_v3(str(tmp_path / "v3.bin"), m, blob.synth_calib(m, seed=1))
+    want3, end3 = _eva_walk(3, 16)
+    assert len(b3.buf) == end3 and b3.off == want3
+    with open(str(tmp_path / "v3.bin"), "rb") as f:
+        assert struct.unpack("<4sIII", f.read(16)) == (b"EVA2", 3, 13, end3)
+    # every v2 tensor's bytes sit at the walk's offset
+    raw = np.fromfile(p2, np.uint8)[256:]
+    f16, f32 = np.float16, np.float32
+    exp = {"pe": (m["pe"], f16), "pos": (m["pos"], f32), "rope": (m["rope"], f32), "fnw": (m["fnw"], f32),
+           "fnb": (m["fnb"], f32), "hw": (m["hw"], f16), "hb": (m["hb"], f32)}
+    for i, L in enumerate(m["layers"]):
+        for k, dt in (("ln1w", f32), ("ln1b", f32), ("wqkv", f16), ("wo", f16), ("ln2w", f32), ("ln2b", f32),
+                      ("w12", f16), ("mlnw", f32), ("mlnb", f32), ("w2", f16)):
+            exp[f"{k}{i}"] = (L[k], dt)
+    assert set(exp) == set(want)
+    for name, (a, dt) in exp.items():
+        bts = np.ascontiguousarray(a, dt).view(np.uint8).reshape(-1)
+        assert np.array_equal(raw[want[name]:want[name] + bts.size], bts), name
+

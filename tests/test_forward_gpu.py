@@ -293,6 +293,96 @@ def test_forward_free_running_chaotic(dev, orc, synth_blob):
         assert top >= env["top50_overlap_per_image"][i] - 6
 
 
+def _pin_block_maxima(w):
+    """w with one element of every 128 x 128 block (rows padded as the kernels pad them) set to the tensor's |max|, so
+    that per-tensor and per-block amax / 448 scales coincide and give the same E4M3 codes."""
+    w = w.astype(np.float32).copy()
+    mx = np.abs(w).max()
+    n, k = w.shape
+    for r0 in range(0, n, 128):
+        for c0 in range(0, k, 128):
+            blk = w[r0:r0 + 128, c0:c0 + 128]
+            if np.abs(blk).max() == 0:
+                continue
+            i = np.unravel_index(np.argmax(np.abs(blk)), blk.shape)
+            blk[i] = np.sign(blk[i]) * mx
+    return w
+
+
+def _v3_engine_vs_v2(tmp_path, orc, m, calib, inp, sparse=False):
+    from xtagger_amd import blob
+    from xtagger_amd.engine import Engine
+    p2, p3 = str(tmp_path / "eq_v2.bin"), str(tmp_path / "eq_v3.bin")
+    blob.write_v2(p2, m)
+    blob.write_v3(p3, m, calib)
+    out = []
+    for p in (p2, p3):
+        e = Engine(p, device=0, nb=len(inp), extra=1, sparse=sparse)
+        e.ready()
+        e.submit(0, inp)
+        out.append((e.wait(0, len(inp))[:, :m["nt"]], e.hpn(0, len(inp))))
+        e.close()
+    return out
+
+
+@pytest.mark.parametrize("sparse", [False, True])
+def test_v3_blob_matches_v2_where_its_quantization_does(dev, orc, tmp_path, sparse):
+    """The reference's production blob (export_eva.py v3: E4M3 weights with one scale per tensor, SmoothQuant folds,
+    the [24][12] scale table, rs | W~2 | c | d) read by the engine. Written here from the conditioned synthetic model
+    with every 128 x 128 block's maximum pinned to its tensor's (so per-tensor and block scales give the same codes),
+    calibration maxima equal to the weight-column maxima (so every smoothing factor is 1) and the MLP LayerNorm's
+    gamma 1 and beta 0: the v3 engine then computes what the v2 engine computes up to the rounding of c (summed by numpy
+    in the blob) and of the fc1 multiplier rs = 1 / adq. Per image: sigmoid within 2e-3 of the v2 engine, identical
+    top-50, fp16 head inputs within the free-running bound of the conditioned model. sparse: both engines 2:4-prune
+    the same codes (EVA_SPARSE24); the v3 engine recomputes c from the pruned W~ with rs."""
+    from tests.golden.make_forward_divergence import CONDITIONED
+    from xtagger_amd import blob
+    m = blob.synth_model(**CONDITIONED)
+    calib = {"act": [], "h": [], "qkv": blob.synth_calib(m, seed=2)["qkv"]}
+    for L in m["layers"]:
+        L["wqkv"] = _pin_block_maxima(L["wqkv"]).astype(np.float16)
+        L["wo"] = _pin_block_maxima(L["wo"]).astype(np.float16)
+        L["w12"] = _pin_block_maxima(L["w12"]).astype(np.float16)
+        L["w2"] = _pin_block_maxima(L["w2"]).astype(np.float16)
+        L["mlnw"] = np.where(np.arange(2736) < 2730, 1.0, 0.0).astype(np.float32)
+        L["mlnb"] = np.zeros(2736, np.float32)
+        cm = lambda w: np.abs(w.astype(np.float32)).max(0)
+        calib["act"].append(np.stack([cm(L["wqkv"]), cm(L["wo"]), cm(L["w12"])]))
+        calib["h"].append(cm(L["w2"]))
+    calib = {k: np.asarray(v, np.float32) for k, v in calib.items()}
+    inp = blob.synth_smooth_inputs(2, seed=1)
+    (s2, pn2), (s3, pn3) = _v3_engine_vs_v2(tmp_path, orc, m, calib, inp, sparse)
+    env = json.load(open(os.path.join(HERE, "golden", "forward_self_divergence.json")))["conditioned"]
+    bound = 2 * max(env["head_input_rel_l2_per_image"])
+    rel = _rel_l2(pn3, pn2)
+    for i in range(len(inp)):
+        d = np.abs(s3[i] - s2[i])
+        same = set(np.argsort(-s3[i], kind="stable")[:50]) == set(np.argsort(-s2[i], kind="stable")[:50])
+        _say(f"  image {i}: v3 vs v2 sigmoid max {d.max():.2e}, top-50 identical {same}, head inputs rel {rel[i]:.2e} "
+             f"(bound {bound:.2e})")
+        assert d.max() <= 2e-3 and same and rel[i] <= bound
+
+
+def test_v3_blob_with_smoothing(dev, orc, tmp_path):
+    """A v3 blob with real SmoothQuant factors (synthetic calibration maxima spread 16x with 20x outlier channels) and
+    per-tensor E4M3 weights: the engine runs the smoothed network, which is the v2 network up to the different weight
+    quantization (one scale per tensor instead of per block, on smoothed columns). Per image the head inputs stay
+    within 2% of the v2 engine's (a v3 scale or multiplier applied wrongly, such as rs without adq carried back into
+    fc2, moves them by far more), and the sigmoid scores within 2e-2."""
+    from tests.golden.make_forward_divergence import CONDITIONED
+    from xtagger_amd import blob
+    m = blob.synth_model(**CONDITIONED)
+    inp = blob.synth_smooth_inputs(2, seed=1)
+    (s2, pn2), (s3, pn3) = _v3_engine_vs_v2(tmp_path, orc, m, blob.synth_calib(m, seed=5), inp)
+    rel = _rel_l2(pn3, pn2)
+    for i in range(len(inp)):
+        d = np.abs(s3[i] - s2[i])
+        top = len(set(np.argsort(-s3[i])[:50]) & set(np.argsort(-s2[i])[:50]))
+        _say(f"  image {i}: v3 (smoothed) vs v2 sigmoid max {d.max():.2e} mean {d.mean():.2e}, top-50 overlap {top}, "
+             f"head inputs rel {rel[i]:.2e}")
+        assert np.isfinite(s3[i]).all() and rel[i] <= 2e-2 and d.max() <= 2e-2
+
+
 def test_partial_batch_and_head_rows(dev, synth_blob):
     from xtagger_amd import blob
     from xtagger_amd.engine import Engine

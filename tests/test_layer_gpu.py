@@ -152,6 +152,43 @@ def test_prep_qkv_pair_split_bitexact(dev, xt, orc):
     assert (d_q.cpu().numpy() == q[perm]).all()
 
 
+def test_prep_w8_v3_bitexact(dev, xt, orc):
+    """eva_k_prep_w8: the v3 blob's E4M3 bytes with one scale per tensor (export_eva.py:64-66) into the kernels'
+    layout: qkv rows pair-split as eva_k_prep_w's perm 1, W12 and W~2 zero-padded to 2816 units; every block scale is
+    the tensor's. eva_k_fold_c_rs: c = sum_k dec(q) s rs against float64."""
+    _say("eva_k_prep_w8 + eva_k_fold_c_rs")
+    r = np.random.default_rng(13)
+    perm = np.arange(3 * D)
+    for h in range(32):
+        for pc in range(64):
+            j, i = pc >> 4, pc & 15
+            perm[h * 64 + pc] = h * 64 + 2 * (16 * (j >> 1) + i) + (j & 1)
+    q = r.integers(0, 256, (3 * D, D)).astype(np.uint8)
+    q[(q & 0x7F) == 0x7F] = 0                                 # no NaN codes in a blob
+    d_q = torch.zeros((3 * D, D), dtype=torch.uint8, device=dev)
+    d_s = torch.zeros((24, 8), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_prep_w8(xt.ptr(_d(q, dev)), D, 3 * D, D, 3 * D, D, 1, 0.0123, xt.ptr(d_q), xt.ptr(d_s), _st()),
+        "prep_w8 qkv")
+    assert (d_q.cpu().numpy() == q[perm]).all() and (d_s.cpu().numpy() == np.float32(0.0123)).all()
+    w2 = r.integers(0, 0x7F, (D, 2736)).astype(np.uint8) | (r.integers(0, 2, (D, 2736)).astype(np.uint8) << 7)
+    w2[:, 2730:] = 0
+    d_q2 = torch.full((D, HIDP), 0xAB, dtype=torch.uint8, device=dev)
+    d_s2 = torch.zeros((8, 22), dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_prep_w8(xt.ptr(_d(w2, dev)), 2736, D, 2730, D, HIDP, 0, 3e-4, xt.ptr(d_q2), xt.ptr(d_s2), _st()),
+        "prep_w8 w2")
+    ref = np.zeros((D, HIDP), np.uint8)
+    ref[:, :2730] = w2[:, :2730]
+    assert (d_q2.cpu().numpy() == ref).all() and (d_s2.cpu().numpy() == np.float32(3e-4)).all()
+    rs = np.zeros(HIDP, np.float32)
+    rs[:2730] = np.exp(r.uniform(-3, 3, 2730))
+    d_c = torch.zeros(D, dtype=torch.float32, device=dev)
+    _ok(xt.lib.eva_k_fold_c_rs(xt.ptr(d_q2), xt.ptr(d_s2), xt.ptr(_d(rs, dev)), xt.ptr(d_c), _st()), "fold_c_rs")
+    dec = orc.e4m3_decode(ref).astype(np.float64) * np.float64(np.float32(3e-4))
+    c64 = dec @ rs.astype(np.float64)
+    terms = np.abs(dec) @ rs.astype(np.float64)
+    assert (np.abs(d_c.cpu().numpy() - c64) <= 1e-5 * terms).all()
+
+
 def test_prep_fc_fold_bitexact(dev, xt, orc):
     _say("eva_k_prep_w w12 / w2 fold + eva_k_fold_cd")
     r = np.random.default_rng(12)
@@ -373,9 +410,12 @@ def test_oproj_residual(dev, xt, orc):
     _check_close("x", _f16_f32(d_x.cpu().numpy().view(np.uint16)), _f16_f32(ref), np.abs(acc).max(), 2.0 ** -10)
 
 
-def test_fc1_swiglu_pack(dev, xt, orc):
+@pytest.mark.parametrize("with_rs", [False, True])
+def test_fc1_swiglu_pack(dev, xt, orc, with_rs):
+    """k_fc1 against the oracle's epilogue on the fp64 product; with_rs: eva_k_fc1_rs, the v3 blob's per-unit
+    multiplier rs (eva_kernels.cu:258-264): the packed operand is h rs, the row sums stay over h."""
     M = 2 * T
-    _say("k_fc1")
+    _say(f"k_fc1 (rs: {with_rs})")
     _, qa, sa = _packed_act(orc, M, D, 61)
     r = np.random.default_rng(62)
     w = (r.standard_normal((2 * HIDP, D)) * 0.02).astype(np.float32)
@@ -390,18 +430,27 @@ def test_fc1_swiglu_pack(dev, xt, orc):
     d_m8 = torch.zeros((M, HIDP), dtype=torch.uint8, device=dev)
     d_ms = torch.zeros((22, lds), dtype=torch.float32, device=dev)
     d_st = torch.zeros((22, lds, 2), dtype=torch.float32, device=dev)
-    _ok(xt.lib.eva_k_fc1(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa_l, dev)), lds, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)),
-                         xt.ptr(d_m8), xt.ptr(d_ms), xt.ptr(d_st), M, _st()), "eva_k_fc1")
+    rs = np.exp(r.uniform(-2, 2, HIDP)).astype(np.float32)   # multipliers over e^-2 .. e^2, as 1 / (adq s~) spread
+    if with_rs:
+        _ok(xt.lib.eva_k_fc1_rs(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa_l, dev)), lds, xt.ptr(_d(qw, dev)),
+                                xt.ptr(_d(sw, dev)), xt.ptr(d_m8), xt.ptr(d_ms), xt.ptr(d_st), xt.ptr(_d(rs, dev)), M,
+                                _st()), "eva_k_fc1_rs")
+    else:
+        _ok(xt.lib.eva_k_fc1(xt.ptr(_d(qa, dev)), xt.ptr(_d(sa_l, dev)), lds, xt.ptr(_d(qw, dev)), xt.ptr(_d(sw, dev)),
+                             xt.ptr(d_m8), xt.ptr(d_ms), xt.ptr(d_st), M, _st()), "eva_k_fc1")
     h, stat = orc.fc1_epi(_acc_ref(orc, qa, sa, qw, sw, 2 * HIDP))
-    q, s = orc.quant_act(h)
+    hq = (h * rs[None, :]).astype(np.float32) if with_rs else h   # one fp32 rounding, as the kernel's multiply
+    q, s = orc.quant_act(hq)
     ms = d_ms.cpu().numpy()[:, :M]
-    assert np.abs(ms / s - 1).max() < 1e-4
+    # each block scale is one GEMM-fed maximum over 128 units; with multipliers spread over e^+-2 that maximum is a
+    # single unit's h rs, which carries the matrix core's summation error relative to its own terms (~1e-4)
+    assert np.abs(ms / s - 1).max() < (5e-4 if with_rs else 1e-4)
     m8 = d_m8.cpu().numpy()
     same = m8 == q
     _say(f"  E4M3 codes differing: {np.mean(~same):.2e}")
     assert np.mean(~same) < 2e-3
     dq = orc.e4m3_decode(m8) * np.repeat(ms.T, 128, 1)
-    assert np.abs(dq - h).max() <= 2.0 ** -3 * np.abs(h).max() + 1e-6
+    assert np.abs(dq - hq).max() <= 2.0 ** -3 * np.abs(hq).max() + 1e-6
     st = d_st.cpu().numpy()[:, :M]
     assert np.abs(st[..., 0] - stat[..., 0]).max() <= 1e-4 * np.abs(stat[..., 1]).max() ** 0.5 + 1e-5
     assert np.abs(st[..., 1] / np.maximum(stat[..., 1], 1e-12) - 1).max() < 1e-4

@@ -23,9 +23,14 @@
 #define EV_HPUT_SLOTS 256     // eva_head_put rows staged at once before a call waits for the oldest copy
 #define EV_HPUT_SLOT 2304     // bytes per slot: 1024 fp16 weights, then the fp32 bias (256-byte multiple)
 
+#define V3_NS 12              // v3 scale table columns per layer: wdq x4, adq x4, q, k, v, pad (eva.h:379)
+
 struct Layer {
     const float *ln1w, *ln1b, *ln2w, *ln2b, *mlnw, *mlnb;  // in the blob
-    const uint16_t *wqkv16, *wo16, *w1216, *w216;          // fp16 block weights in the blob
+    const uint16_t *wqkv16, *wo16, *w1216, *w216;          // v2: fp16 block weights in the blob
+    const uint8_t *wqkv8, *wo8, *w128, *w28;               // v3: E4M3 block weights in the blob, one scale each
+    const float *rs0, *cn0, *dn0;                          // v3: h multipliers [2736], fold terms c, d [1024]
+    float *rs;                                             // v3: rs padded to 2816 units (zeros past 2736)
     uint8_t *wqkv, *wo, *w12, *w2;                         // packed E4M3 (2:4-pruned with EVA_SPARSE24)
     float *sqkv, *so, *s12, *s2, *cn, *dn;
     uint8_t *vqkv, *vo, *v12, *v2;                         // EVA_SPARSE24: pack24 values of the pruned weights
@@ -36,6 +41,8 @@ struct Layer {
 struct eva_impl {
     int devno, bstatus, up, booted;
     uint32_t flags;                                        // EVA_SPARSE24
+    uint32_t ver;                                          // blob version: 2 (fp16 weights) or 3 (E4M3 + scales)
+    float tab[EVA_NL * V3_NS];                             // v3 scale table (host copy, eva.h:379-428)
     pthread_t boot;
     char *path;                                            // own copy of the weights path
     size_t wbytes;
@@ -101,7 +108,9 @@ static int ev_alloc(eva_impl *E, void **p, size_t bytes, bool zero)
         if ((call)) return -1;                                         \
     } while (0)
 
-// Blob layout of export_eva.py v2 (eva.h:380-430 with EVA_VER 2): every tensor on a 256-byte boundary.
+// Blob layout of export_eva.py (eva.h:380-430): every tensor on a 256-byte boundary. v3 leads with the [24][12]
+// scale table and stores the block weights as E4M3 bytes, with rs | W~2 | c | d in place of the MLP LN's gamma | beta
+// | W2.
 static int ev_layout(eva_impl *E, uint32_t ntp)
 {
     size_t off = 0;
@@ -111,6 +120,8 @@ static int ev_layout(eva_impl *E, uint32_t ntp)
         off += bytes;
         return p;
     };
+    const bool v3 = E->ver == 3;
+    if (v3) take((size_t)EVA_NL * V3_NS * 4);
     E->pe = (const uint16_t *)take((size_t)EVA_D * EVA_K0P * 2);
     E->pos = (const float *)take((size_t)EVA_T * EVA_D * 4);
     E->cs = (const float *)take((size_t)EVA_NP * 32 * 2 * 4);
@@ -118,14 +129,27 @@ static int ev_layout(eva_impl *E, uint32_t ntp)
         Layer &L = E->L[i];
         L.ln1w = (const float *)take(EVA_D * 4);
         L.ln1b = (const float *)take(EVA_D * 4);
-        L.wqkv16 = (const uint16_t *)take((size_t)3 * EVA_D * EVA_D * 2);
-        L.wo16 = (const uint16_t *)take((size_t)EVA_D * EVA_D * 2);
+        if (v3) {
+            L.wqkv8 = take((size_t)3 * EVA_D * EVA_D);
+            L.wo8 = take((size_t)EVA_D * EVA_D);
+        } else {
+            L.wqkv16 = (const uint16_t *)take((size_t)3 * EVA_D * EVA_D * 2);
+            L.wo16 = (const uint16_t *)take((size_t)EVA_D * EVA_D * 2);
+        }
         L.ln2w = (const float *)take(EVA_D * 4);
         L.ln2b = (const float *)take(EVA_D * 4);
-        L.w1216 = (const uint16_t *)take((size_t)2 * V2_HIDP * EVA_D * 2);
-        L.mlnw = (const float *)take(V2_HIDP * 4);
-        L.mlnb = (const float *)take(V2_HIDP * 4);
-        L.w216 = (const uint16_t *)take((size_t)EVA_D * V2_HIDP * 2);
+        if (v3) {
+            L.w128 = take((size_t)2 * V2_HIDP * EVA_D);
+            L.rs0 = (const float *)take(V2_HIDP * 4);
+            L.w28 = take((size_t)EVA_D * V2_HIDP);
+            L.cn0 = (const float *)take(EVA_D * 4);
+            L.dn0 = (const float *)take(EVA_D * 4);
+        } else {
+            L.w1216 = (const uint16_t *)take((size_t)2 * V2_HIDP * EVA_D * 2);
+            L.mlnw = (const float *)take(V2_HIDP * 4);
+            L.mlnb = (const float *)take(V2_HIDP * 4);
+            L.w216 = (const uint16_t *)take((size_t)EVA_D * V2_HIDP * 2);
+        }
         L.end = off;
     }
     E->fnw = (const float *)take(EVA_D * 4);
@@ -174,7 +198,9 @@ static int ev_forward(eva *e, hipStream_t fst)
         if (sp) EV_OP(eva_k_oproj_sp(E->h8, E->sh, lds, L.vo, L.xo, L.so, E->x, M, st), 4);
         else EV_OP(eva_k_oproj(E->h8, E->sh, lds, L.wo, L.so, E->x, M, st), 4);
         EV_OP(eva_k_ln(E->x, L.ln2w, L.ln2b, E->h8, E->sh, M, lds, st), 5);
-        if (sp) EV_OP(eva_k_fc1_sp(E->h8, E->sh, lds, L.v12, L.x12, L.s12, E->m8, E->sm, E->stat, M, st), 6);
+        if (sp && L.rs) EV_OP(eva_k_fc1_rs_sp(E->h8, E->sh, lds, L.v12, L.x12, L.s12, E->m8, E->sm, E->stat, L.rs, M, st), 6);
+        else if (sp) EV_OP(eva_k_fc1_sp(E->h8, E->sh, lds, L.v12, L.x12, L.s12, E->m8, E->sm, E->stat, M, st), 6);
+        else if (L.rs) EV_OP(eva_k_fc1_rs(E->h8, E->sh, lds, L.w12, L.s12, E->m8, E->sm, E->stat, L.rs, M, st), 6);
         else EV_OP(eva_k_fc1(E->h8, E->sh, lds, L.w12, L.s12, E->m8, E->sm, E->stat, M, st), 6);
         if (sp) EV_OP(eva_k_fc2_sp(E->m8, E->sm, lds, L.v2, L.x2, L.s2, E->stat, L.cn, L.dn, E->x, M, st), 7);
         else EV_OP(eva_k_fc2(E->m8, E->sm, lds, L.w2, L.s2, E->stat, L.cn, L.dn, E->x, M, st), 7);
@@ -198,10 +224,24 @@ static int ev_pack_layer(eva_impl *E, int i)
 {
     Layer &L = E->L[i];
     void *st = (void *)E->st;
-    EV_CK(eva_k_prep_w(L.wqkv16, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, NULL, E->scratch, L.wqkv, L.sqkv, st));
-    EV_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
-    EV_CK(eva_k_prep_w(L.w1216, EVA_D, 2 * V2_HIDP, EVA_D, 2 * EVA_HIDP, EVA_D, 0, NULL, E->scratch, L.w12, L.s12, st));
-    EV_CK(eva_k_prep_w(L.w216, V2_HIDP, EVA_D, EVA_HID, EVA_D, EVA_HIDP, 0, L.mlnw, E->scratch, L.w2, L.s2, st));
+    if (E->ver == 3) {
+        // v3: the blob's E4M3 bytes with one scale per tensor (table[i][0..3]); the activations keep their own 1x128
+        // scales, so fc1 packs h rs (rs = 1 / (adq s~)) and fc2's scale carries adq back: wdq3 adq3 (eva.h:418)
+        const float *t = E->tab + (size_t)i * V3_NS;
+        EV_CK(eva_k_prep_w8(L.wqkv8, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, t[0], L.wqkv, L.sqkv, st));
+        EV_CK(eva_k_prep_w8(L.wo8, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, t[1], L.wo, L.so, st));
+        EV_CK(eva_k_prep_w8(L.w128, EVA_D, 2 * V2_HIDP, EVA_D, 2 * EVA_HIDP, EVA_D, 0, t[2], L.w12, L.s12, st));
+        EV_CK(eva_k_prep_w8(L.w28, V2_HIDP, EVA_D, EVA_HID, EVA_D, EVA_HIDP, 0, t[3] * t[7], L.w2, L.s2, st));
+        XT_HIP(hipMemsetAsync(L.rs, 0, EVA_HIDP * 4, E->st));
+        XT_HIP(hipMemcpyAsync(L.rs, L.rs0, V2_HIDP * 4, hipMemcpyDeviceToDevice, E->st));
+        XT_HIP(hipMemcpyAsync(L.cn, L.cn0, EVA_D * 4, hipMemcpyDeviceToDevice, E->st));
+        XT_HIP(hipMemcpyAsync(L.dn, L.dn0, EVA_D * 4, hipMemcpyDeviceToDevice, E->st));
+    } else {
+        EV_CK(eva_k_prep_w(L.wqkv16, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, NULL, E->scratch, L.wqkv, L.sqkv, st));
+        EV_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
+        EV_CK(eva_k_prep_w(L.w1216, EVA_D, 2 * V2_HIDP, EVA_D, 2 * EVA_HIDP, EVA_D, 0, NULL, E->scratch, L.w12, L.s12, st));
+        EV_CK(eva_k_prep_w(L.w216, V2_HIDP, EVA_D, EVA_HID, EVA_D, EVA_HIDP, 0, L.mlnw, E->scratch, L.w2, L.s2, st));
+    }
     if (E->flags & EVA_SPARSE24) {
         // 2:4 magnitude pruning of the packed E4M3 weights (prune24.py "mag"); the fold term c below then sums the
         // pruned W~, which keeps the folded LayerNorm exact for the weights the GEMM uses
@@ -213,7 +253,12 @@ static int ev_pack_layer(eva_impl *E, int i)
             EV_CK(eva_k_pack24(t.w, t.n, t.k, t.v, t.x, NULL, st));
         }
     }
-    EV_CK(eva_k_fold_cd(L.w2, L.s2, L.w216, V2_HIDP, L.mlnb, L.cn, L.dn, st));
+    if (E->ver == 3) {
+        // c of the pruned W~ (the blob's c sums the dense one); d is the blob's
+        if (E->flags & EVA_SPARSE24) EV_CK(eva_k_fold_c_rs(L.w2, L.s2, L.rs, L.cn, st));
+    } else {
+        EV_CK(eva_k_fold_cd(L.w2, L.s2, L.w216, V2_HIDP, L.mlnb, L.cn, L.dn, st));
+    }
     return 0;
 }
 
@@ -254,6 +299,7 @@ static int ev_up(eva *e)
         EV_ALLOC(E, L.s2, 8 * 22 * 4, false);
         EV_ALLOC(E, L.cn, EVA_D * 4, false);
         EV_ALLOC(E, L.dn, EVA_D * 4, false);
+        if (E->ver == 3) EV_ALLOC(E, L.rs, EVA_HIDP * 4, false);
         if (E->flags & EVA_SPARSE24) {
             EV_ALLOC(E, L.vqkv, (size_t)3 * EVA_D * EVA_D / 2, false);
             EV_ALLOC(E, L.xqkv, (size_t)3 * EVA_D * EVA_D / 8, false);
@@ -367,13 +413,31 @@ extern "C" int eva_open_ex(eva *e, const char *weights, int device, void *pool, 
     memset(e, 0, sizeof(*e));
     if (nb < 1 || nb > EVA_NBMAX) return xt_fail("eva_open", "batch must be 1..EVA_NBMAX");
     f = fopen(weights, "rb");
-    if (!f || fread(hdr, 4, 4, f) != 4 || memcmp(hdr, "EVA2", 4) || hdr[1] != 2) {
-        fprintf(stderr, "eva: %s is not an eva02.bin v2 (run export_eva.py without a calibration file)\n", weights);
+    if (!f || fread(hdr, 4, 4, f) != 4 || memcmp(hdr, "EVA2", 4) || (hdr[1] != 2 && hdr[1] != 3)) {
+        fprintf(stderr, "eva: %s is not an eva02.bin v2 or v3 (export_eva.py)\n", weights);
         if (f) fclose(f);
         return -1;
     }
+    float tab[EVA_NL * V3_NS];
+    if (hdr[1] == 3) {  // the scale table leads the blob (eva.h:386); its host copy gives the per-tensor scales
+        if (fseek(f, 256, SEEK_SET) || fread(tab, 4, EVA_NL * V3_NS, f) != EVA_NL * V3_NS) {
+            fprintf(stderr, "eva: %s: truncated v3 scale table\n", weights);
+            fclose(f);
+            return -1;
+        }
+        for (int j = 0; j < EVA_NL; j++)
+            for (int c = 0; c < 8; c++)
+                if (!(tab[j * V3_NS + c] > 0.f) || !(tab[j * V3_NS + c] < 3e38f)) {
+                    fprintf(stderr, "eva: %s: v3 scale table entry [%d][%d] is not a positive finite scale\n", weights,
+                            j, c);
+                    fclose(f);
+                    return -1;
+                }
+    }
     fclose(f);
     eva_impl *E = new eva_impl();
+    E->ver = hdr[1];
+    if (E->ver == 3) memcpy(E->tab, tab, sizeof(tab));
     e->impl = E;
     E->path = strdup(weights);
     if (!E->path) return xt_fail("eva_open", "out of memory");

@@ -133,12 +133,13 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
 // and the sums.
 // Each (row, block) partial has one writer: no atomics, deterministic.
 // ---------------------------------------------------------------------------------------------------------------
-template <bool SP>
+template <bool SP, bool RS>
 __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
                                                      int lds, const uint8_t *__restrict__ w,
                                                      const uint32_t *__restrict__ wx,
                                                      const float *__restrict__ ws, uint8_t *__restrict__ m8,
-                                                     float *__restrict__ ms, float *__restrict__ stat, int rows)
+                                                     float *__restrict__ ms, float *__restrict__ stat,
+                                                     const float *__restrict__ rs, int rows)
 {
     using C = LayerCfg;
     constexpr int NP = C::TN / 2;                        // SwiGLU tile pairs per wave (16 units each)
@@ -148,6 +149,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 2 * XT_HIDP, m0, n0);
     args_resident(m8, ms, stat, lds, rows);
+    if constexpr (RS) args_resident(rs);
     // W12 rows past the last 16-unit chunk holding a real unit (2 x 2736) are zero padding
     layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc, BsNoPre(),
                           2 * ((XT_HID + 15) / 16 * 16));
@@ -192,6 +194,11 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     uint32_t rb[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) rb[c] = (uint32_t)(r0 * 128 + ((((4 * k8 + c) ^ r0) & 7) | ((4 * k8 + c) & ~7)) * 4);
+    float4 ru[4];  // RS: the per-unit multipliers of this thread's 16 units (the same units in every item)
+    if constexpr (RS) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) ru[c] = *(const float4 *)(rs + ct * 128 + 16 * k8 + 4 * c);
+    }
 #pragma unroll
     for (int it = 0; it < C::BM * 8 / C::NT; it++) {
         const int idx = threadIdx.x + it * C::NT, rr = idx >> 3, u0 = (idx & 7) * 16, m = m0 + rr;
@@ -201,13 +208,19 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
         float amax = 0.f, s = 0.f, q = 0.f;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            amax = __builtin_fmaxf(__builtin_fmaxf(amax, __builtin_fabsf(v[c].x)), __builtin_fabsf(v[c].y));  // v_max3
-            amax = __builtin_fmaxf(__builtin_fmaxf(amax, __builtin_fabsf(v[c].z)), __builtin_fabsf(v[c].w));
             s += (v[c].x + v[c].y) + (v[c].z + v[c].w);
             q = __builtin_fmaf(v[c].x, v[c].x, q);
             q = __builtin_fmaf(v[c].y, v[c].y, q);
             q = __builtin_fmaf(v[c].z, v[c].z, q);
             q = __builtin_fmaf(v[c].w, v[c].w, q);
+            if constexpr (RS) {  // the sums are over h itself, the packed operand is h rs (eva_kernels.cu:258-264)
+                v[c].x *= ru[c].x;
+                v[c].y *= ru[c].y;
+                v[c].z *= ru[c].z;
+                v[c].w *= ru[c].w;
+            }
+            amax = __builtin_fmaxf(__builtin_fmaxf(amax, __builtin_fabsf(v[c].x)), __builtin_fabsf(v[c].y));  // v_max3
+            amax = __builtin_fmaxf(__builtin_fmaxf(amax, __builtin_fabsf(v[c].z)), __builtin_fabsf(v[c].w));
         }
         amax = row8_absmax(amax);
         s = row8_sum(s);
@@ -472,14 +485,18 @@ static int oproj_launch(const char *what, const void *a8, const float *as, int l
 
 template <bool SP>
 static int fc1_launch(const char *what, const void *h8, const float *hs, int lds, const void *w, const void *wx,
-                      const float *ws, void *m8, float *ms, float *stat, int rows, void *stream)
+                      const float *ws, void *m8, float *ms, float *stat, const float *rs, int rows, void *stream)
 {
     if (layer_rows_ok(what, rows, lds)) return -1;
-    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || !XT_ALIGNED(m8) || (SP && !wx))
-        return xt_fail(what, "h8, w, m8 must be 16-byte aligned");
-    hipLaunchKernelGGL(k_fc1<SP>, dim3(layer_grid(rows, 2 * XT_HIDP, LayerCfg::BM, LayerCfg::BN)), dim3(LayerCfg::NT), 0,
-                       (hipStream_t)stream, (const uint8_t *)h8, hs, lds, (const uint8_t *)w, (const uint32_t *)wx, ws,
-                       (uint8_t *)m8, ms, stat, rows);
+    if (!XT_ALIGNED(h8) || !XT_ALIGNED(w) || !XT_ALIGNED(m8) || !XT_ALIGNED(rs) || (SP && !wx))
+        return xt_fail(what, "h8, w, m8, rs must be 16-byte aligned");
+    const dim3 grid(layer_grid(rows, 2 * XT_HIDP, LayerCfg::BM, LayerCfg::BN));
+    if (rs)
+        hipLaunchKernelGGL((k_fc1<SP, true>), grid, dim3(LayerCfg::NT), 0, (hipStream_t)stream, (const uint8_t *)h8, hs,
+                           lds, (const uint8_t *)w, (const uint32_t *)wx, ws, (uint8_t *)m8, ms, stat, rs, rows);
+    else
+        hipLaunchKernelGGL((k_fc1<SP, false>), grid, dim3(LayerCfg::NT), 0, (hipStream_t)stream, (const uint8_t *)h8, hs,
+                           lds, (const uint8_t *)w, (const uint32_t *)wx, ws, (uint8_t *)m8, ms, stat, rs, rows);
     return xt_check(what);
 }
 
@@ -511,7 +528,14 @@ extern "C" int eva_k_oproj(const void *a8, const float *as, int lds, const void 
 extern "C" int eva_k_fc1(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8, float *ms,
                          float *stat, int rows, void *stream)
 {
-    return fc1_launch<false>("eva_k_fc1", h8, hs, lds, w, nullptr, ws, m8, ms, stat, rows, stream);
+    return fc1_launch<false>("eva_k_fc1", h8, hs, lds, w, nullptr, ws, m8, ms, stat, nullptr, rows, stream);
+}
+
+extern "C" int eva_k_fc1_rs(const void *h8, const float *hs, int lds, const void *w, const float *ws, void *m8,
+                            float *ms, float *stat, const float *rs, int rows, void *stream)
+{
+    if (!rs) return xt_fail("eva_k_fc1_rs", "rs must not be NULL");
+    return fc1_launch<false>("eva_k_fc1_rs", h8, hs, lds, w, nullptr, ws, m8, ms, stat, rs, rows, stream);
 }
 
 extern "C" int eva_k_fc2(const void *m8, const float *ms, int lds, const void *w, const float *ws, const float *stat,
@@ -535,7 +559,15 @@ extern "C" int eva_k_oproj_sp(const void *a8, const float *as, int lds, const vo
 extern "C" int eva_k_fc1_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx,
                             const float *ws, void *m8, float *ms, float *stat, int rows, void *stream)
 {
-    return fc1_launch<true>("eva_k_fc1_sp", h8, hs, lds, vals, idx, ws, m8, ms, stat, rows, stream);
+    return fc1_launch<true>("eva_k_fc1_sp", h8, hs, lds, vals, idx, ws, m8, ms, stat, nullptr, rows, stream);
+}
+
+extern "C" int eva_k_fc1_rs_sp(const void *h8, const float *hs, int lds, const void *vals, const void *idx,
+                               const float *ws, void *m8, float *ms, float *stat, const float *rs, int rows,
+                               void *stream)
+{
+    if (!rs) return xt_fail("eva_k_fc1_rs_sp", "rs must not be NULL");
+    return fc1_launch<true>("eva_k_fc1_rs_sp", h8, hs, lds, vals, idx, ws, m8, ms, stat, rs, rows, stream);
 }
 
 extern "C" int eva_k_fc2_sp(const void *m8, const float *ms, int lds, const void *vals, const void *idx,

@@ -84,3 +84,67 @@ extern "C" int eva_k_fold_cd(const void *q, const float *s, const void *w2, int 
                        (const uint16_t *)w2, ldw2, beta, c, d);
     return xt_check("eva_k_fold_cd");
 }
+
+// v3 blob weights: E4M3 bytes [n_in][ldw] -> q [n_out][k_out] (zero past n_in / k_in, perm 1 as k_prep_f32), one
+// 32-bit word of four bytes per thread
+__global__ void __launch_bounds__(256) k_prep_w8(const uint8_t *__restrict__ w, int ldw, int n_in, int k_in, int n_out,
+                                                 int k_out, int perm, uint8_t *__restrict__ q)
+{
+    const long total = (long)n_out * (k_out / 4);
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+        const int r = (int)(i / (k_out / 4)), c = 4 * (int)(i - (long)r * (k_out / 4));
+        int src = r;
+        if (perm == 1 && r < 2 * XT_D) {
+            const int hd = r & ~63, pc = r & 63, j = pc >> 4, ii = pc & 15;
+            src = hd + 2 * (16 * (j >> 1) + ii) + (j & 1);
+        }
+        uint32_t v = 0;
+        if (src < n_in)
+            for (int b = 0; b < 4; b++)
+                if (c + b < k_in) v |= (uint32_t)w[(size_t)src * ldw + c + b] << (8 * b);
+        *(uint32_t *)(q + (size_t)r * k_out + c) = v;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_fill(float *__restrict__ p, int n, float v)
+{
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = v;
+}
+
+// c[n] = sum_k dec(q[n][k]) s[n/128][k/128] rs[k], one thread per row, k in order (fma chains)
+__global__ void __launch_bounds__(256) k_fold_c_rs(const uint8_t *__restrict__ q, const float *__restrict__ s,
+                                                   const float *__restrict__ rs, float *__restrict__ c)
+{
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= XT_D) return;
+    float cc = 0.f;
+    for (int k = 0; k < XT_HIDP; k++)
+        cc = __builtin_fmaf(e4_dec(q[(size_t)n * XT_HIDP + k]) * s[(size_t)(n >> 7) * (XT_HIDP / 128) + (k >> 7)], rs[k], cc);
+    c[n] = cc;
+}
+
+extern "C" int eva_k_prep_w8(const void *w8, int ldw, int n_in, int k_in, int n_out, int k_out, int perm, float scale,
+                             void *q, float *s, void *stream)
+{
+    if (n_in < 0 || n_in > n_out || k_in > k_out || ldw < k_in || k_out % 128 || n_out % 128 || n_out <= 0 ||
+        (perm != 0 && perm != 1) || !(scale > 0.f))
+        return xt_fail("eva_k_prep_w8", "bad shape or scale (n_in <= n_out, k_in <= k_out <= ldw, n_out and k_out "
+                                        "multiples of 128, scale > 0)");
+    if ((uintptr_t)q & 3) return xt_fail("eva_k_prep_w8", "q must be 4-byte aligned");
+    const long total = (long)n_out * (k_out / 4);
+    long blocks = (total + 255) / 256;
+    if (blocks > 65535) blocks = 65535;
+    hipLaunchKernelGGL(k_prep_w8, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (const uint8_t *)w8, ldw,
+                       n_in, k_in, n_out, k_out, perm, (uint8_t *)q);
+    if (xt_check("eva_k_prep_w8")) return -1;
+    const int ns = (n_out / 128) * (k_out / 128);
+    hipLaunchKernelGGL(k_fill, dim3((ns + 255) / 256), dim3(256), 0, (hipStream_t)stream, s, ns, scale);
+    return xt_check("eva_k_prep_w8");
+}
+
+extern "C" int eva_k_fold_c_rs(const void *q, const float *s, const float *rs, float *c, void *stream)
+{
+    hipLaunchKernelGGL(k_fold_c_rs, dim3(XT_D / 256), dim3(256), 0, (hipStream_t)stream, (const uint8_t *)q, s, rs, c);
+    return xt_check("eva_k_fold_c_rs");
+}
+

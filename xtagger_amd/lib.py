@@ -46,6 +46,10 @@ _SIGS = {
     "eva_k_qkv_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _p]),
     "eva_k_oproj_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _i, _p]),
     "eva_k_fc1_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
+    "eva_k_fc1_rs": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
+    "eva_k_fc1_rs_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _p]),
+    "eva_k_prep_w8": (_i, [_p, _i, _i, _i, _i, _i, _i, _f, _p, _p, _p]),
+    "eva_k_fold_c_rs": (_i, [_p, _p, _p, _p, _p]),
     "eva_k_fc2_sp": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _p]),
     "eva_open": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32]),
     "eva_open_nb": (_i, [_p, C.c_char_p, _i, _p, C.c_size_t, _u32, _u32]),
