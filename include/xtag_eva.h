@@ -264,8 +264,11 @@ typedef struct {
     px_impl *impl;
 } px;
 /* px.h:357. Reads the "PXAI" header and starts the bring-up on its own thread. The blob is version 2
- * (export_pixai.py without a calibration file: fp16 block weights), packed to E4M3 with 128x128 scales on the GPU at
- * bring-up. pool / poolb are accepted and unused (inputs are staged into a pinned slot per buf, as eva_submit). */
+ * (export_pixai.py without a calibration file: fp16 block weights, packed to E4M3 with 128x128 scales on the GPU at
+ * bring-up) or version 3 (with a calibration file: SmoothQuant folds, E4M3 block weights with one scale per tensor
+ * from the [32][12] table that leads the blob, rs = 1 / (adq3 s3)); a v3 table entry 0..7 that is not a positive
+ * finite scale fails px_open. pool / poolb are accepted and unused (inputs are staged into a pinned slot per buf, as
+ * eva_submit). */
 int px_open(px *p, const char *weights, int device, void *pool, size_t poolb);
 /* px_open with the batch (even, 2..100: token rows stay within the kernels' 2^19) as a runtime parameter */
 int px_open_nb(px *p, const char *weights, int device, void *pool, size_t poolb, uint32_t nb);

@@ -66,13 +66,20 @@ def test_open_rejects_bad_header(tmp_path):
 
 
 def test_px_open_rejects_bad_files(tmp_path):
-    """px.h:357-372: a file that is not a pixai.bin v2, or an odd batch, fails px_open with -1 (no device call)."""
+    """px.h:357-372: a file that is not a pixai.bin v2 or v3 (another magic or version, no tags), a v3 file whose scale
+    table is cut short or holds a scale that is not positive and finite, or an odd batch, fails px_open with -1 (no
+    device call)."""
     import struct
     import pytest
     from xtagger_amd.engine import PxEngine
     p = tmp_path / "bad.bin"
-    for hdr in (b"NOPE" + b"\0" * 12, struct.pack("<4sIII", b"PXAI", 3, 100, 0), struct.pack("<4sIII", b"PXAI", 2, 0, 0)):
-        p.write_bytes(hdr + b"\0" * 300)
+    tab = np.full((32, 12), 0.01, np.float32)
+    tab[5, 3] = 0.0
+    bad_tab = struct.pack("<4sIII", b"PXAI", 3, 100, 0) + b"\0" * 240 + tab.tobytes()
+    for data in (b"NOPE" + b"\0" * 312, struct.pack("<4sIII", b"PXAI", 4, 100, 0) + b"\0" * 300,
+                 struct.pack("<4sIII", b"PXAI", 3, 100, 0) + b"\0" * 300,
+                 struct.pack("<4sIII", b"PXAI", 2, 0, 0) + b"\0" * 300, bad_tab):
+        p.write_bytes(data)
         with pytest.raises(RuntimeError):
             PxEngine(str(p))
     p.write_bytes(struct.pack("<4sIII", b"PXAI", 2, 10, 0) + b"\0" * 300)
@@ -82,26 +89,93 @@ def test_px_open_rejects_bad_files(tmp_path):
         PxEngine(str(tmp_path / "missing.bin"))
 
 
-def test_px_blob_layout_matches_engine_walk():
-    """The writer's byte count equals the walk of px.h:196-253 (every tensor on a 256-byte boundary) for nt = 13."""
+def _px_walk(ver, ntp):
+    """Byte offsets of the PixAI blob's tensors as the reference's reader takes them (px.h:196-253 px_layout: EVA_TAKE
+    rounds every offset up to 256; v3, PX_WB 1, leads with the [32][12] fp32 table and holds the four block weights as
+    E4M3 bytes), restated from that walk, independently of the writer."""
+    D, T, LW, HID, K0P, NL = 1024, 5184, 576, 4736, 592, 32
+    wb = 1 if ver == 3 else 2
+    sizes = ([("table", NL * 12 * 4)] if ver == 3 else []) + [
+        ("pe", D * K0P * 2), ("pos", T * D * 4), ("lnpw", D * 4), ("lnpb", D * 4), ("csw", LW * 32 * 2 * 4),
+        ("csg", T * 32 * 2 * 4)]
+    for i in range(NL):
+        sizes += [(f"ln1w{i}", D * 4), (f"ln1b{i}", D * 4), (f"wqkv{i}", 3 * D * D * wb), (f"bqkv{i}", 3 * D * 4),
+                  (f"wo{i}", D * D * wb), (f"bo{i}", D * 4), (f"ln2w{i}", D * 4), (f"ln2b{i}", D * 4),
+                  (f"w1{i}", HID * D * wb), (f"b1{i}", HID * 4), (f"rs{i}", HID * 4), (f"w2{i}", D * HID * wb),
+                  (f"b2{i}", D * 4)]
+    sizes += [("hnw", D * 4), ("hnb", D * 4), ("U", 16 * D * 4), ("hpos", T * D * 2), ("wv", D * D * 2),
+              ("hw", ntp * D * 2), ("hb", ntp * 4)]
+    off, out = 0, {}
+    for name, n in sizes:
+        off = (off + 255) & ~255
+        out[name] = off
+        off += n
+    return out, off
+
+
+def test_px_blob_layouts_match_the_reference_walk(tmp_path):
+    """blob.write_px_v2's and blob.write_px_v3's tensors sit where px.h's px_layout takes them and the header's byte
+    count is the walk's end (the engine checks the same count, px.h:247-250); the v3 file's scale table is at the
+    blob's start and a weight's E4M3 bytes at the walk's offset."""
+    import struct
     from xtagger_amd import blob
-    sizes = [1024 * 592 * 2, 5184 * 1024 * 4, 4096, 4096, 576 * 64 * 4, 5184 * 64 * 4]
-    sizes += [4096, 4096, 3072 * 1024 * 2, 3072 * 4, 1024 * 1024 * 2, 4096, 4096, 4096, 4736 * 1024 * 2, 4736 * 4,
-              4736 * 4, 1024 * 4736 * 2, 4096] * 32
-    sizes += [4096, 4096, 16 * 4096, 5184 * 1024 * 2, 1024 * 1024 * 2, 16 * 1024 * 2, 16 * 4]
-    off = 0
-    for s in sizes:
-        off = (off + 255) // 256 * 256 + s
-    total = 0
-    for name, a, dt in blob.px_tensors(_fake_px_model(13)):
-        total = (total + 255) // 256 * 256 + np.asarray(a).size * np.dtype(dt).itemsize
-    assert total == off
+    m = _fake_px_model(13, fill=0.01)
+    want2, end2 = _px_walk(2, 16)
+    assert blob._px_stream(os.devnull, 2, 13, blob.px_tensors(m)) == (want2, end2)
+    p3 = str(tmp_path / "v3.bin")
+    calib = blob.synth_px_calib(m, seed=1)
+    off3, n3, table = blob.write_px_v3(p3, m, calib)
+    want3, end3 = _px_walk(3, 16)
+    assert (off3, n3) == (want3, end3)
+    with open(p3, "rb") as f:
+        assert struct.unpack("<4sIII", f.read(16)) == (b"PXAI", 3, 13, end3)
+        f.seek(256)
+        assert np.array_equal(np.frombuffer(f.read(table.nbytes), np.float32).reshape(32, 12), table)
+        f.seek(256 + want3["w27"])
+        ts, _ = blob.px_v3_layer(m["layers"][7], calib["act"][7], calib["h"][7], calib["qkv"][7])
+        assert np.array_equal(np.frombuffer(f.read(1024 * 4736), np.uint8), dict((k, a) for k, a, _ in ts)["w2"].ravel())
 
 
-def _fake_px_model(nt):
-    """Zero tensors of the v2 shapes (cheap: broadcast views)."""
+def test_px_v3_layer_keeps_every_gemm():
+    """blob.px_v3_layer restates one block of the calibrated export (export_pixai.py:80-99). SmoothQuant moves a
+    factor from each GEMM's input to its weight columns, so every GEMM of the block must compute what the v2 block
+    computes, up to the E4M3 rounding of its weights (one scale per tensor): for normalised rows xh, attention-like rows
+    z and GELU-like outputs g, LN1'(xh) W~qkv^T wdq0 equals LN1(xh) Wqkv^T on the q and k rows; the v rows, which
+    carry 1 / s1, through W~o wdq1 give the v2 block's v Wo^T; LN2'(xh) W~1^T wdq2 equals LN2(xh) W1^T; and
+    (g rs) (W~2 wdq3 adq3)^T equals g W2^T. Calibration maxima spread 16x with 20x outliers make the factors far from
+    1: a fold left out (the V rows' 1 / s1, rs without 1 / s3) moves a GEMM by 60% or more, the rounding by under 5%.
+    Every weight's largest code is 448 (scale = amax / 448)."""
+    from xtagger_amd import blob
+    r = np.random.default_rng(4)
+    L = blob.synth_px_layer(r)
+    c = blob.synth_px_calib({"layers": [L]}, seed=2, spread=16.0)
+    ts, t = blob.px_v3_layer(L, c["act"][0], c["h"][0], c["qkv"][0])
+    V = {k: a for k, a, _ in ts}
+    f = lambda a: np.asarray(a, np.float64)
+    dec = lambda k: blob._e4m3_values(V[k]).astype(np.float64)
+    rel = lambda a, b: np.linalg.norm(a - b) / np.linalg.norm(b)
+    for k in ("wqkv", "wo", "w1", "w2"):
+        assert V[k].dtype == np.uint8 and np.abs(dec(k)).max() == 448.0
+    xh, z, g = r.standard_normal((64, 1024)), r.standard_normal((64, 1024)), np.abs(r.standard_normal((64, 4736)))
+    y2 = (xh * f(L["ln1w"]) + f(L["ln1b"])) @ f(L["wqkv"]).T
+    y3 = (xh * f(V["ln1w"]) + f(V["ln1b"])) @ (dec("wqkv") * t[0]).T
+    assert rel(y3[:, :2048], y2[:, :2048]) < 0.05
+    o2 = y2[:, 2048:] @ f(L["wo"]).T
+    assert rel(y3[:, 2048:] @ (dec("wo") * t[1]).T, o2) < 0.05
+    assert rel(y3[:, 2048:] @ f(L["wo"]).T, o2) > 0.5                  # V rows left unfolded
+    u2 = (xh * f(L["ln2w"]) + f(L["ln2b"])) @ f(L["w1"]).T
+    assert rel((xh * f(V["ln2w"]) + f(V["ln2b"])) @ (dec("w1") * t[2]).T, u2) < 0.05
+    p2 = g @ f(L["w2"]).T
+    w2 = dec("w2") * (np.float64(t[3]) * t[7])
+    assert rel((g * f(V["rs"])) @ w2.T, p2) < 0.05
+    assert rel((g / t[7]) @ w2.T, p2) > 0.5                              # rs without 1 / s3
+    assert rel(z @ (dec("wo") * t[1]).T, z @ f(L["wo"]).T) > 0.5         # the out-proj columns carry s1
+
+
+def _fake_px_model(nt, fill=0.0):
+    """Constant tensors of the v2 shapes (cheap: broadcast views)."""
     f16, f32 = np.float16, np.float32
-    z = lambda shape, dt: np.broadcast_to(np.zeros(1, dt), shape)
+    z = lambda shape, dt: np.broadcast_to(np.full(1, fill, dt), shape)
     L = {"ln1w": z(1024, f32), "ln1b": z(1024, f32), "wqkv": z((3072, 1024), f16), "bqkv": z(3072, f32),
          "wo": z((1024, 1024), f16), "bo": z(1024, f32), "ln2w": z(1024, f32), "ln2b": z(1024, f32),
          "w1": z((4736, 1024), f16), "b1": z(4736, f32), "rs": z(4736, f32), "w2": z((1024, 4736), f16),

@@ -1,7 +1,8 @@
-"""The PixAI engine (px_open .. px_close, src/engine/px.h) on a synthetic pixai.bin v2: its captured forward gives the
+"""The PixAI engine (px_open .. px_close, src/engine/px.h) on synthetic pixai.bin files: its captured forward gives the
 same scores, bit for bit, as the px_k_* / eva_k_* kernel sequence of px.h:110-190 run by hand on the same tensors
 (each kernel's parity against the oracle is tested on its own), through both the resident-input path and
-px_submit / px_wait, for a full batch and a partial one."""
+px_submit / px_wait, for a full batch and a partial one; on the calibrated v3 blob (export_pixai.py with a
+calibration file) likewise, and equal to the v2 engine where the two files' quantizations coincide."""
 import ctypes as C
 
 import numpy as np
@@ -20,8 +21,11 @@ def _say(*a):
     print(*a, flush=True)
 
 
-def _chain(xt, m, d_in, nb, dev):
-    """px_forward (px.h:110-190) by hand: weights packed as the engine packs them, every kernel in the same order."""
+def _chain(xt, m, d_in, nb, dev, layers=None):
+    """px_forward (px.h:110-190) by hand: weights packed as the engine packs them, every kernel in the same order.
+    layers: the blocks' tensors (default m's v2 blocks); a v3 block (blob.px_v3_layer's tensors with its table row
+    under "t") holds E4M3 weights, packed with one scale per tensor: wdq for qkv, out-proj and fc1, wdq3 adq3 for fc2,
+    whose input fc1 packs as gelu rs."""
     M, P = nb * T5, xt.ptr
     st = torch.cuda.current_stream().cuda_stream
     keep = []
@@ -36,10 +40,14 @@ def _chain(xt, m, d_in, nb, dev):
         keep.append(t)
         return t
 
-    def pack(w16, n_in, k, n_out, perm=0):
+    def pack(w, n_in, k, n_out, perm=0, scale=None):
         q, s = z(n_out, k), z(n_out // 128, k // 128, dt=torch.float32)
-        scratch = torch.empty(n_out * k, dtype=torch.float32, device=dev)
-        assert xt.lib.eva_k_prep_w(P(up(w16)), k, n_in, k, n_out, k, perm, None, P(scratch), P(q), P(s), st) == 0
+        if scale is not None:
+            assert w.dtype == np.uint8
+            assert xt.lib.eva_k_prep_w8(P(up(w)), k, n_in, k, n_out, k, perm, float(scale), P(q), P(s), st) == 0
+        else:
+            scratch = torch.empty(n_out * k, dtype=torch.float32, device=dev)
+            assert xt.lib.eva_k_prep_w(P(up(w)), k, n_in, k, n_out, k, perm, None, P(scratch), P(q), P(s), st) == 0
         torch.cuda.synchronize()
         return q, s
 
@@ -50,12 +58,13 @@ def _chain(xt, m, d_in, nb, dev):
     ok(xt.lib.px_k_pe(P(d_in), P(up(m["pe"])), P(x), M, st))
     ok(xt.lib.px_k_pembed(P(x), P(up(m["pos"])), T5, P(up(m["lnpw"])), P(up(m["lnpb"])), M, st))
     cs = {576: up(m["csw"]), 5184: up(m["csg"])}
-    for i, L in enumerate(m["layers"]):
+    for i, L in enumerate(layers if layers is not None else m["layers"]):
         Ls = 5184 if (i & 7) == 7 else 576
-        wqkv, sqkv = pack(L["wqkv"], 3 * D, D, 3 * D, 1)
-        wo, so = pack(L["wo"], D, D, D)
-        w1, s1 = pack(L["w1"], PH, D, PH)
-        w2, s2 = pack(L["w2"], D, PH, D)
+        t = L.get("t", [None] * 8)
+        wqkv, sqkv = pack(L["wqkv"], 3 * D, D, 3 * D, 1, t[0])
+        wo, so = pack(L["wo"], D, D, D, 0, t[1])
+        w1, s1 = pack(L["w1"], PH, D, PH, 0, t[2])
+        w2, s2 = pack(L["w2"], D, PH, D, 0, None if t[3] is None else np.float32(t[3] * t[7]))
         ok(xt.lib.eva_k_ln(P(x), P(up(L["ln1w"])), P(up(L["ln1b"])), P(h8), P(hs), M, M, st))
         ok(xt.lib.px_k_qkv(P(h8), P(hs), M, P(wqkv), P(sqkv), P(up(L["bqkv"])), P(cs[Ls]), Ls, P(q), P(k), P(vt), M,
                            st))
@@ -166,3 +175,89 @@ def test_px_batch_halves(dev, tmp_path):
         assert np.array_equal(out_t.cpu().numpy(), ref)
     finally:
         e.close()
+
+
+def _inputs(nb, seed):
+    r = np.random.default_rng(seed)
+    inp = np.zeros((nb, T5, 592), np.float16)
+    inp[..., :588] = r.uniform(-1, 1, (nb, T5, 588)).astype(np.float16)
+    return inp
+
+
+def test_px_v3_engine_matches_kernel_chain(dev, xt, tmp_path):
+    """The calibrated blob (export_pixai.py v3: SmoothQuant factors folded into LN1, the V rows, LN2 and the fc2
+    columns, per-tensor E4M3 block weights, the [32][12] scale table leading the blob, rs = 1 / (adq3 s3)) read by
+    px_open: the same scores, bit for bit, as the kernel chain on the blob's own tensors (blob.px_v3_layer), each
+    weight packed by eva_k_prep_w8 with its table scale (fc2: wdq3 adq3) and fc1 run with the blob's rs."""
+    nb = 2
+    _say("px engine: synthetic pixai.bin v3 (synthetic calibration maxima)")
+    m = blob.synth_px_model(seed=5, nt=NT)
+    calib = blob.synth_px_calib(m, seed=3)
+    path = tmp_path / "pixai_v3.bin"
+    _, _, table = blob.write_px_v3(str(path), m, calib)
+    layers = []
+    for i, L in enumerate(m["layers"]):
+        ts, row = blob.px_v3_layer(L, calib["act"][i], calib["h"][i], calib["qkv"][i])
+        assert np.array_equal(row, table[i])
+        d = {k: a for k, a, _ in ts}
+        d["t"] = row
+        layers.append(d)
+    assert not any((d["rs"] == 1).all() for d in layers)
+    inp = _inputs(nb, 6)
+    eng = PxEngine(path, nb=nb)
+    try:
+        eng.ready()
+        assert eng.nt == NT
+        ref = _chain(xt, m, torch.from_numpy(inp).to(dev), nb, dev, layers)
+        eng.submit(0, inp)
+        got = eng.wait(0, nb)
+        _say("  v3 engine scores: min %.4f max %.4f" % (got.min(), got.max()))
+        assert np.isfinite(got).all() and got.std() > 1e-3
+        assert (got == ref).all(), f"v3 engine differs from the kernel chain: max |d| {np.abs(got - ref).max():.3g}"
+    finally:
+        eng.close()
+
+
+def _pin(w, p):
+    """w with the first element of every 128 x 128 block set to +-p (p above every |w|): every block's |max| and the
+    tensor's are p, so the block scales of a v2 file and the per-tensor scale of a v3 file are both p / 448"""
+    w = w.astype(np.float32)
+    assert np.abs(w).max() < p
+    w[::128, ::128] = np.where(w[::128, ::128] < 0, -p, p)
+    return w.astype(np.float16)
+
+
+def test_px_v3_equals_v2_where_quantizations_coincide(dev, tmp_path):
+    """The v3 engine computes what the v2 engine computes, bit for bit, on a model where the two files' quantizations
+    coincide: every 128 x 128 block of every block weight holds the tensor's |max| 1/8 (per-tensor and block scales
+    are both 1/8 / 448, so the E4M3 codes are the same), calibration maxima equal to the weight-column maxima (every
+    SmoothQuant factor is exactly 1) and a headroom that makes adq3 = 2^-6: fc1 then packs gelu 64 (the same codes
+    with block scales 64 times larger, both exact) and fc2's scale wdq3 adq3 brings the product back exactly."""
+    m = blob.synth_px_model(seed=8, nt=NT)
+    cm = lambda w: np.abs(w.astype(np.float32)).max(0)
+    calib = {"act": [], "h": [], "qkv": []}
+    for L in m["layers"]:
+        for k in ("wqkv", "wo", "w1", "w2"):
+            L[k] = _pin(L[k], 0.125)
+        calib["act"].append(np.stack([cm(L["wqkv"]), cm(L["wo"]), cm(L["w1"])]))
+        calib["h"].append(cm(L["w2"]))
+        calib["qkv"].append(np.ones((3, D), np.float32))
+    calib = {k: np.asarray(v, np.float32) for k, v in calib.items()}
+    p2, p3 = tmp_path / "pixai_v2.bin", tmp_path / "pixai_v3.bin"
+    blob.write_px_v2(str(p2), m)
+    _, _, table = blob.write_px_v3(str(p3), m, calib, headroom=56.0)
+    assert (table[:, :4] == np.float32(0.125 / 448)).all() and (table[:, 7] == 2.0 ** -6).all()
+    inp = _inputs(2, 9)
+    out = []
+    for p in (p2, p3):
+        _say(f"px v2 / v3 equality: engine on {p.name}")
+        e = PxEngine(p, nb=2)
+        try:
+            e.ready()
+            e.submit(0, inp)
+            out.append(e.wait(0, 2).copy())
+        finally:
+            e.close()
+    _say("  v3 vs v2: max |d| %.3g" % np.abs(out[1] - out[0]).max())
+    assert np.isfinite(out[0]).all() and out[0].std() > 1e-3
+    assert np.array_equal(out[1], out[0])

@@ -158,6 +158,24 @@ def _e4m3_values(q):
     return torch.from_numpy(np.ascontiguousarray(q, np.uint8)).view(torch.float8_e4m3fn).to(torch.float32).numpy()
 
 
+def _smooth(a, w, alpha):
+    """SmoothQuant factors of one GEMM (export_eva.py:52-58, export_pixai.py:53-58): per input channel
+    clip(amax_act^alpha / amax_wcol^(1 - alpha), 1e-3, 1e3), 1 where either maximum is 0; fp32 as numpy computes them"""
+    f32 = np.float32
+    wa = np.abs(w).max(0)
+    ok = (a > 0) & (wa > 0)
+    sm = np.ones_like(a)
+    sm[ok] = np.clip(a[ok] ** f32(alpha) / wa[ok] ** f32(1 - alpha), 1e-3, 1e3)
+    return sm
+
+
+def _fp8_tensor(w):
+    """E4M3 codes of w with one scale amax / 448 for the whole tensor (export_eva.py:64-66, export_pixai.py:60-62)"""
+    f32 = np.float32
+    sc = float(np.abs(w).max()) / 448.0
+    return _e4m3_codes(np.clip(w / f32(sc), -448.0, 448.0)), f32(sc)
+
+
 def write_v3(path, m, calib, alpha=0.5, headroom=1.25):
     """Write model tensors m (synth_model layout) as an eva02.bin v3 file: the reference's calibrated export
     (export_eva.py:96-153) restated on the v2 tensors and the calibration maxima calib (synth_calib's layout).
@@ -167,18 +185,8 @@ def write_v3(path, m, calib, alpha=0.5, headroom=1.25):
     block weight becomes E4M3 with one scale amax / 448 (64-66); the [24][12] table leads the blob with the weight and
     activation dequantization scales (max * headroom / 448) and q, k, v's; rs = 1 / (adq_h s~)."""
     f32 = np.float32
-
-    def smooth(a, w):
-        wa = np.abs(w).max(0)
-        ok = (a > 0) & (wa > 0)
-        sm = np.ones_like(a)
-        sm[ok] = np.clip(a[ok] ** f32(alpha) / wa[ok] ** f32(1 - alpha), 1e-3, 1e3)
-        return sm
-
-    def fp8(w):
-        sc = float(np.abs(w).max()) / 448.0
-        return _e4m3_codes(np.clip(w / f32(sc), -448.0, 448.0)), f32(sc)
-
+    smooth = lambda a, w: _smooth(a, w, alpha)
+    fp8 = _fp8_tensor
     nl = len(m["layers"])
     assert nl == NL, "the blob always holds 24 layers"
     table = np.zeros((nl, 12), f32)
@@ -390,21 +398,110 @@ def px_tensors(m):
     return out
 
 
-def write_px_v2(path, m):
-    """Write model tensors m (synth_px_model layout) as a pixai.bin v2 file, streamed tensor by tensor."""
-    tensors = px_tensors(m)
-    size = 0
-    for _, a, dt in tensors:
-        size += -size % 256
-        size += np.asarray(a).size * np.dtype(dt).itemsize
+def _px_stream(path, ver, nt, tensors):
+    """Write (name, array, dtype) tensors as a pixai.bin of version ver, each on a 256-byte boundary of the blob, one
+    at a time (a PixAI blob is 0.5 - 0.9 GB); returns each tensor's blob offset and the blob's byte count."""
+    off, pos = {}, 0
     with open(path, "wb") as f:
-        f.write(struct.pack("<4sIII", b"PXAI", 2, m["nt"], size))
+        f.write(struct.pack("<4sIII", b"PXAI", ver, nt, 0))
         f.write(b"\0" * 240)
-        pos = 0
-        for _, a, dt in tensors:
+        for name, a, dt in tensors:
             pad = -pos % 256
             f.write(b"\0" * pad)
+            pos += pad
+            off[name] = pos
             data = np.ascontiguousarray(a, dtype=dt).tobytes()
             f.write(data)
-            pos += pad + len(data)
-    return size
+            pos += len(data)
+        f.seek(12)
+        f.write(struct.pack("<I", pos))
+    return off, pos
+
+
+def write_px_v2(path, m):
+    """Write model tensors m (synth_px_model layout) as a pixai.bin v2 file, streamed tensor by tensor."""
+    return _px_stream(path, 2, m["nt"], px_tensors(m))[1]
+
+
+def synth_px_calib(m, seed=0, spread=4.0):
+    """Synthetic calibration maxima for write_px_v3 in the layout of the reference's PixAI calibration file
+    (export_pixai.py:35-39, written by px.h's -DPX_CALIB engine, which needs CUDA): per block the per-channel |max| of
+    the four block-GEMM inputs (LN1 out, attention out, LN2 out over 1024 channels, the GELU output over 4736 units)
+    and of q, k, v. Each is a log-uniform draw in [1 / spread, spread] times a typical size, with a few outlier
+    channels 20x larger."""
+    r = np.random.default_rng(seed)
+    nl = len(m["layers"])
+
+    def draw(n, typ):
+        a = typ * np.exp(r.uniform(-np.log(spread), np.log(spread), n))
+        a[r.choice(n, 4, replace=False)] *= 20.0
+        return a.astype(np.float32)
+    return {"act": np.stack([np.stack([draw(D, 4.0), draw(D, 0.5), draw(D, 4.0)]) for _ in range(nl)]),
+            "h": np.stack([draw(PX_HID, 1.0) for _ in range(nl)]),
+            "qkv": np.stack([np.stack([draw(D, 1.0), draw(D, 4.0), draw(D, 2.0)]) for _ in range(nl)])}
+
+
+def px_v3_layer(L, act, h, qkv, alpha=0.5, headroom=1.25):
+    """One block of the reference's calibrated PixAI export (export_pixai.py:80-99) on the v2 tensors L and the
+    block's calibration maxima (act [3][1024], h [4736], qkv [3][1024]): SmoothQuant factors folded into LN1's gamma /
+    beta (QKV input), the V rows and bias (out-proj input), LN2's gamma / beta (fc1 input) and the fc2 columns (GELU
+    output, whose 1 / s reaches the activations through rs); each block weight E4M3 with one scale amax / 448.
+    Returns the block's tensors in blob order and its row of the scale table [wdq x4, adq x4, q, k, v, 0]."""
+    f32 = np.float32
+    w1, b1 = L["ln1w"].astype(f32).copy(), L["ln1b"].astype(f32).copy()
+    wqkv, bqkv = L["wqkv"].astype(f32), L["bqkv"].astype(f32).copy()
+    wo, bo = L["wo"].astype(f32), L["bo"].astype(f32)
+    w2, b2 = L["ln2w"].astype(f32).copy(), L["ln2b"].astype(f32).copy()
+    wf1, bf1 = L["w1"].astype(f32), L["b1"].astype(f32)
+    wf2, bf2 = L["w2"].astype(f32), L["b2"].astype(f32)
+    a = [act[0], act[1], act[2], h]
+    s = [_smooth(a[0], wqkv, alpha), _smooth(a[1], wo, alpha), _smooth(a[2], wf1, alpha), _smooth(a[3], wf2, alpha)]
+    w1 /= s[0]
+    b1 /= s[0]
+    wqkv *= s[0]
+    wqkv[2 * D:] /= s[1][:, None]
+    bqkv[2 * D:] /= s[1]
+    wo *= s[1]
+    w2 /= s[2]
+    b2 /= s[2]
+    wf1 *= s[2]
+    wf2 *= s[3]
+    row = np.zeros(12, f32)
+    mats = []
+    for k, w in enumerate((wqkv, wo, wf1, wf2)):
+        q, row[k] = _fp8_tensor(w)
+        mats.append(q)
+        row[4 + k] = f32(float((a[k] / s[k]).max()) * headroom / 448.0)
+    row[8] = f32(float(qkv[0].max()) * headroom / 448.0)
+    row[9] = f32(float(qkv[1].max()) * headroom / 448.0)
+    row[10] = f32(float((qkv[2] / s[1]).max()) * headroom / 448.0)
+    rs = (f32(1.0) / row[7]) / s[3]
+    u8 = np.uint8
+    return [("ln1w", w1, f32), ("ln1b", b1, f32), ("wqkv", mats[0], u8), ("bqkv", bqkv, f32), ("wo", mats[1], u8),
+            ("bo", bo, f32), ("ln2w", w2, f32), ("ln2b", b2, f32), ("w1", mats[2], u8), ("b1", bf1, f32),
+            ("rs", rs, f32), ("w2", mats[3], u8), ("b2", bf2, f32)], row
+
+
+def write_px_v3(path, m, calib, alpha=0.5, headroom=1.25):
+    """Write model tensors m (synth_px_model layout) as a pixai.bin v3 file: the reference's calibrated export
+    (export_pixai.py:68-99 per block by px_v3_layer, 114-132 for the order) with calib in synth_px_calib's layout.
+    The [32][12] scale table leads the blob; it is written last, over its placeholder, once every block is done.
+    Returns (tensor offsets, blob bytes, table)."""
+    nl = len(m["layers"])
+    assert nl == PX_NL, "the blob always holds 32 blocks"
+    table = np.zeros((nl, 12), np.float32)
+    head = px_tensors(m)
+
+    def tensors():
+        yield ("table", table, np.float32)
+        yield from head[:6]
+        for i, L in enumerate(m["layers"]):
+            ts, table[i] = px_v3_layer(L, calib["act"][i], calib["h"][i], calib["qkv"][i], alpha, headroom)
+            for k, a, dt in ts:
+                yield (f"{k}{i}", a, dt)
+        yield from head[6 + 13 * nl:]
+    off, size = _px_stream(path, 3, m["nt"], tensors())
+    with open(path, "r+b") as f:
+        f.seek(256)
+        f.write(table.tobytes())
+    return off, size, table

@@ -20,10 +20,12 @@
 
 #define PX_PW 576             // attention-pool statistics window of px_k_hstat
 #define PX_QW 288             // attention-pool pooling window of px_k_hpool / px_k_hproj
+#define PX_NS 12              // v3 scale table columns per block: wdq x4, adq x4, q, k, v, pad (px.h:204, 226-238)
 
 struct PxLayer {
     const float *ln1w, *ln1b, *bqkv, *bo, *ln2w, *ln2b, *b1, *rs, *b2;  // in the blob
-    const uint16_t *wqkv16, *wo16, *w116, *w216;                        // fp16 block weights in the blob
+    const uint16_t *wqkv16, *wo16, *w116, *w216;                        // v2: fp16 block weights in the blob
+    const uint8_t *wqkv8, *wo8, *w18, *w28;                             // v3: E4M3 weights, one scale per tensor
     uint8_t *wqkv, *wo, *w1, *w2;                                       // packed E4M3
     float *sqkv, *so, *s1, *s2;
     const float *rs_fc1;                                                // rs, or NULL where the file's rs are all 1
@@ -35,6 +37,8 @@ struct px_impl {
     pthread_t boot;
     char *path;
     size_t wbytes;
+    uint32_t ver;                                       // blob version: 2 (fp16 weights) or 3 (E4M3 + scale table)
+    float tab[PX_NL * PX_NS];                           // v3 scale table (host copy)
     uint32_t nb;                                        // inputs per launch (even)
     uint32_t nl, lnb[2], loff[2];                       // lanes in use; inputs per lane (even); first input of a lane
     uint32_t cnb, cM;                                   // inputs and token rows of the lane px_forward works on
@@ -87,7 +91,8 @@ static int px_alloc(px_impl *E, void **p, size_t bytes, bool zero)
         if ((call)) return -1;                                         \
     } while (0)
 
-// Blob layout of export_pixai.py version 2 (px.h:196-253 with PX_VER 2): every tensor on a 256-byte boundary.
+// Blob layout of export_pixai.py (px.h:196-253): every tensor on a 256-byte boundary; version 3 leads with the
+// [32][12] scale table and holds the block weights as E4M3 bytes, version 2 as fp16.
 static int px_layout(px_impl *E, uint32_t ntp)
 {
     size_t off = 0;
@@ -97,6 +102,9 @@ static int px_layout(px_impl *E, uint32_t ntp)
         off += bytes;
         return p;
     };
+    const bool v3 = E->ver == 3;
+    const size_t wb = v3 ? 1 : 2;
+    if (v3) take((size_t)PX_NL * PX_NS * 4);
     E->pe = (const uint16_t *)take((size_t)EVA_D * EVA_K0P * 2);
     E->pos = (const float *)take((size_t)PX_T * EVA_D * 4);
     E->lnpw = (const float *)take(EVA_D * 4);
@@ -107,17 +115,23 @@ static int px_layout(px_impl *E, uint32_t ntp)
         PxLayer &L = E->L[i];
         L.ln1w = (const float *)take(EVA_D * 4);
         L.ln1b = (const float *)take(EVA_D * 4);
-        L.wqkv16 = (const uint16_t *)take((size_t)3 * EVA_D * EVA_D * 2);
+        const uint8_t *wqkv = take((size_t)3 * EVA_D * EVA_D * wb);
         L.bqkv = (const float *)take(3 * EVA_D * 4);
-        L.wo16 = (const uint16_t *)take((size_t)EVA_D * EVA_D * 2);
+        const uint8_t *wo = take((size_t)EVA_D * EVA_D * wb);
         L.bo = (const float *)take(EVA_D * 4);
         L.ln2w = (const float *)take(EVA_D * 4);
         L.ln2b = (const float *)take(EVA_D * 4);
-        L.w116 = (const uint16_t *)take((size_t)PX_HID * EVA_D * 2);
+        const uint8_t *w1 = take((size_t)PX_HID * EVA_D * wb);
         L.b1 = (const float *)take(PX_HID * 4);
         L.rs = (const float *)take(PX_HID * 4);
-        L.w216 = (const uint16_t *)take((size_t)EVA_D * PX_HID * 2);
+        const uint8_t *w2 = take((size_t)EVA_D * PX_HID * wb);
         L.b2 = (const float *)take(EVA_D * 4);
+        if (v3) {
+            L.wqkv8 = wqkv, L.wo8 = wo, L.w18 = w1, L.w28 = w2;
+        } else {
+            L.wqkv16 = (const uint16_t *)wqkv, L.wo16 = (const uint16_t *)wo;
+            L.w116 = (const uint16_t *)w1, L.w216 = (const uint16_t *)w2;
+        }
         L.end = off;
     }
     E->hnw = (const float *)take(EVA_D * 4);
@@ -176,12 +190,24 @@ static int px_forward(px *p, hipStream_t fst)
     return 0;
 }
 
-// bring-up packing of block i's GEMM weights from the blob's fp16 tensors, on E->st; q / k rows of Wqkv pair-split
-// for the RoPE epilogue
+// bring-up packing of block i's GEMM weights from the blob, on E->st; q / k rows of Wqkv pair-split for the RoPE
+// epilogue
 static int px_pack_layer(px_impl *E, int i)
 {
     PxLayer &L = E->L[i];
     void *st = (void *)E->st;
+    if (E->ver == 3) {
+        // v3: the blob's E4M3 bytes with one scale per tensor (table[i][0..3], px.h:234-237); the smoothing is
+        // already folded into the LayerNorms, V rows and weights. The activations keep their own 1x128 scales, so
+        // fc1 packs gelu(u) rs with the blob's rs = 1 / (adq3 s3) (export_pixai.py:98) and fc2's scale carries adq3
+        // back: wdq3 adq3
+        const float *t = E->tab + (size_t)i * PX_NS;
+        PX_CK(eva_k_prep_w8(L.wqkv8, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, t[0], L.wqkv, L.sqkv, st));
+        PX_CK(eva_k_prep_w8(L.wo8, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, t[1], L.wo, L.so, st));
+        PX_CK(eva_k_prep_w8(L.w18, EVA_D, PX_HID, EVA_D, PX_HID, EVA_D, 0, t[2], L.w1, L.s1, st));
+        PX_CK(eva_k_prep_w8(L.w28, PX_HID, EVA_D, PX_HID, EVA_D, PX_HID, 0, t[3] * t[7], L.w2, L.s2, st));
+        return 0;
+    }
     PX_CK(eva_k_prep_w(L.wqkv16, EVA_D, 3 * EVA_D, EVA_D, 3 * EVA_D, EVA_D, 1, NULL, E->scratch, L.wqkv, L.sqkv, st));
     PX_CK(eva_k_prep_w(L.wo16, EVA_D, EVA_D, EVA_D, EVA_D, EVA_D, 0, NULL, E->scratch, L.wo, L.so, st));
     PX_CK(eva_k_prep_w(L.w116, EVA_D, PX_HID, EVA_D, PX_HID, EVA_D, 0, NULL, E->scratch, L.w1, L.s1, st));
@@ -224,7 +250,7 @@ static int px_up(px *p)
     }
 
     // per-unit fc1 multipliers: a file without calibration holds ones (export_pixai.py:83), and multiplying by 1 is
-    // exact, so fc1 then runs without the multiply
+    // exact, so fc1 then runs without the multiply; a v3 file holds 1 / (adq3 s3)
     std::vector<float> rs(PX_HID);
     for (int i = 0; i < PX_NL; i++) {
         PxLayer &L = E->L[i];
@@ -311,13 +337,31 @@ extern "C" int px_open_nb(px *p, const char *weights, int device, void *pool, si
     memset(p, 0, sizeof(*p));
     if (nb < 2 || nb > 100 || (nb & 1)) return xt_fail("px_open", "batch must be even, 2..100");
     f = fopen(weights, "rb");
-    if (!f || fread(hdr, 4, 4, f) != 4 || memcmp(hdr, "PXAI", 4) || hdr[1] != 2 || hdr[2] == 0) {
-        fprintf(stderr, "px: %s is not a pixai.bin v2 (run export_pixai.py without a calibration file)\n", weights);
+    if (!f || fread(hdr, 4, 4, f) != 4 || memcmp(hdr, "PXAI", 4) || (hdr[1] != 2 && hdr[1] != 3) || hdr[2] == 0) {
+        fprintf(stderr, "px: %s is not a pixai.bin v2 or v3 (export_pixai.py)\n", weights);
         if (f) fclose(f);
         return -1;
     }
+    float tab[PX_NL * PX_NS];
+    if (hdr[1] == 3) {  // the scale table leads the blob (px.h:204, 365); its host copy gives the per-tensor scales
+        if (fseek(f, 256, SEEK_SET) || fread(tab, 4, PX_NL * PX_NS, f) != PX_NL * PX_NS) {
+            fprintf(stderr, "px: %s: truncated v3 scale table\n", weights);
+            fclose(f);
+            return -1;
+        }
+        for (int j = 0; j < PX_NL; j++)
+            for (int c = 0; c < 8; c++)
+                if (!(tab[j * PX_NS + c] > 0.f) || !(tab[j * PX_NS + c] < 3e38f)) {
+                    fprintf(stderr, "px: %s: v3 scale table entry [%d][%d] is not a positive finite scale\n", weights,
+                            j, c);
+                    fclose(f);
+                    return -1;
+                }
+    }
     fclose(f);
     px_impl *E = new px_impl();
+    E->ver = hdr[1];
+    if (E->ver == 3) memcpy(E->tab, tab, sizeof(tab));
     p->impl = E;
     E->path = strdup(weights);
     if (!E->path) return xt_fail("px_open", "out of memory");
