@@ -119,6 +119,10 @@ int eva_k_quant_act(const void *x, int in_kind, int ldx, int M, int K, void *q, 
 int eva_k_quant_w(const float *w, int N, int K, void *q, float *s, void *stream);
 /* Encoder check: out[i] = E4M3 of the fp32 with bit pattern first + i (NaN patterns excepted). */
 int eva_k_e4m3_bits(uint32_t first, uint32_t count, void *out, void *stream);
+/* Block-scale rule check: out[i] = bit pattern of the packers' block scale (which 0: amax / 448 correctly rounded, 1
+ * below 2^-116; export_eva.py:64-66 per block) or of its inverse (which 1: 1 / s rounded once; eva.h:408) of the fp32
+ * with bit pattern first + i. */
+int eva_k_scale_bits(uint32_t first, uint32_t count, int which, void *out, void *stream);
 /* Block-scaled GEMM (kern_common.cuh:271-356 gemm8 + alpha epilogue, eva_kernels.cu:134-162):
  * C [M][ldc] = sum_kb sa[kb][m] sw[n/128][kb] sum_k qa[m][k] qw[n][k]; out_kind 0 = bf16 (RNE), 1 = fp32. */
 int eva_k_gemm(const void *qa, int lda, const float *sa, int lds, const void *qw, const float *sw, int M, int N, int K,

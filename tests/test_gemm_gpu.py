@@ -42,6 +42,40 @@ def test_e4m3_encoder_exhaustive(dev, xt, orc):
         assert not bad.any(), f"first mismatch at bits {hex(first + int(np.argmax(bad)))}"
 
 
+# ---------------------------------------------------------------- block scale and its inverse, every input they see
+def test_block_scale_rule_exhaustive(dev, xt):
+    """The packers' block scale s = amax / 448 and its inverse 1 / s (an fma-corrected product and one Newton step from
+    the hardware reciprocal, not the IEEE division sequence) against numpy's IEEE float32 division, bit for bit: s for
+    every non-negative fp32 amax up to +inf (1 below 2^-116), 1 / s for every s from RN(2^-116 / 448) to
+    RN(FLT_MAX / 448), which holds every scale the packers make, and at +inf (0) and NaN."""
+    chunk = 1 << 26
+    out = torch.empty(chunk, dtype=torch.int32, device=dev)
+    f32 = np.float32
+
+    def sweep(lo, hi, which, ref_fn):
+        first = lo
+        while first <= hi:
+            n = min(chunk, hi - first + 1)
+            _run(xt.lib.eva_k_scale_bits(first, n, which, xt.ptr(out), _stream()), "eva_k_scale_bits")
+            got = out[:n].cpu().numpy().view(np.uint32)
+            x = np.arange(first, first + n, dtype=np.uint64).astype(np.uint32).view(f32)
+            with np.errstate(all="ignore"):
+                ref = ref_fn(x).astype(f32).view(np.uint32)
+            nan = np.isnan(ref.view(f32))
+            bad = (got != ref) & ~(nan & np.isnan(got.view(f32)))
+            assert not bad.any(), f"which {which}: first mismatch at bits {hex(first + int(np.argmax(bad)))}"
+            first += n
+
+    bits = lambda v: int(np.array(v, f32).view(np.uint32))
+    _say("block scale: every amax in [0, inf]")
+    sweep(0, 0x7F800000, 0, lambda a: np.where(a < f32(2.0 ** -116), f32(1), a / f32(448)))
+    _say("block scale inverse: every s the packers make")
+    lo, hi = bits(f32(2.0 ** -116) / f32(448)), bits(np.finfo(f32).max / f32(448))
+    sweep(lo, hi, 1, lambda s: f32(1) / s)
+    sweep(0x7F800000, 0x7FC00000, 1, lambda s: f32(1) / s)   # +inf -> 0, then NaN patterns
+    sweep(0x7FC00000, 0x7FC00000, 0, lambda a: a / f32(448))
+
+
 # ---------------------------------------------------------------- activation / weight packing
 def _act_inputs(M, K, seed):
     r = np.random.default_rng(seed)

@@ -101,6 +101,16 @@ __global__ void __launch_bounds__(256) k_e4m3_bits(uint32_t first, uint32_t coun
         out[i] = (uint8_t)e4_pack2(__uint_as_float(first + i), 0.f);
 }
 
+// ---- block-scale rule check: block_scale (which 0) or block_scale_inv (which 1) of the fp32 bit patterns
+// first .. first + count - 1, as bit patterns ----
+__global__ void __launch_bounds__(256) k_scale_bits(uint32_t first, uint32_t count, int which, uint32_t *__restrict__ out)
+{
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) {
+        const float x = __uint_as_float(first + i);
+        out[i] = __float_as_uint(which ? block_scale_inv(x) : block_scale(x));
+    }
+}
+
 // ---- standalone block-scaled GEMM: C [M][ldc] = bf16 or fp32 of the block-scaled product ----
 // bf16: each wave parks 64 x 64 fp32 of its tile in its own LDS slice (row stride 68 floats, conflict-free), then
 // every lane rounds 8 consecutive columns to bf16 (RNE) and writes them with one 16-byte store through a descriptor
@@ -238,6 +248,15 @@ extern "C" int eva_k_e4m3_bits(uint32_t first, uint32_t count, void *out, void *
     hipLaunchKernelGGL(k_e4m3_bits, dim3(grid_for(count)), dim3(256), 0, (hipStream_t)stream, first, count,
                        (uint8_t *)out);
     return xt_check("eva_k_e4m3_bits");
+}
+
+extern "C" int eva_k_scale_bits(uint32_t first, uint32_t count, int which, void *out, void *stream)
+{
+    if (which != 0 && which != 1) return xt_fail("eva_k_scale_bits", "which must be 0 (scale) or 1 (inverse)");
+    if (!count) return 0;
+    hipLaunchKernelGGL(k_scale_bits, dim3(grid_for(count)), dim3(256), 0, (hipStream_t)stream, first, count, which,
+                       (uint32_t *)out);
+    return xt_check("eva_k_scale_bits");
 }
 
 template <bool SP>

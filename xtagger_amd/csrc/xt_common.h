@@ -51,12 +51,27 @@ __device__ __forceinline__ uint32_t e4_pack4_scaled(float a, float b, float c, f
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
 }
 
-// Block scale from a block |max|: amax / 448, one IEEE division (correctly rounded: HIP device code keeps fp32
-// division exact unless fast math is asked for), 1 for a zero block (|max| < 2^-116, where 448 / amax would leave the
-// normal range). The reference's per-tensor rule sc = amax / 448 (export_eva.py:64-66) applied per block.
-__device__ __forceinline__ float block_scale(float amax) { return amax < 0x1p-116f ? 1.0f : amax / XT_E4MAX; }
-// 1 / s, rounded once per block (the reference's qs = 1 / scl, eva.h:408): activations are packed as x * (1 / s)
-__device__ __forceinline__ float block_scale_inv(float s) { return 1.0f / s; }
+// Block scale from a block |max|: amax / 448 correctly rounded, 1 for a zero block (|max| < 2^-116, where 448 / amax
+// would leave the normal range). The reference's per-tensor rule sc = amax / 448 (export_eva.py:64-66) applied per
+// block. The quotient is formed without the IEEE division sequence: q = amax RN(1/448), r = amax - 448 q (exact, one
+// fma), s = RN(q + r RN(1/448)). That is the correctly rounded quotient for every float amax >= 2^-116 (an exhaustive
+// check over all of them, eva_k_scale_bits); at +inf, where r is not finite, q itself is the quotient.
+__device__ __forceinline__ float block_scale(float amax)
+{
+    constexpr float c = 0x1.24924ap-9f;  // RN(1 / 448)
+    const float q = amax * c;
+    const float s = __builtin_fmaf(__builtin_fmaf(-q, XT_E4MAX, amax), c, q);
+    return amax < 0x1p-116f ? 1.0f : (q != __builtin_inff() ? s : q);
+}
+// 1 / s rounded once per block (the reference's qs = 1 / scl, eva.h:408): activations are packed as x * (1 / s). One
+// Newton step y0 + y0 (1 - s y0) from the hardware reciprocal y0, which gives the correctly rounded quotient for every
+// s that block_scale returns (exhaustive check on gfx950, eva_k_scale_bits); 0 at +inf, where the step is not finite.
+__device__ __forceinline__ float block_scale_inv(float s)
+{
+    const float y0 = __builtin_amdgcn_rcpf(s);
+    const float y1 = __builtin_fmaf(__builtin_fmaf(-s, y0, 1.0f), y0, y0);
+    return s != __builtin_inff() ? y1 : 0.0f;
+}
 
 // ---- bf16 / fp16 (round to nearest even) ----
 __device__ __forceinline__ uint16_t f2bf(float x)

@@ -15,6 +15,7 @@ _SIGS = {
     "eva_k_quant_act": (_i, [_p, _i, _i, _i, _i, _p, _i, _p, _i, _p]),
     "eva_k_quant_w": (_i, [_p, _i, _i, _p, _p, _p]),
     "eva_k_e4m3_bits": (_i, [_u32, _u32, _p, _p]),
+    "eva_k_scale_bits": (_i, [_u32, _u32, _i, _p, _p]),
     "eva_k_gemm": (_i, [_p, _i, _p, _i, _p, _p, _i, _i, _i, _p, _i, _i, _p]),
     "eva_k_ln": (_i, [_p, _p, _p, _p, _p, _i, _i, _p]),
     "eva_k_qkv": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _p]),
