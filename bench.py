@@ -476,6 +476,26 @@ def bench_pixai_forward(torch, L, nb=4, nt=13461):
     return nb / (ms_b * 1e-3), ms_b
 
 
+def forward_roofline_ms(nb, nt=10861):
+    """Roofline time of the wd forward for nb images, summed per op kind as max(flops / peak, bytes / HBM peak) at the
+    spec peaks: the block GEMMs on the FP8 matrix cores (5000 TFLOP/s), attention and the patch embedding on bf16 / fp16
+    (2500), LayerNorm + pack, pooling and the head weights on HBM (8 TB/s). Returns (total ms, {op: ms})."""
+    rows, L = nb * T, 24
+    fp8, bf16, hbm = 5000e12, 2500e12, 8e12
+    ops = {
+        "qkv": (2.0 * rows * 3 * D * D * L / fp8, (rows * D + 3 * D * D + rows * 3 * D * 2) * L / hbm),
+        "oproj": (2.0 * rows * D * D * L / fp8, (rows * D + D * D + rows * D * 4) * L / hbm),
+        "fc1": (2.0 * rows * 2 * HID * D * L / fp8, (rows * D + 2 * HIDP * D + rows * HIDP) * L / hbm),
+        "fc2": (2.0 * rows * D * HID * L / fp8, (rows * HIDP + D * HIDP + rows * D * 4) * L / hbm),
+        "attention": (4.0 * nb * T * T * 64 * 16 * L / bf16, nb * T * D * 2 * 4 * L / hbm),
+        "layernorm": (0.0, 2 * L * rows * (D * 3 + 8 * 4) / hbm),
+        "patch": (2.0 * nb * 1024 * 592 * D / bf16, (nb * 1024 * 592 * 2 + rows * D * 2) / hbm),
+        "pool+head": (2.0 * nb * D * nt / fp8, (rows * D * 2 + nt * D) / hbm),
+    }
+    per = {k: max(f, b) * 1e3 for k, (f, b) in ops.items()}
+    return sum(per.values()), per
+
+
 def bench_forward(torch, nb=32, iters=3, extra=0, sparse=False, profile=None):
     """Full wd forward (24 blocks + head 10861 + extra rows) at batch nb on a synthetic v2 blob: images/s with inputs
     resident (the engine runs each batch as two halves at once on its two lanes). sparse: the layer GEMM weights
@@ -800,8 +820,11 @@ def main():
     if not args.no_forward:
         prof = {}
         ips, fms = bench_forward(torch, profile=prof)
+        rl_ms, rl_per = forward_roofline_ms(32)
         out["forward_b32"] = {"images_per_s": round(ips, 1), "ms_per_batch": round(fms, 3),
                               "tflops": round(32 * 723.5e9 / (fms * 1e-3) / 1e12, 1),
+                              "roofline_ms": round(rl_ms, 3), "frac_of_roofline": round(rl_ms / fms, 3),
+                              "roofline_ms_per_op": {k: round(v, 3) for k, v in rl_per.items()},
                               "eva_profile_ms": prof}
         # the reference engine's own batch (EVA_NB = 8)
         ips8, fms8 = bench_forward(torch, nb=8)
