@@ -315,53 +315,66 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
 // (kern_common.cuh:679-727 k_headmv, here an FP8 GEMM). The head rows carry 1x128 scales of their own (planes
 // hs [8][ldh], as activations do), so every row is packed, and repacked by eva_head_put, independently of all others.
 // The head is a weight stream (nt x 1 KB) against at most 128 input rows: one block per 64 output columns and 64 rows,
-// 4 waves, wave w owning columns n0 + 16 w .. + 15 over the 4 row tiles of 16. Fragments come straight from L2 into
-// registers (a row of the weights is read once per row tile); descriptors that end at row nb of pq and row nt of hq
-// load zero past them.
+// 4 waves, wave w owning columns n0 + 16 w .. + 15. A wave issues the loads of all eight K blocks' weight fragments
+// and scales before its first matrix instruction (one memory round trip for the stream instead of eight), then runs
+// only the row tiles of 16 that hold input rows (a batch of 16 runs one of the four). Fragments come straight from L2
+// into registers; descriptors that end at row nb of pq and row nt of hq load zero past them. Each output's K blocks
+// are promoted in order, so a row's scores do not depend on the batch around it.
 // ---------------------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) k_head(const uint8_t *__restrict__ pq, const float *__restrict__ ps, int lds,
                                               const uint8_t *__restrict__ hq, const float *__restrict__ hs, int ldh,
                                               const float *__restrict__ hb, float *__restrict__ out, int nb, int nt)
 {
+    constexpr int KB = XT_D / 128;
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int n0 = blockIdx.x * 64 + 16 * w, m0 = blockIdx.y * 64;
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(pq, (uint32_t)nb * XT_D), rw = buf_rsrc(hq, (uint32_t)nt * XT_D);
     const int nl = n0 + c16;                                  // weight row of this lane's B fragment, output column
     const int ncl = nl < nt ? nl : nt - 1;                    // clamped for the scale and bias reads
-    v4f acc[4];
+    v8i b[KB];
+    float swv[KB];
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-    for (int kb = 0; kb < XT_D / 128; kb++) {
+    for (int kb = 0; kb < KB; kb++) {
         const uint32_t ko = (uint32_t)kb * 128u + 16u * g;
         const v4u blo = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)((uint32_t)nl * XT_D + ko), 0, 0);
         const v4u bhi = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)((uint32_t)nl * XT_D + ko + 64u), 0, 0);
-        const v8i b = {(int)blo[0], (int)blo[1], (int)blo[2], (int)blo[3], (int)bhi[0], (int)bhi[1], (int)bhi[2], (int)bhi[3]};
-        const float swv = hs[(size_t)kb * ldh + ncl];
+        b[kb] = v8i{(int)blo[0], (int)blo[1], (int)blo[2], (int)blo[3], (int)bhi[0], (int)bhi[1], (int)bhi[2], (int)bhi[3]};
+        swv[kb] = hs[(size_t)kb * ldh + ncl];
+    }
+    const int ntile = (nb - m0 + 15) >> 4;                    // row tiles holding input rows (block-uniform, >= 1)
+    const float bias = hb[ncl];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t ar = (uint32_t)(m0 + 16 * i + c16) * XT_D;
+    for (int i = 0; i < 4; i++) {
+        if (i >= ntile) break;
+        v8i a[KB];
+        float sa[KB][4];
+        const uint32_t ar = (uint32_t)(m0 + 16 * i + c16) * XT_D;
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) {
+            const uint32_t ko = (uint32_t)kb * 128u + 16u * g;
             const v4u alo = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(ar + ko), 0, 0);
             const v4u ahi = __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(ar + ko + 64u), 0, 0);
-            const v8i a = {(int)alo[0], (int)alo[1], (int)alo[2], (int)alo[3], (int)ahi[0], (int)ahi[1], (int)ahi[2], (int)ahi[3]};
-            const v4f p = mfma_e4m3_16x16x128(a, b);
+            a[kb] = v8i{(int)alo[0], (int)alo[1], (int)alo[2], (int)alo[3], (int)ahi[0], (int)ahi[1], (int)ahi[2], (int)ahi[3]};
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + 16 * i + 4 * g + r;
-                const float sa = m < nb ? ps[(size_t)kb * lds + m] : 0.f;
-                acc[i][r] = __builtin_fmaf(p[r], sa * swv, acc[i][r]);
+                sa[kb][r] = m < nb ? ps[(size_t)kb * lds + m] : 0.f;
             }
         }
-    }
-    if (nl >= nt) return;
-    const float bias = hb[nl];
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+        for (int kb = 0; kb < KB; kb++) {
+            const v4f p = mfma_e4m3_16x16x128(a[kb], b[kb]);
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = m0 + 16 * i + 4 * g + r;
-            if (m < nb) out[(size_t)m * nt + nl] = 1.0f / (1.0f + __expf(-(acc[i][r] + bias)));
+            for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(p[r], sa[kb][r] * swv[kb], acc[r]);
         }
+        if (nl < nt)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + 16 * i + 4 * g + r;
+                if (m < nb) out[(size_t)m * nt + nl] = 1.0f / (1.0f + __expf(-(acc[r] + bias)));
+            }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
