@@ -174,8 +174,8 @@ int eva_k_pool(const void *x, float *p, int nb, void *stream);
 int eva_k_lnh(const float *p, const float *g, const float *b, void *pn, void *q, float *s, int rows, int lds,
               void *stream);
 /* Weight packing from fp16 (export_eva.py:52-119 transforms, per 128x128 block): w16 [n_in][ldw] -> fp32 scratch
- * [n_out][k_out] (zero past n_in / k_in; perm 1 pair-splits the q and k heads of Wqkv; colscale may be NULL) ->
- * q [ceil(n_out/128)*128][k_out], s [ceil(n_out/128)][k_out/128]. */
+ * [n_out][k_out] (zero past n_in / k_in; perm 1 quad-splits the q and k heads of Wqkv: row 16 j + i of a head holds
+ * dim 4 i + j; colscale may be NULL) -> q [ceil(n_out/128)*128][k_out], s [ceil(n_out/128)][k_out/128]. */
 int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_out, int perm, const float *colscale,
                  float *scratch, void *q, float *s, void *stream);
 /* MLP-LN fold terms (export_eva.py:117-119): c[n] = sum_k dec(q[n][k]) s[n/128][k/128] over the packed W~
@@ -183,7 +183,7 @@ int eva_k_prep_w(const void *w16, int ldw, int n_in, int k_in, int n_out, int k_
 int eva_k_fold_cd(const void *q, const float *s, const void *w2, int ldw2, const float *beta, float *c, float *d,
                   void *stream);
 /* v3 blob weights (export_eva.py:64-66, 133-147: E4M3 with one fp32 scale per tensor) to the kernels' layout: E4M3
- * rows w8 [n_in][ldw] -> q [n_out][k_out] (rows >= n_in and columns >= k_in zero; perm 1 pair-splits the q and k heads
+ * rows w8 [n_in][ldw] -> q [n_out][k_out] (rows >= n_in and columns >= k_in zero; perm 1 quad-splits the q and k heads
  * as eva_k_prep_w), every 128 x 128 block scale s [n_out/128][k_out/128] = scale. */
 int eva_k_prep_w8(const void *w8, int ldw, int n_in, int k_in, int n_out, int k_out, int perm, float scale, void *q,
                   float *s, void *stream);

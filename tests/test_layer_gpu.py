@@ -148,13 +148,13 @@ def test_prep_qkv_pair_split_bitexact(dev, xt, orc):
     for h in range(32):
         for pc in range(64):
             j, i = pc >> 4, pc & 15
-            perm[h * 64 + pc] = h * 64 + 2 * (16 * (j >> 1) + i) + (j & 1)
+            perm[h * 64 + pc] = h * 64 + 4 * i + j         # column tile j, lane i: dim 4 i + j
     assert (d_q.cpu().numpy() == q[perm]).all()
 
 
 def test_prep_w8_v3_bitexact(dev, xt, orc):
     """eva_k_prep_w8: the v3 blob's E4M3 bytes with one scale per tensor (export_eva.py:64-66) into the kernels'
-    layout: qkv rows pair-split as eva_k_prep_w's perm 1, W12 and W~2 zero-padded to 2816 units; every block scale is
+    layout: qkv rows quad-split as eva_k_prep_w's perm 1, W12 and W~2 zero-padded to 2816 units; every block scale is
     the tensor's. eva_k_fold_c_rs: c = sum_k dec(q) s rs against float64."""
     _say("eva_k_prep_w8 + eva_k_fold_c_rs")
     r = np.random.default_rng(13)
@@ -162,7 +162,7 @@ def test_prep_w8_v3_bitexact(dev, xt, orc):
     for h in range(32):
         for pc in range(64):
             j, i = pc >> 4, pc & 15
-            perm[h * 64 + pc] = h * 64 + 2 * (16 * (j >> 1) + i) + (j & 1)
+            perm[h * 64 + pc] = h * 64 + 4 * i + j         # column tile j, lane i: dim 4 i + j
     q = r.integers(0, 256, (3 * D, D)).astype(np.uint8)
     q[(q & 0x7F) == 0x7F] = 0                                 # no NaN codes in a blob
     d_q = torch.zeros((3 * D, D), dtype=torch.uint8, device=dev)

@@ -11,9 +11,9 @@
 // ---------------------------------------------------------------------------------------------------------------
 // k_qkv: h8 [rows][1024] x Wqkv [3072][1024] -> q, k bf16 [nb][16][1088][64] (RoPE on patch tokens), vt bf16
 // [nb][16][64][1088]. A 256-column block is 4 heads of one of q | k | v; each wave owns two heads. The weight rows
-// of q and k heads are stored pair-split (see eva_prep_qkv): within a head, column tile 2p holds dims 2i and tile
-// 2p+1 dims 2i+1 of pair i = 16p + (lane & 15), so a rotary pair meets in one lane. q rows carry log2(e)/8
-// (export_eva.py:71).
+// of q and k heads are stored quad-split (eva_k_prep_w perm 1): within a head, column tile j holds dim 4i + j for
+// i = lane & 15, so a lane holds dims 4i .. 4i + 3, the rotary pairs 2i and 2i + 1 whole: their (cos, sin) come in one
+// 16-byte load and the rotated dims leave in one 8-byte store. q rows carry log2(e)/8 (export_eva.py:71).
 // ---------------------------------------------------------------------------------------------------------------
 template <bool SP>
 __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict__ h8, const float *__restrict__ hs,
@@ -41,8 +41,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
         const int nbi = rows / XT_T;
         const __amdgpu_buffer_rsrc_t rc = buf_rsrc(cs, 1024u * 32u * 8u);
         const __amdgpu_buffer_rsrc_t rd = buf_rsrc(part ? k : q, (uint32_t)nbi * XT_NH * XT_TP * XT_HD * 2u);
-        typedef float v2f __attribute__((ext_vector_type(2)));
-        v2f rot[C::TM][4][2];
+        v4f rot[C::TM][4];  // (cos, sin) of pairs 2 c16 and 2 c16 + 1
         int tok[C::TM][4], img[C::TM][4];
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
@@ -51,10 +50,8 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
                 const int m = m0 + wm0 + 16 * i + 4 * g + r, b = m / XT_T, t = m - b * XT_T;
                 img[i][r] = b;
                 tok[i][r] = t;
-#pragma unroll
-                for (int p = 0; p < 2; p++)
-                    rot[i][r][p] = __builtin_bit_cast(
-                        v2f, __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(((uint32_t)(t - 1) * 32u + 16 * p + c16) * 8u), 0, 0));
+                rot[i][r] = __builtin_bit_cast(
+                    v4f, __builtin_amdgcn_raw_buffer_load_b128(rc, (int)(((uint32_t)(t - 1) * 32u + 2 * c16) * 8u), 0, 0));
             }
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
@@ -62,20 +59,23 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
             for (int r = 0; r < 4; r++) {
                 const int b = img[i][r], t = tok[i][r];
 #pragma unroll
-                for (int hh = 0; hh < 2; hh++)
+                for (int hh = 0; hh < 2; hh++) {
+                    uint32_t two[2];
 #pragma unroll
                     for (int p = 0; p < 2; p++) {
-                        const int pi = 16 * p + c16;
                         float f0 = acc[i][4 * hh + 2 * p][r], f1 = acc[i][4 * hh + 2 * p + 1][r];
                         if (t) {
-                            const v2f a = rot[i][r][p];
-                            const float g0 = f0 * a.x - f1 * a.y;
-                            f1 = f1 * a.x + f0 * a.y;
+                            const float cr = rot[i][r][2 * p], sr = rot[i][r][2 * p + 1];
+                            const float g0 = f0 * cr - f1 * sr;
+                            f1 = f1 * cr + f0 * sr;
                             f0 = g0;
                         }
-                        const uint32_t off = (uint32_t)((((size_t)b * XT_NH + head0 + hh) * XT_TP + t) * XT_HD + 2 * pi) * 2u;
-                        __builtin_amdgcn_raw_buffer_store_b32(pk_bf16(f0, f1), rd, (int)off, 0, 0);
+                        two[p] = pk_bf16(f0, f1);
                     }
+                    const uint32_t off = (uint32_t)((((size_t)b * XT_NH + head0 + hh) * XT_TP + t) * XT_HD + 4 * c16) * 2u;
+                    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+                    __builtin_amdgcn_raw_buffer_store_b64(v2u{two[0], two[1]}, rd, (int)off, 0, 0);
+                }
             }
         return;
     }

@@ -1,8 +1,9 @@
 // prep.hip - weight preparation at bring-up: the reference's v2 fp16 block weights (export_eva.py layout) become
 // E4M3 with 128x128 fp32 scales on the GPU, with the transforms the kernels expect:
-//  - q and k rows of Wqkv pair-split per head: physical column c = 16 j + i of a head holds dim 2(16 (j >> 1) + i)
-//    + (j & 1), so each rotary pair (eva_kernels.cu:74-79) lands in one lane of k_qkv; quantization blocks are
-//    128 rows = 2 heads, so the split never moves a row across a block (same scales as the natural order);
+//  - q and k rows of Wqkv quad-split per head: physical column c = 16 j + i of a head holds dim 4 i + j, so a lane
+//    of k_qkv holds dims 4 i .. 4 i + 3, two whole rotary pairs (eva_kernels.cu:74-79), and stores them as 8 bytes;
+//    quantization blocks are 128 rows = 2 heads, so the split never moves a row across a block (same scales as the
+//    natural order);
 //  - fc1 rows re-padded from 2 x 2736 to 2 x 2816 units (the 16-unit g / x chunks of export_eva.py:60-62 are
 //    chunk-major, so that is a zero tail);
 //  - the MLP LayerNorm folded into fc2 (export_eva.py:101-104, 117-119): W~ = W2 diag(gamma), c = W~ 1 from the
@@ -13,7 +14,7 @@
 
 extern "C" int eva_k_quant_w(const float *w, int N, int K, void *q, float *s, void *stream);
 
-// fp16 [n_in][ldw] -> fp32 [n_out][k_out]: rows >= n_in and columns >= k_in are zero; perm 1 pair-splits the q and
+// fp16 [n_in][ldw] -> fp32 [n_out][k_out]: rows >= n_in and columns >= k_in are zero; perm 1 quad-splits the q and
 // k heads (rows < 2048); colscale (may be NULL) multiplies column k (one rounding).
 __global__ void __launch_bounds__(256) k_prep_f32(const uint16_t *__restrict__ w, int ldw, int n_in, int k_in,
                                                   int n_out, int k_out, int perm, const float *__restrict__ colscale,
@@ -25,7 +26,7 @@ __global__ void __launch_bounds__(256) k_prep_f32(const uint16_t *__restrict__ w
         int src = r;
         if (perm == 1 && r < 2 * XT_D) {
             const int hd = r & ~63, pc = r & 63, j = pc >> 4, ii = pc & 15;
-            src = hd + 2 * (16 * (j >> 1) + ii) + (j & 1);
+            src = hd + 4 * ii + j;
         }
         float v = 0.f;
         if (src < n_in && c < k_in) {
@@ -96,7 +97,7 @@ __global__ void __launch_bounds__(256) k_prep_w8(const uint8_t *__restrict__ w, 
         int src = r;
         if (perm == 1 && r < 2 * XT_D) {
             const int hd = r & ~63, pc = r & 63, j = pc >> 4, ii = pc & 15;
-            src = hd + 2 * (16 * (j >> 1) + ii) + (j & 1);
+            src = hd + 4 * ii + j;
         }
         uint32_t v = 0;
         if (src < n_in)

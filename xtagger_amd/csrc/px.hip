@@ -39,8 +39,8 @@ __device__ __forceinline__ float gelu_erf(float u)
 // ---------------------------------------------------------------------------------------------------------------
 // k_px_qkv: h8 [rows][1024] x Wqkv [3072][1024] + bias -> q, k bf16 [S][16][L][64] (RoPE on every token with table
 // row t = m % L, cs [L][32] (cos, sin) of pair i = dims 2i, 2i+1), vt bf16 [S][16][64][L]; rows = S L. Weight rows of
-// q and k are pair-split as for the wd model (column tile 2p of a head holds dims 2i, tile 2p+1 dims 2i+1 of pair
-// i = 16p + (lane & 15)); the bias stays in natural order. q rows of W and of the bias carry log2(e)/8 (the
+// q and k are quad-split as for the wd model (column tile j of a head holds dim 4i + j, i = lane & 15: a lane holds
+// pairs 2i and 2i + 1 whole); the bias stays in natural order. q rows of W and of the bias carry log2(e)/8 (the
 // reference's cq, px_kernels.cu:84).
 // ---------------------------------------------------------------------------------------------------------------
 template <bool SP>
@@ -66,13 +66,10 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_qkv(const uint8_t *__restri
         // at sequence S: rows past `rows` map to sequence S or later and are dropped without a branch.
         const __amdgpu_buffer_rsrc_t rc = buf_rsrc(cs, (uint32_t)L * 32u * 8u);
         const __amdgpu_buffer_rsrc_t rd = buf_rsrc(part ? k : q, (uint32_t)rows * XT_D * 2u);
-        v2f bq[2][2];
+        v4f bq[2];  // bias of dims 4 c16 .. 4 c16 + 3 of each head
 #pragma unroll
-        for (int hh = 0; hh < 2; hh++)
-#pragma unroll
-            for (int p = 0; p < 2; p++)
-                bq[hh][p] = *(const v2f *)(bias + part * XT_D + (head0 + hh) * XT_HD + 2 * (16 * p + c16));
-        v2f rot[C::TM][4][2];
+        for (int hh = 0; hh < 2; hh++) bq[hh] = *(const v4f *)(bias + part * XT_D + (head0 + hh) * XT_HD + 4 * c16);
+        v4f rot[C::TM][4];  // (cos, sin) of pairs 2 c16 and 2 c16 + 1
         uint32_t base[C::TM][4];  // element offset of (sequence, head head0, token), dims 0
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
@@ -80,27 +77,28 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_qkv(const uint8_t *__restri
             for (int r = 0; r < 4; r++) {
                 const int m = m0 + wm0 + 16 * i + 4 * g + r, s = m / L, t = m - s * L;
                 base[i][r] = ((uint32_t)(s * XT_NH + head0) * (uint32_t)L + (uint32_t)t) * XT_HD;
-#pragma unroll
-                for (int p = 0; p < 2; p++)
-                    rot[i][r][p] = __builtin_bit_cast(
-                        v2f, __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(((uint32_t)t * 32u + 16 * p + c16) * 8u), 0, 0));
+                rot[i][r] = __builtin_bit_cast(
+                    v4f, __builtin_amdgcn_raw_buffer_load_b128(rc, (int)(((uint32_t)t * 32u + 2 * c16) * 8u), 0, 0));
             }
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
             for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int hh = 0; hh < 2; hh++)
+                for (int hh = 0; hh < 2; hh++) {
+                    uint32_t two[2];
 #pragma unroll
                     for (int p = 0; p < 2; p++) {
-                        const int pi = 16 * p + c16;
-                        const float f0 = acc[i][4 * hh + 2 * p][r] + bq[hh][p].x;
-                        const float f1 = acc[i][4 * hh + 2 * p + 1][r] + bq[hh][p].y;
-                        const v2f a = rot[i][r][p];
-                        const float g0 = f0 * a.x - f1 * a.y, g1 = f1 * a.x + f0 * a.y;
-                        const uint32_t off = (base[i][r] + (uint32_t)(hh * L * XT_HD + 2 * pi)) * 2u;
-                        __builtin_amdgcn_raw_buffer_store_b32(pk_bf16(g0, g1), rd, (int)off, 0, 0);
+                        const float f0 = acc[i][4 * hh + 2 * p][r] + bq[hh][2 * p];
+                        const float f1 = acc[i][4 * hh + 2 * p + 1][r] + bq[hh][2 * p + 1];
+                        const float cr = rot[i][r][2 * p], sr = rot[i][r][2 * p + 1];
+                        const float g0 = f0 * cr - f1 * sr, g1 = f1 * cr + f0 * sr;
+                        two[p] = pk_bf16(g0, g1);
                     }
+                    const uint32_t off = (base[i][r] + (uint32_t)(hh * L * XT_HD + 4 * c16)) * 2u;
+                    typedef unsigned v2u __attribute__((ext_vector_type(2)));
+                    __builtin_amdgcn_raw_buffer_store_b64(v2u{two[0], two[1]}, rd, (int)off, 0, 0);
+                }
         return;
     }
     // v (+ bias): transpose the wave's 64 rows x 128 dims (two heads) through LDS, then lanes walk rows (consecutive

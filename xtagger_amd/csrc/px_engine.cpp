@@ -190,7 +190,7 @@ static int px_forward(px *p, hipStream_t fst)
     return 0;
 }
 
-// bring-up packing of block i's GEMM weights from the blob, on E->st; q / k rows of Wqkv pair-split for the RoPE
+// bring-up packing of block i's GEMM weights from the blob, on E->st; q / k rows of Wqkv quad-split for the RoPE
 // epilogue
 static int px_pack_layer(px_impl *E, int i)
 {
