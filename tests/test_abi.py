@@ -172,6 +172,51 @@ def test_px_v3_layer_keeps_every_gemm():
     assert rel(z @ (dec("wo") * t[1]).T, z @ f(L["wo"]).T) > 0.5         # the out-proj columns carry s1
 
 
+def test_wd_v3_layer_keeps_every_gemm():
+    """blob.wd_v3_layer restates one block of the calibrated wd export (export_eva.py:96-153): every GEMM of the v3
+    block must compute what the v2 block computes, up to the E4M3 rounding of its weights. For normalised rows xh:
+    LN1'(xh) W~qkv^T wdq0 equals LN1(xh) Wqkv^T on the q and k rows; the v rows, which carry 1 / s1, through W~o wdq1
+    give the v2 block's v Wo^T; LN2'(xh) W~12^T wdq2 equals LN2(xh) W12^T. The MLP LayerNorm is folded into fc2: for
+    SwiGLU-like rows g with mean mu and 1 / std r over the 2730 units, r ((g rs) (W~2 wdq3 adq3)^T - mu c) + d equals
+    LNm(g) W2^T. g has mean 1 and the MLP LayerNorm bias is made large, so that the c and d terms each carry a
+    visible share; calibration maxima spread 16x with 20x outliers make the smoothing factors far from 1. A fold left
+    out (the V rows' 1 / s1, rs without 1 / s3, c or d) moves a GEMM by 50% or more, the rounding by under 5%."""
+    from xtagger_amd import blob
+    r = np.random.default_rng(4)
+    m = blob.synth_model(seed=7, nt=8, nl=1)
+    L = dict(m["layers"][0])
+    L["mlnb"] = L["mlnb"] * np.float32(50.0)
+    c = blob.synth_calib(m, seed=2, spread=16.0)
+    (w1, b1, mats, w2, b2, rs, cn, dn), t = blob.wd_v3_layer(L, c["act"][0], c["h"][0], c["qkv"][0])
+    f = lambda a: np.asarray(a, np.float64)
+    dec = lambda q: blob._e4m3_values(q).astype(np.float64)
+    rel = lambda a, b: np.linalg.norm(a - b) / np.linalg.norm(b)
+    for q in mats:
+        assert q.dtype == np.uint8 and np.abs(dec(q)).max() == 448.0
+    D, HID, HP = 1024, 2730, 2736
+    xh = r.standard_normal((64, D))
+    y2 = (xh * f(L["ln1w"]) + f(L["ln1b"])) @ f(L["wqkv"]).T
+    y3 = (xh * f(w1) + f(b1)) @ (dec(mats[0]) * t[0]).T
+    assert rel(y3[:, :2 * D], y2[:, :2 * D]) < 0.05
+    o2 = y2[:, 2 * D:] @ f(L["wo"]).T
+    assert rel(y3[:, 2 * D:] @ (dec(mats[1]) * t[1]).T, o2) < 0.05
+    assert rel(y3[:, 2 * D:] @ f(L["wo"]).T, o2) > 0.5                  # V rows left unfolded
+    u2 = (xh * f(L["ln2w"]) + f(L["ln2b"])) @ f(L["w12"]).T
+    assert rel((xh * f(w2) + f(b2)) @ (dec(mats[2]) * t[2]).T, u2) < 0.05
+    g = np.zeros((64, HP))
+    g[:, :HID] = r.standard_normal((64, HID)) * np.abs(r.standard_normal(HID)) + 1.0
+    mu = g[:, :HID].mean(1, keepdims=True)
+    rstd = 1 / np.sqrt(g[:, :HID].var(1, keepdims=True) + 1e-6)
+    gn = np.zeros_like(g)
+    gn[:, :HID] = (g[:, :HID] - mu) * rstd
+    p2 = (gn * f(L["mlnw"]) + f(L["mlnb"])) @ f(L["w2"]).T
+    W = dec(mats[3]) * (np.float64(t[3]) * t[7])
+    assert rel(rstd * ((g * f(rs)) @ W.T - mu * f(cn)) + f(dn), p2) < 0.05
+    assert rel(rstd * ((g / t[7]) @ W.T - mu * f(cn)) + f(dn), p2) > 0.5   # rs without 1 / s3
+    assert rel(rstd * ((g * f(rs)) @ W.T) + f(dn), p2) > 0.5               # c left out
+    assert rel(rstd * ((g * f(rs)) @ W.T - mu * f(cn)), p2) > 0.5          # d left out
+
+
 def _fake_px_model(nt, fill=0.0):
     """Constant tensors of the v2 shapes (cheap: broadcast views)."""
     f16, f32 = np.float16, np.float32

@@ -176,53 +176,62 @@ def _fp8_tensor(w):
     return _e4m3_codes(np.clip(w / f32(sc), -448.0, 448.0)), f32(sc)
 
 
-def write_v3(path, m, calib, alpha=0.5, headroom=1.25):
-    """Write model tensors m (synth_model layout) as an eva02.bin v3 file: the reference's calibrated export
-    (export_eva.py:96-153) restated on the v2 tensors and the calibration maxima calib (synth_calib's layout).
-    Per block, SmoothQuant factors s = clip(amax_act^alpha / amax_wcol^(1 - alpha), 1e-3, 1e3) (52-58) are folded into
-    the producers (LN1 gamma / beta, the Wv rows, LN2 gamma / beta) and the weight columns; the MLP LayerNorm is folded
-    into fc2 (W~ = W2 diag(gamma) with the h smoothing in its columns, c = W~ 1 from the E4M3 W~, d = W2 beta); every
-    block weight becomes E4M3 with one scale amax / 448 (64-66); the [24][12] table leads the blob with the weight and
-    activation dequantization scales (max * headroom / 448) and q, k, v's; rs = 1 / (adq_h s~)."""
+def wd_v3_layer(L, act, h, qkv, alpha=0.5, headroom=1.25):
+    """One block of the calibrated export (export_eva.py:96-153) on the v2 tensors L (synth_model's layer layout) and
+    the block's calibration maxima (act [3][1024]: LN1 out, attention out, LN2 out; h [2736]: the SwiGLU output; qkv
+    [3][1024]: the rotated q, k and v). Returns (w1, b1, [E4M3 Wqkv, Wo, W12, W~2], w2, b2, rs, c, d) and the block's
+    table row: SmoothQuant factors s = clip(amax_act^alpha / amax_wcol^(1 - alpha), 1e-3, 1e3) (52-58) folded into the
+    producers (LN1 gamma / beta, the Wv rows, LN2 gamma / beta) and the weight columns; the MLP LayerNorm folded into
+    fc2 (W~ = W2 diag(gamma) with the h smoothing in its columns, c = W~ 1 from the E4M3 W~, d = W2 beta); every block
+    weight E4M3 with one scale amax / 448 (64-66); row = the four weight and four activation dequantization scales
+    (max * headroom / 448), then q, k, v's; rs = 1 / (adq_h s~)."""
     f32 = np.float32
     smooth = lambda a, w: _smooth(a, w, alpha)
-    fp8 = _fp8_tensor
+    row = np.zeros(12, f32)
+    w1, b1 = L["ln1w"].astype(f32).copy(), L["ln1b"].astype(f32).copy()
+    wqkv = L["wqkv"].astype(f32)
+    wo = L["wo"].astype(f32)
+    w2, b2 = L["ln2w"].astype(f32).copy(), L["ln2b"].astype(f32).copy()
+    w12 = L["w12"].astype(f32)
+    mwp, mbp = L["mlnw"].astype(f32), L["mlnb"].astype(f32)
+    wf2 = L["w2"].astype(f32)
+    dn = wf2 @ mbp
+    wf2 = wf2 * mwp[None, :]
+    a = [act[0], act[1], act[2], h]
+    s = [smooth(a[0], wqkv), smooth(a[1], wo), smooth(a[2], w12), smooth(a[3], wf2)]
+    w1 /= s[0]
+    b1 /= s[0]
+    wqkv *= s[0]
+    wqkv[2 * D:] /= s[1][:, None]
+    wo *= s[1]
+    w2 /= s[2]
+    b2 /= s[2]
+    w12 *= s[2]
+    wf2 *= s[3]
+    mats = []
+    for k, w in enumerate((wqkv, wo, w12, wf2)):
+        q, row[k] = _fp8_tensor(w)
+        mats.append(q)
+        row[4 + k] = f32(float((a[k] / s[k]).max()) * headroom / 448.0)
+    row[8] = f32(float(qkv[0].max()) * headroom / 448.0)
+    row[9] = f32(float(qkv[1].max()) * headroom / 448.0)
+    row[10] = f32(float((qkv[2] / s[1]).max()) * headroom / 448.0)
+    rs = (f32(1.0) / row[7]) / s[3]
+    c = (_e4m3_values(mats[3]) * row[3] / s[3]).sum(1).astype(f32)
+    return (w1, b1, mats, w2, b2, rs, c, dn.astype(f32)), row
+
+
+def write_v3(path, m, calib, alpha=0.5, headroom=1.25):
+    """Write model tensors m (synth_model layout) as an eva02.bin v3 file: the reference's calibrated export
+    (export_eva.py:96-153) restated on the v2 tensors and the calibration maxima calib (synth_calib's layout), one
+    block at a time by wd_v3_layer; the [24][12] table of the blocks' rows leads the blob."""
     nl = len(m["layers"])
     assert nl == NL, "the blob always holds 24 layers"
-    table = np.zeros((nl, 12), f32)
+    table = np.zeros((nl, 12), np.float32)
     layers = []
     for i, L in enumerate(m["layers"]):
-        w1, b1 = L["ln1w"].astype(f32).copy(), L["ln1b"].astype(f32).copy()
-        wqkv = L["wqkv"].astype(f32)
-        wo = L["wo"].astype(f32)
-        w2, b2 = L["ln2w"].astype(f32).copy(), L["ln2b"].astype(f32).copy()
-        w12 = L["w12"].astype(f32)
-        mwp, mbp = L["mlnw"].astype(f32), L["mlnb"].astype(f32)
-        wf2 = L["w2"].astype(f32)
-        dn = wf2 @ mbp
-        wf2 = wf2 * mwp[None, :]
-        a = [calib["act"][i, 0], calib["act"][i, 1], calib["act"][i, 2], calib["h"][i]]
-        s = [smooth(a[0], wqkv), smooth(a[1], wo), smooth(a[2], w12), smooth(a[3], wf2)]
-        w1 /= s[0]
-        b1 /= s[0]
-        wqkv *= s[0]
-        wqkv[2 * D:] /= s[1][:, None]
-        wo *= s[1]
-        w2 /= s[2]
-        b2 /= s[2]
-        w12 *= s[2]
-        wf2 *= s[3]
-        mats = []
-        for k, w in enumerate((wqkv, wo, w12, wf2)):
-            q, table[i, k] = fp8(w)
-            mats.append(q)
-            table[i, 4 + k] = f32(float((a[k] / s[k]).max()) * headroom / 448.0)
-        table[i, 8] = f32(float(calib["qkv"][i, 0].max()) * headroom / 448.0)
-        table[i, 9] = f32(float(calib["qkv"][i, 1].max()) * headroom / 448.0)
-        table[i, 10] = f32(float((calib["qkv"][i, 2] / s[1]).max()) * headroom / 448.0)
-        rs = (f32(1.0) / table[i, 7]) / s[3]
-        c = (_e4m3_values(mats[3]) * table[i, 3] / s[3]).sum(1).astype(f32)
-        layers.append((w1, b1, mats, w2, b2, rs, c, dn.astype(f32)))
+        ly, table[i] = wd_v3_layer(L, calib["act"][i], calib["h"][i], calib["qkv"][i], alpha, headroom)
+        layers.append(ly)
     b = _Blob()
     b.put("table", table, np.float32)
     b.put("pe", m["pe"], np.float16)
