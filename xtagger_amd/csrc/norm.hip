@@ -9,9 +9,9 @@
 #include "xt_common.h"
 
 // LayerNorm of one row held as v[16] (lane layout above), eps 1e-6 (the blocks; 1e-5 for the PixAI head), two-pass:
-// y = fma((x - mean) * rstd, gamma, beta), rstd = 1 / sqrt(var + eps) with IEEE sqrt and division.
-__device__ __forceinline__ void ln16(float *v, const float *__restrict__ g, const float *__restrict__ b, int lane,
-                                     float eps = XT_EPS)
+// y = fma((x - mean) * rstd, gamma, beta), rstd = 1 / sqrt(var + eps) with IEEE sqrt and division. gg / bb hold the
+// lane's 16 gamma / beta values in the same layout.
+__device__ __forceinline__ void ln16_gb(float *v, const float *gg, const float *bb, float eps = XT_EPS)
 {
     float s = 0.f;
 #pragma unroll
@@ -26,15 +26,27 @@ __device__ __forceinline__ void ln16(float *v, const float *__restrict__ g, cons
     const float var = wave_sum(q) * (1.0f / 1024.0f);
     const float rstd = 1.0f / __builtin_sqrtf(var + eps);
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const int e0 = 512 * h + 8 * lane;
-        const float4 g0 = *(const float4 *)(g + e0), g1 = *(const float4 *)(g + e0 + 4);
-        const float4 b0 = *(const float4 *)(b + e0), b1 = *(const float4 *)(b + e0 + 4);
-        const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    for (int j = 0; j < 16; j++) v[j] = __builtin_fmaf((v[j] - mean) * rstd, gg[j], bb[j]);
+}
+
+// the lane's 16 values of a 1024-float vector (gamma or beta) in the row layout
+__device__ __forceinline__ void load_vec16(const float *__restrict__ g, int lane, float *gg)
+{
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[8 * h + j] = __builtin_fmaf((v[8 * h + j] - mean) * rstd, gg[j], bb[j]);
+    for (int h = 0; h < 2; h++) {
+        const float4 g0 = *(const float4 *)(g + 512 * h + 8 * lane), g1 = *(const float4 *)(g + 512 * h + 8 * lane + 4);
+        gg[8 * h + 0] = g0.x; gg[8 * h + 1] = g0.y; gg[8 * h + 2] = g0.z; gg[8 * h + 3] = g0.w;
+        gg[8 * h + 4] = g1.x; gg[8 * h + 5] = g1.y; gg[8 * h + 6] = g1.z; gg[8 * h + 7] = g1.w;
     }
+}
+
+__device__ __forceinline__ void ln16(float *v, const float *__restrict__ g, const float *__restrict__ b, int lane,
+                                     float eps = XT_EPS)
+{
+    float gg[16], bb[16];
+    load_vec16(g, lane, gg);
+    load_vec16(b, lane, bb);
+    ln16_gb(v, gg, bb, eps);
 }
 
 // v[16] -> E4M3 bytes of the row at q (row-major, 1024 bytes) and its 8 scales at s[kb * lds + row]
@@ -57,12 +69,17 @@ __device__ __forceinline__ void quant_row16(const float *v, uint8_t *__restrict_
     }
 }
 
-__device__ __forceinline__ void load_row16_f16(const uint16_t *__restrict__ x, int lane, float *v)
+// the lane's 2 x 16 bytes of a 1024-half row, and their conversion to v[16]
+__device__ __forceinline__ void load_raw16(const uint16_t *__restrict__ x, int lane, uint4 (&u)[2])
+{
+    u[0] = *(const uint4 *)(x + 8 * lane);
+    u[1] = *(const uint4 *)(x + 512 + 8 * lane);
+}
+__device__ __forceinline__ void unpack16_f16(const uint4 (&u)[2], float *v)
 {
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        const uint4 u = *(const uint4 *)(x + 512 * h + 8 * lane);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+        const uint32_t w[4] = {u[h].x, u[h].y, u[h].z, u[h].w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             v[8 * h + 2 * i] = h2f((uint16_t)(w[i] & 0xffffu));
@@ -70,18 +87,44 @@ __device__ __forceinline__ void load_row16_f16(const uint16_t *__restrict__ x, i
         }
     }
 }
-
-// k_ln: x fp16 [rows][1024] -> q E4M3 [rows][1024] + s [8][lds]. 4 rows per 256-thread block.
-__global__ void __launch_bounds__(256) k_ln(const uint16_t *__restrict__ x, const float *__restrict__ g,
-                                            const float *__restrict__ b, uint8_t *__restrict__ q,
-                                            float *__restrict__ s, int rows, int lds)
+__device__ __forceinline__ void load_row16_f16(const uint16_t *__restrict__ x, int lane, float *v)
 {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    uint4 u[2];
+    load_raw16(x, lane, u);
+    unpack16_f16(u, v);
+}
+
+// k_ln: x fp16 [rows][1024] -> q E4M3 [rows][1024] + s [8][lds]. The grid is as many 256-thread blocks as stay
+// resident at once (LN_WAVES_PER_SIMD waves per SIMD on every CU, or fewer blocks for short inputs); wave w of its W
+// waves takes rows w, w + W, w + 2W, ..., so the waves in flight work on W consecutive rows at a time. A wave loads
+// gamma and beta once and holds them in registers (re-reading them per row took 12% of the kernel's time), and
+// issues the next row's 2 KB load before it normalises the current row.
+#define LN_WAVES_PER_SIMD 6
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LN_WAVES_PER_SIMD, 8)))
+k_ln(const uint16_t *__restrict__ x, const float *__restrict__ g, const float *__restrict__ b, uint8_t *__restrict__ q,
+     float *__restrict__ s, int rows, int lds)
+{
+    const int lane = threadIdx.x & 63, W = (int)gridDim.x * 4;
+    int row = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
-    float v[16];
-    load_row16_f16(x + (size_t)row * XT_D, lane, v);
-    ln16(v, g, b, lane);
-    quant_row16(v, q + (size_t)row * XT_D, s, lds, row, lane);
+    uint4 cur[2];
+    load_raw16(x + (size_t)row * XT_D, lane, cur);
+    float gg[16], bb[16];
+    load_vec16(g, lane, gg);
+    load_vec16(b, lane, bb);
+    for (;;) {
+        const int nrow = row + W;  // rows < 2^19 and W < 2^20: no overflow
+        uint4 nxt[2];
+        if (nrow < rows) load_raw16(x + (size_t)nrow * XT_D, lane, nxt);
+        float v[16];
+        unpack16_f16(cur, v);
+        ln16_gb(v, gg, bb);
+        quant_row16(v, q + (size_t)row * XT_D, s, lds, row, lane);
+        if (nrow >= rows) break;
+        row = nrow;
+        cur[0] = nxt[0];
+        cur[1] = nxt[1];
+    }
 }
 
 // k_pool: mean over tokens 1..1024 of each image: x fp16 [nb * 1025][1024] -> p fp32 [nb][1024]. Grid (nb, 8) of
@@ -237,8 +280,19 @@ extern "C" int eva_k_ln(const void *x, const float *g, const float *b, void *q, 
     if (((uintptr_t)x | (uintptr_t)g | (uintptr_t)b | (uintptr_t)q) & 15)
         return xt_fail("eva_k_ln", "x, g, b, q must be 16-byte aligned");
     if (!rows) return 0;
-    hipLaunchKernelGGL(k_ln, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x, g, b,
-                       (uint8_t *)q, s, rows, lds);
+    if (rows > (1 << 19)) return xt_fail("eva_k_ln", "at most 2^19 rows");
+    static int cu_count[64];  // per device, read once (a benign race: every writer stores the same value)
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return xt_fail("eva_k_ln", "no current device");
+    int cus = cu_count[dev];
+    if (cus <= 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return xt_fail("eva_k_ln", "cannot read the device's CU count");
+        cu_count[dev] = cus;
+    }
+    const int need = (rows + 3) / 4, resident = cus * LN_WAVES_PER_SIMD;  // 4 SIMDs a CU, 4 waves a block
+    hipLaunchKernelGGL(k_ln, dim3(need < resident ? need : resident), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t *)x, g, b, (uint8_t *)q, s, rows, lds);
     return xt_check("eva_k_ln");
 }
 
