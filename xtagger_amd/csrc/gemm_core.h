@@ -72,11 +72,6 @@ struct BsCfg {
 // 16-byte chunk swizzle of the attention and patch-embedding tiles (chunk c of row r at c ^ (r & 7))
 __device__ __forceinline__ uint32_t swz(int row, int chunk) { return (uint32_t)(row * 128 + ((chunk ^ (row & 7)) << 4)); }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
-}
-
 // Raw buffer descriptor (base, stride 0, num_records = bytes, 32-bit dword format) in SGPRs.
 __device__ __forceinline__ v4i buf_desc(const void *p, uint32_t bytes)
 {

@@ -58,7 +58,7 @@ __device__ __forceinline__ void quant_row16(const float *v, uint8_t *__restrict_
         float amax = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; j++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[8 * h + j]));
-        amax = group_max<16>(amax);
+        amax = row16_absmax(amax);  // the 16 lanes of the block: one DPP row
         const float sc = block_scale(amax), inv = block_scale_inv(sc);
         const float *w = v + 8 * h;
         uint2 o;
@@ -107,15 +107,28 @@ k_ln(const uint16_t *__restrict__ x, const float *__restrict__ g, const float *_
     const int lane = threadIdx.x & 63, W = (int)gridDim.x * 4;
     int row = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
+    // rows are read through a descriptor that ends at row `rows`: the prefetch past the last row loads zeros and
+    // touches no memory, so it needs no branch (rows <= 2^19: every offset fits 32 bits)
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, (uint32_t)rows * (XT_D * 2u));
+    auto load = [&](int r, uint4 (&u)[2]) {
+        const uint32_t o = (uint32_t)r * (XT_D * 2u) + 16u * (uint32_t)lane;
+        u[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)o, 0, 0));
+        u[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(o + 1024u), 0, 0));
+    };
     uint4 cur[2];
-    load_raw16(x + (size_t)row * XT_D, lane, cur);
+    load(row, cur);
     float gg[16], bb[16];
     load_vec16(g, lane, gg);
     load_vec16(b, lane, bb);
+    // wait for gamma and beta here, once: left to the loop, the waits for them (taken as counts of the memory
+    // operations issued since) would stall every row on the next row's prefetch and this row's stores
+#pragma unroll
+    for (int j = 0; j < 16; j++) asm volatile("" : "+v"(gg[j]), "+v"(bb[j]));
     for (;;) {
         const int nrow = row + W;  // rows < 2^19 and W < 2^20: no overflow
         uint4 nxt[2];
-        if (nrow < rows) load_raw16(x + (size_t)nrow * XT_D, lane, nxt);
+        load(nrow < rows ? nrow : rows, nxt);
+        __builtin_amdgcn_sched_barrier(0);  // the prefetch goes out before this row's work, not sunk into it
         float v[16];
         unpack16_f16(cur, v);
         ln16_gb(v, gg, bb);

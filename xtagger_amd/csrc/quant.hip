@@ -47,7 +47,7 @@ __global__ void __launch_bounds__(256) k_quant_act(const TIn *__restrict__ x, in
         load8<TIn>(x + (size_t)row * ldx + ch * 8, v);
 #pragma unroll
         for (int i = 0; i < 8; i++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
-        amax = group_max<16>(amax);
+        amax = row16_absmax(amax);  // the 16 lanes of the block: one DPP row, all active together
         const float sc = block_scale(amax), inv = block_scale_inv(sc);
         uint2 o;
         o.x = e4_pack4_scaled(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);

@@ -89,11 +89,37 @@ __device__ __forceinline__ uint16_t f2h(float x)
 }
 __device__ __forceinline__ float h2f(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
 
+// Raw buffer resource (base, stride 0, num_records = bytes): loads past `bytes` return zero and touch no memory,
+// stores past it are dropped
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // ---- wave64 reductions (xor butterfly: every lane ends with the same value) ----
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v);
+// Sum over the 64 lanes (all active) by the xor butterfly d = 32, 16, 8, 4, 2, 1: at each step lane i adds the
+// partial of lane i ^ d. The exchanges are register moves, not LDS round trips: the permlane32 / permlane16 swaps
+// hand lane i the value of lane i ^ 32 / i ^ 16, a row rotation by 8 that of i ^ 8, and a row rotation by 4 that of
+// lane i - 4 (mod 16), which after the first three steps holds what lane i ^ 4 holds (a partial then depends on the
+// lane index mod 8 only); quad permutations do 2 and 1. The same pairs meet at every step as in a shuffle butterfly,
+// so the total is the same bit for bit.
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    const int lane = __lane_id();
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v += __uint_as_float(lane < 32 ? r[1] : r[0]);
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v += __uint_as_float((lane & 16) ? r[0] : r[1]);
+    }
+    v += dpp_f<0x128>(v);  // row_ror:8
+    v += dpp_f<0x124>(v);  // row_ror:4
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
     return v;
 }
 __device__ __forceinline__ float wave_max(float v)
