@@ -280,6 +280,7 @@ static int ev_up(eva *e)
     const uint32_t ntp = (e->nt0 + 7) & ~7u, nt = e->nt;
 
     XT_HIP(hipSetDevice(E->devno));
+    if (xt_cu_count() <= 0) return xt_fail("eva_open", "cannot read the device's CU count");  // cached before any capture
     XT_HIP(hipStreamCreateWithFlags(&E->st, hipStreamNonBlocking));
     EV_ALLOC(E, E->blob, E->wbytes, false);
     if (ev_layout(E, ntp)) return -1;

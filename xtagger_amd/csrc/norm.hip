@@ -285,6 +285,19 @@ __global__ void __launch_bounds__(256) k_px_hln(const uint16_t *__restrict__ x, 
     }
 }
 
+int xt_cu_count()
+{
+    static int cu_count[64];  // per device (a benign race: every writer stores the same value)
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int cus = cu_count[dev];
+    if (cus <= 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+        cu_count[dev] = cus;
+    }
+    return cus;
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 extern "C" int eva_k_ln(const void *x, const float *g, const float *b, void *q, float *s, int rows, int lds,
                         void *stream)
@@ -294,15 +307,8 @@ extern "C" int eva_k_ln(const void *x, const float *g, const float *b, void *q, 
         return xt_fail("eva_k_ln", "x, g, b, q must be 16-byte aligned");
     if (!rows) return 0;
     if (rows > (1 << 19)) return xt_fail("eva_k_ln", "at most 2^19 rows");
-    static int cu_count[64];  // per device, read once (a benign race: every writer stores the same value)
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return xt_fail("eva_k_ln", "no current device");
-    int cus = cu_count[dev];
-    if (cus <= 0) {
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            return xt_fail("eva_k_ln", "cannot read the device's CU count");
-        cu_count[dev] = cus;
-    }
+    const int cus = xt_cu_count();
+    if (cus <= 0) return xt_fail("eva_k_ln", "cannot read the device's CU count");
     const int need = (rows + 3) / 4, resident = cus * LN_WAVES_PER_SIMD;  // 4 SIMDs a CU, 4 waves a block
     hipLaunchKernelGGL(k_ln, dim3(need < resident ? need : resident), dim3(256), 0, (hipStream_t)stream,
                        (const uint16_t *)x, g, b, (uint8_t *)q, s, rows, lds);

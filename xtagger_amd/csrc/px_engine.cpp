@@ -220,6 +220,7 @@ static int px_up(px *p)
     px_impl *E = p->impl;
 
     XT_HIP(hipSetDevice(E->devno));
+    if (xt_cu_count() <= 0) return xt_fail("px_open", "cannot read the device's CU count");  // cached before any capture
     XT_HIP(hipStreamCreateWithFlags(&E->st, hipStreamNonBlocking));
     PX_ALLOC(E, E->blob, E->wbytes, false);
     if (px_layout(E, p->ntp)) return -1;

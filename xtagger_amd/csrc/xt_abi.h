@@ -26,3 +26,8 @@ static inline int xt_check(const char *what) { return xt_hip(hipGetLastError(), 
     do {                                             \
         if (xt_hip((call), #call)) return -1;        \
     } while (0)
+
+// Compute units of the current device, read once per device and cached (0 if it cannot be read). Launchers that size
+// a grid to what stays resident use it; the engines call it before their graph capture, so that no device query runs
+// while a stream is being captured.
+__attribute__((visibility("hidden"))) int xt_cu_count();
