@@ -91,8 +91,10 @@ def _packed_w(orc, N, K, seed, std=0.02):
 
 
 # ---------------------------------------------------------------- LayerNorm / pool / final LN: bit-exact
-@pytest.mark.parametrize("M", [1025, 37, 1])
+@pytest.mark.parametrize("M", [1025, 37, 1, 6145, 14000])
 def test_ln_bitexact(dev, xt, orc, M):
+    """k_ln against the oracle, bytes and scales. Above 4 x 6 x (CUs) rows the resident grid's waves take several rows
+    each (M = 6145: one wave a second row on a 256-CU part; 14000: two or three rows a wave)."""
     _say(f"k_ln M={M}")
     r = np.random.default_rng(M)
     x = (r.standard_normal((M, D)) * 2 + 0.3).astype(np.float16)
