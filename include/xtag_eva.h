@@ -129,7 +129,8 @@ int eva_k_gemm(const void *qa, int lda, const float *sa, int lds, const void *qw
                void *c, int ldc, int out_kind, void *stream);
 
 /* LayerNorm -> E4M3 (kern_common.cuh:147-186 k_ln): x fp16 [rows][1024] -> q [rows][1024], s [8][lds];
- * eps 1e-6, two-pass mean / variance, y = fma((x - mean) * rstd, gamma, beta). */
+ * eps 1e-6, two-pass mean / variance, y = fma((x - mean) * rstd, gamma, beta). rows <= 2^19, lds >= rows; x, g, b
+ * and q 16-byte aligned. */
 int eva_k_ln(const void *x, const float *g, const float *b, void *q, float *s, int rows, int lds, void *stream);
 /* QKV projection with the attention layouts as its epilogue (eva_kernels.cu:41-114 k_qkv): rows = nb * 1025;
  * w from eva_k_prep_w(perm 1); cs [1024][32][2] RoPE (cos, sin) of patch tokens; q, k bf16 [nb][16][1088][64],
