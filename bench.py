@@ -217,6 +217,38 @@ def time_calls(torch, fn, calls=50, repeats=5):
     return time_median(torch, g, calls, repeats)[0]
 
 
+def bench_step_two_lanes(torch, L, M, steps, repeats=5):
+    """The layer step's four GEMMs at M rows run as the engines run a batch: two halves of M / 2 rows on two streams,
+    each half's qkv, oproj, fc1 and fc2 in order. Each lane's `steps` steps are one HIP graph; both graphs are
+    replayed at once between HIP events on the current stream (which both lanes wait for and join), `repeats` times.
+    Returns the median ms per step of the whole M."""
+    lanes = [LayerStep(torch, L, M // 2, seed=1 + i) for i in range(2)]
+    for ls in lanes:
+        ls.step()
+    torch.cuda.synchronize()
+    graphs = [capture(torch, ls.step, steps) for ls in lanes]
+    streams = [torch.cuda.Stream() for _ in lanes]
+    main = torch.cuda.current_stream()
+    times = []
+    for _ in range(repeats + 1):  # the first round warms the replays up and is not kept
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(main)
+        for g, s in zip(graphs, streams):
+            s.wait_stream(main)
+            with torch.cuda.stream(s):
+                g.replay()
+        for s in streams:
+            main.wait_stream(s)
+        e1.record(main)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / steps)
+    del graphs, lanes
+    torch.cuda.synchronize()
+    times = times[1:]
+    return sorted(times)[len(times) // 2]
+
+
 def time_engine(torch, eng, runs=3, repeats=5):
     """Median ms per forward of an engine (Engine / PxEngine): `runs` back-to-back eva_run / px_run graph replays
     between HIP events recorded on the engine's own stream, `repeats` times."""
@@ -779,6 +811,7 @@ def main():
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP8, 4), "traffic": traffic_from_profiles(),
             "algorithmic_flops_per_launch": fl["fc1"]}
 
+    ms2 = bench_step_two_lanes(torch, L, M, args.steps)
     qkv1, qkv1_ms = bench_qkv_m1025(torch, L)
     _note("layer step, per-kernel and config-1 lines done")
     peaks = measured_peaks(torch, L)
@@ -792,6 +825,9 @@ def main():
                                   "s = amax/448, promoted per 128-wide K block in fp32",
                       "M": M, "gflop_per_step": round(step_flops / 1e9, 2)},
            "pct_fp8_peak": round(100 * tflops / PEAK_FP8, 2), "per_kernel": per,
+           # the same 206.33 GFLOP scheduled as the engines run a batch: two lanes of M/2 rows, each lane in order
+           "layer_step_two_lanes": {"tflops": round(step_flops / (ms2 * 1e-3) / 1e12, 1), "ms_per_step": round(ms2, 4),
+                                    "lanes": "2 x M=%d on two streams, each lane's qkv, oproj, fc1, fc2 in order" % (M // 2)},
            # config 1 sits at the ridge (613 flop/B against 625): both bounds, at the spec peaks
            "qkv_gemm_m1025": {"tflops": round(qkv1, 1), "us": round(qkv1_ms * 1e3, 2),
                               "frac_fp8_peak": round(qkv1 / 5000.0, 3),
