@@ -243,9 +243,12 @@ __device__ __forceinline__ void bs_step(const uint8_t *st, int wm0, int wn0, v4f
 // keeps the written order (it still allocates registers and places the LDS waits):
 //  - A 0 and B 0 are read first, then the scales, then A 1-3 and B 1: the first MFMA waits for four reads only;
 //  - B fragment j + 2 is read right after MFMA (j, 0), into the slot B fragment j - 1 has left (3-slot ring);
-//  - the promotion of MFMA t - 3 follows MFMA t. In steady state 15 instructions separate an MFMA from the first
-//    VALU read of its result, and 12 after the step's last MFMA (gfx950 asks 12 wait states of this MFMA's result
-//    before a VALU read: hipcc puts s_nop 11 there); the first promotion of a step is preceded by s_nop 7;
+//  - the promotion of MFMA t - 3 follows MFMA t (15 instructions separate an MFMA from the first VALU read of its
+//    result; gfx950 asks 12 wait states); the promotion of MFMA 0 is preceded by s_nop 7. The step's last three
+//    MFMAs are promoted at the start of the next step (pr and scp carry their results and scales), between the
+//    first fragment reads and the first MFMA, where the wave would otherwise wait for the reads; the K loop
+//    promotes the last step's three after it (bs_step_fixed_flush). Each accumulator still takes its K blocks in
+//    order, so the sums are those of promoting at the end of each step, bit for bit;
 //  - the LPS loads of K step dkb (dkb < 0: none) go out one per MFMA from MFMA 1 on, not in a burst that would stall
 //    this wave's issue behind the vector-memory queue.
 __device__ __forceinline__ void mfma_asm(v4f &p, const v8i &a, const v8i &b)
@@ -257,9 +260,27 @@ __device__ __forceinline__ void fmac_asm(float &acc, float p, float s)
     asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(acc) : "v"(p), "v"(s) : "memory");
 }
 
+// Promotion of a step's MFMAs 29-31 (row tiles 1-3 of column tile 7, ring slots 1-3) with that step's scales scp
+template <class C>
+__device__ __forceinline__ void bs_step_fixed_flush(v4f (&acc)[C::TM][C::TN], const v4f (&pr)[4],
+                                                    const float (&scp)[3][4])
+{
+#pragma unroll
+    for (int q = 0; q < 3; q++) {
+        const v4f p = pr[1 + q];
+        float x0 = acc[1 + q][7][0], x1 = acc[1 + q][7][1], x2 = acc[1 + q][7][2], x3 = acc[1 + q][7][3];
+        fmac_asm(x0, p[0], scp[q][0]);
+        fmac_asm(x1, p[1], scp[q][1]);
+        fmac_asm(x2, p[2], scp[q][2]);
+        fmac_asm(x3, p[3], scp[q][3]);
+        acc[1 + q][7] = v4f{x0, x1, x2, x3};
+    }
+}
+
 template <class C>
 __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn0, v4f (&acc)[C::TM][C::TN],
-                                              const BsOperands<C> &op, uint32_t dstage, int dkb)
+                                              const BsOperands<C> &op, uint32_t dstage, int dkb, v4f (&pr)[4],
+                                              float (&scp)[3][4], bool carry)
 {
     static_assert(C::TM == 4 && C::TN == 8 && C::LPS < 32, "schedule written for 64 x 128 wave tiles");
     constexpr int LAG = 3;
@@ -270,6 +291,7 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
     b[0] = ld_frag(tb, wn0);
     a[0] = ld_frag(ta, wm0);
     asm volatile("" ::: "memory");  // the first MFMA waits for these four reads only
+    if (carry) bs_step_fixed_flush<C>(acc, pr, scp);  // the previous step's MFMAs 29-31, while the reads land
     const float swv = *(const float *)(st + C::A_BYTES + C::B_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
     float4 s4[4];
 #pragma unroll
@@ -285,27 +307,28 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
     for (int i = 0; i < 4; i++) {
         sc[i][0] = s4[i].x * swv; sc[i][1] = s4[i].y * swv; sc[i][2] = s4[i].z * swv; sc[i][3] = s4[i].w * swv;
     }
-    v4f pr[LAG + 1];
 #pragma unroll
-    for (int t = 0; t < 32 + LAG; t++) {
-        if (t < 32) {
-            const int j = t >> 2, i = t & 3;
-            mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
-            if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
-            if (t >= 1 && t <= C::LPS && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
-        }
+    for (int t = 0; t < 32; t++) {
+        const int j = t >> 2, i = t & 3;
+        mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
+        if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
+        if (t >= 1 && t <= C::LPS && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
         if (t == LAG) asm volatile("s_nop 7" ::: "memory");
         if (t >= LAG) {
-            const int u = t - LAG, j = u >> 2, i = u & 3;
+            const int u = t - LAG, ju = u >> 2, iu = u & 3;
             const v4f p = pr[u % (LAG + 1)];
-            float x0 = acc[i][j][0], x1 = acc[i][j][1], x2 = acc[i][j][2], x3 = acc[i][j][3];
-            fmac_asm(x0, p[0], sc[i][0]);
-            fmac_asm(x1, p[1], sc[i][1]);
-            fmac_asm(x2, p[2], sc[i][2]);
-            fmac_asm(x3, p[3], sc[i][3]);
-            acc[i][j] = v4f{x0, x1, x2, x3};
+            float x0 = acc[iu][ju][0], x1 = acc[iu][ju][1], x2 = acc[iu][ju][2], x3 = acc[iu][ju][3];
+            fmac_asm(x0, p[0], sc[iu][0]);
+            fmac_asm(x1, p[1], sc[iu][1]);
+            fmac_asm(x2, p[2], sc[iu][2]);
+            fmac_asm(x3, p[3], sc[iu][3]);
+            acc[iu][ju] = v4f{x0, x1, x2, x3};
         }
     }
+#pragma unroll
+    for (int q = 0; q < 3; q++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) scp[q][r] = sc[1 + q][r];  // MFMAs 29-31: row tiles 1-3 of column tile 7
 }
 
 // The K step of a wave of a partial last row tile whose rows below M fill only its first TMV < 4 row tiles of 16:
@@ -423,9 +446,17 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
         }
     };
     if constexpr (C::TM == 4 && C::TN == 8) {
-        if (live > 32)
-            kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_fixed<C>(st, wm0, wn0, acc, op, dst, dkb); });
-        else if (live > 16)
+        if (live > 32) {
+            v4f pr[4];          // the MFMA result ring, and the scales of the last step's MFMAs 29-31 (their
+            float scp[3][4];    // promotions run at the start of the next step)
+            int kbi = 0;
+            kloop([&](const uint8_t *st, uint32_t dst, int dkb) {
+                bs_step_fixed<C>(st, wm0, wn0, acc, op, dst, dkb, pr, scp, kbi > 0);
+                kbi++;
+            });
+            asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // 12+ wait states after the last MFMA
+            bs_step_fixed_flush<C>(acc, pr, scp);
+        } else if (live > 16)
             kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_rows<C, 2>(st, wm0, wn0, acc, op, dst, dkb); });
         else if (live > 0)
             kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_rows<C, 1>(st, wm0, wn0, acc, op, dst, dkb); });
