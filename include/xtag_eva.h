@@ -318,7 +318,7 @@ int px_k_fc2(const void *m8, const float *ms, int lds, const void *w, const floa
              int rows, void *stream);
 /* Attention-pool head (px_kernels.cu:341-503; px.h:170-189), T = 5184 tokens per image, rows = nb * T:
  * px_k_hln = k_phln + k_phscore: y fp16 [rows][1024] = f16(LN_1e-5(x) g + b + hpos[m % T]) (hpos fp16 [T][1024]),
- * s fp32 [rows][16] = U y (U fp32 [16][1024], exp2 domain). */
+ * s fp32 [rows][16] = U y (U fp32 [16][1024], exp2 domain). rows and T at most 2^20. */
 int px_k_hln(const void *x, const float *g, const float *b, const void *hpos, int T, const float *U, void *y, float *s,
              int rows, void *stream);
 /* k_phsoft + k_phpool + k_phv (px_kernels.cu:401-503) as three launches, T % 576 == 0 and T <= 9216:

@@ -246,13 +246,34 @@ __global__ void __launch_bounds__(256) k_px_hln(const uint16_t *__restrict__ x, 
     for (int i = threadIdx.x; i < 16 * XT_D / 4; i += 256) ((float4 *)su)[i] = ((const float4 *)U)[i];
     __syncthreads();
     const int lane = threadIdx.x & 63, r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * PX_HLN_ROWS;
+    if (r0 >= rows) return;
+    // gamma and beta in registers, waited for once; each row's x and position rows are loaded while the row before
+    // is worked on, through descriptors that end at row `rows` of x and row T of hpos (past them: zeros, no traffic)
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, (uint32_t)rows * (XT_D * 2u)), rh = buf_rsrc(hpos, (uint32_t)T * (XT_D * 2u));
+    auto load = [&](__amdgpu_buffer_rsrc_t rsrc, int r, uint4 (&u)[2]) {
+        const uint32_t o = (uint32_t)r * (XT_D * 2u) + 16u * (uint32_t)lane;
+        u[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)o, 0, 0));
+        u[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(o + 1024u), 0, 0));
+    };
+    uint4 cx[2], ch[2];
+    load(rx, r0, cx);
+    load(rh, r0 % T, ch);
+    float gg[16], bb[16];
+    load_vec16(g, lane, gg);
+    load_vec16(b, lane, bb);
+#pragma unroll
+    for (int j = 0; j < 16; j++) asm volatile("" : "+v"(gg[j]), "+v"(bb[j]));
     for (int rr = 0; rr < PX_HLN_ROWS; rr++) {
         const int row = r0 + rr;
-        if (row >= rows) break;
+        const bool more = rr + 1 < PX_HLN_ROWS && row + 1 < rows;
+        uint4 nx[2], nh[2];
+        load(rx, more ? row + 1 : rows, nx);
+        load(rh, more ? (row + 1) % T : T, nh);
+        __builtin_amdgcn_sched_barrier(0);  // the prefetch goes out before this row's work
         float v[16], hp[16];
-        load_row16_f16(x + (size_t)row * XT_D, lane, v);
-        load_row16_f16(hpos + (size_t)(row % T) * XT_D, lane, hp);
-        ln16(v, g, b, lane, 1e-5f);
+        unpack16_f16(cx, v);
+        unpack16_f16(ch, hp);
+        ln16_gb(v, gg, bb, 1e-5f);
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             uint32_t w[4];
@@ -282,6 +303,11 @@ __global__ void __launch_bounds__(256) k_px_hln(const uint16_t *__restrict__ x, 
             mine = lane == hd ? a : mine;
         }
         if (lane < 16) s[(size_t)row * 16 + lane] = mine;
+        if (!more) break;
+        cx[0] = nx[0];
+        cx[1] = nx[1];
+        ch[0] = nh[0];
+        ch[1] = nh[1];
     }
 }
 
@@ -336,7 +362,8 @@ extern "C" int eva_k_lnh(const float *p, const float *g, const float *b, void *p
 extern "C" int px_k_hln(const void *x, const float *g, const float *b, const void *hpos, int T, const float *U, void *y,
                         float *s, int rows, void *stream)
 {
-    if (rows <= 0 || T <= 0) return xt_fail("px_k_hln", "bad shape (rows > 0, T > 0)");
+    if (rows <= 0 || T <= 0 || rows > (1 << 20) || T > (1 << 20))
+        return xt_fail("px_k_hln", "bad shape (0 < rows, T <= 2^20)");
     if (((uintptr_t)x | (uintptr_t)g | (uintptr_t)b | (uintptr_t)hpos | (uintptr_t)U | (uintptr_t)y) & 15)
         return xt_fail("px_k_hln", "x, g, b, hpos, U, y must be 16-byte aligned");
     const int per = 4 * PX_HLN_ROWS;
