@@ -238,7 +238,8 @@ __device__ __forceinline__ void bs_step(const uint8_t *st, int wm0, int wn0, v4f
     }
 }
 
-// The same K step for 64 x 128 wave tiles (TM = 4, TN = 8) in a fixed issue order. The matrix-core instructions and
+// The same K step for 64 x 128 and 64 x 64 wave tiles (TM = 4, TN = 8 or 4) in a fixed issue order (for 64 x 64, the
+// single GEMM's 128 x 128 tiles, 12% faster than bs_step at M = 1025). The matrix-core instructions and
 // the promotion fmas are single-instruction asm statements, and every LDS read sits between them, so the compiler
 // keeps the written order (it still allocates registers and places the LDS waits):
 //  - A 0 and B 0 are read first, then the scales, then A 1-3 and B 1: the first MFMA waits for four reads only;
@@ -260,20 +261,22 @@ __device__ __forceinline__ void fmac_asm(float &acc, float p, float s)
     asm volatile("v_fmac_f32 %0, %1, %2" : "+v"(acc) : "v"(p), "v"(s) : "memory");
 }
 
-// Promotion of a step's MFMAs 29-31 (row tiles 1-3 of column tile 7, ring slots 1-3) with that step's scales scp
+// Promotion of a step's last three MFMAs (row tiles 1-3 of the last column tile, ring slots 1-3) with that step's
+// scales scp
 template <class C>
 __device__ __forceinline__ void bs_step_fixed_flush(v4f (&acc)[C::TM][C::TN], const v4f (&pr)[4],
                                                     const float (&scp)[3][4])
 {
+    constexpr int J = C::TN - 1;
 #pragma unroll
     for (int q = 0; q < 3; q++) {
         const v4f p = pr[1 + q];
-        float x0 = acc[1 + q][7][0], x1 = acc[1 + q][7][1], x2 = acc[1 + q][7][2], x3 = acc[1 + q][7][3];
+        float x0 = acc[1 + q][J][0], x1 = acc[1 + q][J][1], x2 = acc[1 + q][J][2], x3 = acc[1 + q][J][3];
         fmac_asm(x0, p[0], scp[q][0]);
         fmac_asm(x1, p[1], scp[q][1]);
         fmac_asm(x2, p[2], scp[q][2]);
         fmac_asm(x3, p[3], scp[q][3]);
-        acc[1 + q][7] = v4f{x0, x1, x2, x3};
+        acc[1 + q][J] = v4f{x0, x1, x2, x3};
     }
 }
 
@@ -282,8 +285,9 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
                                               const BsOperands<C> &op, uint32_t dstage, int dkb, v4f (&pr)[4],
                                               float (&scp)[3][4], bool carry)
 {
-    static_assert(C::TM == 4 && C::TN == 8 && C::LPS < 32, "schedule written for 64 x 128 wave tiles");
-    constexpr int LAG = 3;
+    static_assert(C::TM == 4 && (C::TN == 8 || C::TN == 4) && C::LPS < 4 * C::TN,
+                  "schedule written for 64 x 128 and 64 x 64 wave tiles");
+    constexpr int LAG = 3, NM = 4 * C::TN;
     const int lane = threadIdx.x & 63, g = lane >> 4;
     const uint8_t *ta = st, *tb = st + C::A_BYTES;
     const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
@@ -291,7 +295,7 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
     b[0] = ld_frag(tb, wn0);
     a[0] = ld_frag(ta, wm0);
     asm volatile("" ::: "memory");  // the first MFMA waits for these four reads only
-    if (carry) bs_step_fixed_flush<C>(acc, pr, scp);  // the previous step's MFMAs 29-31, while the reads land
+    if (carry) bs_step_fixed_flush<C>(acc, pr, scp);  // the previous step's last three MFMAs, while the reads land
     const float swv = *(const float *)(st + C::A_BYTES + C::B_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
     float4 s4[4];
 #pragma unroll
@@ -308,10 +312,10 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
         sc[i][0] = s4[i].x * swv; sc[i][1] = s4[i].y * swv; sc[i][2] = s4[i].z * swv; sc[i][3] = s4[i].w * swv;
     }
 #pragma unroll
-    for (int t = 0; t < 32; t++) {
+    for (int t = 0; t < NM; t++) {
         const int j = t >> 2, i = t & 3;
         mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
-        if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
+        if (i == 0 && j + 2 < C::TN) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
         if (t >= 1 && t <= C::LPS && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
         if (t == LAG) asm volatile("s_nop 7" ::: "memory");
         if (t >= LAG) {
@@ -328,7 +332,7 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
 #pragma unroll
     for (int q = 0; q < 3; q++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) scp[q][r] = sc[1 + q][r];  // MFMAs 29-31: row tiles 1-3 of column tile 7
+        for (int r = 0; r < 4; r++) scp[q][r] = sc[1 + q][r];  // the last three MFMAs: row tiles 1-3
 }
 
 // The K step of a wave of a partial last row tile whose rows below M fill only its first TMV < 4 row tiles of 16:
@@ -339,8 +343,9 @@ template <class C, int TMV>
 __device__ __forceinline__ void bs_step_rows(const uint8_t *st, int wm0, int wn0, v4f (&acc)[C::TM][C::TN],
                                              const BsOperands<C> &op, uint32_t dstage, int dkb)
 {
-    static_assert(C::TM == 4 && C::TN == 8 && TMV >= 1 && TMV < 4, "partial row tiles of 64 x 128 wave tiles");
-    constexpr int LAG = 3, NM = 8 * TMV;
+    static_assert(C::TM == 4 && (C::TN == 8 || C::TN == 4) && TMV >= 1 && TMV < 4,
+                  "partial row tiles of 64 x 128 and 64 x 64 wave tiles");
+    constexpr int LAG = 3, NM = C::TN * TMV;
     if (dkb >= 0) op.issue(dstage, dkb);
     const int lane = threadIdx.x & 63, g = lane >> 4;
     const uint8_t *ta = st, *tb = st + C::A_BYTES;
@@ -363,7 +368,7 @@ __device__ __forceinline__ void bs_step_rows(const uint8_t *st, int wm0, int wn0
         if (t < NM) {
             const int j = t / TMV, i = t % TMV;
             mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
-            if (i == 0 && j + 2 < 8) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
+            if (i == 0 && j + 2 < C::TN) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
         }
         if (t == LAG) asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // an XDL result is read 11+ slots later
         if (t >= LAG) {
@@ -445,7 +450,7 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
             is = is == C::NS - 1 ? 0 : is + 1;
         }
     };
-    if constexpr (C::TM == 4 && C::TN == 8) {
+    if constexpr (C::TM == 4 && (C::TN == 8 || C::TN == 4)) {
         if (live > 32) {
             v4f pr[4];          // the MFMA result ring, and the scales of the last step's MFMAs 29-31 (their
             float scp[3][4];    // promotions run at the start of the next step)
