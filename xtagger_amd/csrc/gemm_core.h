@@ -544,12 +544,24 @@ struct BsSpOperands {
         for (int i = 0; i < C::LV; i++) dma4(rx, stage + m0_x + 256u * i, x_off[i], (uint32_t)kb * 256u);
         dma4(rs, stage + m0_s, s_off, (uint32_t)kb * s_step);
     }
+    // load q (0 .. LPS_SP - 1) of K step kb: the same loads as issue(), one at a time
+    __device__ __forceinline__ void issue_one(int q, uint32_t stage, int kb) const
+    {
+        if (q < C::LA) dma16(ra, stage + m0_a + 1024u * q, a_off[q], (uint32_t)kb * 128u);
+        else if (q < C::LA + C::LV) dma16(rv, stage + m0_v + 1024u * (q - C::LA), v_off[q - C::LA], (uint32_t)kb * 1024u);
+        else if (q < C::LA + 2 * C::LV)
+            dma4(rx, stage + m0_x + 256u * (q - C::LA - C::LV), x_off[q - C::LA - C::LV], (uint32_t)kb * 256u);
+        else dma4(rs, stage + m0_s, s_off, (uint32_t)kb * s_step);
+    }
 };
 
-// One K step: TN x TM sparse MFMAs into the transposed accumulators accT[n tile][m tile].
+// One K step: TN x TM sparse MFMAs into the transposed accumulators accT[n tile][m tile]; the LPS_SP loads of K step
+// dkb (dkb < 0: none) go out one per MFMA from MFMA 1 on.
 template <class C>
-__device__ __forceinline__ void bs_step_sp(const uint8_t *st, int wm0, int wn0, v4f (&accT)[C::TN][C::TM])
+__device__ __forceinline__ void bs_step_sp(const uint8_t *st, int wm0, int wn0, v4f (&accT)[C::TN][C::TM],
+                                           const BsSpOperands<C> &op, uint32_t dstage, int dkb)
 {
+    static_assert(C::LPS_SP < C::TN * C::TM, "one load per MFMA");
     const int lane = threadIdx.x & 63, c16 = lane & 15;
     const uint8_t *ta = st, *tv = st + C::A_BYTES, *tx = st + C::A_BYTES + C::V_BYTES;
     const float *ts = (const float *)(st + C::A_BYTES + C::V_BYTES + C::X_BYTES);
@@ -575,6 +587,7 @@ __device__ __forceinline__ void bs_step_sp(const uint8_t *st, int wm0, int wn0, 
             }
             pr[t % (LAG + 1)] = __builtin_amdgcn_smfmac_f32_16x16x128_fp8_fp8(vcur, xa[j], v4f{0.f, 0.f, 0.f, 0.f},
                                                                                xcur, 0, 0);
+            if (t >= 1 && t <= C::LPS_SP && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
             if (j == C::TM - 1) {
                 vcur = vnext;
                 xcur = xnext;
@@ -656,8 +669,9 @@ __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, in
         if (kb + C::NS - 2 < KB) wait_vmem_n<(C::NS - 2) * C::LPS_SP>();
         else wait_vmem();
         lds_barrier();
-        if (kb + C::NS - 1 < KB) op.issue(base + is * C::STAGE_SP, kb + C::NS - 1);
-        if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT);
+        const int dkb = kb + C::NS - 1 < KB ? kb + C::NS - 1 : -1;
+        if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT, op, base + is * C::STAGE_SP, dkb);
+        else if (dkb >= 0) op.issue(base + is * C::STAGE_SP, dkb);
         cs = cs == C::NS - 1 ? 0 : cs + 1;
         is = is == C::NS - 1 ? 0 : is + 1;
     }
