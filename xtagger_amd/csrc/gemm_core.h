@@ -638,8 +638,11 @@ __device__ __forceinline__ void bs_sp_to_dense(uint8_t *slices, v4f (&accT)[C::T
 
 // Sparse main loop: the same contract as bs_mainloop (dense accumulator layout on return, block synchronised, no load
 // in flight, shared memory free), with the weights given as pack24 values V and indices X plus the dense 128 x 128
-// block scales sw. Uses NW * 17408 bytes of shared memory at the end for the transposition.
-template <class C, class Pre = BsNoPre>
+// block scales sw. Uses NW * 17408 bytes of shared memory at the end for the transposition. SPREAD: the next stage's
+// loads go out one per MFMA (bs_step_sp); otherwise in a burst after the barrier. Spreading them needs K known at
+// compile time: with K a kernel argument the per-load branches of the last step cost the 256 x 256 tile ~40 VGPRs of
+// spills.
+template <class C, class Pre = BsNoPre, bool SPREAD = true>
 __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
                                                int lds, const uint8_t *__restrict__ V, const uint32_t *__restrict__ X,
                                                const float *__restrict__ sw, int M, int Npad, int K, int m0, int n0,
@@ -670,8 +673,13 @@ __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, in
         else wait_vmem();
         lds_barrier();
         const int dkb = kb + C::NS - 1 < KB ? kb + C::NS - 1 : -1;
-        if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT, op, base + is * C::STAGE_SP, dkb);
-        else if (dkb >= 0) op.issue(base + is * C::STAGE_SP, dkb);
+        if constexpr (SPREAD) {
+            if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT, op, base + is * C::STAGE_SP, dkb);
+            else if (dkb >= 0) op.issue(base + is * C::STAGE_SP, dkb);
+        } else {
+            if (dkb >= 0) op.issue(base + is * C::STAGE_SP, dkb);
+            if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT, op, 0u, -1);
+        }
         cs = cs == C::NS - 1 ? 0 : cs + 1;
         is = is == C::NS - 1 ? 0 : is + 1;
     }

@@ -141,7 +141,7 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
     const int m0 = tm * C::BM, n0 = tn * C::BN, lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int Npad = (N + 127) & ~127;
     args_resident(Cp, ldc, N, M, lds);
-    if constexpr (SP) bs_mainloop_sp<C>(A, lda, sa, lds, W, WX, sw, M, Npad, K, m0, n0, smem, acc);
+    if constexpr (SP) bs_mainloop_sp<C, BsNoPre, false>(A, lda, sa, lds, W, WX, sw, M, Npad, K, m0, n0, smem, acc);
     else bs_mainloop<C, BsNoPre, false>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
     int wm0, wn0;
     bs_wave_origin<C>(wm0, wn0);
