@@ -65,7 +65,7 @@ struct BsCfg {
     static constexpr int V_BYTES = BN * 64;
     static constexpr int X_BYTES = BN * 16;
     static constexpr int STAGE_SP = A_BYTES + V_BYTES + X_BYTES + S_BYTES + SW_BYTES;
-    static constexpr int LDS_SP = NS * STAGE_SP;
+    static constexpr int LDS_SP = NS * STAGE_SP + 16;  // the stages, then the 16 zero bytes of bs_step_sp
     static constexpr int LPS_SP = LA + 2 * LV + 1;
 };
 
@@ -555,53 +555,84 @@ struct BsSpOperands {
     }
 };
 
-// One K step: TN x TM sparse MFMAs into the transposed accumulators accT[n tile][m tile]; the LPS_SP loads of K step
-// dkb (dkb < 0: none) go out one per MFMA from MFMA 1 on.
+// One K step: TN x TM sparse MFMAs into the transposed accumulators accT[n tile][m tile], in a fixed issue order (the
+// dense step's: single-instruction asm for the matrix instructions and the promotion fmas, every LDS read between
+// them). MFMA t = 4 j + i takes weight tile j (values and indices, a 3-slot ring: tile j + 2 is read after MFMA
+// (j, 0)) and activation tile i; its partial is promoted after MFMA t + 3, from a ring of 6. v_smfmac's accumulator
+// is tied to its destination, so every partial must start from zeros: the slot a promotion frees is refilled for
+// MFMA t + 6 by a broadcast read of 16 zero bytes of shared memory (zl), two MFMAs ahead of its use, which takes
+// two VALU moves per MFMA off the step (VALU bound here: the sparse MFMA runs in half the dense one's cycles while
+// the promotion keeps its four fmas). 2.4% off the sparse layer step at M=8200 against the compiler's order with
+// moves; the ring of 5 (the read one MFMA ahead) gained 1.7-2.0%, 7 gained 2.0%, and 8 leaves no registers to spare.
+// The LPS_SP loads of K step dkb (dkb < 0: none) go out one per MFMA from MFMA 1 on.
+__device__ __forceinline__ void smfmac_asm(v4f &p, const v4i &w, const v8i &x, int idx)
+{
+    asm volatile("v_smfmac_f32_16x16x128_fp8_fp8 %0, %1, %2, %3" : "+v"(p) : "v"(w), "v"(x), "v"(idx) : "memory");
+}
+// p = 0 here, loaded from 16 zero bytes of shared memory (zl: byte offset): a broadcast LDS read in place of two
+// VALU moves. The load is volatile, so each partial gets its own and keeps its registers until its MFMA.
+typedef __attribute__((address_space(3))) const v4f lds_v4f;
+__device__ __forceinline__ void lds_zero(v4f &p, uint32_t zl)
+{
+    p = *(volatile lds_v4f *)(uintptr_t)zl;
+}
+
 template <class C>
 __device__ __forceinline__ void bs_step_sp(const uint8_t *st, int wm0, int wn0, v4f (&accT)[C::TN][C::TM],
-                                           const BsSpOperands<C> &op, uint32_t dstage, int dkb)
+                                           const BsSpOperands<C> &op, uint32_t dstage, int dkb, uint32_t zl)
 {
-    static_assert(C::LPS_SP < C::TN * C::TM, "one load per MFMA");
+    static_assert(C::TM == 4 && C::TN >= 2 && C::LPS_SP < C::TN * C::TM, "schedule written for 64-row wave tiles");
     const int lane = threadIdx.x & 63, c16 = lane & 15;
     const uint8_t *ta = st, *tv = st + C::A_BYTES, *tx = st + C::A_BYTES + C::V_BYTES;
     const float *ts = (const float *)(st + C::A_BYTES + C::V_BYTES + C::X_BYTES);
-    const float swv = *(const float *)(st + C::A_BYTES + C::V_BYTES + C::X_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
-    v8i xa[C::TM];
-    float sc[C::TM];
-#pragma unroll
-    for (int j = 0; j < C::TM; j++) xa[j] = ld_frag(ta, wm0 + 16 * j);
-#pragma unroll
-    for (int j = 0; j < C::TM; j++) sc[j] = ts[wm0 + 16 * j + c16] * swv;
     const int t0 = wn0 >> 4;
-    v4i vcur = *(const v4i *)(tv + t0 * 1024 + 16 * lane), vnext = vcur;
-    int xcur = *(const int *)(tx + t0 * 256 + 4 * lane), xnext = xcur;
-    constexpr int NS = C::TN * C::TM, LAG = XT_LAG;
-    v4f pr[LAG + 1];
+    constexpr int NS = C::TN * C::TM, LAG = 3, R = 6;
+    v4i v[3];
+    int x[3];
+    v8i xa[4];
+    v[0] = *(const v4i *)(tv + t0 * 1024 + 16 * lane);
+    x[0] = *(const int *)(tx + t0 * 256 + 4 * lane);
+    xa[0] = ld_frag(ta, wm0);
+    asm volatile("" ::: "memory");  // the first MFMA waits for these reads only
+    const float swv = *(const float *)(st + C::A_BYTES + C::V_BYTES + C::X_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
+    float sr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sr[i] = ts[wm0 + 16 * i + c16];
+    asm volatile("" ::: "memory");
+    xa[1] = ld_frag(ta, wm0 + 16);
+    xa[2] = ld_frag(ta, wm0 + 32);
+    xa[3] = ld_frag(ta, wm0 + 48);
+    v[1] = *(const v4i *)(tv + (t0 + 1) * 1024 + 16 * lane);
+    x[1] = *(const int *)(tx + (t0 + 1) * 256 + 4 * lane);
+    asm volatile("" ::: "memory");
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sc[i] = sr[i] * swv;
+    v4f pr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) lds_zero(pr[r], zl);
 #pragma unroll
     for (int t = 0; t < NS + LAG; t++) {
         if (t < NS) {
-            const int i = t / C::TM, j = t % C::TM;
-            if (j == 0 && i + 1 < C::TN) {
-                vnext = *(const v4i *)(tv + (t0 + i + 1) * 1024 + 16 * lane);
-                xnext = *(const int *)(tx + (t0 + i + 1) * 256 + 4 * lane);
+            const int j = t >> 2, i = t & 3;
+            smfmac_asm(pr[t % R], v[j % 3], xa[i], x[j % 3]);
+            if (i == 0 && j + 2 < C::TN) {
+                v[(j + 2) % 3] = *(const v4i *)(tv + (t0 + j + 2) * 1024 + 16 * lane);
+                x[(j + 2) % 3] = *(const int *)(tx + (t0 + j + 2) * 256 + 4 * lane);
             }
-            pr[t % (LAG + 1)] = __builtin_amdgcn_smfmac_f32_16x16x128_fp8_fp8(vcur, xa[j], v4f{0.f, 0.f, 0.f, 0.f},
-                                                                               xcur, 0, 0);
             if (t >= 1 && t <= C::LPS_SP && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
-            if (j == C::TM - 1) {
-                vcur = vnext;
-                xcur = xnext;
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
         }
+        if (t == LAG) asm volatile("s_nop 7" ::: "memory");
         if (t >= LAG) {
-            const int u = t - LAG, i = u / C::TM, j = u % C::TM;
-            const v4f p = pr[u % (LAG + 1)];
-            accT[i][j][0] = __builtin_fmaf(p[0], sc[j], accT[i][j][0]);
-            accT[i][j][1] = __builtin_fmaf(p[1], sc[j], accT[i][j][1]);
-            accT[i][j][2] = __builtin_fmaf(p[2], sc[j], accT[i][j][2]);
-            accT[i][j][3] = __builtin_fmaf(p[3], sc[j], accT[i][j][3]);
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then 4 VALU
+            const int u = t - LAG, ju = u >> 2, iu = u & 3;
+            const v4f p = pr[u % R];
+            float x0 = accT[ju][iu][0], x1 = accT[ju][iu][1], x2 = accT[ju][iu][2], x3 = accT[ju][iu][3];
+            fmac_asm(x0, p[0], sc[iu]);
+            fmac_asm(x1, p[1], sc[iu]);
+            fmac_asm(x2, p[2], sc[iu]);
+            fmac_asm(x3, p[3], sc[iu]);
+            accT[ju][iu] = v4f{x0, x1, x2, x3};
+            if (u + R < NS) lds_zero(pr[u % R], zl);  // for MFMA u + 6
         }
     }
 }
@@ -638,10 +669,10 @@ __device__ __forceinline__ void bs_sp_to_dense(uint8_t *slices, v4f (&accT)[C::T
 
 // Sparse main loop: the same contract as bs_mainloop (dense accumulator layout on return, block synchronised, no load
 // in flight, shared memory free), with the weights given as pack24 values V and indices X plus the dense 128 x 128
-// block scales sw. Uses NW * 17408 bytes of shared memory at the end for the transposition. SPREAD: the next stage's
-// loads go out one per MFMA (bs_step_sp); otherwise in a burst after the barrier. Spreading them needs K known at
-// compile time: with K a kernel argument the per-load branches of the last step cost the 256 x 256 tile ~40 VGPRs of
-// spills.
+// block scales sw. Uses LDS_SP bytes of shared memory during the K loop and NW * 17408 bytes at the end for the
+// transposition. SPREAD: the next stage's loads go out one per MFMA (bs_step_sp); otherwise in a burst after the
+// barrier. Spreading them needs K known at compile time: with K a kernel argument the per-load branches of the last
+// step cost the 256 x 256 tile ~40 VGPRs of spills.
 template <class C, class Pre = BsNoPre, bool SPREAD = true>
 __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
                                                int lds, const uint8_t *__restrict__ V, const uint32_t *__restrict__ X,
@@ -663,6 +694,9 @@ __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, in
 #pragma unroll
     for (int s = 0; s < C::NS - 1; s++)
         if (s < KB) op.issue(base + s * C::STAGE_SP, s);
+    // 16 zero bytes past the stages, published by the K loop's first barrier: every partial starts from them
+    const uint32_t zl = base + C::NS * C::STAGE_SP;
+    if (threadIdx.x < 4) ((float *)(smem + C::NS * C::STAGE_SP))[threadIdx.x] = 0.f;
     pre();
     // a wave whose rows are all past M skips its matrix work (accumulators stay zero)
     const bool live = __builtin_amdgcn_readfirstlane(m0 + wm0) < M &&
@@ -674,11 +708,11 @@ __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, in
         lds_barrier();
         const int dkb = kb + C::NS - 1 < KB ? kb + C::NS - 1 : -1;
         if constexpr (SPREAD) {
-            if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT, op, base + is * C::STAGE_SP, dkb);
+            if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT, op, base + is * C::STAGE_SP, dkb, zl);
             else if (dkb >= 0) op.issue(base + is * C::STAGE_SP, dkb);
         } else {
             if (dkb >= 0) op.issue(base + is * C::STAGE_SP, dkb);
-            if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT, op, 0u, -1);
+            if (live) bs_step_sp<C>(smem + cs * C::STAGE_SP, wm0, wn0, accT, op, 0u, -1, zl);
         }
         cs = cs == C::NS - 1 ? 0 : cs + 1;
         is = is == C::NS - 1 ? 0 : is + 1;
