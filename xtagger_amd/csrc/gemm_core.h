@@ -585,13 +585,14 @@ __device__ __forceinline__ void bs_step_sp(const uint8_t *st, int wm0, int wn0, 
     const int lane = threadIdx.x & 63, c16 = lane & 15;
     const uint8_t *ta = st, *tv = st + C::A_BYTES, *tx = st + C::A_BYTES + C::V_BYTES;
     const float *ts = (const float *)(st + C::A_BYTES + C::V_BYTES + C::X_BYTES);
-    const int t0 = wn0 >> 4;
+    // the wave's weight tiles j = 0 .. TN - 1 at tvl + 1024 j and txl + 256 j (constant offsets of one base each)
+    const uint8_t *tvl = tv + (wn0 >> 4) * 1024 + 16 * lane, *txl = tx + (wn0 >> 4) * 256 + 4 * lane;
     constexpr int NS = C::TN * C::TM, LAG = 3, R = 6;
     v4i v[3];
     int x[3];
     v8i xa[4];
-    v[0] = *(const v4i *)(tv + t0 * 1024 + 16 * lane);
-    x[0] = *(const int *)(tx + t0 * 256 + 4 * lane);
+    v[0] = *(const v4i *)tvl;
+    x[0] = *(const int *)txl;
     xa[0] = ld_frag(ta, wm0);
     asm volatile("" ::: "memory");  // the first MFMA waits for these reads only
     const float swv = *(const float *)(st + C::A_BYTES + C::V_BYTES + C::X_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
@@ -602,8 +603,8 @@ __device__ __forceinline__ void bs_step_sp(const uint8_t *st, int wm0, int wn0, 
     xa[1] = ld_frag(ta, wm0 + 16);
     xa[2] = ld_frag(ta, wm0 + 32);
     xa[3] = ld_frag(ta, wm0 + 48);
-    v[1] = *(const v4i *)(tv + (t0 + 1) * 1024 + 16 * lane);
-    x[1] = *(const int *)(tx + (t0 + 1) * 256 + 4 * lane);
+    v[1] = *(const v4i *)(tvl + 1024);
+    x[1] = *(const int *)(txl + 256);
     asm volatile("" ::: "memory");
     float sc[4];
 #pragma unroll
@@ -617,8 +618,8 @@ __device__ __forceinline__ void bs_step_sp(const uint8_t *st, int wm0, int wn0, 
             const int j = t >> 2, i = t & 3;
             smfmac_asm(pr[t % R], v[j % 3], xa[i], x[j % 3]);
             if (i == 0 && j + 2 < C::TN) {
-                v[(j + 2) % 3] = *(const v4i *)(tv + (t0 + j + 2) * 1024 + 16 * lane);
-                x[(j + 2) % 3] = *(const int *)(tx + (t0 + j + 2) * 256 + 4 * lane);
+                v[(j + 2) % 3] = *(const v4i *)(tvl + 1024 * (j + 2));
+                x[(j + 2) % 3] = *(const int *)(txl + 256 * (j + 2));
             }
             if (t >= 1 && t <= C::LPS_SP && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
         }
