@@ -674,12 +674,15 @@ __device__ __forceinline__ void bs_sp_to_dense(uint8_t *slices, v4f (&accT)[C::T
 // transposition. SPREAD: the next stage's loads go out one per MFMA (bs_step_sp); otherwise in a burst after the
 // barrier. Spreading them needs K known at compile time: with K a kernel argument the per-load branches of the last
 // step cost the 256 x 256 tile ~40 VGPRs of spills.
+// bs_mainloop_sp_t stops before the transposition: it leaves the wave's tile in accT (accT[n tile][m tile][r]:
+// n = wn0 + 16 i + 4 (lane >> 4) + r, m = wm0 + 16 j + (lane & 15)), block synchronised, no load in flight, shared
+// memory free, for an epilogue that reads that layout instead of paying bs_sp_to_dense's pass through shared memory.
 template <class C, class Pre = BsNoPre, bool SPREAD = true>
-__device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
-                                               int lds, const uint8_t *__restrict__ V, const uint32_t *__restrict__ X,
-                                               const float *__restrict__ sw, int M, int Npad, int K, int m0, int n0,
-                                               uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre(),
-                                               int Nlive = -1)
+__device__ __forceinline__ void bs_mainloop_sp_t(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
+                                                 int lds, const uint8_t *__restrict__ V, const uint32_t *__restrict__ X,
+                                                 const float *__restrict__ sw, int M, int Npad, int K, int m0, int n0,
+                                                 uint8_t *smem, v4f (&accT)[C::TN][C::TM], Pre pre = Pre(),
+                                                 int Nlive = -1)
 {
     BsSpOperands<C> op;
     const int KB = K >> 7;
@@ -687,7 +690,6 @@ __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, in
     bs_wave_origin<C>(wm0, wn0);
     op.init(A, lda, sa, lds, V, X, sw, K, M, Npad, m0, n0);
     const uint32_t base = lds_addr(smem);
-    v4f accT[C::TN][C::TM];
 #pragma unroll
     for (int i = 0; i < C::TN; i++)
 #pragma unroll
@@ -719,6 +721,17 @@ __device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, in
         is = is == C::NS - 1 ? 0 : is + 1;
     }
     lds_barrier();
+}
+
+template <class C, class Pre = BsNoPre, bool SPREAD = true>
+__device__ __forceinline__ void bs_mainloop_sp(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
+                                               int lds, const uint8_t *__restrict__ V, const uint32_t *__restrict__ X,
+                                               const float *__restrict__ sw, int M, int Npad, int K, int m0, int n0,
+                                               uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre(),
+                                               int Nlive = -1)
+{
+    v4f accT[C::TN][C::TM];
+    bs_mainloop_sp_t<C, Pre, SPREAD>(A, lda, sa, lds, V, X, sw, M, Npad, K, m0, n0, smem, accT, pre, Nlive);
     bs_sp_to_dense<C>(smem, accT, acc);
     lds_barrier();
 }

@@ -145,45 +145,70 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     constexpr int NP = C::TN / 2;                        // SwiGLU tile pairs per wave (16 units each)
     __shared__ __attribute__((aligned(16))) uint8_t smem[LAYER_SMEM];
     static_assert(C::BM * 8 % C::NT == 0, "packing items split evenly over the threads");
-    v4f acc[C::TM][C::TN];
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 2 * XT_HIDP, m0, n0);
     args_resident(m8, ms, stat, lds, rows);
     if constexpr (RS) args_resident(rs);
     // W12 rows past the last 16-unit chunk holding a real unit (2 x 2736) are zero padding
-    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc, BsNoPre(),
-                          2 * ((XT_HID + 15) / 16 * 16));
-    bs_wave_origin<C>(wm0, wn0);
-    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-    const int wn = wn0 / C::WN, ct = n0 >> 8;
-    // h tile [BM rows][128 units] fp32 in LDS, 16-byte chunk c of row r at chunk c ^ (r & 7). Every address is a
-    // per-lane base plus an immediate: rows wm0 + 16 i + 4 g + r have row & 7 = (4 g + r) & 7, and unit
-    // 64 wn + 16 p + (lane & 15) sits in chunk 16 wn + 8 (p >> 1) + (4 (p & 1) + (lane & 15) / 4), whose low three
-    // bits depend on p & 1 only; so element (i, r, p) is at wb[r][p & 1] + 2048 i + 32 (p >> 1) words.
+    constexpr int nlive = 2 * ((XT_HID + 15) / 16 * 16);
+    // h tile [BM rows][128 units] fp32 in LDS, 16-byte chunk c of row r at chunk c ^ (r & 7)
     float *ht = (float *)smem;
     static_assert(C::BM * 128 * 4 <= LAYER_SMEM, "fc1 staging fits");
     static_assert(NP == 4, "two chunk pairs per 64-unit half");
-    const int cq = c16 >> 2;
-    uint32_t wb[4][2];
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const int ct = n0 >> 8;
+    // silu(g) x, hardware reciprocal (1 ulp)
+    auto swiglu = [](float gg, float xx) { return (gg * __builtin_amdgcn_rcpf(1.0f + __expf(-gg))) * xx; };
+    if constexpr (SP) {
+        // The sparse main loop's transposed tile: lane (g, c16) holds units 64 wn + 16 p + 4 g + r (r = 0..3) of row
+        // wm0 + 16 i + c16 for tile pair p (gate tile 2p, value tile 2p + 1: the same unit in the same register), so
+        // each (i, p) is one 16-byte chunk, 16 wn + 8 (p >> 1) + (4 (p & 1) + g), of a row with row & 7 = c16 & 7:
+        // at tb[p & 1] + 2048 i + 32 (p >> 1) words. The same h values as the dense layout's, without the
+        // transposition through shared memory.
+        static_assert(C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
+        v4f accT[C::TN][C::TM];
+        bs_mainloop_sp_t<C>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, accT, BsNoPre(),
+                            nlive);
+        bs_wave_origin<C>(wm0, wn0);
+        const int wn = wn0 / C::WN;
+        uint32_t tb[2];
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+        for (int ph = 0; ph < 2; ph++)
+            tb[ph] = (uint32_t)((wm0 + c16) * 128 + (16 * wn + ((4 * ph + g) ^ (c16 & 7))) * 4);
 #pragma unroll
-        for (int ph = 0; ph < 2; ph++) {
-            const int rr = wm0 + 4 * g + r, lo = (4 * ph + cq) ^ ((4 * g + r) & 7);
-            wb[r][ph] = (uint32_t)(rr * 128 + (16 * wn + lo) * 4 + (c16 & 3));
-        }
-#pragma unroll
-    for (int i = 0; i < C::TM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
+        for (int i = 0; i < C::TM; i++)
 #pragma unroll
             for (int p = 0; p < NP; p++) {
-                const float gg = acc[i][2 * p][r], xx = acc[i][2 * p + 1][r];
-                const float e = __expf(-gg), den = 1.0f + e;
-                const float v = (gg * __builtin_amdgcn_rcpf(den)) * xx;  // silu(g) x, hardware reciprocal (1 ulp)
-                ht[wb[r][p & 1] + 2048 * i + 32 * (p >> 1)] = v;
+                const v4f gg = accT[2 * p][i], xx = accT[2 * p + 1][i];
+                *(float4 *)(ht + tb[p & 1] + 2048 * i + 32 * (p >> 1)) =
+                    make_float4(swiglu(gg[0], xx[0]), swiglu(gg[1], xx[1]), swiglu(gg[2], xx[2]), swiglu(gg[3], xx[3]));
             }
-        }
+    } else {
+        v4f acc[C::TM][C::TN];
+        layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc, BsNoPre(),
+                              nlive);
+        bs_wave_origin<C>(wm0, wn0);
+        const int wn = wn0 / C::WN;
+        // Every address is a per-lane base plus an immediate: rows wm0 + 16 i + 4 g + r have row & 7 = (4 g + r) & 7,
+        // and unit 64 wn + 16 p + (lane & 15) sits in chunk 16 wn + 8 (p >> 1) + (4 (p & 1) + (lane & 15) / 4), whose
+        // low three bits depend on p & 1 only; so element (i, r, p) is at wb[r][p & 1] + 2048 i + 32 (p >> 1) words.
+        const int cq = c16 >> 2;
+        uint32_t wb[4][2];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int ph = 0; ph < 2; ph++) {
+                const int rr = wm0 + 4 * g + r, lo = (4 * ph + cq) ^ ((4 * g + r) & 7);
+                wb[r][ph] = (uint32_t)(rr * 128 + (16 * wn + lo) * 4 + (c16 & 3));
+            }
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int p = 0; p < NP; p++)
+                    ht[wb[r][p & 1] + 2048 * i + 32 * (p >> 1)] = swiglu(acc[i][2 * p][r], acc[i][2 * p + 1][r]);
+    }
     __syncthreads();
     // 8 consecutive threads per row, 16 consecutive units each: the row's |max| and sums over its 128 units meet in
     // a DPP tree over the 8 lanes; each thread packs its 16 units to E4M3 (one 16-byte store) and the first thread
