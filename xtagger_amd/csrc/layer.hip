@@ -118,6 +118,14 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, XT_D, m0, n0);
     args_resident(x, lds, rows);
+    if constexpr (SP) {  // the sparse main loop's transposed tile goes straight into the residual update
+        static_assert(C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
+        v4f accT[C::TN][C::TM];
+        bs_mainloop_sp_t<C>(a8, XT_D, as, lds, w, wx, ws, rows, XT_D, XT_D, m0, n0, smem, accT);
+        bs_wave_origin<C>(wm0, wn0);
+        residual_add_t<C>(smem, accT, x, m0 + wm0, n0 + wn0, rows);
+        return;
+    }
     layer_mainloop<C, SP>(a8, XT_D, as, lds, w, wx, ws, rows, XT_D, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows);
@@ -308,11 +316,33 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
         }
     };
     args_resident(x, stat, cn, dn, lds, rows);
+    static_assert(C::BM + C::BN <= C::NT, "one thread per row statistic and per column term");
+    if constexpr (SP) {
+        const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+        // the sparse main loop's transposed tile: lane (g, c16) holds row wm0 + 16 im + c16 (one row statistic per m
+        // tile) and columns wn0 + 16 jn + 4 g + r (four column terms, 32 bytes of cd, per n tile); the same fold
+        static_assert(C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
+        v4f accT[C::TN][C::TM];
+        bs_mainloop_sp_t<C>(m8, XT_HIDP, ms, lds, w, wx, ws, rows, XT_D, XT_HIDP, m0, n0, smem, accT, rowstats);
+        bs_wave_origin<C>(wm0, wn0);
+        float2 st[C::TM];
+#pragma unroll
+        for (int im = 0; im < C::TM; im++) st[im] = rs[wm0 + 16 * im + c16];
+        residual_add_t<C>(smem, accT, x, m0 + wm0, n0 + wn0, rows, [&](int jn, int im, v4f v) {
+            const float4 *cq = (const float4 *)(cd + wn0 + 16 * jn + 4 * g);
+            const float4 c01 = cq[0], c23 = cq[1];  // (c, d) of columns 4 g + 0 .. 3
+            v[0] = __builtin_fmaf(st[im].x, v[0], __builtin_fmaf(st[im].y, c01.x, c01.y));
+            v[1] = __builtin_fmaf(st[im].x, v[1], __builtin_fmaf(st[im].y, c01.z, c01.w));
+            v[2] = __builtin_fmaf(st[im].x, v[2], __builtin_fmaf(st[im].y, c23.x, c23.y));
+            v[3] = __builtin_fmaf(st[im].x, v[3], __builtin_fmaf(st[im].y, c23.z, c23.w));
+            return v;
+        });
+        return;
+    }
     layer_mainloop<C, SP>(m8, XT_HIDP, ms, lds, w, wx, ws, rows, XT_D, XT_HIDP, m0, n0, smem, acc, rowstats);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     // fold in registers: the lane's column terms and 16 row statistics read from shared memory in one batch
-    static_assert(C::BM + C::BN <= C::NT, "one thread per row statistic and per column term");
     float cj[C::TN], dj[C::TN];
 #pragma unroll
     for (int j = 0; j < C::TN; j++) {

@@ -103,6 +103,55 @@ __device__ __forceinline__ void residual_add(uint8_t *slices, v4f (&y)[C::TM][C:
     }
 }
 
+// residual_add for a tile in the sparse main loop's transposed layout (yT[n tile][m tile][r]: row
+// mw + 16 im + (lane & 15), column nw + 16 jn + 4 (lane >> 4) + r), f(jn, im, y) giving the four values added: the
+// same update, with the tile parked in the slice by one 16-byte store per (m tile, n tile) (row stride 68 floats:
+// the 16 rows of one store group start 4 banks apart).
+struct ResIdentityT {
+    __device__ __forceinline__ v4f operator()(int, int, v4f v) const { return v; }
+};
+template <class C, class F = ResIdentityT>
+__device__ __forceinline__ void residual_add_t(uint8_t *slices, v4f (&y)[C::TN][C::TM], uint16_t *__restrict__ x,
+                                               int mw, int nw, int rows, F f = F())
+{
+    static_assert(C::TM == 4 && C::TN % 4 == 0, "64-row wave tiles, whole 64-column passes");
+    constexpr int NP = C::TN / 4;
+    float *tr = (float *)(slices + (threadIdx.x >> 6) * LAYER_RES_SLICE);
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    const int rs = lane >> 3, ch = lane & 7;
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, (uint32_t)rows * XT_D * 2u);
+    const uint32_t off0 = (uint32_t)(((mw + rs) * XT_D + nw + 8 * ch) * 2);
+    v4u xv[NP][8];
+#pragma unroll
+    for (int pass = 0; pass < NP; pass++)
+#pragma unroll
+        for (int it = 0; it < 8; it++)
+            xv[pass][it] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
+#pragma unroll
+    for (int pass = 0; pass < NP; pass++) {
+        if (pass) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous pass's slice reads are done
+#pragma unroll
+        for (int im = 0; im < 4; im++)
+#pragma unroll
+            for (int jq = 0; jq < 4; jq++) {
+                const v4f v = f(4 * pass + jq, im, y[4 * pass + jq][im]);
+                *(float4 *)(tr + (16 * im + c16) * 68 + 16 * jq + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+            const int rr = 8 * it + rs;
+            const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
+            const v4u v = xv[pass][it];
+            v4u o;
+            o[0] = f2h(h2f(v[0] & 0xFFFF) + a.x) | (uint32_t)f2h(h2f(v[0] >> 16) + a.y) << 16;
+            o[1] = f2h(h2f(v[1] & 0xFFFF) + a.z) | (uint32_t)f2h(h2f(v[1] >> 16) + a.w) << 16;
+            o[2] = f2h(h2f(v[2] & 0xFFFF) + b.x) | (uint32_t)f2h(h2f(v[2] >> 16) + b.y) << 16;
+            o[3] = f2h(h2f(v[3] & 0xFFFF) + b.z) | (uint32_t)f2h(h2f(v[3] >> 16) + b.w) << 16;
+            __builtin_amdgcn_raw_buffer_store_b128(o, rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
+        }
+    }
+}
 
 static inline unsigned layer_grid(int rows, int N, int BM, int BN)
 {
