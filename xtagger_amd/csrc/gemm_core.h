@@ -263,7 +263,7 @@ __device__ __forceinline__ void fmac_asm(float &acc, float p, float s)
 
 // Promotion of a step's last three MFMAs (row tiles 1-3 of the last column tile, ring slots 1-3) with that step's
 // scales scp
-template <class C>
+template <class C, bool TR = false>
 __device__ __forceinline__ void bs_step_fixed_flush(v4f (&acc)[C::TM][C::TN], const v4f (&pr)[4],
                                                     const float (&scp)[3][4])
 {
@@ -273,14 +273,14 @@ __device__ __forceinline__ void bs_step_fixed_flush(v4f (&acc)[C::TM][C::TN], co
         const v4f p = pr[1 + q];
         float x0 = acc[1 + q][J][0], x1 = acc[1 + q][J][1], x2 = acc[1 + q][J][2], x3 = acc[1 + q][J][3];
         fmac_asm(x0, p[0], scp[q][0]);
-        fmac_asm(x1, p[1], scp[q][1]);
-        fmac_asm(x2, p[2], scp[q][2]);
-        fmac_asm(x3, p[3], scp[q][3]);
+        fmac_asm(x1, p[1], scp[q][TR ? 0 : 1]);
+        fmac_asm(x2, p[2], scp[q][TR ? 0 : 2]);
+        fmac_asm(x3, p[3], scp[q][TR ? 0 : 3]);
         acc[1 + q][J] = v4f{x0, x1, x2, x3};
     }
 }
 
-template <class C>
+template <class C, bool TR = false>
 __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn0, v4f (&acc)[C::TM][C::TN],
                                               const BsOperands<C> &op, uint32_t dstage, int dkb, v4f (&pr)[4],
                                               float (&scp)[3][4], bool carry)
@@ -288,18 +288,21 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
     static_assert(C::TM == 4 && (C::TN == 8 || C::TN == 4) && C::LPS < 4 * C::TN,
                   "schedule written for 64 x 128 and 64 x 64 wave tiles");
     constexpr int LAG = 3, NM = 4 * C::TN;
-    const int lane = threadIdx.x & 63, g = lane >> 4;
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const uint8_t *ta = st, *tb = st + C::A_BYTES;
     const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
     v8i a[4], b[3];
     b[0] = ld_frag(tb, wn0);
     a[0] = ld_frag(ta, wm0);
     asm volatile("" ::: "memory");  // the first MFMA waits for these four reads only
-    if (carry) bs_step_fixed_flush<C>(acc, pr, scp);  // the previous step's last three MFMAs, while the reads land
+    if (carry) bs_step_fixed_flush<C, TR>(acc, pr, scp);  // the previous step's last three MFMAs, while the reads land
     const float swv = *(const float *)(st + C::A_BYTES + C::B_BYTES + C::S_BYTES + 4 * (wn0 >> 7));
     float4 s4[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) s4[i] = *(const float4 *)(ts + wm0 + 16 * i + 4 * g);
+    for (int i = 0; i < 4; i++) {
+        if constexpr (TR) s4[i].x = ts[wm0 + 16 * i + c16];  // TR: one row per lane and row tile
+        else s4[i] = *(const float4 *)(ts + wm0 + 16 * i + 4 * g);
+    }
     asm volatile("" ::: "memory");
     a[1] = ld_frag(ta, wm0 + 16);
     a[2] = ld_frag(ta, wm0 + 32);
@@ -309,12 +312,17 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
     float sc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        sc[i][0] = s4[i].x * swv; sc[i][1] = s4[i].y * swv; sc[i][2] = s4[i].z * swv; sc[i][3] = s4[i].w * swv;
+        if constexpr (TR) {
+            sc[i][0] = s4[i].x * swv;
+        } else {
+            sc[i][0] = s4[i].x * swv; sc[i][1] = s4[i].y * swv; sc[i][2] = s4[i].z * swv; sc[i][3] = s4[i].w * swv;
+        }
     }
 #pragma unroll
     for (int t = 0; t < NM; t++) {
         const int j = t >> 2, i = t & 3;
-        mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
+        if constexpr (TR) mfma_asm(pr[t % (LAG + 1)], b[j % 3], a[i]);  // the tile transposed: weights as A
+        else mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
         if (i == 0 && j + 2 < C::TN) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
         if (t >= 1 && t <= C::LPS && dkb >= 0) op.issue_one(t - 1, dstage, dkb);
         if (t == LAG) asm volatile("s_nop 7" ::: "memory");
@@ -323,23 +331,23 @@ __device__ __forceinline__ void bs_step_fixed(const uint8_t *st, int wm0, int wn
             const v4f p = pr[u % (LAG + 1)];
             float x0 = acc[iu][ju][0], x1 = acc[iu][ju][1], x2 = acc[iu][ju][2], x3 = acc[iu][ju][3];
             fmac_asm(x0, p[0], sc[iu][0]);
-            fmac_asm(x1, p[1], sc[iu][1]);
-            fmac_asm(x2, p[2], sc[iu][2]);
-            fmac_asm(x3, p[3], sc[iu][3]);
+            fmac_asm(x1, p[1], sc[iu][TR ? 0 : 1]);
+            fmac_asm(x2, p[2], sc[iu][TR ? 0 : 2]);
+            fmac_asm(x3, p[3], sc[iu][TR ? 0 : 3]);
             acc[iu][ju] = v4f{x0, x1, x2, x3};
         }
     }
 #pragma unroll
     for (int q = 0; q < 3; q++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) scp[q][r] = sc[1 + q][r];  // the last three MFMAs: row tiles 1-3
+        for (int r = 0; r < (TR ? 1 : 4); r++) scp[q][r] = sc[1 + q][r];  // the last three MFMAs: row tiles 1-3
 }
 
 // The K step of a wave of a partial last row tile whose rows below M fill only its first TMV < 4 row tiles of 16:
 // those row tiles' MFMAs and promotions, with the operands, order of promotion and instructions bs_step_fixed uses
 // for them (so their accumulators are bit-identical), the others left at zero as the zero rows past M would leave
 // them. The stage's loads go out first, all at once.
-template <class C, int TMV>
+template <class C, int TMV, bool TR = false>
 __device__ __forceinline__ void bs_step_rows(const uint8_t *st, int wm0, int wn0, v4f (&acc)[C::TM][C::TN],
                                              const BsOperands<C> &op, uint32_t dstage, int dkb)
 {
@@ -347,7 +355,7 @@ __device__ __forceinline__ void bs_step_rows(const uint8_t *st, int wm0, int wn0
                   "partial row tiles of 64 x 128 and 64 x 64 wave tiles");
     constexpr int LAG = 3, NM = C::TN * TMV;
     if (dkb >= 0) op.issue(dstage, dkb);
-    const int lane = threadIdx.x & 63, g = lane >> 4;
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const uint8_t *ta = st, *tb = st + C::A_BYTES;
     const float *ts = (const float *)(st + C::A_BYTES + C::B_BYTES);
     v8i a[TMV], b[3];
@@ -359,15 +367,20 @@ __device__ __forceinline__ void bs_step_rows(const uint8_t *st, int wm0, int wn0
     float sc[TMV][4];
 #pragma unroll
     for (int i = 0; i < TMV; i++) {
-        const float4 s4 = *(const float4 *)(ts + wm0 + 16 * i + 4 * g);
-        sc[i][0] = s4.x * swv; sc[i][1] = s4.y * swv; sc[i][2] = s4.z * swv; sc[i][3] = s4.w * swv;
+        if constexpr (TR) {
+            sc[i][0] = ts[wm0 + 16 * i + c16] * swv;
+        } else {
+            const float4 s4 = *(const float4 *)(ts + wm0 + 16 * i + 4 * g);
+            sc[i][0] = s4.x * swv; sc[i][1] = s4.y * swv; sc[i][2] = s4.z * swv; sc[i][3] = s4.w * swv;
+        }
     }
     v4f pr[LAG + 1];
 #pragma unroll
     for (int t = 0; t < NM + LAG; t++) {
         if (t < NM) {
             const int j = t / TMV, i = t % TMV;
-            mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
+            if constexpr (TR) mfma_asm(pr[t % (LAG + 1)], b[j % 3], a[i]);
+            else mfma_asm(pr[t % (LAG + 1)], a[i], b[j % 3]);
             if (i == 0 && j + 2 < C::TN) b[(j + 2) % 3] = ld_frag(tb, wn0 + 16 * (j + 2));
         }
         if (t == LAG) asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // an XDL result is read 11+ slots later
@@ -376,9 +389,9 @@ __device__ __forceinline__ void bs_step_rows(const uint8_t *st, int wm0, int wn0
             const v4f p = pr[u % (LAG + 1)];
             float x0 = acc[i][j][0], x1 = acc[i][j][1], x2 = acc[i][j][2], x3 = acc[i][j][3];
             fmac_asm(x0, p[0], sc[i][0]);
-            fmac_asm(x1, p[1], sc[i][1]);
-            fmac_asm(x2, p[2], sc[i][2]);
-            fmac_asm(x3, p[3], sc[i][3]);
+            fmac_asm(x1, p[1], sc[i][TR ? 0 : 1]);
+            fmac_asm(x2, p[2], sc[i][TR ? 0 : 2]);
+            fmac_asm(x3, p[3], sc[i][TR ? 0 : 3]);
             acc[i][j] = v4f{x0, x1, x2, x3};
         }
     }
@@ -404,11 +417,13 @@ struct BsNoPre {
 };
 
 // Main loop (SKIP: waves whose rows are all past M skip their matrix work). On return acc[i][j][r] holds output row m0 + wm0 + 16 i + 4 (lane >> 4) + r, column
-// n0 + wn0 + 16 j + (lane & 15), where (wm0, wn0) = bs_wave_origin(). The block is synchronised, no load is in
+// n0 + wn0 + 16 j + (lane & 15), where (wm0, wn0) = bs_wave_origin(); with TR the tile transposed (the MFMAs take
+// the weights as A): row m0 + wm0 + 16 i + (lane & 15), column n0 + wn0 + 16 j + 4 (lane >> 4) + r, one row scale
+// per lane and row tile. The block is synchronised, no load is in
 // flight and the whole shared memory is free for the epilogue. pre() runs once the first stages' loads are issued
 // (epilogue inputs can be fetched there, under the prologue's memory latency); it may write shared memory only past
 // C::LDS.
-template <class C, class Pre = BsNoPre, bool SKIP = true>
+template <class C, class Pre = BsNoPre, bool SKIP = true, bool TR = false>
 __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int lda, const float *__restrict__ sa,
                                             int lds, const uint8_t *__restrict__ W, const float *__restrict__ sw,
                                             int M, int Npad, int K, int m0, int n0, uint8_t *smem,
@@ -456,20 +471,25 @@ __device__ __forceinline__ void bs_mainloop(const uint8_t *__restrict__ A, int l
             float scp[3][4];    // promotions run at the start of the next step)
             int kbi = 0;
             kloop([&](const uint8_t *st, uint32_t dst, int dkb) {
-                bs_step_fixed<C>(st, wm0, wn0, acc, op, dst, dkb, pr, scp, kbi > 0);
+                bs_step_fixed<C, TR>(st, wm0, wn0, acc, op, dst, dkb, pr, scp, kbi > 0);
                 kbi++;
             });
             asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");  // 12+ wait states after the last MFMA
-            bs_step_fixed_flush<C>(acc, pr, scp);
+            bs_step_fixed_flush<C, TR>(acc, pr, scp);
         } else if (live > 16)
-            kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_rows<C, 2>(st, wm0, wn0, acc, op, dst, dkb); });
+            kloop([&](const uint8_t *st, uint32_t dst, int dkb) {
+                bs_step_rows<C, 2, TR>(st, wm0, wn0, acc, op, dst, dkb);
+            });
         else if (live > 0)
-            kloop([&](const uint8_t *st, uint32_t dst, int dkb) { bs_step_rows<C, 1>(st, wm0, wn0, acc, op, dst, dkb); });
+            kloop([&](const uint8_t *st, uint32_t dst, int dkb) {
+                bs_step_rows<C, 1, TR>(st, wm0, wn0, acc, op, dst, dkb);
+            });
         else
             kloop([&](const uint8_t *, uint32_t dst, int dkb) {
                 if (dkb >= 0) op.issue(dst, dkb);
             });
     } else {
+        static_assert(!TR, "the transposed tile needs the fixed-order steps");
         kloop([&](const uint8_t *st, uint32_t dst, int dkb) {
             if (dkb >= 0) op.issue(dst, dkb);
             bs_step<C>(st, wm0, wn0, acc);

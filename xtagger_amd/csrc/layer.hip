@@ -118,17 +118,18 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_oproj(const uint8_t *__restric
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, XT_D, m0, n0);
     args_resident(x, lds, rows);
-    if constexpr (SP) {  // the sparse main loop's transposed tile goes straight into the residual update
+    // the transposed tile (sparse: as the sparse main loop leaves it; dense: TR) goes straight into the residual update
+    if constexpr (SP) {
         static_assert(C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
         v4f accT[C::TN][C::TM];
         bs_mainloop_sp_t<C>(a8, XT_D, as, lds, w, wx, ws, rows, XT_D, XT_D, m0, n0, smem, accT);
         bs_wave_origin<C>(wm0, wn0);
-        residual_add_t<C>(smem, accT, x, m0 + wm0, n0 + wn0, rows);
-        return;
+        residual_add_t<C>(smem, [&](int jn, int im) { return accT[jn][im]; }, x, m0 + wm0, n0 + wn0, rows);
+    } else {
+        layer_mainloop<C, SP, BsNoPre, true>(a8, XT_D, as, lds, w, wx, ws, rows, XT_D, XT_D, m0, n0, smem, acc);
+        bs_wave_origin<C>(wm0, wn0);
+        residual_add_t<C>(smem, [&](int jn, int im) { return acc[im][jn]; }, x, m0 + wm0, n0 + wn0, rows);
     }
-    layer_mainloop<C, SP>(a8, XT_D, as, lds, w, wx, ws, rows, XT_D, XT_D, m0, n0, smem, acc);
-    bs_wave_origin<C>(wm0, wn0);
-    residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -167,16 +168,11 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
     const int ct = n0 >> 8;
     // silu(g) x, hardware reciprocal (1 ulp)
     auto swiglu = [](float gg, float xx) { return (gg * __builtin_amdgcn_rcpf(1.0f + __expf(-gg))) * xx; };
-    if constexpr (SP) {
-        // The sparse main loop's transposed tile: lane (g, c16) holds units 64 wn + 16 p + 4 g + r (r = 0..3) of row
-        // wm0 + 16 i + c16 for tile pair p (gate tile 2p, value tile 2p + 1: the same unit in the same register), so
-        // each (i, p) is one 16-byte chunk, 16 wn + 8 (p >> 1) + (4 (p & 1) + g), of a row with row & 7 = c16 & 7:
-        // at tb[p & 1] + 2048 i + 32 (p >> 1) words. The same h values as the dense layout's, without the
-        // transposition through shared memory.
-        static_assert(C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
-        v4f accT[C::TN][C::TM];
-        bs_mainloop_sp_t<C>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, accT, BsNoPre(),
-                            nlive);
+    // The transposed tile (sparse: as the sparse main loop leaves it; dense: TR): lane (g, c16) holds units
+    // 64 wn + 16 p + 4 g + r (r = 0..3) of row wm0 + 16 i + c16 for tile pair p (gate tile 2p, value tile 2p + 1: the
+    // same unit in the same register), so each (i, p) is one 16-byte chunk, 16 wn + 8 (p >> 1) + (4 (p & 1) + g), of a
+    // row with row & 7 = c16 & 7: at tb[p & 1] + 2048 i + 32 (p >> 1) words.
+    auto stage_h = [&](auto pair) {
         bs_wave_origin<C>(wm0, wn0);
         const int wn = wn0 / C::WN;
         uint32_t tb[2];
@@ -187,35 +183,23 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc1(const uint8_t *__restrict_
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
             for (int p = 0; p < NP; p++) {
-                const v4f gg = accT[2 * p][i], xx = accT[2 * p + 1][i];
+                v4f gg, xx;
+                pair(i, p, gg, xx);
                 *(float4 *)(ht + tb[p & 1] + 2048 * i + 32 * (p >> 1)) =
                     make_float4(swiglu(gg[0], xx[0]), swiglu(gg[1], xx[1]), swiglu(gg[2], xx[2]), swiglu(gg[3], xx[3]));
             }
+    };
+    if constexpr (SP) {
+        static_assert(C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
+        v4f accT[C::TN][C::TM];
+        bs_mainloop_sp_t<C>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, accT, BsNoPre(),
+                            nlive);
+        stage_h([&](int i, int p, v4f &gg, v4f &xx) { gg = accT[2 * p][i]; xx = accT[2 * p + 1][i]; });
     } else {
         v4f acc[C::TM][C::TN];
-        layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc, BsNoPre(),
-                              nlive);
-        bs_wave_origin<C>(wm0, wn0);
-        const int wn = wn0 / C::WN;
-        // Every address is a per-lane base plus an immediate: rows wm0 + 16 i + 4 g + r have row & 7 = (4 g + r) & 7,
-        // and unit 64 wn + 16 p + (lane & 15) sits in chunk 16 wn + 8 (p >> 1) + (4 (p & 1) + (lane & 15) / 4), whose
-        // low three bits depend on p & 1 only; so element (i, r, p) is at wb[r][p & 1] + 2048 i + 32 (p >> 1) words.
-        const int cq = c16 >> 2;
-        uint32_t wb[4][2];
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int ph = 0; ph < 2; ph++) {
-                const int rr = wm0 + 4 * g + r, lo = (4 * ph + cq) ^ ((4 * g + r) & 7);
-                wb[r][ph] = (uint32_t)(rr * 128 + (16 * wn + lo) * 4 + (c16 & 3));
-            }
-#pragma unroll
-        for (int i = 0; i < C::TM; i++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int p = 0; p < NP; p++)
-                    ht[wb[r][p & 1] + 2048 * i + 32 * (p >> 1)] = swiglu(acc[i][2 * p][r], acc[i][2 * p + 1][r]);
+        layer_mainloop<C, SP, BsNoPre, true>(h8, XT_D, hs, lds, w, wx, ws, rows, 2 * XT_HIDP, XT_D, m0, n0, smem, acc,
+                                             BsNoPre(), nlive);
+        stage_h([&](int i, int p, v4f &gg, v4f &xx) { gg = acc[i][2 * p]; xx = acc[i][2 * p + 1]; });
     }
     __syncthreads();
     // 8 consecutive threads per row, 16 consecutive units each: the row's |max| and sums over its 128 units meet in
@@ -317,52 +301,38 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_fc2(const uint8_t *__restrict_
     };
     args_resident(x, stat, cn, dn, lds, rows);
     static_assert(C::BM + C::BN <= C::NT, "one thread per row statistic and per column term");
+    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+    // The transposed tile (sparse: as the sparse main loop leaves it; dense: TR): lane (g, c16) holds row
+    // wm0 + 16 im + c16 (one row statistic per m tile) and columns wn0 + 16 jn + 4 g + r (four column terms, 32 bytes
+    // of cd, per n tile). The fold is applied as the residual update parks the tile.
+    float2 st[C::TM];
+    auto fold = [&](v4f v, int jn, int im) {
+        const float4 *cq = (const float4 *)(cd + wn0 + 16 * jn + 4 * g);
+        const float4 c01 = cq[0], c23 = cq[1];  // (c, d) of columns 4 g + 0 .. 3
+        v[0] = __builtin_fmaf(st[im].x, v[0], __builtin_fmaf(st[im].y, c01.x, c01.y));
+        v[1] = __builtin_fmaf(st[im].x, v[1], __builtin_fmaf(st[im].y, c01.z, c01.w));
+        v[2] = __builtin_fmaf(st[im].x, v[2], __builtin_fmaf(st[im].y, c23.x, c23.y));
+        v[3] = __builtin_fmaf(st[im].x, v[3], __builtin_fmaf(st[im].y, c23.z, c23.w));
+        return v;
+    };
     if constexpr (SP) {
-        const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-        // the sparse main loop's transposed tile: lane (g, c16) holds row wm0 + 16 im + c16 (one row statistic per m
-        // tile) and columns wn0 + 16 jn + 4 g + r (four column terms, 32 bytes of cd, per n tile); the same fold
         static_assert(C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
         v4f accT[C::TN][C::TM];
         bs_mainloop_sp_t<C>(m8, XT_HIDP, ms, lds, w, wx, ws, rows, XT_D, XT_HIDP, m0, n0, smem, accT, rowstats);
         bs_wave_origin<C>(wm0, wn0);
-        float2 st[C::TM];
 #pragma unroll
         for (int im = 0; im < C::TM; im++) st[im] = rs[wm0 + 16 * im + c16];
-        residual_add_t<C>(smem, accT, x, m0 + wm0, n0 + wn0, rows, [&](int jn, int im, v4f v) {
-            const float4 *cq = (const float4 *)(cd + wn0 + 16 * jn + 4 * g);
-            const float4 c01 = cq[0], c23 = cq[1];  // (c, d) of columns 4 g + 0 .. 3
-            v[0] = __builtin_fmaf(st[im].x, v[0], __builtin_fmaf(st[im].y, c01.x, c01.y));
-            v[1] = __builtin_fmaf(st[im].x, v[1], __builtin_fmaf(st[im].y, c01.z, c01.w));
-            v[2] = __builtin_fmaf(st[im].x, v[2], __builtin_fmaf(st[im].y, c23.x, c23.y));
-            v[3] = __builtin_fmaf(st[im].x, v[3], __builtin_fmaf(st[im].y, c23.z, c23.w));
-            return v;
-        });
-        return;
+        residual_add_t<C>(smem, [&](int jn, int im) { return fold(accT[jn][im], jn, im); }, x, m0 + wm0, n0 + wn0,
+                          rows);
+    } else {
+        layer_mainloop<C, SP, decltype(rowstats), true>(m8, XT_HIDP, ms, lds, w, wx, ws, rows, XT_D, XT_HIDP, m0, n0,
+                                                       smem, acc, rowstats);
+        bs_wave_origin<C>(wm0, wn0);
+#pragma unroll
+        for (int im = 0; im < C::TM; im++) st[im] = rs[wm0 + 16 * im + c16];
+        residual_add_t<C>(smem, [&](int jn, int im) { return fold(acc[im][jn], jn, im); }, x, m0 + wm0, n0 + wn0,
+                          rows);
     }
-    layer_mainloop<C, SP>(m8, XT_HIDP, ms, lds, w, wx, ws, rows, XT_D, XT_HIDP, m0, n0, smem, acc, rowstats);
-    bs_wave_origin<C>(wm0, wn0);
-    const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-    // fold in registers: the lane's column terms and 16 row statistics read from shared memory in one batch
-    float cj[C::TN], dj[C::TN];
-#pragma unroll
-    for (int j = 0; j < C::TN; j++) {
-        const float2 t = cd[wn0 + 16 * j + c16];
-        cj[j] = t.x;
-        dj[j] = t.y;
-    }
-    float2 st[C::TM][4];
-#pragma unroll
-    for (int i = 0; i < C::TM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) st[i][r] = rs[wm0 + 16 * i + 4 * g + r];
-#pragma unroll
-    for (int i = 0; i < C::TM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int j = 0; j < C::TN; j++)
-                acc[i][j][r] = __builtin_fmaf(st[i][r].x, acc[i][j][r], __builtin_fmaf(st[i][r].y, cj[j], dj[j]));
-    residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

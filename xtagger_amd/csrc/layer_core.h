@@ -27,15 +27,17 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b)
 // The layer kernels take their weights dense (w, wx unused) or 2:4-sparse (SP: w = pack24 values, wx = indices).
 // Nlive (default Npad): columns from Nlive on hold zero weights throughout, so waves that own only such columns skip
 // their matrix work.
-template <class C, bool SP, class Pre = BsNoPre>
+// TR (dense weights only): the tile transposed, as bs_mainloop's TR leaves it.
+template <class C, bool SP, class Pre = BsNoPre, bool TR = false>
 __device__ __forceinline__ void layer_mainloop(const uint8_t *A, int lda, const float *sa, int lds, const uint8_t *w,
                                                const uint32_t *wx, const float *ws, int rows, int Npad, int K, int m0,
                                                int n0, uint8_t *smem, v4f (&acc)[C::TM][C::TN], Pre pre = Pre(),
                                                int Nlive = -1)
 {
     static_assert(!SP || C::LDS_SP <= LAYER_ROWSTAT, "sparse stages end before the row statistics");
+    static_assert(!(SP && TR), "the sparse tile comes transposed from bs_mainloop_sp_t");
     if constexpr (SP) bs_mainloop_sp<C>(A, lda, sa, lds, w, wx, ws, rows, Npad, K, m0, n0, smem, acc, pre, Nlive);
-    else bs_mainloop<C>(A, lda, sa, lds, w, ws, rows, Npad, K, m0, n0, smem, acc, pre, Nlive);
+    else bs_mainloop<C, Pre, true, TR>(A, lda, sa, lds, w, ws, rows, Npad, K, m0, n0, smem, acc, pre, Nlive);
 }
 
 template <class C>
@@ -103,16 +105,12 @@ __device__ __forceinline__ void residual_add(uint8_t *slices, v4f (&y)[C::TM][C:
     }
 }
 
-// residual_add for a tile in the sparse main loop's transposed layout (yT[n tile][m tile][r]: row
-// mw + 16 im + (lane & 15), column nw + 16 jn + 4 (lane >> 4) + r), f(jn, im, y) giving the four values added: the
-// same update, with the tile parked in the slice by one 16-byte store per (m tile, n tile) (row stride 68 floats:
-// the 16 rows of one store group start 4 banks apart).
-struct ResIdentityT {
-    __device__ __forceinline__ v4f operator()(int, int, v4f v) const { return v; }
-};
-template <class C, class F = ResIdentityT>
-__device__ __forceinline__ void residual_add_t(uint8_t *slices, v4f (&y)[C::TN][C::TM], uint16_t *__restrict__ x,
-                                               int mw, int nw, int rows, F f = F())
+// residual_add for a transposed tile (the sparse main loop's, or bs_mainloop's with TR): y(jn, im) gives the four
+// values added to row mw + 16 im + (lane & 15), columns nw + 16 jn + 4 (lane >> 4) + r. The same update, with the
+// tile parked in the slice by one 16-byte store per (m tile, n tile) (row stride 68 floats: the 16 rows of one store
+// group start 4 banks apart).
+template <class C, class Y>
+__device__ __forceinline__ void residual_add_t(uint8_t *slices, Y y, uint16_t *__restrict__ x, int mw, int nw, int rows)
 {
     static_assert(C::TM == 4 && C::TN % 4 == 0, "64-row wave tiles, whole 64-column passes");
     constexpr int NP = C::TN / 4;
@@ -134,7 +132,7 @@ __device__ __forceinline__ void residual_add_t(uint8_t *slices, v4f (&y)[C::TN][
         for (int im = 0; im < 4; im++)
 #pragma unroll
             for (int jq = 0; jq < 4; jq++) {
-                const v4f v = f(4 * pass + jq, im, y[4 * pass + jq][im]);
+                const v4f v = y(4 * pass + jq, im);
                 *(float4 *)(tr + (16 * im + c16) * 68 + 16 * jq + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
             }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
