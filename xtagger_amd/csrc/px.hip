@@ -132,11 +132,6 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_qkv(const uint8_t *__restri
 // k_pfc2). The reference rounds (x + alpha acc) + b in fp32 (px_kernels.cu:178); here acc + b is formed first: the
 // two orders differ by at most one fp32 rounding before the fp16 store.
 // ---------------------------------------------------------------------------------------------------------------
-struct PxAddBias {
-    float b[LayerCfg::TN];  // the lane's column biases, held by value (registers)
-    __device__ __forceinline__ float operator()(int, int j, int, float v) const { return v + b[j]; }
-};
-
 template <bool SP, int K>
 __global__ void __launch_bounds__(LayerCfg::NT) k_px_res(const uint8_t *__restrict__ a8, const float *__restrict__ as,
                                                         int lds, const uint8_t *__restrict__ w,
@@ -150,20 +145,24 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_res(const uint8_t *__restri
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, XT_D, m0, n0);
     args_resident(bias, x, lds, rows);
-    layer_mainloop<C, SP>(a8, K, as, lds, w, wx, ws, rows, XT_D, K, m0, n0, smem, acc);
+    // the tile transposed (TR): lane (g, c16) holds columns n0 + wn0 + 16 j + 4 g + r, one 16-byte bias load per j
+    layer_mainloop<C, SP, BsNoPre, true>(a8, K, as, lds, w, wx, ws, rows, XT_D, K, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
-    const int c16 = threadIdx.x & 15;
-    PxAddBias f;
+    const int g = (threadIdx.x & 63) >> 4;
+    float4 b4[C::TN];
 #pragma unroll
-    for (int j = 0; j < C::TN; j++) f.b[j] = bias[n0 + wn0 + 16 * j + c16];
-    residual_add<C>(smem, acc, x, m0 + wm0, n0 + wn0, rows, f);
+    for (int j = 0; j < C::TN; j++) b4[j] = *(const float4 *)(bias + n0 + wn0 + 16 * j + 4 * g);
+    residual_add_t<C>(smem, [&](int j, int i) {
+        const v4f v = acc[i][j];
+        return v4f{v[0] + b4[j].x, v[1] + b4[j].y, v[2] + b4[j].z, v[3] + b4[j].w};
+    }, x, m0 + wm0, n0 + wn0, rows);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 // k_px_fc1: h8 [rows][1024] x W1 [4736][1024] -> h = rs (gelu(acc + b1)), gelu(u) = u Phi(u) (exact normal CDF,
 // px_kernels.cu:228-231, by gelu_erf; rs may be NULL = 1), packed to m8 [rows][4736] E4M3 with 1x128 scales
-// ms [37][lds]. A wave's 128 columns are one scale block: each row's |max| meets in a 16-lane DPP reduction, the
-// values are scaled in registers, parked in the wave's own LDS slice 64 columns at a time and stored 8 consecutive
+// ms [37][lds]. A wave's 128 columns are one scale block: each row's |max| meets in a 4-lane reduction (the tile is
+// transposed), the values are scaled in registers, parked in the wave's own LDS slice 64 columns at a time and stored 8 consecutive
 // bytes per lane (8 rows of 64 bytes per wave instruction). The second half of the last column tile lies past
 // unit 4736 and stores nothing.
 // ---------------------------------------------------------------------------------------------------------------
@@ -181,36 +180,41 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restri
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, PX_HID, m0, n0);
     args_resident(bias, rs, m8, ms, lds, rows);
-    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, PX_HID, XT_D, m0, n0, smem, acc);
+    // the tile transposed (TR): lane (g, c16) holds row m0 + wm0 + 16 i + c16 and units 128 blk + 16 j + 4 g + r, so
+    // a row's 128 units lie in the 4 lanes that share c16: its |max| meets in two lane swaps, one scale per lane and
+    // row tile
+    layer_mainloop<C, SP, BsNoPre, true>(h8, XT_D, hs, lds, w, wx, ws, rows, PX_HID, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int blk = (n0 + wn0) >> 7;
     if (blk >= PX_HID / 128) return;  // no block barrier follows: the epilogue uses the wave's own slice only
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
-    float bj[C::TN], rj[C::TN];
+    float4 b4[C::TN], r4[C::TN];
 #pragma unroll
     for (int j = 0; j < C::TN; j++) {
-        const int u = 128 * blk + 16 * j + c16;
-        bj[j] = bias[u];
-        rj[j] = RS ? rs[u] : 1.0f;
+        const int u = 128 * blk + 16 * j + 4 * g;
+        b4[j] = *(const float4 *)(bias + u);
+        r4[j] = RS ? *(const float4 *)(rs + u) : make_float4(1.f, 1.f, 1.f, 1.f);
     }
-    float inv[C::TM][4];
+    float inv[C::TM];
 #pragma unroll
-    for (int i = 0; i < C::TM; i++)
+    for (int i = 0; i < C::TM; i++) {
+        float amax = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float amax = 0.f;
+        for (int j = 0; j < C::TN; j++) {
+            const float bb[4] = {b4[j].x, b4[j].y, b4[j].z, b4[j].w}, rr[4] = {r4[j].x, r4[j].y, r4[j].z, r4[j].w};
 #pragma unroll
-            for (int j = 0; j < C::TN; j++) {
-                const float g = gelu_erf(acc[i][j][r] + bj[j]), v = RS ? g * rj[j] : g;
+            for (int r = 0; r < 4; r++) {
+                const float g = gelu_erf(acc[i][j][r] + bb[r]), v = RS ? g * rr[r] : g;
                 acc[i][j][r] = v;
                 amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
             }
-            amax = row16_absmax(amax);
-            const float sc = block_scale(amax);
-            inv[i][r] = block_scale_inv(sc);
-            const int m = m0 + wm0 + 16 * i + 4 * g + r;
-            if (c16 == 0 && m < rows) ms[(size_t)blk * lds + m] = sc;
         }
+        amax = col4_absmax(amax);
+        const float sc = block_scale(amax);
+        inv[i] = block_scale_inv(sc);
+        const int m = m0 + wm0 + 16 * i + c16;
+        if (g == 0 && m < rows) ms[(size_t)blk * lds + m] = sc;
+    }
     float *tr = (float *)(smem + (threadIdx.x >> 6) * LAYER_RES_SLICE);
     const __amdgpu_buffer_rsrc_t rm = buf_rsrc(m8, (uint32_t)rows * PX_HID);
     const int rsub = lane >> 3, ch = lane & 7;
@@ -220,10 +224,11 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_fc1(const uint8_t *__restri
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++)
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    tr[(16 * i + 4 * g + r) * 68 + 16 * jj + c16] = acc[i][4 * pass + jj][r] * inv[i][r];
+            for (int jj = 0; jj < 4; jj++) {
+                const v4f v = acc[i][4 * pass + jj];
+                *(float4 *)(tr + (16 * i + c16) * 68 + 16 * jj + 4 * g) =
+                    make_float4(v[0] * inv[i], v[1] * inv[i], v[2] * inv[i], v[3] * inv[i]);
+            }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
 #pragma unroll
         for (int it = 0; it < 8; it++) {

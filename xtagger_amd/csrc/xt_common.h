@@ -182,6 +182,22 @@ __device__ __forceinline__ float row8_absmax(float v)
     u = __builtin_elementwise_max(u, dpp_u<0x141>(u));
     return __uint_as_float(u);
 }
+// |max| of non-negative v over the 4 lanes that share lane & 15 (lanes i, i ^ 16, i ^ 32, i ^ 48): two lane swaps
+__device__ __forceinline__ float col4_absmax(float v)
+{
+    const int lane = __lane_id();
+    uint32_t u = __float_as_uint(v);
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        u = __builtin_elementwise_max(u, lane < 32 ? r[1] : r[0]);
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        u = __builtin_elementwise_max(u, (lane & 16) ? r[0] : r[1]);
+    }
+    return __uint_as_float(u);
+}
+
 __device__ __forceinline__ float row16_absmax(float v)
 {
     uint32_t u = __float_as_uint(v);
