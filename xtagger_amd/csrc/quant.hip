@@ -141,22 +141,39 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
     const int m0 = tm * C::BM, n0 = tn * C::BN, lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int Npad = (N + 127) & ~127;
     args_resident(Cp, ldc, N, M, lds);
-    if constexpr (SP) bs_mainloop_sp<C, BsNoPre, false>(A, lda, sa, lds, W, WX, sw, M, Npad, K, m0, n0, smem, acc);
-    else bs_mainloop<C, BsNoPre, false>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
-    int wm0, wn0;
-    bs_wave_origin<C>(wm0, wn0);
-    if (OUT == 1) {
+    // the tile transposed (acc[i][j][r]: row m0 + wm0 + 16 i + c16, column n0 + wn0 + 16 j + 4 g + r): the sparse
+    // loop's own layout, and the dense loop's with TR
+    if constexpr (SP) {
+        v4f accT[C::TN][C::TM];
+        bs_mainloop_sp_t<C, BsNoPre, false>(A, lda, sa, lds, W, WX, sw, M, Npad, K, m0, n0, smem, accT);
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
-            for (int j = 0; j < C::TN; j++) {
-                const int col = n0 + wn0 + 16 * j + c16;
+            for (int j = 0; j < C::TN; j++) acc[i][j] = accT[j][i];
+    } else {
+        bs_mainloop<C, BsNoPre, false, true>(A, lda, sa, lds, W, sw, M, Npad, K, m0, n0, smem, acc);
+    }
+    int wm0, wn0;
+    bs_wave_origin<C>(wm0, wn0);
+    if (OUT == 1) {
+        const bool v4ok = (ldc | N) % 4 == 0 && (((uintptr_t)Cp) & 15) == 0;  // whole 16-byte column quads
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = m0 + wm0 + 16 * i + 4 * g + r;
-                    if (row < M && col < N) ((float *)Cp)[(size_t)row * ldc + col] = acc[i][j][r];
+        for (int i = 0; i < C::TM; i++) {
+            const int row = m0 + wm0 + 16 * i + c16;
+            if (row >= M) continue;
+            float *crow = (float *)Cp + (size_t)row * ldc;
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                const int col = n0 + wn0 + 16 * j + 4 * g;
+                if (v4ok) {
+                    if (col < N) *(float4 *)(crow + col) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (col + r < N) crow[col + r] = acc[i][j][r];
                 }
             }
+        }
         return;
     }
     uint16_t *Cb = (uint16_t *)Cp;
@@ -165,10 +182,10 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
             for (int j = 0; j < C::TN; j++) {
-                const int col = n0 + wn0 + 16 * j + c16;
+                const int row = m0 + wm0 + 16 * i + c16;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const int row = m0 + wm0 + 16 * i + 4 * g + r;
+                    const int col = n0 + wn0 + 16 * j + 4 * g + r;
                     if (row < M && col < N) Cb[(size_t)row * ldc + col] = f2bf(acc[i][j][r]);
                 }
             }
@@ -183,9 +200,10 @@ __global__ void __launch_bounds__(C::NT) k_gemm(const uint8_t *__restrict__ A, i
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) tr[(16 * i + 4 * g + r) * 68 + 16 * j + c16] = acc[i][4 * pass + j][r];
+            for (int j = 0; j < 4; j++) {
+                const v4f v = acc[i][4 * pass + j];
+                *(float4 *)(tr + (16 * i + c16) * 68 + 16 * j + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
+            }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slice is the wave's own: no block barrier needed
         const int col = n0 + wn0 + 64 * pass + 8 * ch;
 #pragma unroll
