@@ -29,10 +29,43 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
     int m0, n0, wm0, wn0;
     layer_tile<C>(rows, 3 * XT_D, m0, n0);
     args_resident(cs, q, k, vt, lds, rows);
-    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, acc);
     bs_wave_origin<C>(wm0, wn0);
     const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
     const int part = n0 >> 10, head0 = ((n0 & 1023) + wn0) >> 6;
+    // v: the wave's 64 rows x 128 dims (two heads) are transposed through its own LDS slice ([128 dims][68] bf16,
+    // padded rows), then lanes walk rows (consecutive tokens). The slice takes the tile in whichever layout the main
+    // loop leaves it: the sparse loop's transposed tile directly (no pass through the dense layout first), the dense
+    // tile as one 8-byte write of four consecutive tokens per (row tile, column tile).
+    uint16_t *tr = (uint16_t *)(smem + (threadIdx.x >> 6) * 128 * 68 * 2);
+    auto v_out = [&]() {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int m = m0 + wm0 + lane;
+        if (m < rows) {
+            const int b = m / XT_T, t = m - b * XT_T;
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                uint16_t *dst = vt + ((size_t)b * XT_NH + head0 + hh) * XT_HD * XT_TP + t;
+#pragma unroll 8
+                for (int d = 0; d < XT_HD; d++) dst[(size_t)d * XT_TP] = tr[(64 * hh + d) * 68 + lane];
+            }
+        }
+    };
+    if constexpr (SP) {
+        if (part == 2) {  // a separate copy of the sparse loop: its transposed tile goes straight into the slice
+            v4f accT[C::TN][C::TM];  // accT[j][i][r]: dim 16 j + 4 g + r, row 16 i + c16 of the wave tile
+            bs_mainloop_sp_t<C>(h8, XT_D, hs, lds, w, wx, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, accT);
+#pragma unroll
+            for (int j = 0; j < C::TN; j++)
+#pragma unroll
+                for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        tr[(16 * j + 4 * g + r) * 68 + 16 * i + c16] = (uint16_t)pk_bf16(accT[j][i][r], 0.f);
+            v_out();
+            return;
+        }
+    }
+    layer_mainloop<C, SP>(h8, XT_D, hs, lds, w, wx, ws, rows, 3 * XT_D, XT_D, m0, n0, smem, acc);
     if (part < 2) {
         // every (cos, sin) pair of the tile is loaded before the first store: one memory round trip. Patch token t of
         // image b uses row t - 1 of the table (eva_kernels.cu:74-79); cls rows (t = 0) load an out-of-range offset
@@ -79,28 +112,16 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
             }
         return;
     }
-    // v: transpose the wave's 64 rows x 128 dims (two heads) through LDS, then lanes walk rows (consecutive tokens)
-    uint16_t *tr = (uint16_t *)(smem + (threadIdx.x >> 6) * 128 * 66 * 2);  // [128 dims][66] bf16, padded rows
+    // v (dense tile): rows 16 i + 4 g + r of dim 16 j + c16 are four consecutive tokens of one slice row
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
 #pragma unroll
-        for (int j = 0; j < C::TN; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t two = pk_bf16(acc[i][j][r], 0.f);
-                tr[(16 * j + c16) * 66 + 16 * i + 4 * g + r] = (uint16_t)two;
-            }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const int m = m0 + wm0 + lane;
-    if (m < rows) {
-        const int b = m / XT_T, t = m - b * XT_T;
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-            uint16_t *dst = vt + ((size_t)b * XT_NH + head0 + hh) * XT_HD * XT_TP + t;
-#pragma unroll 8
-            for (int d = 0; d < XT_HD; d++) dst[(size_t)d * XT_TP] = tr[(64 * hh + d) * 66 + lane];
+        for (int j = 0; j < C::TN; j++) {
+            typedef unsigned v2u __attribute__((ext_vector_type(2)));
+            *(v2u *)(tr + (16 * j + c16) * 68 + 16 * i + 4 * g) =
+                v2u{pk_bf16(acc[i][j][0], acc[i][j][1]), pk_bf16(acc[i][j][2], acc[i][j][3])};
         }
-    }
+    v_out();
 }
 
 // ---------------------------------------------------------------------------------------------------------------

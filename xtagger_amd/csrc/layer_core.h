@@ -8,14 +8,14 @@
 typedef BsCfg<256, 256, 4, 2, 2> LayerCfg;  // 8 waves of 64 x 128: two heads (qkv) or 64 SwiGLU units (fc1) per wave
 
 // Shared memory of the layer kernels: the main-loop stages, reused by the epilogues (one 64 x 68 fp32 residual slice
-// per wave, one [128][66] bf16 transpose slice per wave, or the fc1 h tile), then 2 KB of per-row statistics and
+// per wave, one [128][68] bf16 transpose slice per wave, or the fc1 h tile), then 2 KB of per-row statistics and
 // 2 KB of per-column fold terms that k_fc2 fills while its first stages load.
 constexpr int LAYER_RES_SLICE = 64 * 68 * 4;
 constexpr int LAYER_ROWSTAT = LayerCfg::NW * LAYER_RES_SLICE;  // byte offset of the per-row statistics
 constexpr int LAYER_SMEM = LAYER_ROWSTAT + 4096;                 // 2 KB row statistics + 2 KB column terms
 static_assert(LAYER_ROWSTAT >= LayerCfg::LDS, "row statistics sit past the main-loop stages");
 static_assert(LAYER_SMEM <= 160 * 1024, "layer kernels fit the LDS");
-static_assert(LayerCfg::NW * 128 * 66 * 2 <= LAYER_ROWSTAT, "v transpose slices fit");
+static_assert(LayerCfg::NW * 128 * 68 * 2 <= LAYER_ROWSTAT, "v transpose slices fit");
 
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b)
 {
