@@ -24,6 +24,15 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b)
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), b2));
 }
 
+// two fp32 values rounded to fp16 (RNE) in one v_cvt_pk_f16_f32, a in the low half
+__device__ __forceinline__ uint32_t pk_f16(float a, float b)
+{
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    asm volatile("" : "+v"(a), "+v"(b));  // fp32 values: no fused fp32-op + fp16-round (v_fma_mix*) single rounding
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
+}
+
 // The layer kernels take their weights dense (w, wx unused) or 2:4-sparse (SP: w = pack24 values, wx = indices).
 // Nlive (default Npad): columns from Nlive on hold zero weights throughout, so waves that own only such columns skip
 // their matrix work.
@@ -96,10 +105,10 @@ __device__ __forceinline__ void residual_add(uint8_t *slices, v4f (&y)[C::TM][C:
             const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
             const v4u v = xv[pass][it];
             v4u o;
-            o[0] = f2h(h2f(v[0] & 0xFFFF) + a.x) | (uint32_t)f2h(h2f(v[0] >> 16) + a.y) << 16;
-            o[1] = f2h(h2f(v[1] & 0xFFFF) + a.z) | (uint32_t)f2h(h2f(v[1] >> 16) + a.w) << 16;
-            o[2] = f2h(h2f(v[2] & 0xFFFF) + b.x) | (uint32_t)f2h(h2f(v[2] >> 16) + b.y) << 16;
-            o[3] = f2h(h2f(v[3] & 0xFFFF) + b.z) | (uint32_t)f2h(h2f(v[3] >> 16) + b.w) << 16;
+            o[0] = pk_f16(h2f(v[0] & 0xFFFF) + a.x, h2f(v[0] >> 16) + a.y);
+            o[1] = pk_f16(h2f(v[1] & 0xFFFF) + a.z, h2f(v[1] >> 16) + a.w);
+            o[2] = pk_f16(h2f(v[2] & 0xFFFF) + b.x, h2f(v[2] >> 16) + b.y);
+            o[3] = pk_f16(h2f(v[3] & 0xFFFF) + b.z, h2f(v[3] >> 16) + b.w);
             __builtin_amdgcn_raw_buffer_store_b128(o, rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
         }
     }
@@ -142,10 +151,10 @@ __device__ __forceinline__ void residual_add_t(uint8_t *slices, Y y, uint16_t *_
             const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
             const v4u v = xv[pass][it];
             v4u o;
-            o[0] = f2h(h2f(v[0] & 0xFFFF) + a.x) | (uint32_t)f2h(h2f(v[0] >> 16) + a.y) << 16;
-            o[1] = f2h(h2f(v[1] & 0xFFFF) + a.z) | (uint32_t)f2h(h2f(v[1] >> 16) + a.w) << 16;
-            o[2] = f2h(h2f(v[2] & 0xFFFF) + b.x) | (uint32_t)f2h(h2f(v[2] >> 16) + b.y) << 16;
-            o[3] = f2h(h2f(v[3] & 0xFFFF) + b.z) | (uint32_t)f2h(h2f(v[3] >> 16) + b.w) << 16;
+            o[0] = pk_f16(h2f(v[0] & 0xFFFF) + a.x, h2f(v[0] >> 16) + a.y);
+            o[1] = pk_f16(h2f(v[1] & 0xFFFF) + a.z, h2f(v[1] >> 16) + a.w);
+            o[2] = pk_f16(h2f(v[2] & 0xFFFF) + b.x, h2f(v[2] >> 16) + b.y);
+            o[3] = pk_f16(h2f(v[3] & 0xFFFF) + b.z, h2f(v[3] >> 16) + b.w);
             __builtin_amdgcn_raw_buffer_store_b128(o, rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
         }
     }
