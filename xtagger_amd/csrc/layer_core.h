@@ -70,6 +70,17 @@ struct ResIdentity {
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
+// x + y for the fp16 x in the low (HI = 0) or high (HI = 1) half of a word and an fp32 y: one v_fma_mix_f32,
+// fma(x, 1, y) with x widened exactly, which rounds once to fp32 as the conversion followed by v_add_f32 does
+template <int HI>
+__device__ __forceinline__ float h_add(uint32_t xw, float y)
+{
+    float r;
+    if constexpr (HI) asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(xw), "v"(y));
+    else asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(xw), "v"(y));
+    return r;
+}
+
 // f(i, j, r, y) maps each accumulator to the value added (row m0 + mw + 16 i + 4 (lane >> 4) + r, column tile j).
 template <class C, class F = ResIdentity>
 __device__ __forceinline__ void residual_add(uint8_t *slices, v4f (&y)[C::TM][C::TN], uint16_t *__restrict__ x,
@@ -105,10 +116,10 @@ __device__ __forceinline__ void residual_add(uint8_t *slices, v4f (&y)[C::TM][C:
             const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
             const v4u v = xv[pass][it];
             v4u o;
-            o[0] = pk_f16(h2f(v[0] & 0xFFFF) + a.x, h2f(v[0] >> 16) + a.y);
-            o[1] = pk_f16(h2f(v[1] & 0xFFFF) + a.z, h2f(v[1] >> 16) + a.w);
-            o[2] = pk_f16(h2f(v[2] & 0xFFFF) + b.x, h2f(v[2] >> 16) + b.y);
-            o[3] = pk_f16(h2f(v[3] & 0xFFFF) + b.z, h2f(v[3] >> 16) + b.w);
+            o[0] = pk_f16(h_add<0>(v[0], a.x), h_add<1>(v[0], a.y));
+            o[1] = pk_f16(h_add<0>(v[1], a.z), h_add<1>(v[1], a.w));
+            o[2] = pk_f16(h_add<0>(v[2], b.x), h_add<1>(v[2], b.y));
+            o[3] = pk_f16(h_add<0>(v[3], b.z), h_add<1>(v[3], b.w));
             __builtin_amdgcn_raw_buffer_store_b128(o, rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
         }
     }
@@ -151,10 +162,10 @@ __device__ __forceinline__ void residual_add_t(uint8_t *slices, Y y, uint16_t *_
             const float4 a = *(const float4 *)(tr + rr * 68 + 8 * ch), b = *(const float4 *)(tr + rr * 68 + 8 * ch + 4);
             const v4u v = xv[pass][it];
             v4u o;
-            o[0] = pk_f16(h2f(v[0] & 0xFFFF) + a.x, h2f(v[0] >> 16) + a.y);
-            o[1] = pk_f16(h2f(v[1] & 0xFFFF) + a.z, h2f(v[1] >> 16) + a.w);
-            o[2] = pk_f16(h2f(v[2] & 0xFFFF) + b.x, h2f(v[2] >> 16) + b.y);
-            o[3] = pk_f16(h2f(v[3] & 0xFFFF) + b.z, h2f(v[3] >> 16) + b.w);
+            o[0] = pk_f16(h_add<0>(v[0], a.x), h_add<1>(v[0], a.y));
+            o[1] = pk_f16(h_add<0>(v[1], a.z), h_add<1>(v[1], a.w));
+            o[2] = pk_f16(h_add<0>(v[2], b.x), h_add<1>(v[2], b.y));
+            o[3] = pk_f16(h_add<0>(v[3], b.z), h_add<1>(v[3], b.w));
             __builtin_amdgcn_raw_buffer_store_b128(o, rx, (int)(off0 + (uint32_t)((8 * it * XT_D + 64 * pass) * 2)), 0, 0);
         }
     }
