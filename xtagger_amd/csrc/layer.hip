@@ -97,10 +97,10 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_qkv(const uint8_t *__restrict_
 #pragma unroll
                     for (int p = 0; p < 2; p++) {
                         float f0 = acc[i][4 * hh + 2 * p][r], f1 = acc[i][4 * hh + 2 * p + 1][r];
-                        if (t) {
+                        if (t) {  // one rounded product and one fma per rotated value
                             const float cr = rot[i][r][2 * p], sr = rot[i][r][2 * p + 1];
-                            const float g0 = f0 * cr - f1 * sr;
-                            f1 = f1 * cr + f0 * sr;
+                            const float g0 = __builtin_fmaf(f0, cr, -(f1 * sr));
+                            f1 = __builtin_fmaf(f1, cr, f0 * sr);
                             f0 = g0;
                         }
                         two[p] = pk_bf16(f0, f1);
