@@ -92,7 +92,7 @@ __global__ void __launch_bounds__(LayerCfg::NT) k_px_qkv(const uint8_t *__restri
                         const float f0 = acc[i][4 * hh + 2 * p][r] + bq[hh][2 * p];
                         const float f1 = acc[i][4 * hh + 2 * p + 1][r] + bq[hh][2 * p + 1];
                         const float cr = rot[i][r][2 * p], sr = rot[i][r][2 * p + 1];
-                        const float g0 = f0 * cr - f1 * sr, g1 = f1 * cr + f0 * sr;
+                        const float g0 = __builtin_fmaf(f0, cr, -(f1 * sr)), g1 = __builtin_fmaf(f1, cr, f0 * sr);
                         two[p] = pk_bf16(g0, g1);
                     }
                     const uint32_t off = (base[i][r] + (uint32_t)(hh * L * XT_HD + 4 * c16)) * 2u;
